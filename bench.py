@@ -1,0 +1,274 @@
+"""Throughput of the bounded differential-attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 64] [--no-cpu]
+
+Workload: 7B-shaped bounded layer, hidden 4096,
+32 query heads, 8 KV heads, head_dim 128, medium cache (W=256, Me=64,
+Ms=64), bf16, random-init weights, state pre-filled with 4096 N(0,1) tokens
+per sequence (chunked prefill, block 256), then decode at batch 64.
+
+A step is one decode token of the hot path for the whole batch: the bank
+kernel (ring FIFO + exact bank + summary bank) and the fused differential
+attention kernel, with the post-projection inputs of every step already
+resident in HBM.  `value` = batch * steps / wall time of the K timed steps.
+
+Also reported (extra keys): the chunked-prefill figure of configs[2]
+(B=4, 32768 tokens, block 256) for the hot path (attention + banks per
+chunk), the dominant kernels' rooflines from HIP events recorded around
+every launch in the timed region, and the CPU oracle timed on a bounded
+sample on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "coda-gqa-l_amd"))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--prefill-tokens", type=int, default=4096, help="tokens pre-filled before decode")
+    ap.add_argument("--prefill-len", type=int, default=32768, help="configs[2] prefill length")
+    ap.add_argument("--prefill-batch", type=int, default=4)
+    ap.add_argument("--block", type=int, default=256)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the configs[2] prefill figure")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    return ap.parse_args()
+
+
+def layer(torch, coda, dtype, dev):
+    torch.manual_seed(0)
+    m = coda.CoDAGQALandmarkPerf2(embed_dim=4096, num_heads=32, num_kv_heads=8, window=256,
+                                  num_landmarks_exact=64, num_landmarks_summary=64, rope_base=1e4)
+    return m.to(dtype=dtype).to(dev).eval()
+
+
+def decode_bytes(m, B, e=2):
+    """Algorithmic HBM bytes of one decode step (bank kernel + attention)."""
+    Hkv, H, Dh, Lbuf, Me, Ms, LF = m.num_kv_heads, m.num_heads, m.head_dim, m.Lbuf, m.Me, m.Ms, m.lf_dim
+    attn = B * Hkv * 2 * Lbuf * Dh * e + B * Lbuf + 2 * B * H * Dh * e + B * H * e
+    bank = (B * Hkv * (Me * Dh * e + Ms * LF * e)          # norm caches read
+            + B * Hkv * Dh * e * 2                         # evicted k, v read
+            + B * Hkv * Dh * e * 2 * 2                     # new k, v read + ring write
+            + B * Hkv * Dh * e * (2 + 1) * 2               # exact slot k, v (r+w) + norm (w)
+            + B * Hkv * Dh * e * 2 * 2 + B * Hkv * LF * e  # summary slot k, v (r+w) + norm (w)
+            + B * (Lbuf + 8 * Me + 16))                    # allowed, LRU stamps, gates
+    return attn, bank
+
+
+def prefill_chunk_flops(m, B, blk, n_prefix):
+    """8*Dh*B*H*(blk*n_prefix + blk*(blk+1)/2): 2 streams x (QK^T + PV)."""
+    return 8 * m.head_dim * B * m.num_heads * (blk * n_prefix + blk * (blk + 1) / 2)
+
+
+def main():
+    a = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: the bounded layer shards by batch with no communication, "
+              "and this build runs on a single GPU only (use --gpus 1).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import coda_gqa_l as coda
+
+    dev = "cuda:0"
+    dt = torch.bfloat16
+    B = a.batch
+    m = layer(torch, coda, dt, dev)
+    H, Hkv, Dh = m.num_heads, m.num_kv_heads, m.head_dim
+    g = torch.Generator(device=dev).manual_seed(1)
+
+    # ---------------------------------------------------------------- state
+    st = m.init_state(batch_size=B, device=dev, dtype=dt)
+    with torch.no_grad():
+        for t0 in range(0, a.prefill_tokens, 2048):
+            n = min(2048, a.prefill_tokens - t0)
+            x = torch.randn(B, n, 4096, generator=g, device=dev, dtype=dt)
+            _, st = m.prefill_chunked(x, st, block_size=a.block, return_outputs=False)
+    torch.cuda.synchronize()
+
+    # ---------------------------------------------------------------- inputs
+    n_steps = a.warmup + a.steps
+    with torch.no_grad():
+        xs = torch.randn(n_steps, B, 1, 4096, generator=g, device=dev, dtype=dt)
+        q_all, k_all, v_all, g_all, lam_all, cs_all = [], [], [], [], [], []
+        p0 = st.pos
+        cos, sin = m.rope(seq_len=n_steps, offset=p0, device=dev, dtype=dt)
+        for i in range(n_steps):
+            x = xs[i]
+            q_all.append(m._project_q(x))
+            kr, v = m._project_kv_raw(x)
+            k_all.append(coda.apply_rope(kr, cos[i:i + 1], sin[i:i + 1], interleaved=m.rope_interleaved))
+            v_all.append(v)
+            g_all.append(m._write_gate(x).reshape(B).contiguous())
+            lam_all.append(m._lambda(x))
+            cs_all.append((cos[i:i + 1].contiguous(), sin[i:i + 1].contiguous()))
+        heads = torch.empty((B, 1, H, Dh), dtype=dt, device=dev)
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+
+    def run_step(i, ev=None):
+        m._write_one(st, k_new=k_all[i], v_new=v_all[i], g_new=g_all[i])
+        if ev is not None:
+            ev[0].record(stream)
+        m.decode_attend_core(q_all[i], lam_all[i], st, cs_all[i][0], cs_all[i][1], out=heads)
+        if ev is not None:
+            ev[1].record(stream)
+
+    with torch.no_grad():
+        for i in range(a.warmup):
+            run_step(i)
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(a.steps)]
+        t0 = time.perf_counter()
+        for j in range(a.steps):
+            run_step(a.warmup + j, evs[j])
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    wall = t1 - t0
+    ms_step = wall * 1e3 / a.steps
+    tok_s = B * a.steps / wall
+    attn_ms = sum(e0.elapsed_time(e1) for e0, e1 in evs) / a.steps
+    attn_bytes, bank_bytes = decode_bytes(m, B)
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+
+    out = {
+        "metric": "decode tok/s/GPU, 7B-shaped bounded layer, medium cache, batch %d (hot path: banks + "
+                  "fused diff attention)" % B,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) inputs, random-init weights (seed 0), state pre-filled with %d tokens"
+                % a.prefill_tokens,
+        "config": {"workload": "configs[1] decode: hidden 4096, H32/Hkv8/Dh128, W256/Me64/Ms64, bf16",
+                   "batch": B, "prefilled_tokens": a.prefill_tokens, "Lbuf": m.Lbuf},
+        "roofline": {"bound": "hbm", "kernel": "attn_rows_bf16", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": attn_bytes, "avg_launch_ms": round(attn_ms, 5)},
+        "step_bytes": attn_bytes + bank_bytes,
+        "step_hbm_frac": round((attn_bytes + bank_bytes) / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+    }
+
+    # ---------------------------------------------------------------- prefill
+    if not a.no_prefill:
+        out["prefill"] = bench_prefill(torch, coda, m, a)
+
+    # ---------------------------------------------------------------- CPU baseline
+    if not a.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a)
+    print(json.dumps(out), flush=True)
+
+
+def bench_prefill(torch, coda, m, a):
+    dev = "cuda:0"
+    dt = torch.bfloat16
+    B, L, blk = a.prefill_batch, a.prefill_len, a.block
+    g = torch.Generator(device=dev).manual_seed(7)
+    st = m.init_state(batch_size=B, device=dev, dtype=dt)
+    x = torch.randn(B, L, 4096, generator=g, device=dev, dtype=dt)
+    with torch.no_grad():
+        q = m._project_q(x)
+        kr, v = m._project_kv_raw(x)
+        cos, sin = m.rope(seq_len=L, offset=0, device=dev, dtype=dt)
+        cos, sin = cos.contiguous(), sin.contiguous()
+        k = torch.empty((B, L, m.num_kv_heads, m.head_dim), dtype=dt, device=dev).permute(0, 2, 1, 3)
+        coda.apply_rope(kr, cos, sin, interleaved=m.rope_interleaved, out=k)
+        gate = m._write_gate(x)
+        lam = m._lambda(x)
+        heads = torch.empty((B, L, m.num_heads, m.head_dim), dtype=dt, device=dev)
+        # warm-up pass over a short prefix (plan / workspace / kernels loaded)
+        st_w = m.init_state(batch_size=B, device=dev, dtype=dt)
+        m.prefill_core(q[:, :, :4 * blk], k[:, :, :4 * blk], v[:, :, :4 * blk], gate[:, :4 * blk],
+                       lam[:, :, :4 * blk], cos, sin, st_w, block_size=blk, out=heads)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m.prefill_core(q, k, v, gate, lam, cos, sin, st, block_size=blk, out=heads)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        # attention-kernel-only timing of a steady-state chunk (full prefix)
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 20
+        t_s = L - blk
+        ct, sn = m._theta_tables(dt)
+        w = m._rms_weight(dt)
+        e0.record(stream)
+        for _ in range(reps):
+            coda.ops.bounded_attention(
+                q=q[:, :, t_s:], rope_cos=cos[t_s:], rope_sin=sin[t_s:], rope_interleaved=m.rope_interleaved,
+                theta_cos=ct, theta_sin=sn, k_prefix=st.k_buf, v_prefix=st.v_buf, allowed=st.allowed,
+                k_block=k[:, :, t_s:], v_block=v[:, :, t_s:], lam=lam[:, :, t_s:], rms_weight=w, eps=m._eps,
+                out=heads[:, t_s:].permute(0, 2, 1, 3))
+        e1.record(stream)
+        torch.cuda.synchronize()
+        attn_ms = e0.elapsed_time(e1) / reps
+        n_prefix = int(st.allowed[0].sum().item())
+    flops = prefill_chunk_flops(m, B, blk, n_prefix)
+    tflops = flops / (attn_ms * 1e-3) / 1e12
+    return {"metric": "chunked-prefill tok/s (configs[2], hot path: attention + banks per chunk)",
+            "value": round(B * L / wall, 1), "unit": "tok/s", "batch": B, "seq_len": L, "block": blk,
+            "ms_total": round(wall * 1e3, 3),
+            "roofline": {"bound": "mfma", "kernel": "attn_tile_bf16", "achieved": round(tflops, 2),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                         "flops_per_launch": flops, "avg_launch_ms": round(attn_ms, 5),
+                         "valid_prefix_slots": n_prefix}}
+
+
+def cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a):
+    """The CPU oracle (a restatement of the reference's CPU eager path) on a
+    bounded sample of the same decode workload, on this host's cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from coda_oracle import OracleLayer, OracleState, banks
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    dt = torch.bfloat16
+    o = OracleLayer(embed_dim=4096, num_heads=32, num_kv_heads=8, window=256, num_landmarks_exact=64,
+                    num_landmarks_summary=64, rope_base=1e4).to(dt).eval()
+    o.load_state_dict({k: v.cpu() for k, v in m.state_dict().items()})
+    so = OracleState(k_buf=st.k_buf.cpu(), v_buf=st.v_buf.cpu(), allowed=st.allowed.cpu(),
+                     g_recent=st.g_recent.cpu(), recent_idx=st.recent_idx, recent_filled=st.recent_filled,
+                     mem_last_exact=st.mem_last_exact.cpu(), pos=st.pos, active_exact=st.active_exact,
+                     active_summary=st.active_summary, _exact_v_norm=st._exact_v_norm.cpu(),
+                     _sum_lf_k_norm=st._sum_lf_k_norm.cpu())
+    B = q_all[0].shape[0]
+    n_done = 0
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        while True:
+            i = n_done % len(q_all)
+            qp = so.pos
+            banks.write_one(o, so, k_all[i].cpu(), v_all[i].cpu(), g_all[i].cpu())
+            o.attend_core(q_all[i].cpu(), lam_all[i].cpu().unsqueeze(-1), so, qp)
+            n_done += 1
+            if time.perf_counter() - t0 > a.cpu_seconds or n_done >= 2000:
+                break
+    wall = time.perf_counter() - t0
+    return {"value": round(B * n_done / wall, 2), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"{n_done} decode steps at batch {B} of the same state "
+                                      f"(banks + attention, post-projection inputs), {wall:.1f} s"}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,414 @@
+"""CoDAGQALandmarkPerf2: bounded differential attention with GQA on MI355X.
+
+    out = RMSNorm( Attn(q, K, V) - lambda * Attn(R_theta(q), K, V) )
+    K/V = [recent window W | exact landmarks Me | summary landmarks Ms]
+
+Same constructor, parameters (names, shapes, init order), state object and
+public methods as the reference (src/coda_gqa_l/attention.py:72-760), so
+checkpoints, pickled states and callers carry over.  The projections are
+GEMMs on the device; everything on the bounded path after them runs in the
+HIP kernels of libcoda_mi355x.so:
+  - decode: one bank kernel (ring + exact + summary) and one attention
+    kernel per step, no host sync;
+  - prefill: one candidate-plan kernel per call, then per chunk one
+    attention kernel and three bank kernels, no host sync.
+Host syncs remain only for the reference's data-dependent host ints
+(dynamic bank expansion, the optional metrics dict).
+
+The layer is inference-only on this path: a module in training mode raises
+(the kernels have no backward).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _hip, ops
+from .memory_banks import METRIC_KEYS, MemoryBankMixin
+from .primitives import HeadwiseRMSNorm, RotaryEmbedding, apply_rope
+from .state import CoDAGQALandmarkStatePerf2
+
+__all__ = ["CoDAGQALandmarkPerf2", "CoDAGQALandmarkStatePerf2"]
+
+
+class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
+    def __init__(
+        self,
+        *,
+        embed_dim: int,
+        num_heads: int,
+        num_kv_heads: int,
+        window: int,
+        num_landmarks_exact: int,
+        num_landmarks_summary: int,
+        rope_base: float = 10_000.0,
+        lambda_init_bias: float = -6.0,
+        theta_init: float = math.pi / 2,
+        write_policy: str = "gated",
+        write_gate_init_bias: float = -2.0,
+        write_gate_threshold_exact: float = 0.10,
+        write_gate_threshold_summary: float = 0.05,
+        exact_match_threshold: float = 0.90,
+        exact_novelty_threshold: float = 0.70,
+        exact_refresh_on_hit: bool = False,
+        exact_candidates_per_block: int = 8,
+        summary_eta_init_logit: float = -3.0,
+        summary_candidates_per_block: int = 64,
+        summary_overwrite_on_insert: bool = True,
+        min_landmarks_exact: Optional[int] = None,
+        max_landmarks_exact: Optional[int] = None,
+        min_landmarks_summary: Optional[int] = None,
+        max_landmarks_summary: Optional[int] = None,
+        expansion_t_max: int = 1_000_000,
+        mem_init: str = "random_normal",
+        mask_unused_memory: bool = True,
+        detach_evicted: bool = True,
+        eps: float = 1e-6,
+        collect_metrics: bool = False,
+        head_norm_mode: str = "full",
+        rope_interleaved: bool = True,
+    ):
+        super().__init__()
+        if embed_dim % num_heads != 0:
+            raise ValueError("embed_dim must be divisible by num_heads")
+        if num_heads % num_kv_heads != 0:
+            raise ValueError("num_heads must be divisible by num_kv_heads")
+        if window <= 0:
+            raise ValueError("window must be positive")
+        if num_landmarks_exact < 0 or num_landmarks_summary < 0:
+            raise ValueError("num_landmarks_* must be non-negative")
+        self.embed_dim = int(embed_dim)
+        self.num_heads = int(num_heads)
+        self.num_kv_heads = int(num_kv_heads)
+        self.head_dim = self.embed_dim // self.num_heads
+        if self.head_dim % 2 != 0:
+            raise ValueError("head_dim must be even (RoPE requirement)")
+        self.lf_start = self.head_dim // 2
+        self.lf_dim = self.head_dim - self.lf_start
+        self.energy_scale = math.sqrt(self.head_dim / self.lf_dim)
+        self.window = int(window)
+        me, ms = int(num_landmarks_exact), int(num_landmarks_summary)
+        self.Me_min = int(min_landmarks_exact) if min_landmarks_exact is not None else me
+        self.Me_max = int(max_landmarks_exact) if max_landmarks_exact is not None else me
+        self.Ms_min = int(min_landmarks_summary) if min_landmarks_summary is not None else ms
+        self.Ms_max = int(max_landmarks_summary) if max_landmarks_summary is not None else ms
+        self.expansion_t_max = int(expansion_t_max)
+        if self.Me_min > self.Me_max:
+            raise ValueError(f"min_landmarks_exact ({self.Me_min}) > max ({self.Me_max})")
+        if self.Ms_min > self.Ms_max:
+            raise ValueError(f"min_landmarks_summary ({self.Ms_min}) > max ({self.Ms_max})")
+        if self.Me_min < 0 or self.Ms_min < 0:
+            raise ValueError("min_landmarks_* must be non-negative")
+        self.Me = self.Me_max
+        self.Ms = self.Ms_max
+        self.Lbuf = self.window + self.Me + self.Ms
+
+        D, H, Hkv, Dh = self.embed_dim, self.num_heads, self.num_kv_heads, self.head_dim
+        # parameter creation order equals the reference's, so a seeded
+        # construction yields identical weights
+        self.q_proj = nn.Linear(D, H * Dh, bias=False)
+        self.k_proj = nn.Linear(D, Hkv * Dh, bias=False)
+        self.v_proj = nn.Linear(D, Hkv * Dh, bias=False)
+        self.theta = nn.Parameter(torch.full((H, Dh // 2), float(theta_init)))
+        self.lambda_proj = nn.Linear(D, H, bias=True)
+        nn.init.constant_(self.lambda_proj.bias, float(lambda_init_bias))
+        self.write_policy = write_policy
+        self.write_proj = nn.Linear(D, 1, bias=True)
+        nn.init.zeros_(self.write_proj.weight)
+        nn.init.constant_(self.write_proj.bias, float(write_gate_init_bias))
+        self.write_gate_threshold_exact = float(write_gate_threshold_exact)
+        self.write_gate_threshold_summary = float(write_gate_threshold_summary)
+        self.exact_match_threshold = float(exact_match_threshold)
+        self.exact_novelty_threshold = float(exact_novelty_threshold)
+        self.exact_refresh_on_hit = bool(exact_refresh_on_hit)
+        self.exact_candidates_per_block = int(max(0, exact_candidates_per_block))
+        self.summary_eta_logit = nn.Parameter(torch.full((Hkv,), float(summary_eta_init_logit)))
+        self.summary_candidates_per_block = int(max(0, summary_candidates_per_block))
+        self.summary_overwrite_on_insert = bool(summary_overwrite_on_insert)
+        self.mem_init = mem_init
+        self.mask_unused_memory = bool(mask_unused_memory)
+        self.detach_evicted = bool(detach_evicted)
+        self.collect_metrics = bool(collect_metrics)
+        self.rope_interleaved = bool(rope_interleaved)
+        self.rope = RotaryEmbedding(Dh, base=float(rope_base))
+        self.head_norm_mode = head_norm_mode
+        if head_norm_mode == "full":
+            self.head_norm = HeadwiseRMSNorm(Dh, eps=eps)
+        elif head_norm_mode == "identity":
+            self.head_norm = nn.Identity()
+        else:
+            raise ValueError(f"head_norm_mode must be 'full' or 'identity', got {head_norm_mode!r}")
+        self.o_proj = nn.Linear(H * Dh, D, bias=False)
+        self._eps = float(eps)
+
+    # ------------------------------------------------------------ state
+    def init_state(self, *, batch_size: int, device: torch.device, dtype: torch.dtype,
+                   mem_init: Optional[str] = None) -> CoDAGQALandmarkStatePerf2:
+        """Zero buffers, N(0, 0.02) bank init, norm caches (attention.py:247-338).
+
+        The random bank init draws from the torch CPU generator with the
+        reference's call sequence, so a given torch.manual_seed yields the
+        same initial banks as the reference's CPU path; the norm caches are
+        computed on the device by the HIP normaliser.
+        """
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("coda_gqa_l (MI355X build) keeps its state on a HIP device; got " + str(device))
+        B, Hkv, Dh, W, Me, Ms = int(batch_size), self.num_kv_heads, self.head_dim, self.window, self.Me, self.Ms
+        mode = mem_init if mem_init is not None else self.mem_init
+        if mode not in ("zeros", "random_normal"):
+            raise ValueError("mem_init must be 'zeros' or 'random_normal'")
+        k_host = torch.zeros((B, Hkv, self.Lbuf, Dh), dtype=dtype)
+        v_host = torch.zeros((B, Hkv, self.Lbuf, Dh), dtype=dtype)
+        if mode == "random_normal":
+            if Me > 0:
+                k_host[:, :, W:W + Me, :].normal_(mean=0.0, std=0.02)
+                v_host[:, :, W:W + Me, :].normal_(mean=0.0, std=0.02)
+            if Ms > 0:
+                k_host[:, :, W + Me:, self.lf_start:].normal_(mean=0.0, std=0.02)
+                v_host[:, :, W + Me:, :].normal_(mean=0.0, std=0.02)
+        k_buf = k_host.to(device)
+        v_buf = v_host.to(device)
+        st = CoDAGQALandmarkStatePerf2(
+            k_buf=k_buf, v_buf=v_buf, allowed=torch.zeros((B, self.Lbuf), dtype=torch.bool, device=device),
+            g_recent=torch.zeros((B, W), dtype=torch.float32, device=device), recent_idx=0, recent_filled=0,
+            mem_last_exact=torch.zeros((B, Me), dtype=torch.int64, device=device), pos=0,
+            active_exact=self.Me_min if Me > 0 else 0, active_summary=self.Ms_min if Ms > 0 else 0)
+        L = _hip.lib()
+        code = _hip.dtype_code(dtype)
+        stream = _hip.stream_of(k_buf)
+        if Me > 0:
+            st._exact_v_norm = torch.empty((B, Hkv, Me, Dh), dtype=dtype, device=device)
+            _hip.check(L.coda_unit_rows(code, st._exact_v_norm.data_ptr(), Me * Dh, Dh,
+                                        v_buf[:, :, W:W + Me].data_ptr(), self.Lbuf * Dh, Dh, B * Hkv, Me, Dh,
+                                        stream))
+        if Ms > 0:
+            LF = self.lf_dim
+            st._sum_lf_k_norm = torch.empty((B, Hkv, Ms, LF), dtype=dtype, device=device)
+            _hip.check(L.coda_unit_rows(code, st._sum_lf_k_norm.data_ptr(), Ms * LF, LF,
+                                        k_buf[:, :, W + Me:, self.lf_start:].data_ptr(), self.Lbuf * Dh, Dh,
+                                        B * Hkv, Ms, LF, stream))
+        if self.collect_metrics:
+            st.metrics = {k: (0.0 if k.endswith("ratio") else 0) for k in METRIC_KEYS}
+            st.metrics["active_exact"] = st.active_exact
+            st.metrics["active_summary"] = st.active_summary
+        return st
+
+    # ------------------------------------------------------------ expansion
+    def _log_ceiling(self, tokens_seen: int) -> Tuple[int, int]:
+        """Capacity ceiling after `tokens_seen` tokens (attention.py:344-356)."""
+        if self.expansion_t_max <= 0:
+            return self.Me_max, self.Ms_max
+        ratio = min(math.log(1 + tokens_seen) / math.log(1 + self.expansion_t_max), 1.0)
+        return (self.Me_min + int((self.Me_max - self.Me_min) * ratio),
+                self.Ms_min + int((self.Ms_max - self.Ms_min) * ratio))
+
+    def _try_expand(self, state: CoDAGQALandmarkStatePerf2, frustrated_exact: int, frustrated_summary: int) -> None:
+        """Grow the active bank sizes under pressure (attention.py:358-390)."""
+        if self.Me_min == self.Me_max and self.Ms_min == self.Ms_max:
+            return
+        if frustrated_exact <= 0 and frustrated_summary <= 0:
+            return
+        ce, cs = self._log_ceiling(state.pos)
+        de = ds = 0
+        if frustrated_exact > 0 and state.active_exact < ce:
+            de = min(frustrated_exact, ce - state.active_exact)
+            state.active_exact += de
+        if frustrated_summary > 0 and state.active_summary < cs:
+            ds = min(frustrated_summary, cs - state.active_summary)
+            state.active_summary += ds
+        if state.metrics is not None:
+            state.metrics["active_exact"] = state.active_exact
+            state.metrics["active_summary"] = state.active_summary
+            state.metrics["expansions_exact"] += de
+            state.metrics["expansions_summary"] += ds
+
+    # ------------------------------------------------------------ projections
+    def _inference_only(self):
+        if self.training:
+            raise NotImplementedError("CoDAGQALandmarkPerf2 on MI355X is inference-only (no backward kernels); "
+                                      "call .eval()")
+
+    def _project_q(self, x: torch.Tensor) -> torch.Tensor:
+        """(B, L, D) -> (B, H, L, Dh) view of the projection."""
+        B, L, _ = x.shape
+        return self.q_proj(x).view(B, L, self.num_heads, self.head_dim).permute(0, 2, 1, 3)
+
+    def _project_kv_raw(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        B, L, _ = x.shape
+        k = self.k_proj(x).view(B, L, self.num_kv_heads, self.head_dim).permute(0, 2, 1, 3)
+        v = self.v_proj(x).view(B, L, self.num_kv_heads, self.head_dim).permute(0, 2, 1, 3)
+        return k, v
+
+    def _write_gate(self, x: torch.Tensor) -> torch.Tensor:
+        """(B, L) float32 write gate (attention.py:406-410)."""
+        B, L, _ = x.shape
+        if self.write_policy == "none":
+            return torch.ones((B, L), dtype=torch.float32, device=x.device)
+        return torch.sigmoid(self.write_proj(x)).squeeze(-1).to(torch.float32)
+
+    def _lambda(self, x: torch.Tensor) -> torch.Tensor:
+        """(B, H, L) view of sigmoid(lambda_proj(x))."""
+        return torch.sigmoid(self.lambda_proj(x)).permute(0, 2, 1)
+
+    def _theta_tables(self, dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+        return torch.cos(self.theta).to(dtype=dtype).contiguous(), torch.sin(self.theta).to(dtype=dtype).contiguous()
+
+    def _rms_weight(self, dtype) -> Optional[torch.Tensor]:
+        if self.head_norm_mode != "full":
+            return None
+        return self.head_norm.weight.detach().to(dtype).contiguous()
+
+    # ------------------------------------------------------------ decode
+    def decode_attend_core(self, q: torch.Tensor, lam: torch.Tensor, state: CoDAGQALandmarkStatePerf2,
+                           rope_cos: torch.Tensor, rope_sin: torch.Tensor,
+                           out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Attention of one token over the bounded cache: q (B,H,1,Dh)
+        pre-RoPE, lam (B,H,1), tables (1, Dh/2) at the query position.
+        Returns head outputs (B, 1, H, Dh)."""
+        B = q.shape[0]
+        H, Dh = self.num_heads, self.head_dim
+        if out is None:
+            out = torch.empty((B, 1, H, Dh), dtype=q.dtype, device=q.device)
+        ct, sn = self._theta_tables(q.dtype)
+        ops.bounded_attention(
+            q=q, rope_cos=rope_cos.contiguous(), rope_sin=rope_sin.contiguous(),
+            rope_interleaved=self.rope_interleaved, theta_cos=ct, theta_sin=sn, k_prefix=state.k_buf,
+            v_prefix=state.v_buf, allowed=state.allowed if self.mask_unused_memory else None, k_block=None,
+            v_block=None, lam=lam, rms_weight=self._rms_weight(q.dtype), eps=self._eps,
+            out=out.permute(0, 2, 1, 3))
+        return out
+
+    def attend_step(self, x: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *,
+                    query_pos: Optional[int] = None) -> torch.Tensor:
+        """Attend one token over the current cache (attention.py:476-514)."""
+        self._inference_only()
+        _hip.require_device(x)
+        B, L, _ = x.shape
+        assert L == 1
+        self._check_state(state)
+        qp = int(state.pos if query_pos is None else query_pos)
+        cos, sin = self.rope(seq_len=1, offset=qp, device=x.device, dtype=x.dtype)
+        heads = self.decode_attend_core(self._project_q(x), self._lambda(x), state, cos, sin)
+        return self.o_proj(heads.view(B, 1, self.num_heads * self.head_dim))
+
+    def step(self, x: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *, attend: bool = True,
+             write_cache: bool = True, include_current_in_attention: bool = True
+             ) -> Tuple[torch.Tensor, CoDAGQALandmarkStatePerf2]:
+        """One decode token (attention.py:516-547): by default write, then attend."""
+        self._inference_only()
+        _hip.require_device(x)
+        B, L, _ = x.shape
+        assert L == 1
+        q_pos = int(state.pos)
+
+        def write():
+            k_raw, v_new = self._project_kv_raw(x)
+            cosk, sink = self.rope(seq_len=1, offset=q_pos, device=x.device, dtype=x.dtype)
+            k_new = apply_rope(k_raw, cosk, sink, interleaved=self.rope_interleaved)
+            self._write_one(state, k_new=k_new, v_new=v_new, g_new=self._write_gate(x))
+
+        if attend and include_current_in_attention and write_cache:
+            write()
+            return self.attend_step(x, state, query_pos=q_pos), state
+        y = self.attend_step(x, state, query_pos=q_pos) if attend else torch.zeros_like(x)
+        if write_cache:
+            write()
+        return y, state
+
+    # ------------------------------------------------------------ prefill
+    def prefill_core(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, lam: torch.Tensor,
+                     rope_cos: torch.Tensor, rope_sin: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *,
+                     block_size: int, write_cache: bool = True, return_heads: bool = True,
+                     out: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
+        """The chunk loop after the projections (attention.py:611-724).
+
+        q (B,H,L,Dh) pre-RoPE; k (B,Hkv,L,Dh) post-RoPE; v (B,Hkv,L,Dh);
+        g (B,L) float32; lam (B,H,L); tables (L, Dh/2) of the positions.
+        Returns head outputs (B, L, H, Dh) when return_heads.
+        """
+        B, H, L, Dh = q.shape
+        if return_heads and out is None:
+            out = torch.empty((B, L, H, Dh), dtype=q.dtype, device=q.device)
+        ct, sn = self._theta_tables(q.dtype)
+        w = self._rms_weight(q.dtype)
+        self._check_state(state)
+        g = g if g.stride(-1) == 1 else g.contiguous()
+        plan = kmax = None
+        do_e = do_s = False
+        ws = eta = None
+        head = int(state.recent_idx) if state.recent_filled >= self.window else 0
+        filled = int(state.recent_filled)
+        if write_cache:
+            plan, kmax, do_e, do_s = self._plan_candidates(state, g, L, block_size)
+            ws = self._block_workspace(state, kmax)
+            eta = self._eta_logit_f32(q.device) if self.Ms > 0 else None
+        p0 = int(state.pos)
+        t = 0
+        c = 0
+        while t < L:
+            blk = min(int(block_size), L - t)
+            if return_heads:
+                ops.bounded_attention(
+                    q=q[:, :, t:t + blk], rope_cos=rope_cos[t:t + blk], rope_sin=rope_sin[t:t + blk],
+                    rope_interleaved=self.rope_interleaved, theta_cos=ct, theta_sin=sn, k_prefix=state.k_buf,
+                    v_prefix=state.v_buf, allowed=state.allowed if self.mask_unused_memory else None,
+                    k_block=k[:, :, t:t + blk], v_block=v[:, :, t:t + blk], lam=lam[:, :, t:t + blk],
+                    rms_weight=w, eps=self._eps, out=out[:, t:t + blk].permute(0, 2, 1, 3))
+            if write_cache:
+                head, filled = self._write_block(
+                    state, k_blk=k[:, :, t:t + blk], v_blk=v[:, :, t:t + blk], g_blk=g[:, t:t + blk],
+                    pos0=p0 + t, ring_head=head, ring_filled=filled, plan_c=plan[c], kmax=kmax, do_e=do_e,
+                    do_s=do_s, workspace=ws, eta=eta)
+                state.pos = p0 + t + blk
+            t += blk
+            c += 1
+        if write_cache:
+            self._ring_to_time_order(state, head, filled)
+        return out
+
+    def prefill_chunked(self, x_seq: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *, block_size: int = 256,
+                        write_cache: bool = True, return_outputs: bool = True
+                        ) -> Tuple[Optional[torch.Tensor], CoDAGQALandmarkStatePerf2]:
+        """Chunked prefill over the bounded cache (attention.py:567-728)."""
+        self._inference_only()
+        _hip.require_device(x_seq)
+        B, L, _ = x_seq.shape
+        if L == 0:
+            return (x_seq[:, :0, :].clone() if return_outputs else None), state
+        if block_size <= 0:
+            raise ValueError("block_size must be positive")
+        p0 = int(state.pos)
+        q = self._project_q(x_seq)
+        k_raw, v = self._project_kv_raw(x_seq)
+        cos, sin = self.rope(seq_len=L, offset=p0, device=x_seq.device, dtype=x_seq.dtype)
+        cos, sin = cos.contiguous(), sin.contiguous()
+        # roped keys in the token-major layout of v, so K and V share strides
+        k = torch.empty((B, L, self.num_kv_heads, self.head_dim), dtype=x_seq.dtype,
+                        device=x_seq.device).permute(0, 2, 1, 3)
+        apply_rope(k_raw, cos, sin, interleaved=self.rope_interleaved, out=k)
+        heads = self.prefill_core(q, k, v, self._write_gate(x_seq), self._lambda(x_seq), cos, sin, state,
+                                  block_size=block_size, write_cache=write_cache, return_heads=return_outputs)
+        if not return_outputs:
+            return None, state
+        return self.o_proj(heads.view(B, L, self.num_heads * self.head_dim)), state
+
+    # ------------------------------------------------------------ utility
+    def cache_bytes(self, *, batch_size: int, dtype: torch.dtype) -> int:
+        """Inference state size in bytes (attention.py:734-751)."""
+        B = int(batch_size)
+        e = torch.tensor([], dtype=dtype).element_size()
+        kv = 2 * B * self.num_kv_heads * self.Lbuf * self.head_dim * e
+        exact_norm = B * self.num_kv_heads * self.Me * self.head_dim * e if self.Me > 0 else 0
+        sum_norm = B * self.num_kv_heads * self.Ms * self.lf_dim * e if self.Ms > 0 else 0
+        return int(kv + exact_norm + sum_norm + B * self.window * 4 + B * self.Lbuf + B * self.Me * 8)
+
+    def reset_metrics(self, state: CoDAGQALandmarkStatePerf2) -> None:
+        """Zero every metrics counter (attention.py:753-760)."""
+        if state.metrics is not None:
+            for k in state.metrics:
+                state.metrics[k] = 0 if isinstance(state.metrics[k], int) else 0.0

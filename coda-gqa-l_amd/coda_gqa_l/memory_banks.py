@@ -1,0 +1,232 @@
+"""Host orchestration of the bank kernels (ring FIFO, exact bank, summary bank).
+
+The reference implements bank maintenance as ~100 eager torch ops per
+prefill chunk and ~40 per decode token with several host syncs each
+(src/coda_gqa_l/memory_banks.py:183-950).  Here a decode token is one
+kernel (coda_decode_write) and a prefill chunk is three (coda_block_write);
+the candidate choice of every chunk of a prefill call is planned up front
+by one kernel (coda_block_plan), since the evicted gates depend only on the
+token stream.  Within a prefill call the ring stays circular (head =
+oldest slot); the call ends with the reference's layout (time order at
+slots 0..filled-1, recent_idx = 0).
+
+Host syncs happen only where the reference's semantics need host ints that
+depend on device data: dynamic bank expansion (min < max capacities) and
+the optional metrics dict.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _hip
+from .state import CoDAGQALandmarkStatePerf2
+
+METRIC_KEYS = ("exact_hits", "exact_inserts", "exact_overwrites", "exact_fill_ratio", "summary_updates",
+               "summary_inserts", "summary_fill_ratio", "tokens_gated_out", "total_evictions", "exact_frustrated",
+               "summary_frustrated", "active_exact", "active_summary", "expansions_exact", "expansions_summary")
+
+_COUNTER_KEYS = {
+    _hip.CNT_EXACT_HITS: "exact_hits", _hip.CNT_EXACT_INSERTS: "exact_inserts",
+    _hip.CNT_EXACT_OVERWRITES: "exact_overwrites", _hip.CNT_SUMMARY_UPDATES: "summary_updates",
+    _hip.CNT_SUMMARY_INSERTS: "summary_inserts", _hip.CNT_TOKENS_GATED_OUT: "tokens_gated_out",
+    _hip.CNT_EXACT_FRUSTRATED: "exact_frustrated",
+}
+
+
+class MemoryBankMixin:
+    """Bank maintenance for CoDAGQALandmarkPerf2 (memory_banks.py:36-950)."""
+
+    # ------------------------------------------------------------ plumbing
+    def _expandable(self) -> bool:
+        return self.Me_min < self.Me_max or self.Ms_min < self.Ms_max
+
+    def _check_state(self, st: CoDAGQALandmarkStatePerf2) -> None:
+        _hip.require_device(st.k_buf, st.v_buf, st.allowed, st.g_recent, st.mem_last_exact)
+        B, Hkv, Lbuf, Dh = st.k_buf.shape
+        if (Hkv, Lbuf, Dh) != (self.num_kv_heads, self.Lbuf, self.head_dim):
+            raise ValueError(f"state k_buf shape {tuple(st.k_buf.shape)} does not match the layer")
+        for name in ("k_buf", "v_buf", "allowed", "g_recent", "mem_last_exact"):
+            if not getattr(st, name).is_contiguous():
+                setattr(st, name, getattr(st, name).contiguous())
+        if st.allowed.dtype != torch.bool or st.g_recent.dtype != torch.float32 or \
+                st.mem_last_exact.dtype != torch.int64:
+            raise ValueError("state metadata dtypes must be allowed=bool, g_recent=float32, mem_last_exact=int64")
+        for name in ("_exact_v_norm", "_sum_lf_k_norm"):
+            t = getattr(st, name)
+            if t is not None:
+                if t.dtype != st.k_buf.dtype:
+                    # norm caches follow the buffer dtype (a state moved with a
+                    # dtype cast of the caches is brought back to it)
+                    t = t.to(st.k_buf.dtype)
+                setattr(st, name, t.contiguous())
+
+    def _eta_logit_f32(self, device) -> torch.Tensor:
+        return self.summary_eta_logit.detach().to(device=device, dtype=torch.float32).contiguous()
+
+    def _bank_desc(self, st: CoDAGQALandmarkStatePerf2, eta: Optional[torch.Tensor],
+                   metrics: Optional[torch.Tensor], frustrated: Optional[torch.Tensor]) -> _hip.BankDesc:
+        d = _hip.BankDesc()
+        d.dtype = _hip.dtype_code(st.k_buf.dtype)
+        d.B = st.k_buf.shape[0]
+        d.Hkv, d.Dh, d.W, d.Me, d.Ms, d.lf = self.num_kv_heads, self.head_dim, self.window, self.Me, self.Ms, \
+            self.lf_start
+        d.active_exact, d.active_summary = int(st.active_exact), int(st.active_summary)
+        d.k_buf, d.v_buf = st.k_buf.data_ptr(), st.v_buf.data_ptr()
+        d.allowed, d.g_recent, d.mem_last = st.allowed.data_ptr(), st.g_recent.data_ptr(), \
+            st.mem_last_exact.data_ptr()
+        d.exact_v_norm = _hip.ptr(st._exact_v_norm)
+        d.sum_lf_k_norm = _hip.ptr(st._sum_lf_k_norm)
+        d.eta_logit = _hip.ptr(eta)
+        d.gated = int(self.write_policy != "none")
+        d.tau_exact, d.tau_summary = self.write_gate_threshold_exact, self.write_gate_threshold_summary
+        d.tau_match, d.tau_novel = self.exact_match_threshold, self.exact_novelty_threshold
+        d.refresh_on_hit, d.overwrite_on_insert = int(self.exact_refresh_on_hit), \
+            int(self.summary_overwrite_on_insert)
+        d.energy_scale = self.energy_scale
+        d.metrics = _hip.ptr(metrics)
+        d.frustrated = _hip.ptr(frustrated)
+        return d
+
+    def _aux_buffers(self, st, device):
+        metrics = torch.zeros(_hip.NUM_COUNTERS, dtype=torch.int64, device=device) if st.metrics is not None \
+            else None
+        need_fr = (self._expandable() and not self.training) or st.metrics is not None
+        frustrated = torch.zeros(4, dtype=torch.int64, device=device) if need_fr else None
+        return metrics, frustrated
+
+    def _fold_metrics(self, st, counters: Optional[torch.Tensor], evictions: int, exact_ran: bool,
+                      summary_ran: bool) -> None:
+        """Device counters -> the state's metrics dict (reference keys)."""
+        mt = st.metrics
+        if mt is None or counters is None:
+            return
+        c = counters.tolist()
+        for i, key in _COUNTER_KEYS.items():
+            mt[key] += int(c[i])
+        mt["total_evictions"] += int(evictions)
+        W, Me = self.window, self.Me
+        if exact_ran and Me > 0:
+            mt["exact_fill_ratio"] = float(st.allowed[:, W:W + Me].any(dim=0).float().mean().item())
+        if summary_ran and self.Ms > 0:
+            mt["summary_fill_ratio"] = float(st.allowed[:, W + Me:].any(dim=0).float().mean().item())
+
+    def _expand_from(self, st, fr: Optional[torch.Tensor], exact_count_mode: bool, ran_e: bool, ran_s: bool):
+        """Dynamic expansion after a bank update (attention.py:358-390)."""
+        if fr is None:
+            return
+        f = fr.tolist()
+        if ran_e:
+            fr_e = int(f[0]) if exact_count_mode else int(f[0] > 0)
+            if fr_e > 0 and not self.training:
+                self._try_expand(st, fr_e, 0)
+        if ran_s:
+            fr_s = int(f[1] == 0 and f[2] > 0)
+            if st.metrics is not None:
+                st.metrics["summary_frustrated"] += fr_s
+            if fr_s > 0 and not self.training:
+                self._try_expand(st, 0, fr_s)
+
+    # ------------------------------------------------------------ decode
+    def _write_one(self, st: CoDAGQALandmarkStatePerf2, *, k_new: torch.Tensor, v_new: torch.Tensor,
+                   g_new: torch.Tensor) -> None:
+        """One token into the ring; evict into the banks when full
+        (memory_banks.py:183-224).  k_new, v_new (B, Hkv, 1, Dh); g_new (B,)."""
+        self._check_state(st)
+        B = st.k_buf.shape[0]
+        dev = st.k_buf.device
+        kn = k_new.reshape(B, self.num_kv_heads, self.head_dim)
+        vn = v_new.reshape(B, self.num_kv_heads, self.head_dim)
+        if kn.stride(-1) != 1 or kn.stride() != vn.stride():
+            kn, vn = kn.contiguous(), vn.contiguous()
+        g = g_new.reshape(B).to(torch.float32).contiguous()
+        evict = st.recent_filled >= self.window
+        metrics, fr = self._aux_buffers(st, dev) if evict else (None, None)
+        eta = self._eta_logit_f32(dev) if self.Ms > 0 else None
+        d = self._bank_desc(st, eta, metrics, fr)
+        _hip.check(_hip.lib().coda_decode_write(
+            d, kn.data_ptr(), vn.data_ptr(), kn.stride(0), kn.stride(1), g.data_ptr(), int(st.recent_idx),
+            int(st.recent_filled), int(st.pos), _hip.stream_of(kn)))
+        if not evict:
+            st.recent_filled += 1
+        else:
+            j = int(st.recent_idx)
+            self._fold_metrics(st, metrics, 1, self.Me > 0, self.Ms > 0)
+            self._expand_from(st, fr, False, self.Me > 0, self.Ms > 0)
+            st.recent_idx = (j + 1) % self.window
+        st.pos += 1
+
+    # ------------------------------------------------------------ prefill
+    def _plan_candidates(self, st, g_seq: torch.Tensor, L: int, block_size: int):
+        """Candidate order of every chunk (memory_banks.py:459-510)."""
+        do_e = self.Me > 0 and self.exact_candidates_per_block > 0
+        do_s = self.Ms > 0 and self.summary_candidates_per_block > 0
+        kmax = max(self.exact_candidates_per_block if do_e else 0, self.summary_candidates_per_block if do_s else 0)
+        kmax = max(1, min(kmax, block_size))
+        n_chunks = (L + block_size - 1) // block_size
+        B = g_seq.shape[0]
+        plan = torch.empty((n_chunks, B, kmax), dtype=torch.int32, device=g_seq.device)
+        if do_e or do_s:
+            head = int(st.recent_idx) if st.recent_filled >= self.window else 0
+            _hip.check(_hip.lib().coda_block_plan(
+                st.g_recent.data_ptr(), head, int(st.recent_filled), self.window, g_seq.data_ptr(),
+                g_seq.stride(0), B, L, block_size, self.exact_candidates_per_block,
+                self.summary_candidates_per_block, int(do_e), int(do_s), plan.data_ptr(), kmax,
+                _hip.stream_of(g_seq)))
+        return plan, kmax, do_e, do_s
+
+    def _write_block(self, st, *, k_blk: torch.Tensor, v_blk: torch.Tensor, g_blk: torch.Tensor, pos0: int,
+                     ring_head: int, ring_filled: int, plan_c: torch.Tensor, kmax: int, do_e: bool, do_s: bool,
+                     workspace: Optional[torch.Tensor], eta: Optional[torch.Tensor]):
+        """Evict / update banks / ring write for one chunk (memory_banks.py:438-564).
+
+        k_blk, v_blk (B, Hkv, blk, Dh) views; g_blk (B, blk) float32 view.
+        Returns the ring (head, filled) after the chunk.
+        """
+        B, Hkv, blk, Dh = k_blk.shape
+        W = self.window
+        total = ring_filled + blk
+        keep_len = min(W, total)
+        n_ev = total - keep_len
+        Te = min(self.exact_candidates_per_block, n_ev) if do_e else 0
+        Ts = min(self.summary_candidates_per_block, n_ev) if do_s else 0
+        metrics, fr = self._aux_buffers(st, k_blk.device) if n_ev > 0 else (None, None)
+        d = self._bank_desc(st, eta, metrics, fr)
+        ws_ptr, ws_bytes = (workspace.data_ptr(), workspace.numel()) if workspace is not None else (None, 0)
+        if k_blk.stride() != v_blk.stride():
+            v_blk = v_blk.contiguous()
+            k_blk = k_blk.contiguous()
+        _hip.check(_hip.lib().coda_block_write(
+            d, k_blk.data_ptr(), v_blk.data_ptr(), k_blk.stride(0), k_blk.stride(1), k_blk.stride(2),
+            g_blk.data_ptr(), g_blk.stride(0), blk, ring_head, ring_filled, int(pos0), _hip.ptr(plan_c), kmax,
+            Te, Ts, ws_ptr, ws_bytes, _hip.stream_of(k_blk)))
+        if n_ev > 0:
+            self._fold_metrics(st, metrics, n_ev, Te > 0, Ts > 0)
+            self._expand_from(st, fr, True, Te > 0, Ts > 0)
+        head = ring_head if ring_filled == W else 0
+        if keep_len == W:
+            head = (head + n_ev) % W
+        return head, keep_len
+
+    def _block_workspace(self, st, kmax: int) -> Optional[torch.Tensor]:
+        need = ctypes.c_size_t(0)
+        d = self._bank_desc(st, None, None, None)
+        _hip.check(_hip.lib().coda_block_workspace_bytes(d, kmax, need))
+        if need.value == 0:
+            return None
+        return torch.empty(need.value, dtype=torch.uint8, device=st.k_buf.device)
+
+    def _ring_to_time_order(self, st, head: int, filled: int) -> None:
+        """Circular ring -> time order at slots 0..filled-1 (memory_banks.py:152-177)."""
+        if filled == self.window and head != 0:
+            B = st.k_buf.shape[0]
+            e = st.k_buf.element_size()
+            need = B * self.num_kv_heads * self.window * self.head_dim * 2 * e + B * self.window * 4
+            ws = torch.empty(need, dtype=torch.uint8, device=st.k_buf.device)
+            d = self._bank_desc(st, None, None, None)
+            _hip.check(_hip.lib().coda_ring_rotate(d, head, ws.data_ptr(), need, _hip.stream_of(st.k_buf)))
+        st.recent_idx = 0
+        st.recent_filled = int(filled)

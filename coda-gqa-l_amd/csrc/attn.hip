@@ -1,0 +1,830 @@
+// Fused two-stream differential attention for gfx950.
+//
+//   out = Norm( softmax(q K^T) V  -  lam * softmax(q_noise K^T) V )
+//
+// One launch covers the whole seam of the reference: RoPE of q, the
+// per-head pairwise rotation that makes q_noise, GQA sharing of K/V (every
+// K/V byte is read once for the G query heads of its KV head and for both
+// streams), the prefix mask of the bounded cache (ring | exact | summary
+// slots gated by `allowed`), the lower-right causal block, the lambda
+// difference and HeadwiseRMSNorm.  Reference seam:
+// src/coda_gqa_l/attention.py:416-465 (+ mask policy :635-693, :476-514).
+//
+// Kernels
+//   attn_rows_bf16   decode shape (2*G*Lq <= 16 query rows per KV head):
+//                    all rows of a KV head packed in one 16-row MFMA tile,
+//                    the 4 waves of a workgroup split the keys; optional
+//                    split over workgroups with a merge kernel.  HBM-bound:
+//                    K/V stream straight from HBM into MFMA fragments (K)
+//                    and a per-wave LDS transpose (V).
+//   attn_tile_bf16   prefill / unbounded shape: a workgroup owns one KV
+//                    head and 16*NQ queries of its G heads; each wave owns
+//                    a (head, 16 queries) pair as two 16-row tiles (signal,
+//                    noise) sharing every K/V fragment; K/V tiles of 64
+//                    keys are staged through LDS once per workgroup.
+//                    MFMA-bound.
+//   attn_generic     fp32 (VALU): config-C1-sized problems and tests.
+//
+// MFMA fragment layouts (wave64, l = lane, n = l % 16, g4 = l / 16):
+//   v_mfma_f32_16x16x32_bf16 A[m=n][k=8*g4+j], B[k=8*g4+j][col=n], j<8
+//   v_mfma_f32_16x16x16_bf16 A[m=n][k=4*g4+j], B[k=4*g4+j][col=n], j<4
+//   both:                    D[m=4*g4+j][col=n], j<4
+// S^T = K Q^T puts keys on m and query rows on n, so the D fragment of S^T
+// is directly the B fragment (P^T, keys on k) of O^T = V^T P^T.
+
+#include "common.h"
+
+#include <math.h>
+
+namespace coda {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+static constexpr float kLog2e = 1.4426950408889634f;
+
+// ------------------------------------------------------------ query prep
+// Eight consecutive channels [d0, d0+8) of the (roped) signal query or of
+// the noise query of (b, h, qi), with the rounding of the reference's eager
+// ops (primitives.py:58-80 rotation, :83-113 RoPE: one rounding per op).
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float x[8]) {
+  if constexpr (sizeof(T) == 2) {
+    uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = bf2f((bf16_t)(w[i] & 0xffffu));
+      x[2 * i + 1] = bf2f((bf16_t)(w[i] >> 16));
+    }
+  } else {
+    float4 a = *reinterpret_cast<const float4*>(p);
+    float4 b = *reinterpret_cast<const float4*>(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void rotate_pairs8(float x[8], const T* c, const T* s) {
+  using E = Elt<T>;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float cc = E::ld(c[p]), ss = E::ld(s[p]);
+    const float e = x[2 * p], o = x[2 * p + 1];
+    x[2 * p] = E::rnd(E::rnd(e * cc) - E::rnd(o * ss));
+    x[2 * p + 1] = E::rnd(E::rnd(e * ss) + E::rnd(o * cc));
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void prep_q8(const coda_attn_desc& a, int b, int h, int qi, int d0,
+                                        int stream, float x[8]) {
+  using E = Elt<T>;
+  const int half = a.Dh >> 1;
+  if (stream == 1 && a.q_noise) {
+    load8<T>((const T*)a.q_noise + b * a.qn_sb + h * a.qn_sh + qi * a.qn_sl + d0, x);
+    return;
+  }
+  const T* qrow = (const T*)a.q + b * a.q_sb + h * a.q_sh + qi * a.q_sl;
+  load8<T>(qrow + d0, x);
+  if (a.rope_cos) {
+    const T* c = (const T*)a.rope_cos + (int64_t)qi * half;
+    const T* s = (const T*)a.rope_sin + (int64_t)qi * half;
+    if (a.rope_interleaved) {
+      rotate_pairs8<T>(x, c + (d0 >> 1), s + (d0 >> 1));
+    } else {
+      float y[8];
+      const bool lo = d0 < half;
+      load8<T>(qrow + (lo ? d0 + half : d0 - half), y);
+      const int f0 = lo ? d0 : d0 - half;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float rot = lo ? -y[j] : y[j];
+        const float cc = E::ld(c[f0 + j]), ss = E::ld(s[f0 + j]);
+        x[j] = E::rnd(E::rnd(x[j] * cc) + E::rnd(rot * ss));
+      }
+    }
+  }
+  if (stream == 1) {
+    rotate_pairs8<T>(x, (const T*)a.theta_cos + (int64_t)h * half + (d0 >> 1),
+                     (const T*)a.theta_sin + (int64_t)h * half + (d0 >> 1));
+  }
+}
+
+// Key visibility for query qi at key index kidx in [0, Lp + Lb).
+__device__ __forceinline__ bool key_visible(const coda_attn_desc& a, int b, int qi, int kidx) {
+  if (kidx < a.Lp) return a.allowed ? (a.allowed[(int64_t)b * a.al_sb + kidx] != 0) : true;
+  const int j = kidx - a.Lp;
+  if (j >= a.Lb) return false;
+  return !a.causal || j <= qi + (a.causal == 2 ? 0 : a.Lb - a.Lq);
+}
+
+template <typename T>
+__device__ __forceinline__ const T* key_ptr(const coda_attn_desc& a, int b, int hk, int kidx,
+                                            bool value) {
+  if (kidx < a.Lp)
+    return (const T*)(value ? a.vp : a.kp) + b * a.p_sb + hk * a.p_sh + (int64_t)kidx * a.p_sl;
+  return (const T*)(value ? a.vb : a.kb) + b * a.b_sb + hk * a.b_sh +
+         (int64_t)(kidx - a.Lp) * a.b_sl;
+}
+
+// ------------------------------------------------------------ epilogue
+// One output row (values os[], on[] of the two streams at this lane's
+// channels) -> Norm(os - lam * on).  bf16 follows the eager op sequence of
+// attention.py:463-464 + primitives.py:23-27 (round after every op; the eps
+// add rounds eps to bf16 like torch's tensor+scalar add); fp32 is plain.
+template <typename T, int NV>
+__device__ __forceinline__ void diff_norm(float (&y)[NV], const float (&os)[NV],
+                                          const float (&on)[NV], const bool (&act)[NV], float lam,
+                                          const T* w, const int (&dd)[NV], float eps, int Dh,
+                                          bool wave_reduce_all, int xor_lo, int xor_hi) {
+  using E = Elt<T>;
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const float s = E::rnd(os[i]), n = E::rnd(on[i]);
+    y[i] = E::rnd(s - E::rnd(lam * n));
+    if (act[i]) sq += E::rnd(y[i] * y[i]);
+  }
+  if (!w) return;
+  if (wave_reduce_all) {
+    sq = wave_sum(sq);
+  } else {
+    for (int o = xor_lo; o <= xor_hi; o <<= 1) sq += __shfl_xor(sq, o, 64);
+  }
+  const float ms = E::rnd(sq / (float)Dh);
+  const float r = E::rnd(1.0f / sqrtf(E::rnd(ms + E::rnd(eps))));
+#pragma unroll
+  for (int i = 0; i < NV; ++i) y[i] = act[i] ? E::rnd(E::rnd(y[i] * r) * E::ld(w[dd[i]])) : 0.f;
+}
+
+// ------------------------------------------------------------ fp32 / VALU
+// Workgroup = (query qi, KV head, batch); rows = 2 streams x G heads.
+template <typename T, int DH>
+__global__ __launch_bounds__(256) void attn_generic(const coda_attn_desc a) {
+  using E = Elt<T>;
+  constexpr int KT = 256, RMAX = 16;
+  __shared__ float qs[RMAX][DH];
+  __shared__ float sc[RMAX][KT];
+  __shared__ float red_alpha[RMAX];
+  __shared__ float m_run[RMAX], l_run[RMAX];
+  const int qi = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int G = a.H / a.Hkv, R = 2 * G;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH));
+
+  for (int i = t; i < R * (DH / 8); i += 256) {
+    const int r = i / (DH / 8), c = i % (DH / 8);
+    const int s = r / G, g = r % G;
+    float x[8];
+    prep_q8<T>(a, b, hk * G + g, qi, c * 8, s, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qs[r][c * 8 + j] = x[j];
+  }
+  if (t < RMAX) { m_run[t] = -INFINITY; l_run[t] = 0.f; }
+  constexpr int TPR = 256 / DH;                 // threads per row group
+  constexpr int RPT = (RMAX + TPR - 1) / TPR;   // rows per thread
+  const int dcol = t % DH, rg = t / DH;
+  float o[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) o[i] = 0.f;
+  __syncthreads();
+
+  const int Lk = a.Lp + a.Lb;
+  for (int k0 = 0; k0 < Lk; k0 += KT) {
+    const int kidx = k0 + t;
+    if (kidx < Lk) {
+      const T* kr = key_ptr<T>(a, b, hk, kidx, false);
+      float acc[RMAX];
+#pragma unroll
+      for (int r = 0; r < RMAX; ++r) acc[r] = 0.f;
+      for (int d = 0; d < DH; d += 8) {
+        float kx[8];
+        load8<T>(kr + d, kx);
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+          if (r < R) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[r] = fmaf(qs[r][d + j], kx[j], acc[r]);
+          }
+        }
+      }
+      const bool vis = key_visible(a, b, qi, kidx);
+      for (int r = 0; r < R; ++r) sc[r][t] = vis ? acc[r] * scale : -INFINITY;
+    } else {
+      for (int r = 0; r < R; ++r) sc[r][t] = -INFINITY;
+    }
+    __syncthreads();
+    for (int r = wv; r < R; r += 4) {
+      float mx = -INFINITY;
+      for (int i = lane; i < KT; i += 64) mx = fmaxf(mx, sc[r][i]);
+      mx = wave_max(mx);
+      const float mold = m_run[r];
+      const float mnew = fmaxf(mold, mx);
+      const float muse = (mnew == -INFINITY) ? 0.f : mnew;
+      float ps = 0.f;
+      for (int i = lane; i < KT; i += 64) {
+        const float p = expf(sc[r][i] - muse);
+        sc[r][i] = p;
+        ps += p;
+      }
+      ps = wave_sum(ps);
+      if (lane == 0) {
+        const float al = expf(mold - muse);
+        red_alpha[r] = al;
+        l_run[r] = l_run[r] * al + ps;
+        m_run[r] = mnew;
+      }
+    }
+    __syncthreads();
+    const int kn = min(KT, Lk - k0);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int r = rg + i * TPR;
+      if (r < R) o[i] *= red_alpha[r];
+    }
+    for (int kk = 0; kk < kn; ++kk) {
+      const float v = E::ld(key_ptr<T>(a, b, hk, k0 + kk, true)[dcol]);
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        const int r = rg + i * TPR;
+        if (r < R) o[i] = fmaf(sc[r][kk], v, o[i]);
+      }
+    }
+    __syncthreads();
+  }
+  // normalise into qs (reused as the output staging buffer)
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    const int r = rg + i * TPR;
+    if (r < R) qs[r][dcol] = l_run[r] > 0.f ? o[i] / l_run[r] : 0.f;
+  }
+  __syncthreads();
+  // epilogue: wave per head of the group
+  constexpr int NV = (DH + 63) / 64;
+  for (int g = wv; g < G; g += 4) {
+    const int h = hk * G + g;
+    float os[NV], on[NV], y[NV];
+    bool act[NV];
+    int dd[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = lane + 64 * i;
+      act[i] = d < DH;
+      dd[i] = act[i] ? d : 0;
+      os[i] = act[i] ? qs[g][dd[i]] : 0.f;
+      on[i] = act[i] ? qs[G + g][dd[i]] : 0.f;
+    }
+    const float lam = E::ld(((const T*)a.lam)[b * a.lam_sb + h * a.lam_sh + qi * a.lam_sl]);
+    diff_norm<T, NV>(y, os, on, act, lam, (const T*)a.rms_w, dd, a.eps, DH, true, 0, 0);
+    T* orow = (T*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_sl;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (act[i]) orow[dd[i]] = E::st(y[i]);
+  }
+}
+
+// ------------------------------------------------------------ MFMA helpers
+__device__ __forceinline__ f32x4 mfma_k32(const bf16x8_t& a, const bf16x8_t& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_k16(const short4_t& a, const short4_t& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8_t pack8(const float x[8]) {
+  uint4 u;
+  u.x = (uint32_t)f2bf(x[0]) | ((uint32_t)f2bf(x[1]) << 16);
+  u.y = (uint32_t)f2bf(x[2]) | ((uint32_t)f2bf(x[3]) << 16);
+  u.z = (uint32_t)f2bf(x[4]) | ((uint32_t)f2bf(x[5]) << 16);
+  u.w = (uint32_t)f2bf(x[6]) | ((uint32_t)f2bf(x[7]) << 16);
+  return __builtin_bit_cast(bf16x8_t, u);
+}
+__device__ __forceinline__ short4_t pack4(float a, float b, float c, float d) {
+  uint2 u;
+  u.x = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+  u.y = (uint32_t)f2bf(c) | ((uint32_t)f2bf(d) << 16);
+  return __builtin_bit_cast(short4_t, u);
+}
+
+// V^T staging for one 16-key sub-tile: [key group kg (4 keys)][channel d]
+// [4 keys] as 8-byte cells.  The row swizzle d ^ (((d >> 5) & 3) << 1) and
+// the 128-byte pad per key group keep both the transposing writes (8 d of
+// one lane) and the MFMA reads (16 consecutive d per lane group) at the
+// minimum of two LDS cycles per wave instruction.
+template <int DH>
+struct VtLayout {
+  static constexpr int kGroupBytes = DH * 8 + 128;
+  static constexpr int kTileBytes = 4 * kGroupBytes;
+  static __device__ __forceinline__ int off(int kg, int d) {
+    return kg * kGroupBytes + ((d ^ (((d >> 5) & 3) << 1)) << 3);
+  }
+};
+
+// Transpose 4 keys x 8 channels (four 16-byte rows) into 8 cells of
+// 4 keys and store them.
+template <int DH>
+__device__ __forceinline__ void store_vt(char* base, int kg, int d0, const uint4 (&v)[4]) {
+  const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&v[0]);
+  const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&v[1]);
+  const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&v[2]);
+  const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&v[3]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int sh = (e & 1) * 16;
+    const int wi = e >> 1;
+    uint2 cell;
+    cell.x = ((w0[wi] >> sh) & 0xffffu) | (((w1[wi] >> sh) & 0xffffu) << 16);
+    cell.y = ((w2[wi] >> sh) & 0xffffu) | (((w3[wi] >> sh) & 0xffffu) << 16);
+    *reinterpret_cast<uint2*>(base + VtLayout<DH>::off(kg, d0 + e)) = cell;
+  }
+}
+
+// ------------------------------------------------------------ decode rows
+// Workgroup = (split, KV head, batch); 4 waves take 16-key tiles in turn.
+// Partial (m, l, O) of the 4 waves merge in LDS; with nsplit > 1 each
+// workgroup leaves its merged partial in `ws` for attn_rows_merge.
+template <int DH>
+__global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, int keys_per_split,
+                                                      float* ws) {
+  constexpr int NC = DH / 32, NM = DH / 16, NW = 4;
+  __shared__ __attribute__((aligned(16))) char vt_smem[NW][VtLayout<DH>::kTileBytes];
+  __shared__ float red_m[NW][16], red_l[NW][16];
+  __shared__ float red_o[NW][16][DH + 4];
+  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int nsplit = gridDim.x;
+  const int G = a.H / a.Hkv, GL = G * a.Lq, R = 2 * GL;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int n = lane & 15, g4 = lane >> 4;
+  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
+
+  // query fragments (B operand of S^T): row n, channels 32c + 8 g4 + j
+  bf16x8_t qf[NC];
+  int row_qi = 0;
+  {
+    const bool live = n < R;
+    const int s = live ? n / GL : 0, rem = live ? n % GL : 0;
+    const int g = rem / a.Lq;
+    row_qi = rem % a.Lq;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (live) prep_q8<bf16_t>(a, b, hk * G + g, row_qi, 32 * c + 8 * g4, s, x);
+      qf[c] = pack8(x);
+    }
+  }
+  const int Lk = a.Lp + a.Lb;
+  const int kbeg = split * keys_per_split;
+  const int kend = min(Lk, kbeg + keys_per_split);
+  float m_i = -INFINITY, l_i = 0.f;
+  f32x4 o[NM];
+#pragma unroll
+  for (int i = 0; i < NM; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  char* vt = vt_smem[wv];
+  // V load roles: lane -> (key group kgl, 8-channel chunk dcl)
+  constexpr int DCH = DH / 8;
+  const int kgl = lane / DCH, dcl = lane % DCH;
+  const bool vload = kgl < 4;
+
+  for (int kt = kbeg + 16 * wv; kt < kend; kt += 16 * NW) {
+    // K fragments straight from memory: key kt + n, channels 32c + 8 g4
+    const int kidx = kt + n;
+    const bool kin = kidx < kend;
+    bf16x8_t kf[NC];
+    {
+      const bf16_t* kr = kin ? key_ptr<bf16_t>(a, b, hk, kidx, false) : nullptr;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        uint4 u = kin ? *reinterpret_cast<const uint4*>(kr + 32 * c + 8 * g4) : uint4{0, 0, 0, 0};
+        kf[c] = __builtin_bit_cast(bf16x8_t, u);
+      }
+    }
+    uint4 vv[4];
+    if (vload) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int vk = kt + 4 * kgl + jj;
+        vv[jj] = vk < kend ? *reinterpret_cast<const uint4*>(key_ptr<bf16_t>(a, b, hk, vk, true) + 8 * dcl)
+                           : uint4{0, 0, 0, 0};
+      }
+    }
+    f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) st = mfma_k32(kf[c], qf[c], st);
+    // this lane: keys kt + 4 g4 + j, query row n
+    float sv[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kk = kt + 4 * g4 + j;
+      const bool vis = kk < kend && key_visible(a, b, row_qi, kk);
+      sv[j] = vis ? st[j] * scale : -INFINITY;
+      tmax = fmaxf(tmax, sv[j]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mnew = fmaxf(m_i, tmax);
+    const float muse = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = exp2f(m_i - muse);
+    float p[4], ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      p[j] = bf2f(f2bf(exp2f(sv[j] - muse)));
+      ps += p[j];
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l_i = l_i * alpha + ps;
+    m_i = mnew;
+    const short4_t pf = pack4(p[0], p[1], p[2], p[3]);
+    if (vload) store_vt<DH>(vt, kgl, 8 * dcl, vv);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes of this wave done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt) {
+      const uint2 cell = *reinterpret_cast<const uint2*>(vt + VtLayout<DH>::off(g4, 16 * mt + n));
+      o[mt] *= alpha;
+      o[mt] = mfma_k16(__builtin_bit_cast(short4_t, cell), pf, o[mt]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // merge the 4 waves
+  if (g4 == 0) { red_m[wv][n] = m_i; red_l[wv][n] = l_i; }
+#pragma unroll
+  for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red_o[wv][n][16 * mt + 4 * g4 + j] = o[mt][j];
+  __syncthreads();
+
+  if (nsplit > 1) {
+    // partial row r: [m, l, O(DH)] unnormalised w.r.t. the merged max
+    float* base = ws + ((((int64_t)b * a.Hkv + hk) * nsplit + split) * 16) * (DH + 2);
+    for (int i = threadIdx.x; i < R * (DH + 2); i += 256) {
+      const int r = i / (DH + 2), c = i % (DH + 2);
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, red_m[w][r]);
+      const float Mu = M == -INFINITY ? 0.f : M;
+      float v = 0.f;
+      if (c == 0) {
+        v = M;
+      } else if (c == 1) {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red_l[w][r] * exp2f(red_m[w][r] - Mu);
+      } else {
+#pragma unroll
+        for (int w = 0; w < NW; ++w) v += red_o[w][r][c - 2] * exp2f(red_m[w][r] - Mu);
+      }
+      base[r * (DH + 2) + c] = v;
+    }
+    return;
+  }
+  // single split: merge + epilogue, one wave per (head, query) output row
+  constexpr int NV = (DH + 63) / 64;
+  for (int orow = wv; orow < GL; orow += NW) {
+    const int g = orow / a.Lq, qi = orow % a.Lq, h = hk * G + g;
+    float os[NV], on[NV], y[NV];
+    bool act[NV];
+    int dd[NV];
+    float M[2] = {-INFINITY, -INFINITY}, L[2] = {0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int r = s * GL + orow;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M[s] = fmaxf(M[s], red_m[w][r]);
+      const float Mu = M[s] == -INFINITY ? 0.f : M[s];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) L[s] += red_l[w][r] * exp2f(red_m[w][r] - Mu);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = lane + 64 * i;
+      act[i] = d < DH;
+      dd[i] = act[i] ? d : 0;
+      float acc[2] = {0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const int r = s * GL + orow;
+        const float Mu = M[s] == -INFINITY ? 0.f : M[s];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc[s] += red_o[w][r][dd[i]] * exp2f(red_m[w][r] - Mu);
+        acc[s] = L[s] > 0.f ? acc[s] / L[s] : 0.f;
+      }
+      os[i] = act[i] ? acc[0] : 0.f;
+      on[i] = act[i] ? acc[1] : 0.f;
+    }
+    const float lam = bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + qi * a.lam_sl]);
+    diff_norm<bf16_t, NV>(y, os, on, act, lam, (const bf16_t*)a.rms_w, dd, a.eps, DH, true, 0, 0);
+    bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_sl;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (act[i]) orow_p[dd[i]] = f2bf(y[i]);
+  }
+}
+
+// Merge the per-split partials of attn_rows_bf16 and apply the epilogue.
+template <int DH>
+__global__ __launch_bounds__(256) void attn_rows_merge(const coda_attn_desc a, int nsplit,
+                                                       const float* ws) {
+  const int hk = blockIdx.x, b = blockIdx.y;
+  const int G = a.H / a.Hkv, GL = G * a.Lq;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const float* base = ws + (((int64_t)b * a.Hkv + hk) * nsplit) * 16 * (DH + 2);
+  constexpr int NV = (DH + 63) / 64;
+  for (int orow = wv; orow < GL; orow += 4) {
+    const int g = orow / a.Lq, qi = orow % a.Lq, h = hk * G + g;
+    float os[NV], on[NV], y[NV];
+    bool act[NV];
+    int dd[NV];
+    float M[2] = {-INFINITY, -INFINITY}, L[2] = {0.f, 0.f};
+    for (int s = 0; s < 2; ++s) {
+      const int r = s * GL + orow;
+      for (int sp = 0; sp < nsplit; ++sp) M[s] = fmaxf(M[s], base[(sp * 16 + r) * (DH + 2)]);
+      const float Mu = M[s] == -INFINITY ? 0.f : M[s];
+      for (int sp = 0; sp < nsplit; ++sp) {
+        const float* pr = base + (sp * 16 + r) * (DH + 2);
+        L[s] += pr[1] * exp2f(pr[0] - Mu);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = lane + 64 * i;
+      act[i] = d < DH;
+      dd[i] = act[i] ? d : 0;
+      float acc[2] = {0.f, 0.f};
+      for (int s = 0; s < 2; ++s) {
+        const int r = s * GL + orow;
+        const float Mu = M[s] == -INFINITY ? 0.f : M[s];
+        for (int sp = 0; sp < nsplit; ++sp) {
+          const float* pr = base + (sp * 16 + r) * (DH + 2);
+          acc[s] += pr[2 + dd[i]] * exp2f(pr[0] - Mu);
+        }
+        acc[s] = L[s] > 0.f ? acc[s] / L[s] : 0.f;
+      }
+      os[i] = act[i] ? acc[0] : 0.f;
+      on[i] = act[i] ? acc[1] : 0.f;
+    }
+    const float lam = bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + qi * a.lam_sl]);
+    diff_norm<bf16_t, NV>(y, os, on, act, lam, (const bf16_t*)a.rms_w, dd, a.eps, DH, true, 0, 0);
+    bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_sl;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (act[i]) orow_p[dd[i]] = f2bf(y[i]);
+  }
+}
+
+// ------------------------------------------------------------ prefill tiles
+// Workgroup = (query block of 16*NQ, KV head, batch), NW = G*NQ waves;
+// wave w owns head g = w / NQ and queries q0 + 16*(w % NQ) + [0,16) as two
+// 16-row tiles (signal, noise).
+template <int DH, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_tile_bf16(const coda_attn_desc a, int NQ) {
+  constexpr int NC = DH / 32, NM = DH / 16, KT = 64;
+  constexpr int KROW = DH * 2 + 16;  // padded K row bytes
+  __shared__ __attribute__((aligned(16))) char k_smem[KT * KROW];
+  __shared__ __attribute__((aligned(16))) char v_smem[4 * VtLayout<DH>::kTileBytes];
+  const int qb = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int G = a.H / a.Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int n = lane & 15, g4 = lane >> 4;
+  const int g = wv / NQ, qsub = wv % NQ, h = hk * G + g;
+  const int q0 = qb * 16 * NQ + 16 * qsub;
+  const int qrow = q0 + n;
+  const bool qlive = qrow < a.Lq;
+  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
+
+  bf16x8_t qf[2][NC];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (qlive) prep_q8<bf16_t>(a, b, h, qrow, 32 * c + 8 * g4, s, x);
+      qf[s][c] = pack8(x);
+    }
+  float m_i[2] = {-INFINITY, -INFINITY}, l_i[2] = {0.f, 0.f};
+  f32x4 o[2][NM];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < NM; ++i) o[s][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int Lk = a.Lp + a.Lb;
+  // last key any query of this workgroup can see
+  const int qlast = min(a.Lq - 1, qb * 16 * NQ + 16 * NQ - 1);
+  const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
+  const int klim = a.causal ? min(Lk, a.Lp + qlast + coff + 1) : Lk;
+  constexpr int DCH = DH / 8;
+  const int nthreads = NW * 64;
+
+  for (int k0 = 0; k0 < klim; k0 += KT) {
+    __syncthreads();
+    // K tile: 64 keys x DCH chunks of 16 bytes, row-major (padded rows)
+    for (int i = tid; i < KT * DCH; i += nthreads) {
+      const int kk = i / DCH, dc = i % DCH;
+      const int kidx = k0 + kk;
+      uint4 u = uint4{0, 0, 0, 0};
+      if (kidx < Lk) u = *reinterpret_cast<const uint4*>(key_ptr<bf16_t>(a, b, hk, kidx, false) + 8 * dc);
+      *reinterpret_cast<uint4*>(k_smem + kk * KROW + dc * 16) = u;
+    }
+    // V tile: 16 key groups x DCH chunks, transposed into 4 sub-tiles
+    for (int i = tid; i < 16 * DCH; i += nthreads) {
+      const int kg = i / DCH, dc = i % DCH;
+      uint4 vv[4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int kidx = k0 + 4 * kg + jj;
+        vv[jj] = kidx < Lk ? *reinterpret_cast<const uint4*>(key_ptr<bf16_t>(a, b, hk, kidx, true) + 8 * dc)
+                           : uint4{0, 0, 0, 0};
+      }
+      store_vt<DH>(v_smem + (kg >> 2) * VtLayout<DH>::kTileBytes, kg & 3, 8 * dc, vv);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int sub = 0; sub < KT / 16; ++sub) {
+      const int kt = k0 + 16 * sub;
+      if (kt >= klim) break;
+      f32x4 st[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 u = *reinterpret_cast<const uint4*>(k_smem + (16 * sub + n) * KROW + (32 * c + 8 * g4) * 2);
+        const bf16x8_t kf = __builtin_bit_cast(bf16x8_t, u);
+        st[0] = mfma_k32(kf, qf[0][c], st[0]);
+        st[1] = mfma_k32(kf, qf[1][c], st[1]);
+      }
+      bool vis[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vis[j] = key_visible(a, b, qrow, kt + 4 * g4 + j);
+      short4_t pf[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float sv[4], tmax = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          sv[j] = vis[j] ? st[s][j] * scale : -INFINITY;
+          tmax = fmaxf(tmax, sv[j]);
+        }
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float mnew = fmaxf(m_i[s], tmax);
+        const float muse = mnew == -INFINITY ? 0.f : mnew;
+        const float alpha = exp2f(m_i[s] - muse);
+        float p[4], ps = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          p[j] = bf2f(f2bf(exp2f(sv[j] - muse)));
+          ps += p[j];
+        }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        l_i[s] = l_i[s] * alpha + ps;
+        m_i[s] = mnew;
+        pf[s] = pack4(p[0], p[1], p[2], p[3]);
+#pragma unroll
+        for (int mt = 0; mt < NM; ++mt) o[s][mt] *= alpha;
+      }
+      const char* vsub = v_smem + sub * VtLayout<DH>::kTileBytes;
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) {
+        const uint2 cell = *reinterpret_cast<const uint2*>(vsub + VtLayout<DH>::off(g4, 16 * mt + n));
+        const short4_t vf = __builtin_bit_cast(short4_t, cell);
+        o[0][mt] = mfma_k16(vf, pf[0], o[0][mt]);
+        o[1][mt] = mfma_k16(vf, pf[1], o[1][mt]);
+      }
+    }
+  }
+  // epilogue in registers: lane holds channels 16 mt + 4 g4 + j of row n
+  constexpr int NV = NM * 4;
+  float os[NV], on[NV], y[NV];
+  bool act[NV];
+  int dd[NV];
+#pragma unroll
+  for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = mt * 4 + j;
+      dd[i] = 16 * mt + 4 * g4 + j;
+      act[i] = true;
+      os[i] = l_i[0] > 0.f ? o[0][mt][j] / l_i[0] : 0.f;
+      on[i] = l_i[1] > 0.f ? o[1][mt][j] / l_i[1] : 0.f;
+    }
+  const float lam = qlive ? bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + qrow * a.lam_sl]) : 0.f;
+  diff_norm<bf16_t, NV>(y, os, on, act, lam, (const bf16_t*)a.rms_w, dd, a.eps, DH, false, 16, 32);
+  if (qlive) {
+    bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt) {
+      uint2 u;
+      u.x = (uint32_t)f2bf(y[mt * 4 + 0]) | ((uint32_t)f2bf(y[mt * 4 + 1]) << 16);
+      u.y = (uint32_t)f2bf(y[mt * 4 + 2]) | ((uint32_t)f2bf(y[mt * 4 + 3]) << 16);
+      *reinterpret_cast<uint2*>(orow_p + 16 * mt + 4 * g4) = u;
+    }
+  }
+}
+
+// ------------------------------------------------------------ host side
+static int rows_nsplit(const coda_attn_desc* d) {
+  const int Lk = d->Lp + d->Lb;
+  const int pairs = d->B * d->Hkv;
+  if (pairs >= 512) return 1;
+  int ns = (512 + pairs - 1) / pairs;
+  const int max_ns = (Lk + 63) / 64;
+  ns = ns < max_ns ? ns : max_ns;
+  return ns < 1 ? 1 : ns;
+}
+
+static bool use_rows(const coda_attn_desc* d) {
+  return d->dtype == CODA_BF16 && 2 * (d->H / d->Hkv) * d->Lq <= 16;
+}
+
+static int validate(const coda_attn_desc* d) {
+  CODA_REQUIRE(d != nullptr, "coda_diff_attn_fwd: null descriptor");
+  CODA_REQUIRE(d->dtype == CODA_F32 || d->dtype == CODA_BF16,
+               "coda_diff_attn_fwd: dtype must be CODA_F32 or CODA_BF16 (got %d)", d->dtype);
+  CODA_REQUIRE(d->B >= 0 && d->H > 0 && d->Hkv > 0 && d->Lq >= 0,
+               "coda_diff_attn_fwd: bad sizes B=%d H=%d Hkv=%d Lq=%d", d->B, d->H, d->Hkv, d->Lq);
+  CODA_REQUIRE(d->H % d->Hkv == 0, "coda_diff_attn_fwd: H=%d not a multiple of Hkv=%d", d->H, d->Hkv);
+  CODA_REQUIRE(d->Dh == 32 || d->Dh == 64 || d->Dh == 128,
+               "coda_diff_attn_fwd: head_dim %d unsupported (32, 64, 128)", d->Dh);
+  const int G = d->H / d->Hkv;
+  CODA_REQUIRE(G <= 8, "coda_diff_attn_fwd: %d query heads per KV head unsupported (max 8)", G);
+  CODA_REQUIRE(d->Lp >= 0 && d->Lb >= 0, "coda_diff_attn_fwd: negative key count");
+  CODA_REQUIRE(d->Lp == 0 || (d->kp && d->vp), "coda_diff_attn_fwd: prefix keys missing");
+  CODA_REQUIRE(d->Lb == 0 || (d->kb && d->vb), "coda_diff_attn_fwd: block keys missing");
+  CODA_REQUIRE(d->causal >= 0 && d->causal <= 2, "coda_diff_attn_fwd: causal mode %d unknown", d->causal);
+  CODA_REQUIRE(d->causal != 1 || d->Lb >= d->Lq || d->Lb == 0,
+               "coda_diff_attn_fwd: lower-right causal block needs Lb >= Lq (Lb=%d Lq=%d)", d->Lb, d->Lq);
+  CODA_REQUIRE(d->q && d->lam && d->out, "coda_diff_attn_fwd: q, lam, out are required");
+  CODA_REQUIRE(d->q_noise || (d->theta_cos && d->theta_sin),
+               "coda_diff_attn_fwd: need q_noise or theta tables");
+  CODA_REQUIRE(!d->rope_cos == !d->rope_sin, "coda_diff_attn_fwd: rope_cos/rope_sin come in pairs");
+  CODA_REQUIRE(d->Lp + d->Lb < (1 << 30), "coda_diff_attn_fwd: too many keys");
+  return CODA_OK;
+}
+
+}  // namespace coda
+
+using namespace coda;
+
+extern "C" int coda_attn_workspace_bytes(const coda_attn_desc* d, size_t* bytes) {
+  int rc = validate(d);
+  if (rc) return rc;
+  CODA_REQUIRE(bytes != nullptr, "coda_attn_workspace_bytes: null out pointer");
+  *bytes = 0;
+  if (use_rows(d)) {
+    const int ns = rows_nsplit(d);
+    if (ns > 1) *bytes = (size_t)d->B * d->Hkv * ns * 16 * (d->Dh + 2) * sizeof(float);
+  }
+  return CODA_OK;
+}
+
+template <int DH>
+static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
+  const int G = d->H / d->Hkv;
+  if (d->dtype == CODA_F32) {
+    hipLaunchKernelGGL((attn_generic<float, DH>), dim3(d->Lq, d->Hkv, d->B), dim3(256), 0, st, *d);
+    return check_launch("attn_generic<f32>");
+  }
+  if (use_rows(d)) {
+    const int ns = rows_nsplit(d);
+    const int Lk = d->Lp + d->Lb;
+    int per = ((Lk + ns - 1) / ns + 15) / 16 * 16;
+    if (per < 16) per = 16;
+    const int ns_eff = Lk > 0 ? (Lk + per - 1) / per : 1;
+    if (ns_eff > 1) {
+      size_t need = (size_t)d->B * d->Hkv * ns_eff * 16 * (d->Dh + 2) * sizeof(float);
+      if (!d->workspace || d->workspace_bytes < need)
+        return fail(CODA_ESMALL, "coda_diff_attn_fwd: workspace %zu < %zu bytes", d->workspace_bytes, need);
+    }
+    hipLaunchKernelGGL((attn_rows_bf16<DH>), dim3(ns_eff > 0 ? ns_eff : 1, d->Hkv, d->B), dim3(256), 0, st, *d,
+                       per, (float*)d->workspace);
+    int rc = check_launch("attn_rows_bf16");
+    if (rc || ns_eff <= 1) return rc;
+    hipLaunchKernelGGL((attn_rows_merge<DH>), dim3(d->Hkv, d->B), dim3(256), 0, st, *d, ns_eff,
+                       (const float*)d->workspace);
+    return check_launch("attn_rows_merge");
+  }
+  int NQ = G >= 4 ? 1 : 4 / G;
+  const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
+  if (G == 8) {
+    hipLaunchKernelGGL((attn_tile_bf16<DH, 8>), dim3(nblk, d->Hkv, d->B), dim3(512), 0, st, *d, NQ);
+  } else if (G == 4 || G == 2 || G == 1) {
+    hipLaunchKernelGGL((attn_tile_bf16<DH, 4>), dim3(nblk, d->Hkv, d->B), dim3(256), 0, st, *d, NQ);
+  } else {
+    return fail(CODA_EUNSUP, "coda_diff_attn_fwd: G=%d with Lq=%d unsupported for bf16 tiles", G, d->Lq);
+  }
+  return check_launch("attn_tile_bf16");
+}
+
+extern "C" int coda_diff_attn_fwd(const coda_attn_desc* d, void* stream) {
+  int rc = validate(d);
+  if (rc) return rc;
+  if (d->B == 0 || d->Lq == 0) return CODA_OK;
+  hipStream_t st = (hipStream_t)stream;
+  switch (d->Dh) {
+    case 32: return launch_attn<32>(d, st);
+    case 64: return launch_attn<64>(d, st);
+    default: return launch_attn<128>(d, st);
+  }
+}

@@ -1,0 +1,261 @@
+/*
+ * coda_mi355x.h - C ABI of the MI355X (gfx950) bounded differential-attention
+ * hot path of CoDA-GQA-L.
+ *
+ * Every entry point:
+ *   - takes caller-owned device pointers (plain pointers, element strides,
+ *     sizes); the library never allocates device memory except where an
+ *     entry point documents a workspace the caller passes in;
+ *   - validates its arguments on the host before any HIP call, so a bad
+ *     shape / stride / size returns a nonzero code without touching the GPU;
+ *   - enqueues its kernels on `stream` (a hipStream_t passed as void*, NULL
+ *     = the null stream) and returns without synchronising;
+ *   - returns 0 on success, a CODA_E* code otherwise; the message of the
+ *     last failure on the calling thread is returned by coda_last_error().
+ *
+ * Element types: CODA_F32 (float), CODA_BF16 (bfloat16 bits, uint16_t),
+ * CODA_F16 (half bits, standalone epilogue only).
+ *
+ * Bit-exactness contract: every bank decision (candidate order, slot index,
+ * overwrite / touch flags, LRU stamps) and every bank write follows the
+ * reference's CPU eager path operation by operation, including reduced
+ * precision rounding points; attention outputs agree to fp32 1e-4 and
+ * bf16 2e-2 (max error over the output, relative to its max magnitude).
+ */
+#ifndef CODA_MI355X_H
+#define CODA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CODA_ABI_VERSION 1
+
+enum { CODA_F32 = 0, CODA_BF16 = 1, CODA_F16 = 2 };
+
+enum {
+  CODA_OK = 0,
+  CODA_EINVAL = 1,   /* bad argument: shape, stride, pointer, dtype */
+  CODA_EUNSUP = 2,   /* valid request this build does not implement */
+  CODA_EHIP = 3,     /* HIP runtime error (launch / attribute query) */
+  CODA_ESMALL = 4    /* caller workspace too small */
+};
+
+/* Library version of this header (CODA_ABI_VERSION). */
+int coda_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* coda_last_error(void);
+
+/* Number of HIP devices visible (0 on a host without a GPU; never fails). */
+int coda_device_count(void);
+
+/* ------------------------------------------------------------------------
+ * Fused differential attention + epilogue.
+ *
+ *   out = Norm( Attn(q, K, V) - lam * Attn(q_noise, K, V) )
+ *
+ * Keys are the concatenation [prefix | block]:
+ *   prefix: kp/vp (B, Hkv, Lp, Dh), slot s visible iff allowed[b, s] != 0
+ *           (allowed == NULL: all visible).  This is the bounded cache
+ *           (ring window + exact bank + summary bank) of the state.
+ *   block : kb/vb (B, Hkv, Lb, Dh); causal == 1: query i sees block key j
+ *           iff j <= i + (Lb - Lq) (lower-right alignment); causal == 2:
+ *           iff j <= i (upper-left, torch SDPA is_causal); causal == 0: all.
+ * q is taken pre-RoPE when rope_cos/rope_sin are given ((Lq, Dh/2) tables
+ * of the query positions; interleaved pairs (2i,2i+1) or, with
+ * rope_interleaved == 0, half-split pairs (i, i+Dh/2)), else post-RoPE.
+ * q_noise == NULL: q_noise = pairwise rotation of (roped) q by per-head
+ * angle tables theta_cos/theta_sin (H, Dh/2).
+ * Norm: RMSNorm over Dh with weight rms_w (eps), or identity (rms_w NULL).
+ * GQA: query head h reads KV head h / (H / Hkv).
+ *
+ * Replaces: the attention seam CoDAGQALandmarkPerf2._sdpa_stacked_two_stream
+ *   (src/coda_gqa_l/attention.py:416-465) together with the prefix / causal
+ *   mask policy of prefill_chunked (attention.py:635-693) and attend_step
+ *   (attention.py:476-514), and the operator
+ *   diff_flash_attn(q, q_noise, k, v, lam, rms_weight, eps, is_causal,
+ *   sm_scale) (src/coda_gqa_l/triton_diff_flash/__init__.py:86-146).
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int dtype;                  /* CODA_F32 or CODA_BF16 */
+  int B, H, Hkv, Lq, Dh;
+  const void* q;              /* (B,H,Lq,Dh) */
+  int64_t q_sb, q_sh, q_sl;   /* element strides; d stride is 1 */
+  const void* q_noise;        /* (B,H,Lq,Dh) or NULL */
+  int64_t qn_sb, qn_sh, qn_sl;
+  const void* theta_cos;      /* (H, Dh/2) contiguous, used iff q_noise == NULL */
+  const void* theta_sin;
+  const void* rope_cos;       /* (Lq, Dh/2) contiguous or NULL */
+  const void* rope_sin;
+  int rope_interleaved;
+  const void* kp;             /* prefix keys (B,Hkv,Lp,Dh) or NULL when Lp == 0 */
+  const void* vp;
+  int Lp;
+  int64_t p_sb, p_sh, p_sl;
+  const uint8_t* allowed;     /* (B, Lp) bool bytes, row stride al_sb, or NULL */
+  int64_t al_sb;
+  const void* kb;             /* block keys (B,Hkv,Lb,Dh) or NULL when Lb == 0 */
+  const void* vb;
+  int Lb;
+  int64_t b_sb, b_sh, b_sl;
+  int causal;                 /* 0 none, 1 lower-right, 2 upper-left */
+  const void* lam;            /* (B,H,Lq) */
+  int64_t lam_sb, lam_sh, lam_sl;
+  const void* rms_w;          /* (Dh) or NULL */
+  float eps;
+  float sm_scale;             /* <= 0: 1/sqrt(Dh) */
+  void* out;                  /* (B,H,Lq,Dh) */
+  int64_t o_sb, o_sh, o_sl;
+  void* workspace;            /* device scratch, >= coda_attn_workspace_bytes() */
+  size_t workspace_bytes;
+} coda_attn_desc;
+
+/* Device scratch bytes coda_diff_attn_fwd needs for this descriptor. */
+int coda_attn_workspace_bytes(const coda_attn_desc* d, size_t* bytes);
+
+int coda_diff_attn_fwd(const coda_attn_desc* d, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Standalone differential epilogue over rows of Dh:
+ *   out = RMSNorm(sig - lam * noise) * w     (coda_diff_epilogue_fwd)
+ *   out = sig - lam * noise                  (coda_diff_sub_only_fwd)
+ * sig/noise/out are contiguous (num_rows, head_dim); lam is (num_rows,).
+ * Replaces: diff_epilogue_forward_{bf16,fp16,fp32} and
+ *   diff_sub_only_forward_{bf16,fp16,fp32}
+ *   (kernels/coda_diff_epilogue/kernel_src/diff_epilogue.cu:465-568), bound
+ *   as torch ops coda_kernels::diff_epilogue_forward / diff_sub_only_forward
+ *   (kernels/coda_diff_epilogue/torch-ext/torch_binding.cpp:203-213).
+ * ---------------------------------------------------------------------- */
+int coda_diff_epilogue_fwd(int dtype, void* out, const void* sig, const void* noise,
+                           const void* lam, const void* w, int num_rows, int head_dim,
+                           float eps, void* stream);
+int coda_diff_sub_only_fwd(int dtype, void* out, const void* sig, const void* noise,
+                           const void* lam, int num_rows, int head_dim, void* stream);
+
+/* ------------------------------------------------------------------------
+ * RoPE of a (B, Hx, L, Dh) tensor into out (same shape, own strides), with
+ * (L, Dh/2) cos/sin tables, rounding after every multiply / add in the
+ * element type exactly like the reference's eager apply_rope.
+ * Replaces: apply_rope (src/coda_gqa_l/primitives.py:83-113) on the key
+ *   path of step / prefill_chunked (attention.py:531-532, :598-600).
+ * ---------------------------------------------------------------------- */
+int coda_rope_fwd(int dtype, void* out, int64_t o_sb, int64_t o_sh, int64_t o_sl,
+                  const void* x, int64_t x_sb, int64_t x_sh, int64_t x_sl,
+                  const void* cos_t, const void* sin_t, int B, int Hx, int L, int Dh,
+                  int interleaved, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Bounded-cache state (CoDAGQALandmarkStatePerf2, src/coda_gqa_l/state.py:24-54)
+ * and the layer constants the bank kernels read.  Buffers are contiguous:
+ *   k_buf, v_buf  (B, Hkv, Lbuf, Dh), Lbuf = W + Me + Ms, element type dtype
+ *   allowed       (B, Lbuf) uint8 (torch.bool)
+ *   g_recent      (B, W) float
+ *   mem_last      (B, Me) int64
+ *   exact_v_norm  (B, Hkv, Me, Dh) dtype       (NULL iff Me == 0)
+ *   sum_lf_k_norm (B, Hkv, Ms, Dh - lf) dtype  (NULL iff Ms == 0)
+ *   eta_logit     (Hkv,) float (sigmoid taken on device, cast to dtype)
+ * metrics: optional (CODA_NUM_COUNTERS,) int64 device counters, or NULL.
+ * ---------------------------------------------------------------------- */
+enum {
+  CODA_CNT_EXACT_HITS = 0, CODA_CNT_EXACT_INSERTS, CODA_CNT_EXACT_OVERWRITES,
+  CODA_CNT_SUMMARY_UPDATES, CODA_CNT_SUMMARY_INSERTS, CODA_CNT_TOKENS_GATED_OUT,
+  CODA_CNT_EXACT_FRUSTRATED, CODA_CNT_SUMMARY_FRUSTRATED, CODA_NUM_COUNTERS = 8
+};
+
+typedef struct {
+  int dtype;
+  int B, Hkv, Dh, W, Me, Ms, lf;      /* lf = low-frequency band start (Dh/2) */
+  int active_exact, active_summary;   /* Ae <= Me, As <= Ms */
+  void* k_buf;
+  void* v_buf;
+  uint8_t* allowed;
+  float* g_recent;
+  int64_t* mem_last;
+  void* exact_v_norm;
+  void* sum_lf_k_norm;
+  const float* eta_logit;
+  int gated;                          /* write_policy == "gated" */
+  float tau_exact, tau_summary;       /* gate thresholds (fp32 compare) */
+  float tau_match, tau_novel;         /* exact-bank cosine thresholds */
+  int refresh_on_hit, overwrite_on_insert;
+  float energy_scale;                 /* sqrt(Dh / (Dh - lf)) */
+  int64_t* metrics;
+  int64_t* frustrated;                /* (2,) device int64 or NULL: exact, summary */
+} coda_bank_desc;
+
+/* One decode token per sequence: ring FIFO write; when the ring is full the
+ * evicted slot `ring_idx` (its absolute position pos - W) first goes through
+ * the exact bank (V-cosine novelty, first-free / LRU slot, blend, norm cache,
+ * LRU stamp) and the summary bank (LF-K cosine argmax, gated EMA, norm cache).
+ * k_new, v_new: (B, Hkv, Dh) with strides (nb_sb, nb_sh); g_new: (B,) float.
+ * ring_filled < W: write slot ring_filled, no eviction.
+ * Replaces: MemoryBankMixin._write_one / _exact_update_one /
+ *   _summary_update_one (src/coda_gqa_l/memory_banks.py:183-432). */
+int coda_decode_write(const coda_bank_desc* s, const void* k_new, const void* v_new,
+                      int64_t nb_sb, int64_t nb_sh, const float* g_new,
+                      int ring_idx, int ring_filled, int64_t pos, void* stream);
+
+/* Candidate plan of a chunked prefill: for every chunk c (block_size
+ * tokens, last one ragged) and sequence b, the evicted-token indices picked
+ * by the reference's CPU topk(g_e, k, sorted=False) (libstdc++ nth_element /
+ * partial_sort order, ties included), as positions into the time-ordered
+ * [ring | block] sequence of that chunk.
+ *   g_ring (B, W) float ring gates in slot order, g_seq (B, L) float (row
+ *   stride g_sl), plan (n_chunks, B, Kmax) int32 written; n_ev / k per chunk
+ *   follow from ring_filled, W, L, block_size; Kmax = max candidates.
+ * Replaces: the candidate selection of _write_block_fast
+ *   (src/coda_gqa_l/memory_banks.py:459-510). */
+int coda_block_plan(const float* g_ring, int ring_head, int ring_filled, int W,
+                    const float* g_seq, int64_t g_sb, int B, int L, int block_size,
+                    int k_exact, int k_summary, int do_exact, int do_summary,
+                    int32_t* plan, int Kmax, void* stream);
+
+/* Bank update + ring write for one prefill chunk (block of `blk` tokens).
+ * kb/vb: (B, Hkv, blk, Dh) roped keys / values of the chunk with strides
+ * (b_sb, b_sh, b_sl); gb (B, blk) float with row stride g_sb; plan_c points
+ * at this chunk's (B, Kmax) candidate rows of coda_block_plan.
+ * The ring is kept circular: head = oldest slot, filled = occupancy.
+ * Replaces: _write_block_fast (memory_banks.py:438-564) with
+ *   _exact_update_block_vectorized (:570-774, PyTorch branch) and
+ *   _summary_update_block_hard (:780-950, PyTorch branch). */
+int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb,
+                     int64_t b_sb, int64_t b_sh, int64_t b_sl, const float* gb, int64_t g_sb,
+                     int blk, int ring_head, int ring_filled, int64_t pos0,
+                     const int32_t* plan_c, int Kmax, int Te, int Ts,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device scratch for coda_block_write. */
+int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, size_t* bytes);
+
+/* Rotate a full circular ring (head != 0) into time order at slots 0..W-1
+ * (k_buf, v_buf, g_recent, allowed), as the reference leaves it after every
+ * prefill chunk (_set_recent_from_sequence, memory_banks.py:152-177).
+ * workspace >= B * Hkv * W * Dh * 2 elements + B * W floats. */
+int coda_ring_rotate(const coda_bank_desc* s, int ring_head, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* out row (o, i) = F.normalize(x row (o, i), dim=-1, eps=1e-6) over `len`
+ * channels (len <= 128), rows at x + o*x_so + i*x_si (out likewise), with
+ * the reference's rounding (fp32 sum of squares, norm rounded to the element
+ * type, clamp_min(eps), rounded division).
+ * Replaces: the norm-cache initialisation of init_state
+ *   (src/coda_gqa_l/attention.py:309-316). */
+int coda_unit_rows(int dtype, void* out, int64_t o_so, int64_t o_si, const void* x, int64_t x_so,
+                   int64_t x_si, int64_t outer, int inner, int len, void* stream);
+
+/* Host-only restatement check of the selection order used by the bank
+ * kernels (no GPU needed): indices of torch's CPU topk(vals, k, largest,
+ * sorted) for float / int64 keys, ties included.  No reference
+ * counterpart: exported so the order can be tested against torch.topk. */
+int coda_topk_order_host(const float* vals, int n, int k, int largest, int sorted, int64_t* out_idx);
+int coda_topk_order_host_i64(const int64_t* vals, int n, int k, int largest, int sorted, int64_t* out_idx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CODA_MI355X_H */

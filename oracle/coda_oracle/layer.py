@@ -224,28 +224,36 @@ class OracleLayer(nn.Module):
         B, H, L, Dh = oh.shape
         return self.o_proj(oh.transpose(1, 2).contiguous().view(B, L, H * Dh))
 
-    def attend_step(self, x, st, *, query_pos=None):
-        """attention.py:476-514."""
-        B, L, _ = x.shape
-        assert L == 1
+    def attend_core(self, q, lam, st, qp):
+        """Heads (B,H,1,Dh) of one token: q pre-RoPE (B,H,1,Dh), lam (B,H,1,1)
+        (attention.py:486-514 after the projections)."""
+        B = q.shape[0]
         k_att, v_att, mask = st.k_buf, st.v_buf, None
         if self.mask_unused_memory:
             if not bool(st.allowed.any()):
-                return torch.zeros_like(x)
+                return torch.zeros_like(q)
             if not bool(st.allowed.all()):
                 if B == 1:
                     vi = st.allowed[0].nonzero(as_tuple=True)[0]
                     k_att, v_att = st.k_buf[:, :, vi], st.v_buf[:, :, vi]
                 else:
                     mask = st.allowed[:, None, None, :]
+        c, s = self.rope_tables(1, qp, q.dtype)
+        q = rope(q, c, s, self.rope_interleaved)
+        ct, sn = self.theta_tables(q.dtype)
+        qn = noise_rotation(q, ct, sn)
+        return self.two_stream(q, qn, k_att, v_att, mask, lam)
+
+    def attend_step(self, x, st, *, query_pos=None):
+        """attention.py:476-514."""
+        B, L, _ = x.shape
+        assert L == 1
+        if self.mask_unused_memory and not bool(st.allowed.any()):
+            return torch.zeros_like(x)
         q = self.q_proj(x).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
         qp = st.pos if query_pos is None else int(query_pos)
-        c, s = self.rope_tables(1, qp, x.dtype)
-        q = rope(q, c, s, self.rope_interleaved)
-        ct, sn = self.theta_tables(x.dtype)
-        qn = noise_rotation(q, ct, sn)
         lam = torch.sigmoid(self.lambda_proj(x)).transpose(1, 2).unsqueeze(-1)
-        return self.out_proj(self.two_stream(q, qn, k_att, v_att, mask, lam))
+        return self.out_proj(self.attend_core(q, lam, st, qp))
 
     def _new_kv(self, x, q_pos):
         B, L, _ = x.shape
@@ -274,20 +282,16 @@ class OracleLayer(nn.Module):
             banks.write_one(self, st, k, v, g, trace)
         return y, st
 
-    def prefill_chunked(self, x_seq, st, *, block_size=256, write_cache=True, return_outputs=True, trace=None):
-        """attention.py:567-728 (hoisted projections, chunk loop, mask policy)."""
-        B, L, _ = x_seq.shape
-        if L == 0:
-            return (x_seq[:, :0, :].clone() if return_outputs else None), st
-        if block_size <= 0:
-            raise ValueError("block_size must be positive")
-        dt = x_seq.dtype
+    def prefill_core(self, q_seq, k_seq, v_seq, g_seq, lam_seq, st, *, block_size, write_cache=True,
+                     return_heads=True, trace=None):
+        """Chunk loop after the projections (attention.py:611-724).
+
+        q_seq (B,H,L,Dh) roped, k_seq (B,Hkv,L,Dh) roped, v_seq, g_seq (B,L)
+        fp32, lam_seq (B,H,L,1).  Returns heads (B,H,L,Dh) or None.
+        """
+        B, H, L, Dh = q_seq.shape
         p0 = int(st.pos)
-        q_seq, k_raw, v_seq, g_seq, lam_seq = self.project(x_seq)
-        c, s = self.rope_tables(L, p0, dt)
-        q_seq = rope(q_seq, c, s, self.rope_interleaved)
-        k_seq = rope(k_raw, c, s, self.rope_interleaved)
-        ct, sn = self.theta_tables(dt)
+        ct, sn = self.theta_tables(q_seq.dtype)
         outs = []
         t = 0
         while t < L:
@@ -320,14 +324,34 @@ class OracleLayer(nn.Module):
                     else:
                         ok = torch.ones((B, Lk), dtype=torch.bool)
                     mask = cm.view(1, 1, blk, Lk) & ok[:, None, None, :]
-            qn = noise_rotation(q, ct, sn)
-            oh = self.two_stream(q, qn, k_all, v_all, mask, lam, causal)
-            if return_outputs:
-                outs.append(self.out_proj(oh))
+            if return_heads:
+                qn = noise_rotation(q, ct, sn)
+                outs.append(self.two_stream(q, qn, k_all, v_all, mask, lam, causal))
             if write_cache:
                 banks.write_block(self, st, kb, vb, gb, pos0, trace)
             t += blk
-        return (torch.cat(outs, dim=1) if return_outputs else None), st
+        return torch.cat(outs, dim=2) if return_heads else None
+
+    def project_seq(self, x_seq, p0):
+        """Hoisted projections of prefill_chunked (attention.py:590-608):
+        q, k roped with the tables of positions p0.., v, g, lam."""
+        B, L, _ = x_seq.shape
+        q_seq, k_raw, v_seq, g_seq, lam_seq = self.project(x_seq)
+        c, s = self.rope_tables(L, p0, x_seq.dtype)
+        return (rope(q_seq, c, s, self.rope_interleaved), rope(k_raw, c, s, self.rope_interleaved), v_seq, g_seq,
+                lam_seq)
+
+    def prefill_chunked(self, x_seq, st, *, block_size=256, write_cache=True, return_outputs=True, trace=None):
+        """attention.py:567-728 (hoisted projections, chunk loop, mask policy)."""
+        B, L, _ = x_seq.shape
+        if L == 0:
+            return (x_seq[:, :0, :].clone() if return_outputs else None), st
+        if block_size <= 0:
+            raise ValueError("block_size must be positive")
+        q_seq, k_seq, v_seq, g_seq, lam_seq = self.project_seq(x_seq, int(st.pos))
+        heads = self.prefill_core(q_seq, k_seq, v_seq, g_seq, lam_seq, st, block_size=block_size,
+                                  write_cache=write_cache, return_heads=return_outputs, trace=trace)
+        return (self.out_proj(heads) if return_outputs else None), st
 
     def cache_bytes(self, *, batch_size, dtype):
         """attention.py:734-751."""
