@@ -901,7 +901,8 @@ __global__ __launch_bounds__(256) void unit_rows_kernel(T* out, int64_t o_so, in
 }
 
 // ------------------------------------------------------------ validation
-static int validate_bank(const coda_bank_desc* s, const char* who) {
+// Sizes and constants only (entry points that never touch the bank data).
+static int validate_sizes(const coda_bank_desc* s, const char* who) {
   CODA_REQUIRE(s != nullptr, "%s: null state descriptor", who);
   CODA_REQUIRE(s->dtype == CODA_F32 || s->dtype == CODA_BF16, "%s: dtype must be CODA_F32 or CODA_BF16", who);
   CODA_REQUIRE(s->Dh == 32 || s->Dh == 64 || s->Dh == 128, "%s: head_dim %d unsupported (32, 64, 128)", who,
@@ -913,10 +914,16 @@ static int validate_bank(const coda_bank_desc* s, const char* who) {
                s->active_exact, s->Me);
   CODA_REQUIRE(s->active_summary >= 0 && s->active_summary <= s->Ms, "%s: active_summary %d outside [0, %d]",
                who, s->active_summary, s->Ms);
+  CODA_REQUIRE(s->Me <= 1024 && s->Ms <= 1024, "%s: bank sizes above 1024 unsupported", who);
+  return CODA_OK;
+}
+
+static int validate_bank(const coda_bank_desc* s, const char* who) {
+  int rc = validate_sizes(s, who);
+  if (rc) return rc;
   CODA_REQUIRE(s->k_buf && s->v_buf && s->allowed && s->g_recent, "%s: state buffers missing", who);
   CODA_REQUIRE(s->Me == 0 || (s->mem_last && s->exact_v_norm), "%s: exact bank buffers missing", who);
   CODA_REQUIRE(s->Ms == 0 || (s->sum_lf_k_norm && s->eta_logit), "%s: summary bank buffers missing", who);
-  CODA_REQUIRE(s->Me <= 1024 && s->Ms <= 1024, "%s: bank sizes above 1024 unsupported", who);
   return CODA_OK;
 }
 
@@ -982,7 +989,8 @@ extern "C" int coda_block_plan(const float* g_ring, int ring_head, int ring_fill
   CODA_REQUIRE(Kmax >= 1, "coda_block_plan: Kmax must be positive");
   const int K = (do_exact && do_summary) ? (k_exact > k_summary ? k_exact : k_summary)
                                          : (do_exact ? k_exact : (do_summary ? k_summary : 0));
-  CODA_REQUIRE(K <= Kmax, "coda_block_plan: Kmax %d below candidate count %d", Kmax, K);
+  const int K_eff = K < block_size ? K : block_size;  // a chunk evicts at most block_size tokens
+  CODA_REQUIRE(K_eff <= Kmax, "coda_block_plan: Kmax %d below candidate count %d", Kmax, K_eff);
   const int n_chunks = (L + block_size - 1) / block_size;
   if (B == 0 || n_chunks == 0 || (!do_exact && !do_summary)) return CODA_OK;
   const size_t lds = sizeof(sel::Item<float>) * (size_t)block_size;
@@ -998,7 +1006,7 @@ static size_t block_ws_bytes(const coda_bank_desc* s, int Te, int Ts) {
 }
 
 extern "C" int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, size_t* bytes) {
-  int rc = validate_bank(s, "coda_block_workspace_bytes");
+  int rc = validate_sizes(s, "coda_block_workspace_bytes");
   if (rc) return rc;
   CODA_REQUIRE(bytes != nullptr, "coda_block_workspace_bytes: null out pointer");
   *bytes = block_ws_bytes(s, Kmax, Kmax);
@@ -1071,8 +1079,9 @@ extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const v
 
 extern "C" int coda_ring_rotate(const coda_bank_desc* s, int ring_head, void* workspace, size_t workspace_bytes,
                                 void* stream) {
-  int rc = validate_bank(s, "coda_ring_rotate");
+  int rc = validate_sizes(s, "coda_ring_rotate");
   if (rc) return rc;
+  CODA_REQUIRE(s->k_buf && s->v_buf && s->g_recent, "coda_ring_rotate: state buffers missing");
   CODA_REQUIRE(ring_head >= 0 && ring_head < s->W, "coda_ring_rotate: ring_head outside [0, W)");
   const size_t esz = s->dtype == CODA_BF16 ? 2 : 4;
   const size_t need = (size_t)s->B * s->Hkv * s->W * s->Dh * 2 * esz + (size_t)s->B * s->W * sizeof(float);

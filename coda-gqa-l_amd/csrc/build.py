@@ -25,6 +25,9 @@ ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          # packed fp32 instructions are kept out of every kernel
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # no implicit multiply-add fusion: the reference rounds every product
+         # before the add; accumulations that want FMA call fmaf explicitly
+         "-ffp-contract=off",
          "-Wno-unused-result"]
 
 

@@ -12,6 +12,8 @@ def max_rel(a: torch.Tensor, b: torch.Tensor) -> float:
     """max |a - b| / max |b| over the whole tensor (0 for an all-zero b)."""
     a = a.detach().float().cpu()
     b = b.detach().float().cpu()
+    if b.numel() == 0:
+        return 0.0
     den = b.abs().max().item()
     err = (a - b).abs().max().item() if a.numel() else 0.0
     return err / den if den > 0 else err
