@@ -171,11 +171,14 @@ def main():
         "step_hbm_frac": round((attn_bytes + bank_bytes) / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
     }
 
+    print(f"# decode: {tok_s:.0f} tok/s, {ms_step * 1e3:.1f} us/step, attention {attn_ms * 1e3:.1f} us "
+          f"({achieved:.0f} GB/s)", file=sys.stderr, flush=True)
     # ---------------------------------------------------------------- prefill
     if not a.no_prefill:
         out["prefill"] = bench_prefill(torch, coda, m, a)
 
     # ---------------------------------------------------------------- CPU baseline
+        print(f"# prefill: {out['prefill']['value']:.0f} tok/s", file=sys.stderr, flush=True)
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a)
     print(json.dumps(out), flush=True)
@@ -259,7 +262,7 @@ def cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a):
         while True:
             i = n_done % len(q_all)
             qp = so.pos
-            banks.write_one(o, so, k_all[i].cpu(), v_all[i].cpu(), g_all[i].cpu())
+            banks.write_one(o, so, k_all[i].cpu(), v_all[i].cpu(), g_all[i].cpu().view(B, 1))
             o.attend_core(q_all[i].cpu(), lam_all[i].cpu().unsqueeze(-1), so, qp)
             n_done += 1
             if time.perf_counter() - t0 > a.cpu_seconds or n_done >= 2000:
