@@ -256,12 +256,16 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         return torch.sigmoid(self.lambda_proj(x)).permute(0, 2, 1)
 
     def _theta_tables(self, dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
-        return torch.cos(self.theta).to(dtype=dtype).contiguous(), torch.sin(self.theta).to(dtype=dtype).contiguous()
+        """cos / sin of the noise angles in the compute dtype (attention.py:504-506)."""
+        th = self.theta
+        return self._derived("theta", th, dtype, lambda: (torch.cos(th).to(dtype=dtype).contiguous(),
+                                                          torch.sin(th).to(dtype=dtype).contiguous()))
 
     def _rms_weight(self, dtype) -> Optional[torch.Tensor]:
         if self.head_norm_mode != "full":
             return None
-        return self.head_norm.weight.detach().to(dtype).contiguous()
+        w = self.head_norm.weight
+        return self._derived("rms_w", w, dtype, lambda: w.detach().to(dtype).contiguous())
 
     # ------------------------------------------------------------ decode
     def decode_attend_core(self, q: torch.Tensor, lam: torch.Tensor, state: CoDAGQALandmarkStatePerf2,
@@ -281,6 +285,30 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             v_prefix=state.v_buf, allowed=state.allowed if self.mask_unused_memory else None, k_block=None,
             v_block=None, lam=lam, rms_weight=self._rms_weight(q.dtype), eps=self._eps,
             out=out.permute(0, 2, 1, 3))
+        return out
+
+    def decode_step_core(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, g_new: torch.Tensor,
+                         lam: torch.Tensor, state: CoDAGQALandmarkStatePerf2, rope_cos: torch.Tensor,
+                         rope_sin: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Write one token into the bounded cache, then attend with its query
+        (attention.py:526-536 after the projections), as one library call.
+
+        q (B,H,1,Dh) pre-RoPE, k_new (B,Hkv,1,Dh) roped, v_new, g_new (B,)
+        float32, lam (B,H,1), tables (1, Dh/2) at the token's position.
+        Returns head outputs (B, 1, H, Dh)."""
+        B = q.shape[0]
+        H, Dh = self.num_heads, self.head_dim
+        if out is None:
+            out = torch.empty((B, 1, H, Dh), dtype=q.dtype, device=q.device)
+        self._check_state(state)
+        ct, sn = self._theta_tables(q.dtype)
+        desc, keep = ops.attention_desc(
+            q=q, rope_cos=rope_cos.contiguous(), rope_sin=rope_sin.contiguous(),
+            rope_interleaved=self.rope_interleaved, theta_cos=ct, theta_sin=sn, k_prefix=state.k_buf,
+            v_prefix=state.v_buf, allowed=state.allowed if self.mask_unused_memory else None, k_block=None,
+            v_block=None, lam=lam, rms_weight=self._rms_weight(q.dtype), eps=self._eps,
+            out=out.permute(0, 2, 1, 3))
+        self._decode_step(state, k_new=k_new, v_new=v_new, g_new=g_new, attn_desc=desc)
         return out
 
     def attend_step(self, x: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *,
@@ -313,8 +341,13 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             self._write_one(state, k_new=k_new, v_new=v_new, g_new=self._write_gate(x))
 
         if attend and include_current_in_attention and write_cache:
-            write()
-            return self.attend_step(x, state, query_pos=q_pos), state
+            self._check_state(state)
+            k_raw, v_new = self._project_kv_raw(x)
+            cos, sin = self.rope(seq_len=1, offset=q_pos, device=x.device, dtype=x.dtype)
+            k_new = apply_rope(k_raw, cos, sin, interleaved=self.rope_interleaved)
+            heads = self.decode_step_core(self._project_q(x), k_new, v_new, self._write_gate(x), self._lambda(x),
+                                          state, cos, sin)
+            return self.o_proj(heads.view(B, 1, self.num_heads * self.head_dim)), state
         y = self.attend_step(x, state, query_pos=q_pos) if attend else torch.zeros_like(x)
         if write_cache:
             write()

@@ -64,8 +64,24 @@ class MemoryBankMixin:
                     t = t.to(st.k_buf.dtype)
                 setattr(st, name, t.contiguous())
 
+    def _derived(self, name: str, src: torch.Tensor, key, fn) -> torch.Tensor:
+        """Tensor derived from a parameter, recomputed only when the parameter
+        changes (in-place version counter or storage), so a decode step
+        launches no conversion kernels."""
+        cache = self.__dict__.setdefault("_derived_cache", {})
+        tag = (src._version, src.data_ptr(), src.dtype, src.device)
+        hit = cache.get((name, key))
+        if hit is not None and hit[0] == tag:
+            return hit[1]
+        with torch.no_grad():
+            val = fn()
+        cache[(name, key)] = (tag, val)
+        return val
+
     def _eta_logit_f32(self, device) -> torch.Tensor:
-        return self.summary_eta_logit.detach().to(device=device, dtype=torch.float32).contiguous()
+        p = self.summary_eta_logit
+        return self._derived("eta", p, device,
+                             lambda: p.detach().to(device=device, dtype=torch.float32).contiguous())
 
     def _bank_desc(self, st: CoDAGQALandmarkStatePerf2, eta: Optional[torch.Tensor],
                    metrics: Optional[torch.Tensor], frustrated: Optional[torch.Tensor]) -> _hip.BankDesc:
@@ -158,6 +174,51 @@ class MemoryBankMixin:
             self._expand_from(st, fr, False, self.Me > 0, self.Ms > 0)
             st.recent_idx = (j + 1) % self.window
         st.pos += 1
+
+    def _decode_step(self, st: CoDAGQALandmarkStatePerf2, *, k_new: torch.Tensor, v_new: torch.Tensor,
+                     g_new: torch.Tensor, attn_desc) -> None:
+        """Write one token then attend (coda_decode_step): the bank update of
+        _write_one and the attention described by attn_desc, in one call."""
+        self._check_state(st)
+        B = st.k_buf.shape[0]
+        dev = st.k_buf.device
+        kn = k_new.reshape(B, self.num_kv_heads, self.head_dim)
+        vn = v_new.reshape(B, self.num_kv_heads, self.head_dim)
+        if kn.stride(-1) != 1 or kn.stride() != vn.stride():
+            kn, vn = kn.contiguous(), vn.contiguous()
+        g = g_new.reshape(B).to(torch.float32).contiguous()
+        evict = st.recent_filled >= self.window
+        metrics, fr = self._aux_buffers(st, dev) if evict else (None, None)
+        eta = self._eta_logit_f32(dev) if self.Ms > 0 else None
+        d = self._bank_desc(st, eta, metrics, fr)
+        L = _hip.lib()
+        need = ctypes.c_size_t(0)
+        _hip.check(L.coda_decode_step_workspace_bytes(d, attn_desc, need))
+        ws = self._workspace(dev, need.value)
+        _hip.check(L.coda_decode_step(
+            d, attn_desc, kn.data_ptr(), vn.data_ptr(), kn.stride(0), kn.stride(1), g.data_ptr(),
+            int(st.recent_idx), int(st.recent_filled), int(st.pos), _hip.ptr(ws), need.value, _hip.stream_of(kn)))
+        if not evict:
+            st.recent_filled += 1
+        else:
+            j = int(st.recent_idx)
+            self._fold_metrics(st, metrics, 1, self.Me > 0, self.Ms > 0)
+            self._expand_from(st, fr, False, self.Me > 0, self.Ms > 0)
+            st.recent_idx = (j + 1) % self.window
+        st.pos += 1
+
+    def _workspace(self, device, nbytes: int) -> Optional[torch.Tensor]:
+        """Device scratch reused across calls (grown on demand); calls on one
+        stream run in order, so reuse needs no synchronisation."""
+        if nbytes == 0:
+            return None
+        cache = self.__dict__.setdefault("_ws_cache", {})
+        key = str(device)
+        buf = cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            cache[key] = buf
+        return buf
 
     # ------------------------------------------------------------ prefill
     def _plan_candidates(self, st, g_seq: torch.Tensor, L: int, block_size: int):

@@ -98,13 +98,14 @@ def diff_flash_attn(q: torch.Tensor, q_noise: torch.Tensor, k: torch.Tensor, v: 
     return out
 
 
-def bounded_attention(*, q: torch.Tensor, rope_cos: Optional[torch.Tensor], rope_sin: Optional[torch.Tensor],
-                      rope_interleaved: bool, theta_cos: torch.Tensor, theta_sin: torch.Tensor,
-                      k_prefix: Optional[torch.Tensor], v_prefix: Optional[torch.Tensor],
-                      allowed: Optional[torch.Tensor], k_block: Optional[torch.Tensor],
-                      v_block: Optional[torch.Tensor], lam: torch.Tensor, rms_weight: Optional[torch.Tensor],
-                      eps: float, out: torch.Tensor, causal: int = 1) -> torch.Tensor:
-    """Attention of the layer's bounded path into `out` (B,H,Lq,Dh view).
+def attention_desc(*, q: torch.Tensor, rope_cos: Optional[torch.Tensor], rope_sin: Optional[torch.Tensor],
+                   rope_interleaved: bool, theta_cos: torch.Tensor, theta_sin: torch.Tensor,
+                   k_prefix: Optional[torch.Tensor], v_prefix: Optional[torch.Tensor],
+                   allowed: Optional[torch.Tensor], k_block: Optional[torch.Tensor],
+                   v_block: Optional[torch.Tensor], lam: torch.Tensor, rms_weight: Optional[torch.Tensor],
+                   eps: float, out: torch.Tensor, causal: int = 1):
+    """coda_attn_desc of the layer's bounded attention, plus the tensors it
+    points to (kept alive by the caller until the launch is enqueued).
 
     q (B,H,Lq,Dh) pre-RoPE with (Lq, Dh/2) tables (or post-RoPE with
     rope_cos None); prefix = state cache (B,Hkv,Lbuf,Dh) masked by allowed
@@ -113,6 +114,7 @@ def bounded_attention(*, q: torch.Tensor, rope_cos: Optional[torch.Tensor], rope
     (torch SDPA is_causal), 0 none; lam (B,H,Lq) view.
     """
     B, H, Lq, Dh = q.shape
+    keep = []
     d = _hip.AttnDesc()
     d.dtype = _hip.dtype_code(q.dtype)
     d.B, d.H, d.Lq, d.Dh = B, H, Lq, Dh
@@ -124,8 +126,10 @@ def bounded_attention(*, q: torch.Tensor, rope_cos: Optional[torch.Tensor], rope
     Hkv = None
     if k_prefix is not None and k_prefix.stride() != v_prefix.stride():
         k_prefix, v_prefix = k_prefix.contiguous(), v_prefix.contiguous()
+        keep += [k_prefix, v_prefix]
     if k_block is not None and (k_block.stride() != v_block.stride() or k_block.stride(-1) != 1):
         k_block, v_block = k_block.contiguous(), v_block.contiguous()
+        keep += [k_block, v_block]
     if k_prefix is not None:
         Hkv = k_prefix.shape[1]
         d.kp, d.vp, d.Lp = k_prefix.data_ptr(), v_prefix.data_ptr(), k_prefix.shape[2]
@@ -144,8 +148,14 @@ def bounded_attention(*, q: torch.Tensor, rope_cos: Optional[torch.Tensor], rope
     d.eps = float(eps)
     d.sm_scale = 1.0 / math.sqrt(Dh)
     d.out = out.data_ptr(); d.o_sb, d.o_sh, d.o_sl = _strides3(out)
-    _run_attn(d, q)
-    return out
+    return d, keep
+
+
+def bounded_attention(**kw) -> torch.Tensor:
+    """Attention of the layer's bounded path into `out` (see attention_desc)."""
+    d, keep = attention_desc(**kw)
+    _run_attn(d, kw["q"])
+    return kw["out"]
 
 
 def _epilogue(out_sig, out_noise, lam, weight, eps, out, norm: bool):

@@ -32,9 +32,11 @@
 // S^T = K Q^T puts keys on m and query rows on n, so the D fragment of S^T
 // is directly the B fragment (P^T, keys on k) of O^T = V^T P^T.
 
+#include "bank_ops.h"
 #include "common.h"
 
 #include <math.h>
+#include <stdlib.h>
 
 namespace coda {
 
@@ -43,6 +45,7 @@ typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 static constexpr float kLog2e = 1.4426950408889634f;
+static constexpr int kMaxRowsPrefix = 2048;  // prefix slots whose `allowed` bytes fit the LDS copy
 
 // ------------------------------------------------------------ query prep
 // Eight consecutive channels [d0, d0+8) of the (roped) signal query or of
@@ -110,6 +113,71 @@ __device__ __forceinline__ void prep_q8(const coda_attn_desc& a, int b, int h, i
   if (stream == 1) {
     rotate_pairs8<T>(x, (const T*)a.theta_cos + (int64_t)h * half + (d0 >> 1),
                      (const T*)a.theta_sin + (int64_t)h * half + (d0 >> 1));
+  }
+}
+
+// Cooperative query staging into LDS (bf16 rows of Dh): row r of the
+// workgroup maps to (stream s, head h, query qi) through `map(r, s, h, qi)`.
+// One thread prepares 4 channels {2i, 2i+1, half+2i, half+2i+1}, which
+// closes both pairings (interleaved RoPE / noise rotation pairs and
+// half-split RoPE pairs) inside one thread; all of its loads are issued
+// before any arithmetic.  Rounding as prep_q8.
+template <typename MapF>
+__device__ __forceinline__ void stage_queries(const coda_attn_desc& a, int b, int rows, bf16_t* qs, int qs_stride,
+                                              MapF map) {
+  using E = Elt<bf16_t>;
+  const int Dh = a.Dh, half = Dh >> 1, quarter = Dh >> 2;
+  for (int it = threadIdx.x; it < rows * quarter; it += blockDim.x) {
+    const int r = it / quarter, i = it % quarter;
+    int st, h, qi;
+    const bool live = map(r, st, h, qi);
+    const int d0 = 2 * i, d1 = 2 * i + 1, d2 = half + 2 * i, d3 = half + 2 * i + 1;
+    float x[4] = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+      const bool given_noise = st == 1 && a.q_noise;
+      const bf16_t* src = given_noise ? (const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh + qi * a.qn_sl
+                                      : (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + qi * a.q_sl;
+      const uint32_t w01 = *reinterpret_cast<const uint32_t*>(src + d0);
+      const uint32_t w23 = *reinterpret_cast<const uint32_t*>(src + d2);
+      x[0] = bf2f((bf16_t)(w01 & 0xffffu)); x[1] = bf2f((bf16_t)(w01 >> 16));
+      x[2] = bf2f((bf16_t)(w23 & 0xffffu)); x[3] = bf2f((bf16_t)(w23 >> 16));
+      if (!given_noise) {
+        if (a.rope_cos) {
+          const bf16_t* c = (const bf16_t*)a.rope_cos + (int64_t)qi * half;
+          const bf16_t* sn = (const bf16_t*)a.rope_sin + (int64_t)qi * half;
+          if (a.rope_interleaved) {
+            // pairs (d0, d1) with angle i, (d2, d3) with angle quarter + i
+            const float c0 = E::ld(c[i]), s0 = E::ld(sn[i]), c1 = E::ld(c[quarter + i]), s1 = E::ld(sn[quarter + i]);
+            const float e0 = x[0], o0 = x[1], e1 = x[2], o1 = x[3];
+            x[0] = E::rnd(E::rnd(e0 * c0) - E::rnd(o0 * s0));
+            x[1] = E::rnd(E::rnd(e0 * s0) + E::rnd(o0 * c0));
+            x[2] = E::rnd(E::rnd(e1 * c1) - E::rnd(o1 * s1));
+            x[3] = E::rnd(E::rnd(e1 * s1) + E::rnd(o1 * c1));
+          } else {
+            // half-split pairs (d0, d2) and (d1, d3) with angles 2i, 2i+1
+            const float c0 = E::ld(c[d0]), s0 = E::ld(sn[d0]), c1 = E::ld(c[d1]), s1 = E::ld(sn[d1]);
+            const float lo0 = x[0], lo1 = x[1], hi0 = x[2], hi1 = x[3];
+            x[0] = E::rnd(E::rnd(lo0 * c0) + E::rnd(-hi0 * s0));
+            x[1] = E::rnd(E::rnd(lo1 * c1) + E::rnd(-hi1 * s1));
+            x[2] = E::rnd(E::rnd(hi0 * c0) + E::rnd(lo0 * s0));
+            x[3] = E::rnd(E::rnd(hi1 * c1) + E::rnd(lo1 * s1));
+          }
+        }
+        if (st == 1) {
+          const bf16_t* tc = (const bf16_t*)a.theta_cos + (int64_t)h * half;
+          const bf16_t* ts = (const bf16_t*)a.theta_sin + (int64_t)h * half;
+          const float c0 = E::ld(tc[i]), s0 = E::ld(ts[i]), c1 = E::ld(tc[quarter + i]), s1 = E::ld(ts[quarter + i]);
+          const float e0 = x[0], o0 = x[1], e1 = x[2], o1 = x[3];
+          x[0] = E::rnd(E::rnd(e0 * c0) - E::rnd(o0 * s0));
+          x[1] = E::rnd(E::rnd(e0 * s0) + E::rnd(o0 * c0));
+          x[2] = E::rnd(E::rnd(e1 * c1) - E::rnd(o1 * s1));
+          x[3] = E::rnd(E::rnd(e1 * s1) + E::rnd(o1 * c1));
+        }
+      }
+    }
+    bf16_t* dst = qs + r * qs_stride;
+    *reinterpret_cast<uint32_t*>(dst + d0) = (uint32_t)f2bf(x[0]) | ((uint32_t)f2bf(x[1]) << 16);
+    *reinterpret_cast<uint32_t*>(dst + d2) = (uint32_t)f2bf(x[2]) | ((uint32_t)f2bf(x[3]) << 16);
   }
 }
 
@@ -345,9 +413,24 @@ __device__ __forceinline__ void store_vt(char* base, int kg, int d0, const uint4
 // Workgroup = (split, KV head, batch); 4 waves take 16-key tiles in turn.
 // Partial (m, l, O) of the 4 waves merge in LDS; with nsplit > 1 each
 // workgroup leaves its merged partial in `ws` for attn_rows_merge.
-template <int DH>
+// Bank update applied by the decode attention kernel itself (two-kernel
+// decode step): each (head, sequence) workgroup recomputes the sequence's
+// decision from decode_route_kernel's per-head dots and metadata snapshot,
+// writes its own head's modified rows, and attends over the updated cache.
+struct DecodeApply {
+  coda_bank_desc s;
+  const void* k_new;
+  const void* v_new;
+  int64_t nb_sb, nb_sh;
+  const float* g_new;
+  int j;
+  int64_t pos;
+  float* ws;
+};
+
+template <int DH, bool APPLY>
 __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, int keys_per_split,
-                                                      float* ws) {
+                                                      float* ws, const DecodeApply ap) {
   constexpr int NC = DH / 32, NM = DH / 16, NW = 4;
   __shared__ __attribute__((aligned(16))) char vt_smem[NW][VtLayout<DH>::kTileBytes];
   __shared__ float red_m[NW][16], red_l[NW][16];
@@ -359,19 +442,78 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
   const int n = lane & 15, g4 = lane >> 4;
   const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
 
+  // queries (roped, rotated) and the allowed row go to LDS once
+  __shared__ __attribute__((aligned(16))) bf16_t q_lds[16][DH + 8];
+  __shared__ uint8_t al_lds[kMaxRowsPrefix];
+  stage_queries(a, b, R, &q_lds[0][0], DH + 8, [&](int r, int& st, int& h, int& qi) {
+    st = r / GL;
+    const int rem = r % GL;
+    h = hk * G + rem / a.Lq;
+    qi = rem % a.Lq;
+    return true;
+  });
+  // visibility bytes of the prefix (1 where unmasked); the host guarantees
+  // Lp <= kMaxRowsPrefix, so the tile loop reads them from LDS without a branch
+  for (int i = threadIdx.x; i < a.Lp; i += blockDim.x)
+    al_lds[i] = a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1;
+  if constexpr (APPLY) {
+    // LDS: dots [Hkv][Me+Ms] | used [Me+Ms] | last [Me] i64 | ke [DH] | ve [DH]
+    extern __shared__ __attribute__((aligned(16))) float ap_smem[];
+    __shared__ DecodeDecision dec;
+    const coda_bank_desc& bs = ap.s;
+    const int Me = bs.Me, Ms = bs.Ms, W = bs.W, MM = Me + Ms;
+    const int Lbuf = W + MM;
+    float* dots = ap_smem;
+    int* used = reinterpret_cast<int*>(ap_smem + bs.Hkv * MM);
+    int64_t* last = reinterpret_cast<int64_t*>(ap_smem + ((bs.Hkv * MM + MM + 1) & ~1));
+    float* ke = reinterpret_cast<float*>(last + Me);
+    float* ve = ke + DH;
+    DStepWs w = dstep_ws(ap.ws, b, bs.Hkv, Me, Ms);
+    for (int i = threadIdx.x; i < bs.Hkv * MM; i += blockDim.x) dots[i] = w.dots[i];
+    for (int i = threadIdx.x; i < MM; i += blockDim.x) used[i] = w.used[i];
+    for (int i = threadIdx.x; i < Me; i += blockDim.x) last[i] = w.last[i];
+    const bf16_t* kr = (const bf16_t*)bs.k_buf + (((int64_t)b * bs.Hkv + hk) * Lbuf + ap.j) * DH;
+    const bf16_t* vr = (const bf16_t*)bs.v_buf + (((int64_t)b * bs.Hkv + hk) * Lbuf + ap.j) * DH;
+    for (int d = threadIdx.x; d < DH; d += blockDim.x) {
+      ke[d] = bf2f(kr[d]);
+      ve[d] = bf2f(vr[d]);
+    }
+    const float g_e = *w.g_e;
+    __syncthreads();
+    if (wv == 0 && Me > 0) decide_exact<bf16_t>(bs, dots, used, last, g_e, dec, hk == 0, lane);
+    if (wv == 1 && Ms > 0) decide_summary<bf16_t>(bs, dots + bs.Hkv * Me, used + Me, g_e, dec, hk == 0, lane);
+    __syncthreads();
+    if (wv == 0) {
+      apply_head<bf16_t, DH>(bs, b, hk, dec, ke, ve, (const bf16_t*)ap.k_new + b * ap.nb_sb + hk * ap.nb_sh,
+                             (const bf16_t*)ap.v_new + b * ap.nb_sb + hk * ap.nb_sh, ap.j, g_e, lane);
+      if (lane == 0) {
+        // the written slots are visible regardless of when another head's
+        // workgroup copied `allowed`
+        if (Me > 0 && dec.ow_e) al_lds[W + dec.idx_e] = 1;
+        if (Ms > 0 && dec.keep_s) al_lds[W + Me + dec.idx_s] = 1;
+        al_lds[ap.j] = 1;
+        if (hk == 0) commit_decode_meta(bs, b, dec, ap.j, ap.pos - W, ap.g_new[b]);
+      }
+      // the rows just stored were loaded into this CU's L1 above and the L1
+      // is write-through without update: wait for the stores to reach L2
+      // and drop the stale L1 lines before any wave re-reads them
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
+    }
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
   // query fragments (B operand of S^T): row n, channels 32c + 8 g4 + j
   bf16x8_t qf[NC];
   int row_qi = 0;
   {
     const bool live = n < R;
-    const int s = live ? n / GL : 0, rem = live ? n % GL : 0;
-    const int g = rem / a.Lq;
+    const int rem = live ? n % GL : 0;
     row_qi = rem % a.Lq;
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      float x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (live) prep_q8<bf16_t>(a, b, hk * G + g, row_qi, 32 * c + 8 * g4, s, x);
-      qf[c] = pack8(x);
+      uint4 u = live ? *reinterpret_cast<const uint4*>(&q_lds[n][32 * c + 8 * g4]) : uint4{0, 0, 0, 0};
+      qf[c] = __builtin_bit_cast(bf16x8_t, u);
     }
   }
   const int Lk = a.Lp + a.Lb;
@@ -387,28 +529,50 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
   const int kgl = lane / DCH, dcl = lane % DCH;
   const bool vload = kgl < 4;
 
-  for (int kt = kbeg + 16 * wv; kt < kend; kt += 16 * NW) {
-    // K fragments straight from memory: key kt + n, channels 32c + 8 g4
-    const int kidx = kt + n;
-    const bool kin = kidx < kend;
-    bf16x8_t kf[NC];
-    {
-      const bf16_t* kr = kin ? key_ptr<bf16_t>(a, b, hk, kidx, false) : nullptr;
+  // Tile loads (K fragments straight from memory, V rows for the LDS
+  // transpose, visibility of this lane's 4 keys) are issued one tile ahead
+  // of the MFMA work so the HBM latency overlaps the previous tile.  Every
+  // load is unconditional (addresses clamped into the valid key range,
+  // prefix / block chosen by selects) so no branch splits the loop and the
+  // compiler keeps the next tile's loads in flight across the MFMA work;
+  // out-of-range keys are removed by the visibility mask.
+  const bf16_t* kpre = a.Lp > 0 ? (const bf16_t*)a.kp + b * a.p_sb + hk * a.p_sh : nullptr;
+  const bf16_t* vpre = a.Lp > 0 ? (const bf16_t*)a.vp + b * a.p_sb + hk * a.p_sh : nullptr;
+  const bf16_t* kblk = a.Lb > 0 ? (const bf16_t*)a.kb + b * a.b_sb + hk * a.b_sh : nullptr;
+  const bf16_t* vblk = a.Lb > 0 ? (const bf16_t*)a.vb + b * a.b_sb + hk * a.b_sh : nullptr;
+  const int kmax = kend - 1;
+  const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
+  auto rowp = [&](int kidx, bool value) -> const bf16_t* {
+    const bool pre = kidx < a.Lp;
+    const bf16_t* base = pre ? (value ? vpre : kpre) : (value ? vblk : kblk);
+    const int64_t sl = pre ? a.p_sl : a.b_sl;
+    const int r = pre ? kidx : kidx - a.Lp;
+    return base + (int64_t)r * sl;
+  };
+  auto load_tile = [&](int kt, bf16x8_t (&kf)[NC], uint4 (&vv)[4], int& vmask) {
+    const bf16_t* kr = rowp(min(kt + n, kmax), false);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        uint4 u = kin ? *reinterpret_cast<const uint4*>(kr + 32 * c + 8 * g4) : uint4{0, 0, 0, 0};
-        kf[c] = __builtin_bit_cast(bf16x8_t, u);
-      }
-    }
-    uint4 vv[4];
-    if (vload) {
+    for (int c = 0; c < NC; ++c) kf[c] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(kr + 32 * c + 8 * g4));
+    // every lane loads (lanes past the 4 key groups re-read group kgl & 3)
+    // so the loads stay unconditional; only their LDS store is predicated
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int vk = kt + 4 * kgl + jj;
-        vv[jj] = vk < kend ? *reinterpret_cast<const uint4*>(key_ptr<bf16_t>(a, b, hk, vk, true) + 8 * dcl)
-                           : uint4{0, 0, 0, 0};
-      }
+    for (int jj = 0; jj < 4; ++jj)
+      vv[jj] = *reinterpret_cast<const uint4*>(rowp(min(kt + 4 * (kgl & 3) + jj, kmax), true) + 8 * dcl);
+    int m4 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kk = kt + 4 * g4 + j;
+      const int kc = min(kk, kmax);
+      const bool pre = kc < a.Lp;
+      const int al_ok = al_lds[pre ? kc : 0];
+      const int blk_ok = (a.causal == 0) | (kc - a.Lp <= row_qi + coff);
+      const int vis = (kk <= kmax) & (pre ? (al_ok != 0) : blk_ok);
+      m4 |= vis << j;
     }
+    vmask = m4;
+  };
+  // One tile of MFMA + online-softmax work on already-loaded registers.
+  auto consume = [&](int kt, const bf16x8_t (&kf)[NC], const uint4 (&vv)[4], int vmask) {
     f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NC; ++c) st = mfma_k32(kf[c], qf[c], st);
@@ -417,9 +581,7 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
     float tmax = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int kk = kt + 4 * g4 + j;
-      const bool vis = kk < kend && key_visible(a, b, row_qi, kk);
-      sv[j] = vis ? st[j] * scale : -INFINITY;
+      sv[j] = ((vmask >> j) & 1) ? st[j] * scale : -INFINITY;
       tmax = fmaxf(tmax, sv[j]);
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
@@ -448,6 +610,26 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
       o[mt] = mfma_k16(__builtin_bit_cast(short4_t, cell), pf, o[mt]);
     }
     __builtin_amdgcn_wave_barrier();
+  };
+  // ping-pong register buffers: tile i+1 loads while tile i computes, with
+  // no register copies between iterations (a copy would wait for the loads).
+  // Every wave runs the same trip count and always prefetches: tiles past
+  // the end clamp to the last key row (one cached line) and are masked, so
+  // no branch splits the loop and the loads stay in flight.
+  bf16x8_t kf0[NC], kf1[NC];
+  uint4 vv0[4], vv1[4];
+  int vm0 = 0, vm1 = 0;
+  const int ntile = (kend - kbeg + 15) >> 4;
+  const int nt_w = (ntile + NW - 1) / NW;
+  auto kt_of = [&](int i) { return kbeg + 16 * (wv + i * NW); };
+  if (nt_w > 0) load_tile(kt_of(0), kf0, vv0, vm0);
+  for (int i = 0; i < nt_w; i += 2) {
+    load_tile(kt_of(i + 1), kf1, vv1, vm1);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(kt_of(i), kf0, vv0, vm0);
+    load_tile(kt_of(i + 2), kf0, vv0, vm0);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(kt_of(i + 1), kf1, vv1, vm1);
   }
   // merge the 4 waves
   if (g4 == 0) { red_m[wv][n] = m_i; red_l[wv][n] = l_i; }
@@ -726,6 +908,12 @@ __global__ __launch_bounds__(NW * 64) void attn_tile_bf16(const coda_attn_desc a
 // ------------------------------------------------------------ host side
 static int rows_nsplit(const coda_attn_desc* d) {
   const int Lk = d->Lp + d->Lb;
+  // CODA_ATTN_SPLIT=n forces the decode key split (launch-shape tuning)
+  static const int forced = [] {
+    const char* e = getenv("CODA_ATTN_SPLIT");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced > 0) return forced;
   const int pairs = d->B * d->Hkv;
   if (pairs >= 512) return 1;
   int ns = (512 + pairs - 1) / pairs;
@@ -760,6 +948,8 @@ static int validate(const coda_attn_desc* d) {
                "coda_diff_attn_fwd: need q_noise or theta tables");
   CODA_REQUIRE(!d->rope_cos == !d->rope_sin, "coda_diff_attn_fwd: rope_cos/rope_sin come in pairs");
   CODA_REQUIRE(d->Lp + d->Lb < (1 << 30), "coda_diff_attn_fwd: too many keys");
+  CODA_REQUIRE(d->Lp <= kMaxRowsPrefix, "coda_diff_attn_fwd: prefix of %d slots (max %d)", d->Lp,
+               kMaxRowsPrefix);
   return CODA_OK;
 }
 
@@ -797,8 +987,8 @@ static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
       if (!d->workspace || d->workspace_bytes < need)
         return fail(CODA_ESMALL, "coda_diff_attn_fwd: workspace %zu < %zu bytes", d->workspace_bytes, need);
     }
-    hipLaunchKernelGGL((attn_rows_bf16<DH>), dim3(ns_eff > 0 ? ns_eff : 1, d->Hkv, d->B), dim3(256), 0, st, *d,
-                       per, (float*)d->workspace);
+    hipLaunchKernelGGL((attn_rows_bf16<DH, false>), dim3(ns_eff > 0 ? ns_eff : 1, d->Hkv, d->B), dim3(256), 0, st,
+                       *d, per, (float*)d->workspace, DecodeApply{});
     int rc = check_launch("attn_rows_bf16");
     if (rc || ns_eff <= 1) return rc;
     hipLaunchKernelGGL((attn_rows_merge<DH>), dim3(d->Hkv, d->B), dim3(256), 0, st, *d, ns_eff,
@@ -827,4 +1017,84 @@ extern "C" int coda_diff_attn_fwd(const coda_attn_desc* d, void* stream) {
     case 64: return launch_attn<64>(d, st);
     default: return launch_attn<128>(d, st);
   }
+}
+
+// ------------------------------------------------------------ decode step
+static bool step_fused(const coda_bank_desc* s, const coda_attn_desc* a, int ring_filled) {
+  return s->dtype == CODA_BF16 && ring_filled >= s->W && use_rows(a) && rows_nsplit(a) == 1;
+}
+
+static size_t step_apply_lds(const coda_bank_desc* s) {
+  const int MM = s->Me + s->Ms;
+  return sizeof(float) * ((size_t)((s->Hkv * MM + MM + 1) & ~1) + 2 * (size_t)s->Me + 2 * (size_t)s->Dh);
+}
+
+static int validate_step(const coda_bank_desc* s, const coda_attn_desc* a) {
+  int rc = validate(a);
+  if (rc) return rc;
+  CODA_REQUIRE(s != nullptr, "coda_decode_step: null state descriptor");
+  const int Lbuf = s->W + s->Me + s->Ms;
+  CODA_REQUIRE(a->dtype == s->dtype && a->B == s->B && a->Hkv == s->Hkv && a->Dh == s->Dh,
+               "coda_decode_step: attention and state descriptors disagree (dtype/B/Hkv/Dh)");
+  CODA_REQUIRE(a->Lq == 1 && a->Lb == 0 && a->Lp == Lbuf && a->kp == s->k_buf && a->vp == s->v_buf,
+               "coda_decode_step: attention must read one query over the state cache (Lq=1, Lb=0, Lp=Lbuf)");
+  CODA_REQUIRE(a->p_sl == s->Dh && a->p_sh == (int64_t)Lbuf * s->Dh && a->p_sb == (int64_t)s->Hkv * Lbuf * s->Dh,
+               "coda_decode_step: state cache must be contiguous (B, Hkv, Lbuf, Dh)");
+  return CODA_OK;
+}
+
+extern "C" int coda_decode_step_workspace_bytes(const coda_bank_desc* s, const coda_attn_desc* a, size_t* bytes) {
+  int rc = validate_step(s, a);
+  if (rc) return rc;
+  CODA_REQUIRE(bytes != nullptr, "coda_decode_step_workspace_bytes: null out pointer");
+  size_t att = 0;
+  rc = coda_attn_workspace_bytes(a, &att);
+  if (rc) return rc;
+  const size_t fused = sizeof(float) * (size_t)s->B * dstep_words(s->Hkv, s->Me, s->Ms);
+  *bytes = att > fused ? att : fused;
+  return CODA_OK;
+}
+
+extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new, const void* v_new,
+                                int64_t nb_sb, int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled,
+                                int64_t pos, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = validate_step(s, a);
+  if (rc) return rc;
+  if (!step_fused(s, a, ring_filled)) {
+    // ring still filling, fp32, key split or a shape outside the decode
+    // tile: bank kernel, then the attention kernel
+    rc = coda_decode_write(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, stream);
+    if (rc) return rc;
+    coda_attn_desc d = *a;
+    d.workspace = workspace;
+    d.workspace_bytes = workspace_bytes;
+    return coda_diff_attn_fwd(&d, stream);
+  }
+  CODA_REQUIRE(k_new && v_new && g_new, "coda_decode_step: new token pointers missing");
+  CODA_REQUIRE(ring_idx >= 0 && ring_idx < s->W, "coda_decode_step: ring_idx %d outside [0, %d)", ring_idx, s->W);
+  CODA_REQUIRE(s->k_buf && s->v_buf && s->allowed && s->g_recent, "coda_decode_step: state buffers missing");
+  CODA_REQUIRE(s->Me == 0 || (s->mem_last && s->exact_v_norm), "coda_decode_step: exact bank buffers missing");
+  CODA_REQUIRE(s->Ms == 0 || (s->sum_lf_k_norm && s->eta_logit), "coda_decode_step: summary bank buffers missing");
+  const size_t need = sizeof(float) * (size_t)s->B * dstep_words(s->Hkv, s->Me, s->Ms);
+  if (!workspace || workspace_bytes < need)
+    return fail(CODA_ESMALL, "coda_decode_step: workspace %zu < %zu bytes", workspace_bytes, need);
+  if (s->B == 0) return CODA_OK;
+  hipStream_t st = (hipStream_t)stream;
+  rc = launch_decode_route(s, ring_idx, (float*)workspace, st);
+  if (rc) return rc;
+  DecodeApply ap{*s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, (float*)workspace};
+  const size_t lds = step_apply_lds(s);
+  const int Lk = a->Lp;
+  const dim3 grid(1, a->Hkv, a->B), block(256);
+  switch (a->Dh) {
+    case 32:
+      hipLaunchKernelGGL((attn_rows_bf16<32, true>), grid, block, lds, st, *a, Lk, nullptr, ap);
+      break;
+    case 64:
+      hipLaunchKernelGGL((attn_rows_bf16<64, true>), grid, block, lds, st, *a, Lk, nullptr, ap);
+      break;
+    default:
+      hipLaunchKernelGGL((attn_rows_bf16<128, true>), grid, block, lds, st, *a, Lk, nullptr, ap);
+  }
+  return check_launch("attn_rows_bf16<apply>");
 }

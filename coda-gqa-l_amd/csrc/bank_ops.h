@@ -1,0 +1,376 @@
+// Device-side building blocks of bank maintenance shared by the bank
+// kernels (banks.hip) and the decode attention kernel (attn.hip), which
+// applies one head's bank update in its prologue.
+//
+// Every arithmetic step that feeds a decision or a stored value repeats the
+// rounding of the reference's eager CPU ops (src/coda_gqa_l/memory_banks.py;
+// one rounding to the element type per torch op, fp32 accumulation inside
+// matmul / mean / norm / scatter_add).
+#pragma once
+
+#include "common.h"
+
+#include <math.h>
+
+namespace coda {
+
+static constexpr int64_t kNegBig = -(int64_t(1) << 62);
+static constexpr int64_t kPosBig = int64_t(1) << 62;
+
+template <typename T>
+__device__ __forceinline__ float eps_r() {
+  return Elt<T>::rnd(1e-6f);
+}
+template <typename T>
+__device__ __forceinline__ float neg_fill() {
+  return Elt<T>::rnd(-1e9f);
+}
+
+// (value, index) arg-max with first-occurrence ties, across a wave.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+  }
+}
+__device__ __forceinline__ void wave_argmin_i64(int64_t& v, int& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const int64_t ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(i, o, 64);
+    if (ov < v || (ov == v && oi < i)) { v = ov; i = oi; }
+  }
+}
+__device__ __forceinline__ int wave_or(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ int wave_and(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v &= __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ void atomic_add_i64(int64_t* p, int64_t v) {
+  if (p && v) atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
+}
+
+// F.normalize(x, dim=-1, eps=1e-6) of one row held by one wave (lane owns
+// channels lane + 64 i, i < NV): fp32 sum of squares, norm rounded to the
+// element type, clamp_min(eps), rounded division.
+template <typename T, int NV>
+__device__ __forceinline__ void wave_unit(float (&x)[NV], const bool (&act)[NV]) {
+  using E = Elt<T>;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (act[i]) ss = fmaf(x[i], x[i], ss);
+  ss = wave_sum(ss);
+  const float den = fmaxf(E::rnd(sqrtf(ss)), eps_r<T>());
+#pragma unroll
+  for (int i = 0; i < NV; ++i) x[i] = act[i] ? E::rnd(x[i] / den) : 0.f;
+}
+
+// Dots of rows of a [rows][len] device matrix (element T) against one fp32
+// vector in LDS, cooperatively by a wave: `len/8` lanes per row, 8 channels
+// per lane (one 16-byte load), group reduction by xor shuffles.
+template <typename T>
+__device__ __forceinline__ void load8f(const T* p, float x[8]) {
+  if constexpr (sizeof(T) == 2) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = bf2f((bf16_t)(w[i] & 0xffffu));
+      x[2 * i + 1] = bf2f((bf16_t)(w[i] >> 16));
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  }
+}
+
+// out[item] = rnd(dot(vec(item), mat_row(item))), items enumerated by the
+// caller through `row_ptr(item)` / `vec_ptr(item)`; len in {16,32,64,128}.
+// Each lane owns 8 channels of one row (len/8 lanes per row); a wave issues
+// the 16-byte loads of U rows per lane before reducing any of them, so U
+// loads are in flight per lane (the dot phase is latency bound otherwise).
+template <typename T, int U = 8, typename RowF, typename VecF, typename OutF>
+__device__ __forceinline__ void wave_dots(int n_items, int len, int wave, int n_waves, int lane, RowF row_ptr,
+                                          VecF vec_ptr, OutF out) {
+  const int lpi = len >> 3;          // lanes per item
+  const int ipw = 64 / lpi;          // items per wave per unrolled slot
+  const int grp = lane / lpi, sub = lane % lpi;
+  for (int base = wave * ipw * U; base < n_items; base += n_waves * ipw * U) {
+    float x[U][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int item = base + u * ipw + grp;
+      if (item < n_items) {
+        load8f<T>(row_ptr(item) + 8 * sub, x[u]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[u][j] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int item = base + u * ipw + grp;
+      float acc = 0.f;
+      if (item < n_items) {
+        const float* v = vec_ptr(item) + 8 * sub;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = fmaf(v[j], x[u][j], acc);
+      }
+      for (int o = lpi >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+      if (item < n_items && sub == 0) out(item, Elt<T>::rnd(acc));
+    }
+  }
+}
+
+// ------------------------------------------------------------ decode decision
+// Outcome of the exact and summary decisions for one evicted token.
+struct DecodeDecision {
+  int idx_e, ow_e, keep_e;
+  int idx_s, keep_s, new_s;
+};
+
+// Exact bank decision for one token by one wave (memory_banks.py:240-290):
+// de[h * Me + m] per-head cosine dots (rounded), used[m] (0/1) and last[m]
+// the bank metadata before the update.  Lane 0 writes dec; with `count`
+// it also adds the metrics / frustration counters.
+template <typename T>
+__device__ __forceinline__ void decide_exact(const coda_bank_desc& s, const float* de, const int* used,
+                                             const int64_t* last, float g_e, DecodeDecision& dec, bool count,
+                                             int lane) {
+  using E = Elt<T>;
+  const int Me = s.Me, Ae = s.active_exact, Hkv = s.Hkv;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  int any_used = 0, free_i = 0x7fffffff;
+  int64_t lv = kPosBig + 1;
+  int li = 0x7fffffff;
+  for (int m = lane; m < Me; m += 64) {
+    float acc = 0.f;
+    for (int h = 0; h < Hkv; ++h) acc += de[h * Me + m];
+    float sc = E::rnd(acc / (float)Hkv);
+    const bool u = used[m] != 0;
+    if (m >= Ae || !u) sc = neg_fill<T>();
+    if (sc > bv || (sc == bv && m < bi)) { bv = sc; bi = m; }
+    if (m < Ae && u) any_used = 1;
+    if (m < Ae && !u && m < free_i) free_i = m;
+    const int64_t lk = (m < Ae && u) ? last[m] : kPosBig;
+    if (lk < lv || (lk == lv && m < li)) { lv = lk; li = m; }
+  }
+  wave_argmax(bv, bi);
+  any_used = wave_or(any_used);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) free_i = min(free_i, __shfl_xor(free_i, o, 64));
+  wave_argmin_i64(lv, li);
+  if (lane == 0) {
+    const bool keep = s.gated ? (g_e >= s.tau_exact) : true;
+    const bool novel = !any_used || bv < E::rnd(s.tau_novel);
+    const bool hit = any_used && bv >= E::rnd(s.tau_match);
+    const bool free_exists = free_i != 0x7fffffff;
+    const int idx = novel ? (free_exists ? free_i : li) : bi;
+    const bool ow = (s.refresh_on_hit ? (novel || hit) : novel) && keep;
+    dec.idx_e = idx;
+    dec.ow_e = ow;
+    dec.keep_e = keep;
+    if (count) {
+      if (s.metrics) {
+        if (s.gated && !keep) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, 1);
+        if (hit) atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, 1);
+        if (novel && keep) atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, 1);
+        if (ow) atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, 1);
+      }
+      if (s.frustrated && novel && keep && !free_exists) atomic_add_i64(s.frustrated + 0, 1);
+    }
+  }
+}
+
+// Summary bank routing for one token by one wave (memory_banks.py:352-392):
+// ds[h * Ms + m] per-head LF-key dots, used[m] summary used bits before the
+// update.
+template <typename T>
+__device__ __forceinline__ void decide_summary(const coda_bank_desc& s, const float* ds, const int* used, float g_e,
+                                               DecodeDecision& dec, bool count, int lane) {
+  using E = Elt<T>;
+  const int Ms = s.Ms, As = s.active_summary, Hkv = s.Hkv;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int m = lane; m < Ms; m += 64) {
+    float acc = 0.f;
+    for (int h = 0; h < Hkv; ++h) acc += ds[h * Ms + m];
+    float sc = E::rnd(acc / (float)Hkv);
+    if (m >= As) sc = neg_fill<T>();
+    if (sc > bv || (sc == bv && m < bi)) { bv = sc; bi = m; }
+  }
+  wave_argmax(bv, bi);
+  const bool keep = s.gated ? (g_e >= s.tau_summary) : true;
+  int all_used = 1;
+  for (int m = lane; m < As; m += 64)
+    if (!(used[m] != 0 || (keep && m == bi))) all_used = 0;
+  all_used = wave_and(all_used);
+  if (lane == 0) {
+    dec.idx_s = bi;
+    dec.keep_s = keep;
+    dec.new_s = used[bi] == 0;
+    if (count) {
+      if (s.metrics) {
+        if (keep) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, 1);
+        if (s.overwrite_on_insert && dec.new_s && keep) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, 1);
+      }
+      if (s.frustrated) {
+        if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
+        if (keep) atomic_add_i64(s.frustrated + 2, 1);
+      }
+    }
+  }
+}
+
+// Bank writes of one head for one evicted token, by one wave; every old
+// row this head needs (exact slot, summary slot) and the new token are
+// loaded together, then:
+//   exact  : new = mem + w * (k_e - mem), w = one-hot(idx) * overwrite,
+//            V-norm cache row refreshed
+//   summary: eta = sigmoid(logit_h) (* gate) (1 if new) * keep;
+//            K_LF += eta * (k_e_LF * energy - K_LF), V += eta * (v_e - V),
+//            LF-K-norm cache row refreshed
+//   ring   : slot j <- new token
+// (memory_banks.py:296-331, :381-416, :214-222).  ke / ve: the evicted
+// row of head h as floats; kn_src / vn_src: the new token of head h.
+template <typename T, int DH>
+__device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h, const DecodeDecision& dec,
+                                           const float* ke, const float* ve, const T* kn_src, const T* vn_src,
+                                           int j, float g_e, int lane) {
+  using E = Elt<T>;
+  constexpr int NV = (DH + 63) / 64;
+  const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, lf = s.lf, LF = DH - lf;
+  const int Lbuf = W + Me + Ms;
+  T* kb = (T*)s.k_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
+  T* vb = (T*)s.v_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
+  const bool do_e = Me > 0 && dec.ow_e;
+  const bool do_s = Ms > 0 && dec.keep_s;
+  const int idx_e = Me > 0 ? dec.idx_e : 0, idx_s = Ms > 0 ? dec.idx_s : 0;
+  T* kre = kb + (int64_t)(W + idx_e) * DH;
+  T* vre = vb + (int64_t)(W + idx_e) * DH;
+  T* krs = kb + (int64_t)(W + Me + idx_s) * DH;
+  T* vrs = vb + (int64_t)(W + Me + idx_s) * DH;
+  float mke[NV], mve[NV], mks[NV], mvs[NV], kn[NV], vn[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int d = min(lane + 64 * i, DH - 1);
+    mke[i] = do_e ? E::ld(kre[d]) : 0.f;
+    mve[i] = do_e ? E::ld(vre[d]) : 0.f;
+    mks[i] = do_s ? E::ld(krs[d]) : 0.f;
+    mvs[i] = do_s ? E::ld(vrs[d]) : 0.f;
+    kn[i] = E::ld(kn_src[d]);
+    vn[i] = E::ld(vn_src[d]);
+  }
+  if (do_e) {
+    float nv[NV];
+    bool act[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = lane + 64 * i;
+      act[i] = d < DH;
+      nv[i] = 0.f;
+      if (act[i]) {
+        kre[d] = E::st(mke[i] + E::rnd(ke[d] - mke[i]));
+        nv[i] = E::rnd(mve[i] + E::rnd(ve[d] - mve[i]));
+        vre[d] = E::st(nv[i]);
+      }
+    }
+    wave_unit<T, NV>(nv, act);
+    T* nr = (T*)s.exact_v_norm + (((int64_t)b * Hkv + h) * Me + idx_e) * DH;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (act[i]) nr[lane + 64 * i] = E::st(nv[i]);
+  }
+  if (do_s) {
+    float eta = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
+    if (s.gated) eta = E::rnd(eta * E::rnd(g_e));
+    if (s.overwrite_on_insert && dec.new_s) eta = 1.f;
+    float nk[NV];
+    bool act[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = lane + 64 * i;
+      act[i] = false;
+      nk[i] = 0.f;
+      if (d < DH) {
+        vrs[d] = E::st(mvs[i] + E::rnd(eta * E::rnd(ve[d] - mvs[i])));
+        if (d >= lf) {
+          const float dk = E::rnd(E::rnd(ke[d] * s.energy_scale) - mks[i]);
+          nk[i] = E::rnd(mks[i] + E::rnd(eta * dk));
+          krs[d] = E::st(nk[i]);
+          act[i] = true;
+        }
+      }
+    }
+    wave_unit<T, NV>(nk, act);
+    T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + idx_s) * LF;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (act[i]) nr[lane + 64 * i - lf] = E::st(nk[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int d = lane + 64 * i;
+    if (d < DH) {
+      kb[(int64_t)j * DH + d] = E::st(kn[i]);
+      vb[(int64_t)j * DH + d] = E::st(vn[i]);
+    }
+  }
+}
+
+// Per-sequence metadata after a decode update (one thread): used bits of
+// the written slots, the LRU stamp, the ring gate.
+__device__ __forceinline__ void commit_decode_meta(const coda_bank_desc& s, int b, const DecodeDecision& dec, int j,
+                                                   int64_t pos_e, float g_new) {
+  const int W = s.W, Me = s.Me, Ms = s.Ms;
+  uint8_t* al = s.allowed + (int64_t)b * (W + Me + Ms);
+  if (Me > 0) {
+    if (dec.ow_e) al[W + dec.idx_e] = 1;
+    if (dec.keep_e) s.mem_last[(int64_t)b * Me + dec.idx_e] = pos_e;
+  }
+  if (Ms > 0 && dec.keep_s) al[W + Me + dec.idx_s] = 1;
+  s.g_recent[(int64_t)b * W + j] = g_new;
+}
+
+// Workspace of the two-kernel decode step, per sequence (4-byte words):
+//   dots  [Hkv][Me + Ms] f32  per-head exact / summary cosine dots (rounded)
+//   used  [Me + Ms] i32       bank used bits before the update
+//   last  [Me] i64            LRU stamps before the update (8-byte aligned)
+//   g_e   f32                 gate of the evicted ring slot
+__host__ __device__ __forceinline__ int dstep_words(int Hkv, int Me, int Ms) {
+  const int a = Hkv * (Me + Ms) + (Me + Ms);
+  return ((a + 1) & ~1) + 2 * Me + 2;
+}
+struct DStepWs {
+  float* dots;
+  int32_t* used;
+  int64_t* last;
+  float* g_e;
+};
+__host__ __device__ __forceinline__ DStepWs dstep_ws(float* ws, int b, int Hkv, int Me, int Ms) {
+  float* base = ws + (int64_t)b * dstep_words(Hkv, Me, Ms);
+  DStepWs w;
+  w.dots = base;
+  w.used = reinterpret_cast<int32_t*>(base + Hkv * (Me + Ms));
+  const int a = Hkv * (Me + Ms) + (Me + Ms);
+  w.last = reinterpret_cast<int64_t*>(base + ((a + 1) & ~1));
+  w.g_e = base + ((a + 1) & ~1) + 2 * Me;
+  return w;
+}
+
+// Host launcher of decode_route_kernel (defined with the bank kernels).
+int launch_decode_route(const coda_bank_desc* s, int j, float* ws, hipStream_t st);
+
+}  // namespace coda

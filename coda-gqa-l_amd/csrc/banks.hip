@@ -11,6 +11,7 @@
 //
 // Layout (contiguous): k_buf/v_buf [B][Hkv][Lbuf][Dh], Lbuf = W + Me + Ms,
 // slots [0,W) ring, [W,W+Me) exact bank, [W+Me,Lbuf) summary bank.
+#include "bank_ops.h"
 #include "common.h"
 #include "select.h"
 
@@ -21,118 +22,12 @@
 
 namespace coda {
 
-static constexpr int64_t kNegBig = -(int64_t(1) << 62);
-static constexpr int64_t kPosBig = int64_t(1) << 62;
-
-template <typename T>
-__device__ __forceinline__ float eps_r() {
-  return Elt<T>::rnd(1e-6f);
-}
-template <typename T>
-__device__ __forceinline__ float neg_fill() {
-  return Elt<T>::rnd(-1e9f);
-}
-
-// (value, index) arg-max with first-occurrence ties, across a wave.
-__device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-  }
-}
-__device__ __forceinline__ void wave_argmin_i64(int64_t& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const int64_t ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    if (ov < v || (ov == v && oi < i)) { v = ov; i = oi; }
-  }
-}
-__device__ __forceinline__ int wave_or(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
-  return v;
-}
-__device__ __forceinline__ int wave_and(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v &= __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ void atomic_add_i64(int64_t* p, int64_t v) {
-  if (p && v) atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
-}
-
-// F.normalize(x, dim=-1, eps=1e-6) of one row held by one wave (lane owns
-// channels lane + 64 i, i < NV): fp32 sum of squares, norm rounded to the
-// element type, clamp_min(eps), rounded division.
-template <typename T, int NV>
-__device__ __forceinline__ void wave_unit(float (&x)[NV], const bool (&act)[NV]) {
-  using E = Elt<T>;
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (act[i]) ss = fmaf(x[i], x[i], ss);
-  ss = wave_sum(ss);
-  const float den = fmaxf(E::rnd(sqrtf(ss)), eps_r<T>());
-#pragma unroll
-  for (int i = 0; i < NV; ++i) x[i] = act[i] ? E::rnd(x[i] / den) : 0.f;
-}
-
-// Dots of rows of a [rows][len] device matrix (element T) against one fp32
-// vector in LDS, cooperatively by a wave: `len/8` lanes per row, 8 channels
-// per lane (one 16-byte load), group reduction by xor shuffles.
-template <typename T>
-__device__ __forceinline__ void load8f(const T* p, float x[8]) {
-  if constexpr (sizeof(T) == 2) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[2 * i] = bf2f((bf16_t)(w[i] & 0xffffu));
-      x[2 * i + 1] = bf2f((bf16_t)(w[i] >> 16));
-    }
-  } else {
-    const float4 a = *reinterpret_cast<const float4*>(p);
-    const float4 b = *reinterpret_cast<const float4*>(p + 4);
-    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
-    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
-  }
-}
-
-// out[item] = rnd(dot(vec(item), mat_row(item))), items enumerated by the
-// caller through `row_ptr(item)` / `vec_ptr(item)`; len in {16,32,64,128}.
-template <typename T, typename RowF, typename VecF, typename OutF>
-__device__ __forceinline__ void wave_dots(int n_items, int len, int wave, int n_waves, int lane, RowF row_ptr,
-                                          VecF vec_ptr, OutF out) {
-  const int lpi = len >> 3;          // lanes per item
-  const int ipw = 64 / lpi;          // items per wave step
-  const int grp = lane / lpi, sub = lane % lpi;
-  for (int base = wave * ipw; base < n_items; base += n_waves * ipw) {
-    const int item = base + grp;
-    float acc = 0.f;
-    if (item < n_items) {
-      float x[8];
-      load8f<T>(row_ptr(item) + 8 * sub, x);
-      const float* v = vec_ptr(item) + 8 * sub;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc = fmaf(v[j], x[j], acc);
-    }
-    for (int o = lpi >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-    if (item < n_items && sub == 0) out(item, Elt<T>::rnd(acc));
-  }
-}
-
-struct DecodeDecision {
-  int idx_e, ow_e, keep_e;
-  int idx_s, keep_s, new_s;
-};
 
 // ------------------------------------------------------------ decode
-// One workgroup (512 threads) per sequence b.  Reference: _write_one,
-// _exact_update_one, _summary_update_one (memory_banks.py:183-432).
+// One workgroup (512 threads) per sequence b: the whole update of one
+// evicted token (memory_banks.py:183-432).  The two-kernel decode step
+// (decode_route_kernel + the attention kernel's apply prologue) spreads
+// the same work over (sequence, head) workgroups.
 template <typename T, int DH>
 __global__ __launch_bounds__(512) void decode_write_kernel(const coda_bank_desc s, const T* __restrict__ k_new,
                                                            const T* __restrict__ v_new, int64_t nb_sb,
@@ -164,18 +59,24 @@ __global__ __launch_bounds__(512) void decode_write_kernel(const coda_bank_desc 
     return;
   }
 
-  // LDS: ke, ve [Hkv][DH]; vn [Hkv][DH]; kn [Hkv][LF]; de [Hkv][Me]; ds [Hkv][Ms]
+  // LDS: ke, ve, vn [Hkv][DH]; kn [Hkv][LF]; de [Hkv][Me]; ds [Hkv][Ms];
+  //      used [Me + Ms] i32; last [Me] i64
   float* ke = smem;
   float* ve = ke + Hkv * DH;
   float* vnrm = ve + Hkv * DH;
   float* knrm = vnrm + Hkv * DH;
   float* de = knrm + Hkv * LF;
   float* dsum = de + Hkv * Me;
+  // int64 stamps need 8-byte alignment: both offsets are rounded to even words
+  int* used = reinterpret_cast<int*>(smem + ((3 * Hkv * DH + Hkv * LF + Hkv * (Me + Ms) + 1) & ~1));
+  int64_t* last = reinterpret_cast<int64_t*>(used + ((Me + Ms + 1) & ~1));
   for (int i = t; i < Hkv * DH; i += NT) {
     const int h = i / DH, d = i % DH;
     ke[i] = E::ld(kb[((int64_t)h * Lbuf + j) * DH + d]);
     ve[i] = E::ld(vb[((int64_t)h * Lbuf + j) * DH + d]);
   }
+  for (int m = t; m < Me + Ms; m += NT) used[m] = al[W + m];
+  for (int m = t; m < Me; m += NT) last[m] = s.mem_last[(int64_t)b * Me + m];
   const float g_e = s.g_recent[(int64_t)b * W + j];
   const int64_t pos_e = pos - W;
   __syncthreads();
@@ -203,179 +104,87 @@ __global__ __launch_bounds__(512) void decode_write_kernel(const coda_bank_desc 
   // per-head cosine dots against the norm caches
   if (Me > 0) {
     const T* en = (const T*)s.exact_v_norm + (int64_t)b * Hkv * Me * DH;
-    wave_dots<T>(
+    wave_dots<T, 16>(
         Hkv * Me, DH, wv, NWV, lane, [&](int it) { return en + (int64_t)it * DH; },
         [&](int it) { return (const float*)(vnrm + (it / Me) * DH); }, [&](int it, float v) { de[it] = v; });
   }
   if (Ms > 0) {
     const T* sn = (const T*)s.sum_lf_k_norm + (int64_t)b * Hkv * Ms * LF;
-    wave_dots<T>(
+    wave_dots<T, 16>(
         Hkv * Ms, LF, wv, NWV, lane, [&](int it) { return sn + (int64_t)it * LF; },
         [&](int it) { return (const float*)(knrm + (it / Ms) * LF); }, [&](int it, float v) { dsum[it] = v; });
   }
   __syncthreads();
-  if (wv == 0 && Me > 0) {
-    // exact decision (memory_banks.py:240-290)
-    const int Ae = s.active_exact;
-    const uint8_t* used = al + W;
-    const int64_t* last = s.mem_last + (int64_t)b * Me;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    int any_used = 0, free_i = 0x7fffffff;
-    int64_t lv = kPosBig + 1;
-    int li = 0x7fffffff;
-    for (int m = lane; m < Me; m += 64) {
-      float acc = 0.f;
-      for (int h = 0; h < Hkv; ++h) acc += de[h * Me + m];
-      float sc = E::rnd(acc / (float)Hkv);
-      const bool u = used[m] != 0;
-      if (m >= Ae || !u) sc = neg_fill<T>();
-      if (sc > bv || (sc == bv && m < bi)) { bv = sc; bi = m; }
-      if (m < Ae && u) any_used = 1;
-      if (m < Ae && !u && m < free_i) free_i = m;
-      const int64_t lk = (m < Ae && u) ? last[m] : kPosBig;
-      if (lk < lv || (lk == lv && m < li)) { lv = lk; li = m; }
-    }
-    wave_argmax(bv, bi);
-    any_used = wave_or(any_used);
-    {
-      int fi = free_i;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) fi = min(fi, __shfl_xor(fi, o, 64));
-      free_i = fi;
-    }
-    wave_argmin_i64(lv, li);
-    if (lane == 0) {
-      const bool keep = s.gated ? (g_e >= s.tau_exact) : true;
-      const bool novel = !any_used || bv < E::rnd(s.tau_novel);
-      const bool hit = any_used && bv >= E::rnd(s.tau_match);
-      const bool free_exists = free_i != 0x7fffffff;
-      const int idx = novel ? (free_exists ? free_i : li) : bi;
-      const bool ow = (s.refresh_on_hit ? (novel || hit) : novel) && keep;
-      dec.idx_e = idx;
-      dec.ow_e = ow;
-      dec.keep_e = keep;
-      if (s.metrics) {
-        if (s.gated && !keep) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, 1);
-        if (hit) atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, 1);
-        if (novel && keep) atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, 1);
-        if (ow) atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, 1);
-      }
-      if (s.frustrated && novel && keep && !free_exists) atomic_add_i64(s.frustrated + 0, 1);
-    }
+  if (wv == 0 && Me > 0) decide_exact<T>(s, de, used, last, g_e, dec, true, lane);
+  if (wv == 1 && Ms > 0) decide_summary<T>(s, dsum, used + Me, g_e, dec, true, lane);
+  __syncthreads();
+  for (int h = wv; h < Hkv; h += NWV)
+    apply_head<T, DH>(s, b, h, dec, ke + h * DH, ve + h * DH, kn_src + h * nb_sh, vn_src + h * nb_sh, j, g_e,
+                      lane);
+  if (t == 0) commit_decode_meta(s, b, dec, j, pos_e, g_new[b]);
+}
+
+// First kernel of the two-kernel decode step: one workgroup per (head h,
+// sequence b) normalises head h of the evicted ring row and takes its
+// cosine dots with head h's norm caches; the h == 0 workgroup also
+// snapshots the sequence's bank metadata before any update.
+template <typename T, int DH>
+__global__ __launch_bounds__(256) void decode_route_kernel(const coda_bank_desc s, int j, float* ws) {
+  using E = Elt<T>;
+  constexpr int NV = (DH + 63) / 64;
+  __shared__ __attribute__((aligned(16))) float ke[DH], ve[DH], vnrm[DH], knrm[DH];
+  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, lf = s.lf, LF = DH - lf;
+  const int Lbuf = W + Me + Ms;
+  DStepWs w = dstep_ws(ws, b, Hkv, Me, Ms);
+  const T* kr = (const T*)s.k_buf + (((int64_t)b * Hkv + h) * Lbuf + j) * DH;
+  const T* vr = (const T*)s.v_buf + (((int64_t)b * Hkv + h) * Lbuf + j) * DH;
+  if (h == 0) {
+    const uint8_t* al = s.allowed + (int64_t)b * Lbuf;
+    for (int m = t; m < Me + Ms; m += 256) w.used[m] = al[W + m];
+    for (int m = t; m < Me; m += 256) w.last[m] = s.mem_last[(int64_t)b * Me + m];
+    if (t == 0) *w.g_e = s.g_recent[(int64_t)b * W + j];
   }
-  if (wv == 1 && Ms > 0) {
-    // summary routing (memory_banks.py:352-392)
-    const int As = s.active_summary;
-    const uint8_t* used = al + W + Me;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    int all_used = 1;
-    for (int m = lane; m < Ms; m += 64) {
-      float acc = 0.f;
-      for (int h = 0; h < Hkv; ++h) acc += dsum[h * Ms + m];
-      float sc = E::rnd(acc / (float)Hkv);
-      if (m >= As) sc = neg_fill<T>();
-      if (sc > bv || (sc == bv && m < bi)) { bv = sc; bi = m; }
-    }
-    wave_argmax(bv, bi);
-    const bool keep = s.gated ? (g_e >= s.tau_summary) : true;
-    for (int m = lane; m < As; m += 64)
-      if (!(used[m] != 0 || (keep && m == bi))) all_used = 0;
-    all_used = wave_and(all_used);
-    if (lane == 0) {
-      dec.idx_s = bi;
-      dec.keep_s = keep;
-      dec.new_s = used[bi] == 0;
-      if (s.metrics) {
-        if (keep) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, 1);
-        if (s.overwrite_on_insert && dec.new_s && keep) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, 1);
-      }
-      if (s.frustrated) {
-        if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
-        if (keep) atomic_add_i64(s.frustrated + 2, 1);
-      }
-    }
+  for (int d = t; d < DH; d += 256) {
+    ke[d] = E::ld(kr[d]);
+    ve[d] = E::ld(vr[d]);
   }
   __syncthreads();
-  // exact write: w = one-hot(idx) * overwrite; new = mem + w * (k - mem)
-  if (Me > 0) {
-    const int idx = dec.idx_e;
-    if (dec.ow_e) {
-      for (int h = wv; h < Hkv; h += NWV) {
-        T* kr = kb + ((int64_t)h * Lbuf + W + idx) * DH;
-        T* vr = vb + ((int64_t)h * Lbuf + W + idx) * DH;
-        float nv[NV];
-        bool act[NV];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int d = lane + 64 * i;
-          act[i] = d < DH;
-          nv[i] = 0.f;
-          if (act[i]) {
-            const float mk = E::ld(kr[d]), mv = E::ld(vr[d]);
-            kr[d] = E::st(mk + E::rnd(ke[h * DH + d] - mk));
-            nv[i] = E::rnd(mv + E::rnd(ve[h * DH + d] - mv));
-            vr[d] = E::st(nv[i]);
-          }
-        }
-        wave_unit<T, NV>(nv, act);
-        T* nr = (T*)s.exact_v_norm + (((int64_t)b * Hkv + h) * Me + idx) * DH;
-#pragma unroll
-        for (int i = 0; i < NV; ++i)
-          if (act[i]) nr[lane + 64 * i] = E::st(nv[i]);
-      }
-      if (t == 0) al[W + idx] = 1;
-    }
-    if (t == 0 && dec.keep_e) s.mem_last[(int64_t)b * Me + idx] = pos_e;
-  }
-  // summary write: eta = sigmoid(logit_h) (* gate) (1 if new) * keep
-  if (Ms > 0 && dec.keep_s) {
-    const int idx = dec.idx_s;
-    for (int h = wv; h < Hkv; h += NWV) {
-      float eta = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
-      if (s.gated) eta = E::rnd(eta * E::rnd(g_e));
-      if (s.overwrite_on_insert && dec.new_s) eta = 1.f;
-      T* kr = kb + ((int64_t)h * Lbuf + W + Me + idx) * DH;
-      T* vr = vb + ((int64_t)h * Lbuf + W + Me + idx) * DH;
-      float nk[NV];
+  if (wv < 2) {
+    const bool is_v = wv == 0;
+    if ((is_v && Me > 0) || (!is_v && Ms > 0)) {
+      const int len = is_v ? DH : LF;
+      float x[NV];
       bool act[NV];
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int d = lane + 64 * i;
-        act[i] = d < LF;
-        nk[i] = 0.f;
-        if (d < DH) {
-          const float mv = E::ld(vr[d]);
-          vr[d] = E::st(mv + E::rnd(eta * E::rnd(ve[h * DH + d] - mv)));
-        }
+        act[i] = d < len;
+        x[i] = act[i] ? (is_v ? ve[d] : ke[lf + d]) : 0.f;
       }
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int d = lf + lane + 64 * i;
-        if (act[i]) {
-          const float mk = E::ld(kr[d]);
-          const float dk = E::rnd(E::rnd(ke[h * DH + d] * s.energy_scale) - mk);
-          nk[i] = E::rnd(mk + E::rnd(eta * dk));
-          kr[d] = E::st(nk[i]);
-        }
-      }
-      wave_unit<T, NV>(nk, act);
-      T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + idx) * LF;
+      wave_unit<T, NV>(x, act);
 #pragma unroll
       for (int i = 0; i < NV; ++i)
-        if (act[i]) nr[lane + 64 * i] = E::st(nk[i]);
+        if (act[i]) (is_v ? vnrm : knrm)[lane + 64 * i] = x[i];
     }
-    if (t == 0) al[W + Me + idx] = 1;
   }
   __syncthreads();
-  // ring overwrite of the evicted slot
-  for (int i = t; i < Hkv * DH; i += NT) {
-    const int h = i / DH, d = i % DH;
-    kb[((int64_t)h * Lbuf + j) * DH + d] = kn_src[h * nb_sh + d];
-    vb[((int64_t)h * Lbuf + j) * DH + d] = vn_src[h * nb_sh + d];
+  // dots layout: exact [Hkv][Me] then summary [Hkv][Ms]
+  float* out_e = w.dots + (int64_t)h * Me;
+  float* out_s = w.dots + (int64_t)Hkv * Me + (int64_t)h * Ms;
+  // waves 0-1: exact rows, waves 2-3: summary rows
+  if (wv < 2 && Me > 0) {
+    const T* en = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + h) * Me * DH;
+    wave_dots<T, 16>(
+        Me, DH, wv, 2, lane, [&](int it) { return en + (int64_t)it * DH; }, [&](int) { return (const float*)vnrm; },
+        [&](int it, float v) { out_e[it] = v; });
   }
-  if (t == 0) s.g_recent[(int64_t)b * W + j] = g_new[b];
+  if (wv >= 2 && Ms > 0) {
+    const T* sn = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + h) * Ms * LF;
+    wave_dots<T, 16>(
+        Ms, LF, wv - 2, 2, lane, [&](int it) { return sn + (int64_t)it * LF; },
+        [&](int) { return (const float*)knrm; }, [&](int it, float v) { out_s[it] = v; });
+  }
 }
 
 // ------------------------------------------------------------ block plan
@@ -426,36 +235,59 @@ __global__ __launch_bounds__(64) void block_plan_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------ block write
-// Workspace layout per call (4-byte words), T = max(Te, Ts):
-//   dot_e [B][Hkv][Te][Me] f32   per-head exact cosine dots (rounded)
-//   dot_s [B][Hkv][Ts][Ms] f32   per-head summary cosine dots (rounded)
-//   dec   [B][3][T] i32          idx_e, ow | touch << 1, idx_s
-//   wtok  [B][Ts] f32            summary weight (rounded to the element type)
-//   slot  [B][Me + 2 Ms]         exact overwrite flag (i32), summary count
-//                                (f32, rounded), summary flags (i32: 1 active,
-//                                2 fresh = active and previously unused)
+// Two kernels per chunk:
+//   route  grid (Hkv + 1, B): blocks h < Hkv normalise head h of the
+//          candidate rows and take their cosine dots with the head's norm
+//          caches (staged in LDS); block Hkv snapshots the pre-update bank
+//          metadata of sequence b (used bits, LRU stamps, candidate gates)
+//          and computes the LRU victim order.
+//   update grid (Hkv, B): every head block recomputes the per-sequence
+//          decisions from the dots and snapshots (cheap, deterministic,
+//          identical in every block, so no cross-block barrier is needed),
+//          applies them to its own head's rows, and writes its head of the
+//          ring; block h == 0 also writes the per-sequence metadata.
+// Workspace (4-byte words), TT = max(Te, Ts):
+//   dot_e [B][Hkv][Te][Me] f32, dot_s [B][Hkv][Ts][Ms] f32,
+//   snap  [B][SNAP]: used (Me+Ms) i32 | last (Me) i64 | gate (TT) f32 | lru (Me) i32
 struct BlockGeom {
   int blk, ring_head, ring_filled, n_ev, Kmax, Te, Ts;
   int64_t pos0;
   int64_t b_sb, b_sh, b_sl, g_sb;
 };
 
+__host__ __device__ __forceinline__ int even_up(int x) { return (x + 1) & ~1; }
+__host__ __device__ __forceinline__ int snap_words(int Me, int Ms, int TT) {
+  return even_up(even_up(Me + Ms) + 2 * Me + TT + Me);
+}
 __host__ __device__ __forceinline__ size_t ws_dot_s(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
   return (size_t)B * Hkv * Te * Me;
 }
-__host__ __device__ __forceinline__ size_t ws_dec(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
-  return ws_dot_s(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * Hkv * Ts * Ms;
-}
-__host__ __device__ __forceinline__ size_t ws_wtok(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
-  return ws_dec(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * 3 * (Te > Ts ? Te : Ts);
-}
-__host__ __device__ __forceinline__ size_t ws_slot(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
-  return ws_wtok(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * Ts;
+__host__ __device__ __forceinline__ size_t ws_snap(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
+  return (ws_dot_s(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * Hkv * Ts * Ms + 1) & ~(size_t)1;  // 8-byte aligned
 }
 __host__ __device__ __forceinline__ size_t ws_total(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
-  return ws_slot(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * (Me + 2 * Ms);
+  return ws_snap(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * snap_words(Me, Ms, Te > Ts ? Te : Ts) + 2;
 }
 #define CODA_WS(fn, s, g) fn((s).B, (s).Hkv, (s).Me, (s).Ms, (g).Te, (g).Ts)
+
+struct Snap {
+  int32_t* used;
+  int64_t* last;
+  float* gate;
+  int32_t* lru;
+};
+__device__ __forceinline__ Snap snap_of(const coda_bank_desc& s, const BlockGeom& g, float* ws, int b) {
+  const int TT = max(g.Te, g.Ts);
+  int32_t* base = reinterpret_cast<int32_t*>(ws + CODA_WS(ws_snap, s, g)) + (int64_t)b * snap_words(s.Me, s.Ms, TT);
+  Snap sn;
+  sn.used = base;
+  // int64 stamps at an 8-byte aligned word offset: the snap area starts at
+  // an even word and (Me + Ms) may be odd, so stamps follow a pad word
+  sn.last = reinterpret_cast<int64_t*>(base + even_up(s.Me + s.Ms));
+  sn.gate = reinterpret_cast<float*>(base + even_up(s.Me + s.Ms) + 2 * s.Me);
+  sn.lru = base + even_up(s.Me + s.Ms) + 2 * s.Me + TT;
+  return sn;
+}
 
 // Source row of evicted candidate e (index into the chunk's time-ordered
 // [ring | block] sequence) for KV head h: ring slot or block token.
@@ -480,368 +312,482 @@ __device__ __forceinline__ float cand_gate(const coda_bank_desc& s, const BlockG
   return gb[(int64_t)b * g.g_sb + (e - g.ring_filled)];
 }
 
-// K1: per (b, h): unit() of the candidate rows and their per-head cosine
-// dots against the exact V-norm and summary LF-K-norm caches
-// (memory_banks.py:492-500, :640-644, :866-868).
+// Rows x cands dots from LDS, 4 x 4 register blocks, fp32 FMA in channel
+// order; result rounded to the element type (the matmul output dtype).
+template <typename T>
+__device__ __forceinline__ void lds_dots(const float* rows, int n_rows, const float* cands, int n_c, int len,
+                                         int stride, float* out /* [n_c][n_rows] */) {
+  const int nbr = (n_rows + 3) >> 2, nbc = (n_c + 3) >> 2;
+  for (int blk = threadIdx.x; blk < nbr * nbc; blk += blockDim.x) {
+    const int r0 = 4 * (blk % nbr), c0 = 4 * (blk / nbr);
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+    for (int d = 0; d < len; d += 4) {
+      float4 rv[4], cv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = min(r0 + i, n_rows - 1), c = min(c0 + i, n_c - 1);
+        rv[i] = *reinterpret_cast<const float4*>(rows + r * stride + d);
+        cv[i] = *reinterpret_cast<const float4*>(cands + c * stride + d);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[i][j] = fmaf(cv[j].x, rv[i].x, acc[i][j]);
+          acc[i][j] = fmaf(cv[j].y, rv[i].y, acc[i][j]);
+          acc[i][j] = fmaf(cv[j].z, rv[i].z, acc[i][j]);
+          acc[i][j] = fmaf(cv[j].w, rv[i].w, acc[i][j]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (r0 + i < n_rows && c0 + j < n_c) out[(c0 + j) * n_rows + r0 + i] = Elt<T>::rnd(acc[i][j]);
+  }
+}
+
+// Stage `n` rows of `len` elements (row stride `rs` elements) into LDS fp32
+// with row stride `ls` floats; 16-byte loads, all issued before use.
+template <typename T>
+__device__ __forceinline__ void stage_rows(float* dst, int ls, const T* src, int64_t rs, int n, int len) {
+  const int chunks = len >> 3;
+  for (int i = threadIdx.x; i < n * chunks; i += blockDim.x) {
+    const int r = i / chunks, c = i % chunks;
+    float x[8];
+    load8f<T>(src + r * rs + 8 * c, x);
+    float4* d = reinterpret_cast<float4*>(dst + r * ls + 8 * c);
+    d[0] = make_float4(x[0], x[1], x[2], x[3]);
+    d[1] = make_float4(x[4], x[5], x[6], x[7]);
+  }
+}
+
+// Normalised candidate rows (one wave per row) into LDS.
 template <typename T, int DH>
-__global__ __launch_bounds__(256) void block_route_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
-                                                          const T* vbk, const int32_t* __restrict__ plan_c,
-                                                          float* __restrict__ ws) {
-  constexpr int NV = (DH + 63) / 64, NWV = 4;
-  extern __shared__ __attribute__((aligned(16))) float rsm[];
-  const int h = blockIdx.x, b = blockIdx.y;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int LF = DH - s.lf;
-  float* vn = rsm;                 // [Te][DH]
-  float* kn = vn + g.Te * DH;      // [Ts][LF]
-  const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
-  for (int r = wv; r < g.Te + g.Ts; r += NWV) {
-    const bool is_v = r < g.Te;
-    const int tt = is_v ? r : r - g.Te;
-    const int e = pc[tt];
-    const T* src = is_v ? cand_row<T, DH>(s, g, vbk, b, h, e, true) : cand_row<T, DH>(s, g, kbk, b, h, e, false);
-    const int len = is_v ? DH : LF;
-    const int off = is_v ? 0 : s.lf;
+__device__ __forceinline__ void stage_cands(float* dst, int ls, const coda_bank_desc& s, const BlockGeom& g,
+                                            const T* src_blk, const int32_t* pc, int b, int h, int n, int off,
+                                            int len, bool value) {
+  constexpr int NV = (DH + 63) / 64;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int r = wv; r < n; r += nw) {
+    const T* row = cand_row<T, DH>(s, g, src_blk, b, h, pc[r], value);
     float x[NV];
     bool act[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int d = lane + 64 * i;
       act[i] = d < len;
-      x[i] = act[i] ? Elt<T>::ld(src[off + d]) : 0.f;
+      x[i] = act[i] ? Elt<T>::ld(row[off + d]) : 0.f;
     }
     wave_unit<T, NV>(x, act);
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      if (act[i]) (is_v ? vn[tt * DH + lane + 64 * i] : kn[tt * LF + lane + 64 * i]) = x[i];
+      if (act[i]) dst[r * ls + lane + 64 * i] = x[i];
   }
-  __syncthreads();
+}
+
+template <typename T, int DH>
+__global__ __launch_bounds__(256) void block_route_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
+                                                          const T* vbk, const float* gb,
+                                                          const int32_t* __restrict__ plan_c, float* ws) {
+  extern __shared__ __attribute__((aligned(16))) float rsm[];
+  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int Me = s.Me, Ms = s.Ms, W = s.W, LF = DH - s.lf;
+  const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
+  if (h == s.Hkv) {
+    Snap sn = snap_of(s, g, ws, b);
+    const uint8_t* al = s.allowed + (int64_t)b * (W + Me + Ms);
+    for (int m = t; m < Me + Ms; m += blockDim.x) sn.used[m] = al[W + m];
+    for (int m = t; m < Me; m += blockDim.x) sn.last[m] = s.mem_last[(int64_t)b * Me + m];
+    const int TT = max(g.Te, g.Ts);
+    for (int i = t; i < TT; i += blockDim.x) sn.gate[i] = cand_gate(s, g, gb, b, pc[i]);
+    if (g.Te > 0) {
+      sel::Item<int64_t>* rk = reinterpret_cast<sel::Item<int64_t>*>(rsm);
+      const int Ae = s.active_exact;
+      for (int m = t; m < Me; m += blockDim.x) {
+        const bool u = al[W + m] != 0 && m < Ae;
+        rk[m] = sel::Item<int64_t>{u ? s.mem_last[(int64_t)b * Me + m] : kNegBig, (int64_t)m};
+      }
+      __syncthreads();
+      const int n_lru = min(g.Te, Ae);
+      if (t == 0) sel::topk_order<int64_t>(rk, Me, n_lru, false, true);
+      __syncthreads();
+      for (int r = t; r < n_lru; r += blockDim.x) sn.lru[r] = (int32_t)rk[r].i;
+    }
+    return;
+  }
   if (g.Te > 0) {
-    const T* en = (const T*)s.exact_v_norm + ((int64_t)b * s.Hkv + h) * s.Me * DH;
-    float* out = ws + (((int64_t)b * s.Hkv + h) * g.Te) * s.Me;
-    const int Me = s.Me;
-    wave_dots<T>(
-        g.Te * Me, DH, wv, NWV, lane, [&](int it) { return en + (int64_t)(it % Me) * DH; },
-        [&](int it) { return (const float*)(vn + (it / Me) * DH); }, [&](int it, float v) { out[it] = v; });
+    const int ls = DH + 4;
+    float* nrm = rsm;
+    float* cnd = rsm + Me * ls;
+    stage_rows<T>(nrm, ls, (const T*)s.exact_v_norm + ((int64_t)b * s.Hkv + h) * Me * DH, DH, Me, DH);
+    stage_cands<T, DH>(cnd, ls, s, g, vbk, pc, b, h, g.Te, 0, DH, true);
+    __syncthreads();
+    lds_dots<T>(nrm, Me, cnd, g.Te, DH, ls, ws + (((int64_t)b * s.Hkv + h) * g.Te) * Me);
+    __syncthreads();
   }
   if (g.Ts > 0) {
-    const T* sn = (const T*)s.sum_lf_k_norm + ((int64_t)b * s.Hkv + h) * s.Ms * LF;
-    float* out = ws + CODA_WS(ws_dot_s, s, g) + (((int64_t)b * s.Hkv + h) * g.Ts) * s.Ms;
-    const int Ms = s.Ms;
-    wave_dots<T>(
-        g.Ts * Ms, LF, wv, NWV, lane, [&](int it) { return sn + (int64_t)(it % Ms) * LF; },
-        [&](int it) { return (const float*)(kn + (it / Ms) * LF); }, [&](int it, float v) { out[it] = v; });
+    const int ls = LF + 4;
+    float* nrm = rsm;
+    float* cnd = rsm + Ms * ls;
+    stage_rows<T>(nrm, ls, (const T*)s.sum_lf_k_norm + ((int64_t)b * s.Hkv + h) * Ms * LF, LF, Ms, LF);
+    stage_cands<T, DH>(cnd, ls, s, g, kbk, pc, b, h, g.Ts, s.lf, LF, false);
+    __syncthreads();
+    lds_dots<T>(nrm, Ms, cnd, g.Ts, LF, ls, ws + CODA_WS(ws_dot_s, s, g) + (((int64_t)b * s.Hkv + h) * g.Ts) * Ms);
   }
 }
 
-// K2: per b: head means, exact decisions (novelty, LRU topk, cumsum rank,
-// touch / overwrite, LRU stamps, used), summary routing, weights, counts.
-// Reference: memory_banks.py:635-697 + :721-727 (exact), :513-528 +
-// :866-918 (summary).  Per-slot results go to the workspace; `allowed` is
-// updated here, after every read of the pre-update bits.
-template <typename T, int DH>
-__global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc s, BlockGeom g, const float* gb,
-                                                           const int32_t* __restrict__ plan_c,
-                                                           float* __restrict__ ws) {
-  using E = Elt<T>;
-  extern __shared__ __attribute__((aligned(16))) char dsm[];
-  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int W = s.W, Me = s.Me, Ms = s.Ms, Hkv = s.Hkv, Te = g.Te, Ts = g.Ts;
-  const int Lbuf = W + Me + Ms;
-  uint8_t* al = s.allowed + (int64_t)b * Lbuf;
-  const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
-  const int TT = max(Te, Ts);
-  int32_t* dec = reinterpret_cast<int32_t*>(ws + CODA_WS(ws_dec, s, g)) + (int64_t)b * 3 * TT;
-  float* wtok = ws + CODA_WS(ws_wtok, s, g) + (int64_t)b * Ts;
-  int32_t* eflag = reinterpret_cast<int32_t*>(ws + CODA_WS(ws_slot, s, g)) + (int64_t)b * (Me + 2 * Ms);
-  float* cnt = reinterpret_cast<float*>(eflag + Me);
-  int32_t* sflag = eflag + Me + Ms;
-
-  if (Te > 0) {
-    // LDS: rk [Me] items (16 B each) | sc [Te][Me] f32 | best [Te] f32 | best_i [Te] i32
-    sel::Item<int64_t>* rk = reinterpret_cast<sel::Item<int64_t>*>(dsm);
-    float* sc = reinterpret_cast<float*>(rk + Me);
-    float* best = sc + Te * Me;
-    int* best_i = reinterpret_cast<int*>(best + Te);
-    const float* de = ws + (int64_t)b * Hkv * Te * Me;
-    for (int i = t; i < Te * Me; i += 256) {
-      float acc = 0.f;
-      for (int h = 0; h < Hkv; ++h) acc += de[(int64_t)h * Te * Me + i];
-      float v = E::rnd(acc / (float)Hkv);
-      const int m = i % Me;
-      if (m >= s.active_exact || al[W + m] == 0) v = neg_fill<T>();
-      sc[i] = v;
-    }
-    for (int m = t; m < Me; m += 256) {
-      const bool u = al[W + m] != 0 && m < s.active_exact;
-      rk[m] = sel::Item<int64_t>{u ? s.mem_last[(int64_t)b * Me + m] : kNegBig, (int64_t)m};
-    }
-    __syncthreads();
-    for (int tt = wv; tt < Te; tt += 4) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int m = lane; m < Me; m += 64) {
-        const float v = sc[tt * Me + m];
-        if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
-      }
-      wave_argmax(bv, bi);
-      if (lane == 0) { best[tt] = bv; best_i[tt] = bi; }
-    }
-    __syncthreads();
-    if (t == 0) {
-      const int Ae = s.active_exact;
-      int any_used = 0;
-      for (int m = 0; m < Me; ++m) any_used |= al[W + m] != 0;
-      const int n_lru = min(Te, Ae);
-      sel::topk_order<int64_t>(rk, Me, n_lru, false, true);
-      int64_t* last = s.mem_last + (int64_t)b * Me;
-      int rank = -1;
-      int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
-      for (int tt = 0; tt < Te; ++tt) {
-        const float gate = cand_gate(s, g, gb, b, pc[tt]);
-        const bool keep = s.gated ? (gate >= s.tau_exact) : true;
-        const float bv = best[tt];
-        const bool novel = !any_used || bv < E::rnd(s.tau_novel);
-        const bool hit = any_used && bv >= E::rnd(s.tau_match);
-        const bool nk = novel && keep;
-        if (nk) ++rank;                       // rank = cumsum(nk) - 1 at tt
-        const bool cap = nk && rank < Ae;
-        int idx = best_i[tt];
-        if (cap) {
-          int r = rank < 0 ? 0 : rank;
-          if (r > n_lru - 1) r = n_lru - 1;
-          idx = (int)rk[r].i;
-        }
-        const bool touch = keep && (!novel || cap);
-        const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
-        dec[tt] = idx;
-        dec[TT + tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
-        cnt_ow += ow;
-        cnt_cap += cap;
-        cnt_hit += (hit && keep);
-        cnt_gated += !keep;
-        cnt_fr += (nk && !cap);
-      }
-      // LRU stamps: last[m] = max pos of the tokens touching m
-      for (int m = 0; m < Me; ++m) {
-        int64_t pv = kNegBig;
-        bool tm = false;
-        int f = 0;
-        for (int tt = 0; tt < Te; ++tt) {
-          if (dec[tt] != m) continue;
-          if (dec[TT + tt] & 2) {
-            tm = true;
-            const int64_t p = g.pos0 - g.ring_filled + pc[tt];
-            if (p > pv) pv = p;
-          }
-          f |= dec[TT + tt] & 1;
-        }
-        if (tm) last[m] = pv;
-        eflag[m] = f;
-      }
-      if (s.metrics) {
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, cnt_ow);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, cnt_fr);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, cnt_cap);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, cnt_hit);
-        if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, cnt_gated);
-      }
-      if (s.frustrated) atomic_add_i64(s.frustrated + 0, cnt_fr);
-    }
-    __syncthreads();
-  } else {
-    for (int m = t; m < Me; m += 256) eflag[m] = 0;
-  }
-  if (Ts > 0) {
-    float* sc = reinterpret_cast<float*>(dsm);  // [Ts][Ms]; the exact scratch is dead
-    const float* dsd = ws + CODA_WS(ws_dot_s, s, g) + (int64_t)b * Hkv * Ts * Ms;
-    for (int i = t; i < Ts * Ms; i += 256) {
-      float acc = 0.f;
-      for (int h = 0; h < Hkv; ++h) acc += dsd[(int64_t)h * Ts * Ms + i];
-      float v = E::rnd(acc / (float)Hkv);
-      if (i % Ms >= s.active_summary) v = neg_fill<T>();
-      sc[i] = v;
-    }
-    __syncthreads();
-    for (int tt = wv; tt < Ts; tt += 4) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int m = lane; m < Ms; m += 64) {
-        const float v = sc[tt * Ms + m];
-        if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
-      }
-      wave_argmax(bv, bi);
-      if (lane == 0) {
-        dec[2 * TT + tt] = bi;
-        const float gate = cand_gate(s, g, gb, b, pc[tt]);
-        wtok[tt] = (!s.gated || gate >= s.tau_summary) ? E::rnd(gate) : 0.f;
-      }
-    }
-    __syncthreads();
-    for (int m = t; m < Ms; m += 256) {
-      float c = 0.f;
-      for (int tt = 0; tt < Ts; ++tt)
-        if (dec[2 * TT + tt] == m) c += wtok[tt];
-      cnt[m] = E::rnd(c);
-      const bool active = cnt[m] > 0.f;
-      const bool fresh = active && al[W + Me + m] == 0;
-      sflag[m] = (active ? 1 : 0) | (fresh ? 2 : 0);
-    }
-  } else {
-    for (int m = t; m < Ms; m += 256) { cnt[m] = 0.f; sflag[m] = 0; }
-  }
-  __syncthreads();
-  if (t == 0) {
-    int64_t upd = 0, ins = 0;
-    int all_used = 1, any_cnt = 0;
-    for (int m = 0; m < Ms; ++m) {
-      const int f = sflag[m];
-      upd += f & 1;
-      ins += (f >> 1) & 1;
-      if (m < s.active_summary) {
-        if (!(al[W + Me + m] != 0 || (f & 1))) all_used = 0;
-        if (f & 1) any_cnt = 1;
-      }
-    }
-    if (Ts > 0) {
-      if (s.metrics) {
-        atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, upd);
-        if (s.overwrite_on_insert) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, ins);
-      }
-      if (s.frustrated) {
-        if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
-        if (any_cnt) atomic_add_i64(s.frustrated + 2, 1);
-      }
-    }
-    for (int m = 0; m < Me; ++m)
-      if (eflag[m]) al[W + m] = 1;
-    for (int m = 0; m < Ms; ++m)
-      if (sflag[m] & 1) al[W + Me + m] = 1;
-  }
+struct UpdLds {
+  int32_t *idx_e, *fl_e, *idx_s, *used, *eflag, *sflag, *best_i, *misc;
+  float *wtok, *cnt, *best, *big;
+};
+__host__ __device__ __forceinline__ size_t upd_small_words(int Me, int Ms, int TT) {
+  return (size_t)6 * TT + (Me + Ms) + Me + 2 * Ms + 8 + Ms;  // + active-slot list
+}
+__host__ __device__ __forceinline__ size_t upd_big_words(int Me, int Ms, int Te, int Ts, int DH, int LF) {
+  const size_t a = (size_t)Te * Me, b2 = (size_t)Ts * Ms, c = (size_t)Ms * (DH + LF);
+  return a > b2 ? (a > c ? a : c) : (b2 > c ? b2 : c);
 }
 
-// K3: per (b, h): exact delta writeback + V-norm cache, summary
-// accumulation + EMA + LF-K-norm cache (memory_banks.py:707-742,
-// :880-932), then the ring write of this chunk's surviving block tokens for
-// head h (every candidate row of head h is read before it).
 template <typename T, int DH>
-__global__ __launch_bounds__(256) void block_apply_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
-                                                          const T* vbk, const float* gb,
-                                                          const int32_t* __restrict__ plan_c,
-                                                          const float* __restrict__ ws) {
+__global__ __launch_bounds__(256) void block_update_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
+                                                           const T* vbk, const float* gb,
+                                                           const int32_t* __restrict__ plan_c, float* ws) {
   using E = Elt<T>;
-  constexpr int NV = (DH + 63) / 64, NWV = 4;
+  constexpr int NV = (DH + 63) / 64;
+  extern __shared__ __attribute__((aligned(16))) float usm[];
   const int h = blockIdx.x, b = blockIdx.y;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
   const int W = s.W, Me = s.Me, Ms = s.Ms, Hkv = s.Hkv, Te = g.Te, Ts = g.Ts, lf = s.lf, LF = DH - lf;
   const int Lbuf = W + Me + Ms;
   const int TT = max(Te, Ts);
-  const int32_t* dec = reinterpret_cast<const int32_t*>(ws + CODA_WS(ws_dec, s, g)) + (int64_t)b * 3 * TT;
-  const float* wtok = ws + CODA_WS(ws_wtok, s, g) + (int64_t)b * Ts;
-  const int32_t* eflag = reinterpret_cast<const int32_t*>(ws + CODA_WS(ws_slot, s, g)) + (int64_t)b * (Me + 2 * Ms);
-  const float* cnt = reinterpret_cast<const float*>(eflag + Me);
-  const int32_t* sflag = eflag + Me + Ms;
+  const bool lead = h == 0;
+  // LDS carve-up
+  UpdLds L;
+  {
+    int32_t* p = reinterpret_cast<int32_t*>(usm);
+    L.big = usm;  // union: scores, then summary accumulators
+    p += upd_big_words(Me, Ms, Te, Ts, DH, LF);
+    L.idx_e = p; p += TT;
+    L.fl_e = p; p += TT;
+    L.idx_s = p; p += TT;
+    L.wtok = reinterpret_cast<float*>(p); p += TT;
+    L.best = reinterpret_cast<float*>(p); p += TT;
+    L.best_i = p; p += TT;
+    L.used = p; p += Me + Ms;
+    L.eflag = p; p += Me;
+    L.sflag = p; p += Ms;
+    L.cnt = reinterpret_cast<float*>(p); p += Ms;
+    L.misc = p;
+  }
   const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
+  uint8_t* al = s.allowed + (int64_t)b * Lbuf;
   T* kb = (T*)s.k_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
   T* vb = (T*)s.v_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
-
-  if (g.n_ev > 0 && Te > 0) {
-    for (int m = wv; m < Me; m += NWV) {
-      if (!eflag[m]) continue;
-      float nv[NV];
-      bool act[NV];
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int d = lane + 64 * i;
-        act[i] = d < DH;
-        nv[i] = 0.f;
-        if (!act[i]) continue;
-        T* kr = kb + (int64_t)(W + m) * DH;
-        T* vr = vb + (int64_t)(W + m) * DH;
-        const float mk = E::ld(kr[d]), mv = E::ld(vr[d]);
-        float ak = 0.f, av = 0.f;
+  const bool evict = g.n_ev > 0;
+  if (evict) {
+    Snap sn = snap_of(s, g, ws, b);
+    for (int m = t; m < Me + Ms; m += 256) L.used[m] = sn.used[m];
+    for (int m = t; m < Me; m += 256) L.eflag[m] = 0;
+    for (int m = t; m < Ms; m += 256) { L.sflag[m] = 0; L.cnt[m] = 0.f; }
+    if (t < 8) L.misc[t] = 0;
+    __syncthreads();
+    // ---------------- exact decisions (memory_banks.py:640-697)
+    if (Te > 0) {
+      float* sc = L.big;
+      const float* de = ws + (int64_t)b * Hkv * Te * Me;
+      for (int i = t; i < Te * Me; i += 256) {
+        float acc = 0.f;
+        for (int hh = 0; hh < Hkv; ++hh) acc += de[(int64_t)hh * Te * Me + i];
+        float v = E::rnd(acc / (float)Hkv);
+        const int m = i % Me;
+        if (m >= s.active_exact || L.used[m] == 0) v = neg_fill<T>();
+        sc[i] = v;
+      }
+      __syncthreads();
+      for (int tt = wv; tt < Te; tt += 4) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int m = lane; m < Me; m += 64) {
+          const float v = sc[tt * Me + m];
+          if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
+        }
+        wave_argmax(bv, bi);
+        if (lane == 0) { L.best[tt] = bv; L.best_i[tt] = bi; }
+      }
+      __syncthreads();
+      if (t == 0) {
+        const int Ae = s.active_exact;
+        int any_used = 0;
+        for (int m = 0; m < Me; ++m) any_used |= L.used[m] != 0;
+        const int n_lru = min(Te, Ae);
+        int rank = -1;
+        int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
         for (int tt = 0; tt < Te; ++tt) {
-          if (dec[tt] != m || !(dec[TT + tt] & 1)) continue;
-          const int e = pc[tt];
-          ak += E::rnd(E::ld(cand_row<T, DH>(s, g, kbk, b, h, e, false)[d]) - mk);
-          av += E::rnd(E::ld(cand_row<T, DH>(s, g, vbk, b, h, e, true)[d]) - mv);
+          const bool keep = s.gated ? (sn.gate[tt] >= s.tau_exact) : true;
+          const float bv = L.best[tt];
+          const bool novel = !any_used || bv < E::rnd(s.tau_novel);
+          const bool hit = any_used && bv >= E::rnd(s.tau_match);
+          const bool nk = novel && keep;
+          if (nk) ++rank;  // cumsum(novel & keep) - 1 at tt
+          const bool cap = nk && rank < Ae;
+          int idx = L.best_i[tt];
+          if (cap) {
+            int r = rank < 0 ? 0 : rank;
+            if (r > n_lru - 1) r = n_lru - 1;
+            idx = sn.lru[r];
+          }
+          const bool touch = keep && (!novel || cap);
+          const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
+          L.idx_e[tt] = idx;
+          L.fl_e[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
+          cnt_ow += ow;
+          cnt_cap += cap;
+          cnt_hit += (hit && keep);
+          cnt_gated += !keep;
+          cnt_fr += (nk && !cap);
         }
-        kr[d] = E::st(mk + E::rnd(ak));
-        nv[i] = E::rnd(mv + E::rnd(av));
-        vr[d] = E::st(nv[i]);
+        if (lead) {
+          if (s.metrics) {
+            atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, cnt_ow);
+            atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, cnt_fr);
+            atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, cnt_cap);
+            atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, cnt_hit);
+            if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, cnt_gated);
+          }
+          if (s.frustrated) atomic_add_i64(s.frustrated + 0, cnt_fr);
+        }
       }
-      wave_unit<T, NV>(nv, act);
-      T* nr = (T*)s.exact_v_norm + (((int64_t)b * Hkv + h) * Me + m) * DH;
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (act[i]) nr[lane + 64 * i] = E::st(nv[i]);
+      __syncthreads();
+      for (int m = t; m < Me; m += 256) {
+        int f = 0;
+        bool tm = false;
+        int64_t pv = kNegBig;
+        for (int tt = 0; tt < Te; ++tt) {
+          if (L.idx_e[tt] != m) continue;
+          f |= L.fl_e[tt] & 1;
+          if (L.fl_e[tt] & 2) {
+            tm = true;
+            const int64_t p = g.pos0 - g.ring_filled + pc[tt];
+            if (p > pv) pv = p;
+          }
+        }
+        L.eflag[m] = f;
+        if (lead && tm) s.mem_last[(int64_t)b * Me + m] = pv;  // LRU: max pos of the touching tokens
+      }
+      __syncthreads();
     }
-  }
-  if (g.n_ev > 0 && Ts > 0) {
-    const float eta_h = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
-    for (int m = wv; m < Ms; m += NWV) {
-      const int f = sflag[m];
-      if (!(f & 1)) continue;
-      const float eta = (s.overwrite_on_insert && (f & 2)) ? 1.f : eta_h;
-      const float den = fmaxf(cnt[m], eps_r<T>());
-      T* kr = kb + (int64_t)(W + Me + m) * DH;
-      T* vr = vb + (int64_t)(W + Me + m) * DH;
-      float nk[NV];
-      bool act[NV];
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int d = lane + 64 * i;
-        act[i] = d < LF;
-        nk[i] = 0.f;
-        if (d >= DH) continue;
-        float sv = 0.f;
-        for (int tt = 0; tt < Ts; ++tt) {
-          if (dec[2 * TT + tt] != m) continue;
-          sv += E::rnd(E::ld(cand_row<T, DH>(s, g, vbk, b, h, pc[tt], true)[d]) * wtok[tt]);
-        }
-        const float mv = E::ld(vr[d]);
-        const float avg_v = E::rnd(E::rnd(sv) / den);
-        vr[d] = E::st(mv + E::rnd(eta * E::rnd(avg_v - mv)));
+    // ---------------- summary routing + counts (memory_banks.py:513-528, :866-898)
+    if (Ts > 0) {
+      float* sc = L.big;
+      const float* dsd = ws + CODA_WS(ws_dot_s, s, g) + (int64_t)b * Hkv * Ts * Ms;
+      for (int i = t; i < Ts * Ms; i += 256) {
+        float acc = 0.f;
+        for (int hh = 0; hh < Hkv; ++hh) acc += dsd[(int64_t)hh * Ts * Ms + i];
+        float v = E::rnd(acc / (float)Hkv);
+        if (i % Ms >= s.active_summary) v = neg_fill<T>();
+        sc[i] = v;
       }
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int d = lf + lane + 64 * i;
-        if (!act[i]) continue;
-        float sk = 0.f;
-        for (int tt = 0; tt < Ts; ++tt) {
-          if (dec[2 * TT + tt] != m) continue;
-          sk += E::rnd(E::ld(cand_row<T, DH>(s, g, kbk, b, h, pc[tt], false)[d]) * wtok[tt]);
+      __syncthreads();
+      for (int tt = wv; tt < Ts; tt += 4) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int m = lane; m < Ms; m += 64) {
+          const float v = sc[tt * Ms + m];
+          if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
         }
-        const float mk = E::ld(kr[d]);
-        const float avg_k = E::rnd(E::rnd(sk) / den);
-        const float dk = E::rnd(E::rnd(avg_k * s.energy_scale) - mk);
-        nk[i] = E::rnd(mk + E::rnd(eta * dk));
-        kr[d] = E::st(nk[i]);
+        wave_argmax(bv, bi);
+        if (lane == 0) {
+          L.idx_s[tt] = bi;
+          const float gate = sn.gate[tt];
+          L.wtok[tt] = (!s.gated || gate >= s.tau_summary) ? E::rnd(gate) : 0.f;
+        }
       }
-      wave_unit<T, NV>(nk, act);
-      T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + m) * LF;
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (act[i]) nr[lane + 64 * i] = E::st(nk[i]);
+      __syncthreads();
+      for (int m = t; m < Ms; m += 256) {
+        float c = 0.f;
+        for (int tt = 0; tt < Ts; ++tt)
+          if (L.idx_s[tt] == m) c += L.wtok[tt];  // fp32 accumulation in token order
+        L.cnt[m] = E::rnd(c);
+        const bool active = L.cnt[m] > 0.f;
+        L.sflag[m] = (active ? 1 : 0) | ((active && L.used[Me + m] == 0) ? 2 : 0);
+      }
+      __syncthreads();
     }
+    // ---------------- exact writeback of head h (memory_banks.py:707-742)
+    if (Te > 0) {
+      for (int m = wv; m < Me; m += 4) {
+        if (!L.eflag[m]) continue;
+        float nv[NV];
+        bool act[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int d = lane + 64 * i;
+          act[i] = d < DH;
+          nv[i] = 0.f;
+          if (!act[i]) continue;
+          T* kr = kb + (int64_t)(W + m) * DH;
+          T* vr = vb + (int64_t)(W + m) * DH;
+          const float mk = E::ld(kr[d]), mv = E::ld(vr[d]);
+          float ak = 0.f, av = 0.f;
+          for (int tt = 0; tt < Te; ++tt) {
+            if (L.idx_e[tt] != m || !(L.fl_e[tt] & 1)) continue;
+            ak += E::rnd(E::ld(cand_row<T, DH>(s, g, kbk, b, h, pc[tt], false)[d]) - mk);
+            av += E::rnd(E::ld(cand_row<T, DH>(s, g, vbk, b, h, pc[tt], true)[d]) - mv);
+          }
+          kr[d] = E::st(mk + E::rnd(ak));
+          nv[i] = E::rnd(mv + E::rnd(av));
+          vr[d] = E::st(nv[i]);
+        }
+        wave_unit<T, NV>(nv, act);
+        T* nr = (T*)s.exact_v_norm + (((int64_t)b * Hkv + h) * Me + m) * DH;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+          if (act[i]) nr[lane + 64 * i] = E::st(nv[i]);
+      }
+    }
+    // ---------------- summary accumulate + EMA of head h (memory_banks.py:880-932)
+    if (Ts > 0) {
+      // accumulators [Ms][DH + LF]: V channels then K's LF channels; one
+      // thread per channel walks the tokens in order (fp32 scatter_add order)
+      float* acc = L.big;
+      const int ncol = DH + LF;
+      for (int i = t; i < Ms * ncol; i += 256) acc[i] = 0.f;
+      __syncthreads();
+      for (int col = t; col < ncol; col += 256) {
+        const bool is_v = col < DH;
+        const int d = is_v ? col : lf + (col - DH);
+        const T* src = is_v ? vbk : kbk;
+        // 8 independent row loads in flight, then the in-order accumulation
+        for (int t0 = 0; t0 < Ts; t0 += 8) {
+          float xv[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int tt = min(t0 + u, Ts - 1);
+            xv[u] = E::ld(cand_row<T, DH>(s, g, src, b, h, pc[tt], is_v)[d]);
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int tt = t0 + u;
+            if (tt < Ts) acc[L.idx_s[tt] * ncol + col] += E::rnd(xv[u] * L.wtok[tt]);
+          }
+        }
+      }
+      __syncthreads();
+      // active slots, compacted (in slot order)
+      int* act_list = L.misc + 8;
+      if (t == 0) {
+        int na = 0;
+        for (int m = 0; m < Ms; ++m)
+          if (L.sflag[m] & 1) act_list[na++] = m;
+        L.misc[0] = na;
+      }
+      __syncthreads();
+      const int n_act = L.misc[0];
+      const float eta_h = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
+#pragma unroll 4
+      for (int it = t; it < n_act * ncol; it += 256) {
+        const int m = act_list[it / ncol], col = it % ncol;
+        const bool is_v = col < DH;
+        const int d = is_v ? col : lf + (col - DH);
+        const int f = L.sflag[m];
+        const float eta = (s.overwrite_on_insert && (f & 2)) ? 1.f : eta_h;
+        const float den = fmaxf(L.cnt[m], eps_r<T>());
+        const float avg = E::rnd(E::rnd(acc[m * ncol + col]) / den);
+        T* row = (is_v ? vb : kb) + (int64_t)(W + Me + m) * DH;
+        const float mem = E::ld(row[d]);
+        if (is_v) {
+          row[d] = E::st(mem + E::rnd(eta * E::rnd(avg - mem)));
+        } else {
+          const float dk = E::rnd(E::rnd(avg * s.energy_scale) - mem);
+          const float nk = E::rnd(mem + E::rnd(eta * dk));
+          row[d] = E::st(nk);
+          acc[m * ncol + col] = nk;  // new LF key, read back for the norm cache
+        }
+      }
+      __syncthreads();
+      for (int m = wv; m < Ms; m += 4) {
+        if (!(L.sflag[m] & 1)) continue;
+        float x[NV];
+        bool act[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int d = lane + 64 * i;
+          act[i] = d < LF;
+          x[i] = act[i] ? acc[m * ncol + DH + d] : 0.f;
+        }
+        wave_unit<T, NV>(x, act);
+        T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + m) * LF;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+          if (act[i]) nr[lane + 64 * i] = E::st(x[i]);
+      }
+    }
+    // ---------------- per-sequence metadata (lead block)
+    if (lead) {
+      for (int m = t; m < Me; m += 256)
+        if (L.eflag[m]) al[W + m] = 1;
+      for (int m = t; m < Ms; m += 256)
+        if (L.sflag[m] & 1) al[W + Me + m] = 1;
+      if (Ts > 0 && wv == 0) {
+        int64_t upd = 0, ins = 0;
+        int all_used = 1, any_cnt = 0;
+        for (int m = lane; m < Ms; m += 64) {
+          const int f = L.sflag[m];
+          upd += f & 1;
+          ins += (f >> 1) & 1;
+          if (m < s.active_summary) {
+            if (!(L.used[Me + m] != 0 || (f & 1))) all_used = 0;
+            if (f & 1) any_cnt = 1;
+          }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+          upd += __shfl_xor(upd, o, 64);
+          ins += __shfl_xor(ins, o, 64);
+        }
+        all_used = wave_and(all_used);
+        any_cnt = wave_or(any_cnt);
+        if (lane == 0) {
+          if (s.metrics) {
+            atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, upd);
+            if (s.overwrite_on_insert) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, ins);
+          }
+          if (s.frustrated) {
+            if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
+            if (any_cnt) atomic_add_i64(s.frustrated + 2, 1);
+          }
+        }
+      }
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  // ring write of the surviving block tokens (combined index i >= Lr)
-  uint8_t* al = s.allowed + (int64_t)b * Lbuf;
+  // ---------------- ring write of the surviving block tokens (combined index i >= Lr)
   const int Lr = g.ring_filled;
   const int first = max(Lr, g.n_ev);
   const int total = Lr + g.blk;
   const int head = (Lr == W) ? g.ring_head : 0;
-  for (int i = first + wv; i < total; i += NWV) {
-    const int slot = (head + i) % W;
-    const int jb = i - Lr;
+  constexpr int CH = DH / 8;
+  for (int i = t; i < (total - first) * CH; i += 256) {
+    const int r = first + i / CH, c = i % CH;
+    const int slot = (head + r) % W;
+    const int jb = r - Lr;
     const T* ks = kbk + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl;
     const T* vs = vbk + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl;
-    for (int d = lane; d < DH; d += 64) {
-      kb[(int64_t)slot * DH + d] = ks[d];
-      vb[(int64_t)slot * DH + d] = vs[d];
+    if constexpr (sizeof(T) == 2) {
+      *reinterpret_cast<uint4*>(kb + (int64_t)slot * DH + 8 * c) = *reinterpret_cast<const uint4*>(ks + 8 * c);
+      *reinterpret_cast<uint4*>(vb + (int64_t)slot * DH + 8 * c) = *reinterpret_cast<const uint4*>(vs + 8 * c);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        reinterpret_cast<float4*>(kb + (int64_t)slot * DH + 8 * c)[j] = reinterpret_cast<const float4*>(ks + 8 * c)[j];
+        reinterpret_cast<float4*>(vb + (int64_t)slot * DH + 8 * c)[j] = reinterpret_cast<const float4*>(vs + 8 * c)[j];
+      }
     }
-    if (h == 0 && lane == 0) {
+    if (lead && c == 0) {
       s.g_recent[(int64_t)b * W + slot] = gb[(int64_t)b * g.g_sb + jb];
       al[slot] = 1;
     }
@@ -927,9 +873,29 @@ static int validate_bank(const coda_bank_desc* s, const char* who) {
   return CODA_OK;
 }
 
+int launch_decode_route(const coda_bank_desc* s, int j, float* ws, hipStream_t st) {
+  const dim3 grid(s->Hkv, s->B), block(256);
+  const bool bf = s->dtype == CODA_BF16;
+  switch (s->Dh) {
+    case 32:
+      if (bf) hipLaunchKernelGGL((decode_route_kernel<bf16_t, 32>), grid, block, 0, st, *s, j, ws);
+      else hipLaunchKernelGGL((decode_route_kernel<float, 32>), grid, block, 0, st, *s, j, ws);
+      break;
+    case 64:
+      if (bf) hipLaunchKernelGGL((decode_route_kernel<bf16_t, 64>), grid, block, 0, st, *s, j, ws);
+      else hipLaunchKernelGGL((decode_route_kernel<float, 64>), grid, block, 0, st, *s, j, ws);
+      break;
+    default:
+      if (bf) hipLaunchKernelGGL((decode_route_kernel<bf16_t, 128>), grid, block, 0, st, *s, j, ws);
+      else hipLaunchKernelGGL((decode_route_kernel<float, 128>), grid, block, 0, st, *s, j, ws);
+  }
+  return check_launch("decode_route");
+}
+
 static size_t decode_lds(const coda_bank_desc* s) {
   const int LF = s->Dh - s->lf;
-  return sizeof(float) * ((size_t)s->Hkv * s->Dh * 3 + (size_t)s->Hkv * LF + (size_t)s->Hkv * (s->Me + s->Ms));
+  return sizeof(float) * ((size_t)s->Hkv * s->Dh * 3 + (size_t)s->Hkv * LF + (size_t)s->Hkv * (s->Me + s->Ms) + 1 +
+                          (size_t)((s->Me + s->Ms + 1) & ~1) + 2 * (size_t)s->Me);
 }
 
 template <typename T, int DH>
@@ -1013,28 +979,39 @@ extern "C" int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, siz
   return CODA_OK;
 }
 
+template <typename K>
+static int ensure_lds(K kern, size_t lds, const char* who) {
+  if (lds > 160 * 1024) return fail(CODA_EUNSUP, "%s: %zu bytes of LDS needed (max 160 KiB)", who, lds);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail(CODA_EHIP, "%s: LDS attribute: %s", who, hipGetErrorString(e));
+  }
+  return CODA_OK;
+}
+
 template <typename T, int DH>
 static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb, const float* gb, BlockGeom g,
                         const int32_t* plan_c, float* ws, hipStream_t st) {
   const int LF = DH - s->lf;
-  if (g.n_ev > 0 && (g.Te > 0 || g.Ts > 0)) {
-    const size_t lds1 = sizeof(float) * ((size_t)g.Te * DH + (size_t)g.Ts * LF);
-    const size_t lds2 = std::max(sizeof(sel::Item<int64_t>) * (size_t)s->Me +
-                                     sizeof(float) * ((size_t)g.Te * s->Me + 2 * (size_t)g.Te),
-                                 sizeof(float) * (size_t)g.Ts * s->Ms);
-    if (lds1 > 64 * 1024 || lds2 > 64 * 1024)
-      return fail(CODA_EUNSUP, "coda_block_write: candidate counts Te=%d Ts=%d too large", g.Te, g.Ts);
-    hipLaunchKernelGGL((block_route_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(256), lds1, st, *s, g, (const T*)kb,
-                       (const T*)vb, plan_c, ws);
-    int rc = check_launch("block_route");
+  const int TT = g.Te > g.Ts ? g.Te : g.Ts;
+  if (g.n_ev > 0 && TT > 0) {
+    const size_t lds1 = std::max(std::max(sizeof(float) * (size_t)(s->Me + g.Te) * (DH + 4),
+                                          sizeof(float) * (size_t)(s->Ms + g.Ts) * (LF + 4)),
+                                 sizeof(sel::Item<int64_t>) * (size_t)s->Me);
+    int rc = ensure_lds(block_route_kernel<T, DH>, lds1, "coda_block_write");
     if (rc) return rc;
-    hipLaunchKernelGGL((block_decide_kernel<T, DH>), dim3(s->B), dim3(256), lds2, st, *s, g, gb, plan_c, ws);
-    rc = check_launch("block_decide");
+    hipLaunchKernelGGL((block_route_kernel<T, DH>), dim3(s->Hkv + 1, s->B), dim3(256), lds1, st, *s, g,
+                       (const T*)kb, (const T*)vb, gb, plan_c, ws);
+    rc = check_launch("block_route");
     if (rc) return rc;
   }
-  hipLaunchKernelGGL((block_apply_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(256), 0, st, *s, g, (const T*)kb,
+  const size_t lds2 = sizeof(float) * (upd_big_words(s->Me, s->Ms, g.Te, g.Ts, DH, LF) +
+                                       upd_small_words(s->Me, s->Ms, TT));
+  int rc = ensure_lds(block_update_kernel<T, DH>, lds2, "coda_block_write");
+  if (rc) return rc;
+  hipLaunchKernelGGL((block_update_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(256), lds2, st, *s, g, (const T*)kb,
                      (const T*)vb, gb, plan_c, ws);
-  return check_launch("block_apply");
+  return check_launch("block_update");
 }
 
 extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb, int64_t b_sh,

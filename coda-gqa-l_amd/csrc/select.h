@@ -235,13 +235,14 @@ __host__ __device__ inline void partial_sort(Item<V>* a, int64_t first, int64_t 
 template <typename V, typename C>
 __host__ __device__ inline void sort(Item<V>* a, int64_t first, int64_t last, const C& before) {
   if (first == last) return;
+  // each partition level pushes two frames and pops one, and levels are
+  // bounded by the depth limit 2*floor(log2 n) <= 40 for n <= 2^20
   struct Frame {
-    int64_t first, last;
-    int depth;
+    int32_t first, last, depth;
   };
-  Frame stack[64];
+  Frame stack[48];
   int sp = 0;
-  stack[sp++] = Frame{first, last, floor_log2(last - first) * 2};
+  stack[sp++] = Frame{(int32_t)first, (int32_t)last, floor_log2(last - first) * 2};
   while (sp > 0) {
     Frame f = stack[--sp];
     // __introsort_loop(f.first, f.last, f.depth): iterate on [first, cut),
@@ -259,8 +260,8 @@ __host__ __device__ inline void sort(Item<V>* a, int64_t first, int64_t last, co
       }
       --depth;
       const int64_t cut = partition_pivot(a, lo, hi, before);
-      stack[sp++] = Frame{lo, cut, depth};   // loop continuation, runs after the right part
-      stack[sp++] = Frame{cut, hi, depth};   // recursive call, runs first
+      stack[sp++] = Frame{(int32_t)lo, (int32_t)cut, depth};  // loop continuation, runs after the right part
+      stack[sp++] = Frame{(int32_t)cut, (int32_t)hi, depth};  // recursive call, runs first
     }
   }
   // __final_insertion_sort

@@ -199,6 +199,23 @@ int coda_decode_write(const coda_bank_desc* s, const void* k_new, const void* v_
                       int64_t nb_sb, int64_t nb_sh, const float* g_new,
                       int ring_idx, int ring_filled, int64_t pos, void* stream);
 
+/* One decode token of the hot path: ring / exact / summary update of the
+ * evicted slot followed by attention of the token's query over the updated
+ * cache (the reference's default step order, write then attend).  `a`
+ * describes that attention: Lq = 1, prefix = the state cache of `s`
+ * (Lp = Lbuf, contiguous), no block keys.  With a full ring and bf16 the
+ * update is spread over (head, sequence) workgroups: a routing kernel takes
+ * the per-head cosine dots and the attention kernel applies its own head's
+ * rows before attending (two launches); otherwise coda_decode_write then
+ * coda_diff_attn_fwd.  workspace >= coda_decode_step_workspace_bytes().
+ * Replaces: CoDAGQALandmarkPerf2.step after its projections
+ *   (src/coda_gqa_l/attention.py:526-536 -> memory_banks.py:183-432 and
+ *   attention.py:476-514). */
+int coda_decode_step_workspace_bytes(const coda_bank_desc* s, const coda_attn_desc* a, size_t* bytes);
+int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new, const void* v_new,
+                     int64_t nb_sb, int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled,
+                     int64_t pos, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Candidate plan of a chunked prefill: for every chunk c (block_size
  * tokens, last one ragged) and sequence b, the evicted-token indices picked
  * by the reference's CPU topk(g_e, k, sorted=False) (libstdc++ nth_element /

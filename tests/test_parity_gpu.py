@@ -250,3 +250,42 @@ def test_run_twice_is_bit_identical():
         outs.append((y.cpu(), yd.cpu(), st.k_buf.cpu(), st.v_buf.cpu(), st.allowed.cpu()))
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@torch.no_grad()
+def test_decode_step_matches_oracle_large_batch(dtype):
+    """The one-call decode step at a batch large enough for the fused
+    (routing kernel + apply-in-attention) path in bf16; fp32 takes the
+    bank-kernel + attention path.  Teacher-forced per step."""
+    _need_gpu()
+    from coda_oracle import OracleLayer, banks, prims
+    print(f"[decode_step] {dtype}", flush=True)
+    kw = dict(embed_dim=128, num_heads=4, num_kv_heads=2, window=32, num_landmarks_exact=16,
+              num_landmarks_summary=16)
+    case = {"kw": kw}
+    torch.manual_seed(5)
+    m = OracleLayer(**kw).to(dtype).eval()
+    p = product_like(m, case, dtype, DEV)
+    B = 256
+    torch.manual_seed(6)
+    st_o = m.init_state(batch_size=B, dtype=dtype)
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(B, 80, 128, generator=g).to(dtype)
+    m.prefill_chunked(x, st_o, block_size=32, return_outputs=False)
+    W, Me = m.window, m.Me
+    for t in range(12):
+        xt = torch.randn(B, 1, 128, generator=g).to(dtype)
+        st_p = to_product_state(st_o, DEV)
+        qp = int(st_o.pos)
+        kn, vn, gn = m._new_kv(xt, qp)
+        banks.write_one(m, st_o, kn, vn, gn)
+        qt = m.q_proj(xt).view(B, 1, 4, 32).transpose(1, 2)
+        lamt = torch.sigmoid(m.lambda_proj(xt)).transpose(1, 2).unsqueeze(-1)
+        ho = m.attend_core(qt, lamt, st_o, qp)
+        ct, sn = m.rope_tables(1, qp, dtype)
+        hp = p.decode_step_core(qt.to(DEV), kn.to(DEV), vn.to(DEV), gn.reshape(B).to(DEV), lamt.squeeze(-1).to(DEV),
+                                st_p, ct.to(DEV), sn.to(DEV))
+        torch.cuda.synchronize()
+        assert_close(hp.permute(0, 2, 1, 3), ho, dtype, f"decode_step {t} heads")
+        compare_states(st_p, st_o, dtype, W, Me, f"decode_step {t}")
