@@ -494,14 +494,11 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
         al_lds[ap.j] = 1;
         if (hk == 0) commit_decode_meta(bs, b, dec, ap.j, ap.pos - W, ap.g_new[b]);
       }
-      // the rows just stored were loaded into this CU's L1 above and the L1
-      // is write-through without update: wait for the stores to reach L2
-      // and drop the stale L1 lines before any wave re-reads them
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
     }
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
+  // (workgroup barrier: its release / acquire fences at workgroup scope
+  // order wave 0's row stores before every wave's loads of those rows; all
+  // waves of the workgroup share one CU and its L1)
   __syncthreads();
   // query fragments (B operand of S^T): row n, channels 32c + 8 g4 + j
   bf16x8_t qf[NC];
