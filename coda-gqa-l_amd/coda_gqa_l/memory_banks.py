@@ -178,7 +178,14 @@ class MemoryBankMixin:
     def _decode_step(self, st: CoDAGQALandmarkStatePerf2, *, k_new: torch.Tensor, v_new: torch.Tensor,
                      g_new: torch.Tensor, attn_desc) -> None:
         """Write one token then attend (coda_decode_step): the bank update of
-        _write_one and the attention described by attn_desc, in one call."""
+        _write_one and the attention described by attn_desc, in one call.
+
+        The library leaves the routing record of the next token in the
+        workspace; it is handed back (one launch per token) only while this
+        module sees an unbroken sequence of decode steps on the same state:
+        same state object, same buffers, no in-place edit of them through
+        torch (version counters), position and ring index as the last step
+        left them."""
         self._check_state(st)
         B = st.k_buf.shape[0]
         dev = st.k_buf.device
@@ -192,12 +199,20 @@ class MemoryBankMixin:
         eta = self._eta_logit_f32(dev) if self.Ms > 0 else None
         d = self._bank_desc(st, eta, metrics, fr)
         L = _hip.lib()
-        need = ctypes.c_size_t(0)
-        _hip.check(L.coda_decode_step_workspace_bytes(d, attn_desc, need))
-        ws = self._workspace(dev, need.value)
+        wkey = (B, attn_desc.H, st.k_buf.shape[2], st.k_buf.dtype)
+        sizes = self.__dict__.setdefault("_step_ws_bytes", {})
+        need = sizes.get(wkey)
+        if need is None:
+            nb = ctypes.c_size_t(0)
+            _hip.check(L.coda_decode_step_workspace_bytes(d, attn_desc, nb))
+            need = sizes[wkey] = nb.value
+        ws = self._route_workspace(dev, need)
+        routed = ctypes.c_int(1 if self.__dict__.get("_route_tag") == self._route_key(st, ws) else 0)
+        self.__dict__["_route_tag"] = None
         _hip.check(L.coda_decode_step(
             d, attn_desc, kn.data_ptr(), vn.data_ptr(), kn.stride(0), kn.stride(1), g.data_ptr(),
-            int(st.recent_idx), int(st.recent_filled), int(st.pos), _hip.ptr(ws), need.value, _hip.stream_of(kn)))
+            int(st.recent_idx), int(st.recent_filled), int(st.pos), _hip.ptr(ws), need, ctypes.byref(routed),
+            _hip.stream_of(kn)))
         if not evict:
             st.recent_filled += 1
         else:
@@ -206,6 +221,27 @@ class MemoryBankMixin:
             self._expand_from(st, fr, False, self.Me > 0, self.Ms > 0)
             st.recent_idx = (j + 1) % self.window
         st.pos += 1
+        if routed.value:
+            self.__dict__["_route_tag"] = self._route_key(st, ws)
+
+    @staticmethod
+    def _route_key(st: CoDAGQALandmarkStatePerf2, ws: Optional[torch.Tensor]):
+        ts = (st.k_buf, st.v_buf, st.allowed, st.g_recent, st.mem_last_exact, st._exact_v_norm, st._sum_lf_k_norm)
+        return (id(st), int(st.pos), int(st.recent_idx), None if ws is None else ws.data_ptr()) + tuple(
+            (None, None) if t is None else (t.data_ptr(), t._version) for t in ts)
+
+    def _route_workspace(self, device, nbytes: int) -> Optional[torch.Tensor]:
+        """Workspace of the decode step (routing records), kept apart from
+        the other scratch buffers so nothing else overwrites a record."""
+        if nbytes == 0:
+            return None
+        cache = self.__dict__.setdefault("_route_ws", {})
+        key = str(device)
+        buf = cache.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+            cache[key] = buf
+        return buf
 
     def _workspace(self, device, nbytes: int) -> Optional[torch.Tensor]:
         """Device scratch reused across calls (grown on demand); calls on one

@@ -245,10 +245,13 @@ __device__ __forceinline__ void decide_summary(const coda_bank_desc& s, const fl
 //   ring   : slot j <- new token
 // (memory_banks.py:296-331, :381-416, :214-222).  ke / ve: the evicted
 // row of head h as floats; kn_src / vn_src: the new token of head h.
+// With patch_e / patch_s (may be null) the refreshed V-norm row and LF-K-norm
+// row are also written to those copies (rows of DH and LF elements).
 template <typename T, int DH>
 __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h, const DecodeDecision& dec,
                                            const float* ke, const float* ve, const T* kn_src, const T* vn_src,
-                                           int j, float g_e, int lane) {
+                                           int j, float g_e, int lane, T* patch_e = nullptr,
+                                           T* patch_s = nullptr) {
   using E = Elt<T>;
   constexpr int NV = (DH + 63) / 64;
   const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, lf = s.lf, LF = DH - lf;
@@ -291,7 +294,10 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
     T* nr = (T*)s.exact_v_norm + (((int64_t)b * Hkv + h) * Me + idx_e) * DH;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      if (act[i]) nr[lane + 64 * i] = E::st(nv[i]);
+      if (act[i]) {
+        nr[lane + 64 * i] = E::st(nv[i]);
+        if (patch_e) patch_e[lane + 64 * i] = E::st(nv[i]);
+      }
   }
   if (do_s) {
     float eta = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
@@ -318,7 +324,10 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
     T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + idx_s) * LF;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
-      if (act[i]) nr[lane + 64 * i - lf] = E::st(nk[i]);
+      if (act[i]) {
+        nr[lane + 64 * i - lf] = E::st(nk[i]);
+        if (patch_s) patch_s[lane + 64 * i - lf] = E::st(nk[i]);
+      }
   }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -344,14 +353,16 @@ __device__ __forceinline__ void commit_decode_meta(const coda_bank_desc& s, int 
   s.g_recent[(int64_t)b * W + j] = g_new;
 }
 
-// Workspace of the two-kernel decode step, per sequence (4-byte words):
+// Routing record of one decode step, per sequence (4-byte words):
 //   dots  [Hkv][Me + Ms] f32  per-head exact / summary cosine dots (rounded)
 //   used  [Me + Ms] i32       bank used bits before the update
 //   last  [Me] i64            LRU stamps before the update (8-byte aligned)
 //   g_e   f32                 gate of the evicted ring slot
+// padded to a multiple of 4 words, so every record is 16-byte aligned and
+// moves to LDS in 16-byte pieces.
 __host__ __device__ __forceinline__ int dstep_words(int Hkv, int Me, int Ms) {
   const int a = Hkv * (Me + Ms) + (Me + Ms);
-  return ((a + 1) & ~1) + 2 * Me + 2;
+  return (((a + 1) & ~1) + 2 * Me + 1 + 3) & ~3;
 }
 struct DStepWs {
   float* dots;
@@ -368,6 +379,61 @@ __host__ __device__ __forceinline__ DStepWs dstep_ws(float* ws, int b, int Hkv, 
   w.last = reinterpret_cast<int64_t*>(base + ((a + 1) & ~1));
   w.g_e = base + ((a + 1) & ~1) + 2 * Me;
   return w;
+}
+
+// Routing dots of head h for evicting ring slot j of sequence b, by the
+// 256 threads of a workgroup (every thread must call it): the evicted row
+// (k, v) goes to LDS as floats (ke, ve: DH each), its unit V and unit LF-K
+// band (vnrm: DH, knrm: LF) are formed by waves 0-1, then waves 0-1 take the
+// dots with head h's exact V-norm cache rows (out_e[Me]) and waves 2-3 with
+// its summary LF-K-norm rows (out_s[Ms]), each rounded to T
+// (memory_banks.py:240-252, :352-364 per head, before the head mean).
+template <typename T, int DH>
+__device__ __forceinline__ void route_head_dots(const coda_bank_desc& s, int b, int h, int j, float* ke, float* ve,
+                                                float* vnrm, float* knrm, float* out_e, float* out_s) {
+  using E = Elt<T>;
+  constexpr int NV = (DH + 63) / 64;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, lf = s.lf, LF = DH - lf;
+  const int Lbuf = W + Me + Ms;
+  const T* kr = (const T*)s.k_buf + (((int64_t)b * Hkv + h) * Lbuf + j) * DH;
+  const T* vr = (const T*)s.v_buf + (((int64_t)b * Hkv + h) * Lbuf + j) * DH;
+  for (int d = t; d < DH; d += 256) {
+    ke[d] = E::ld(kr[d]);
+    ve[d] = E::ld(vr[d]);
+  }
+  __syncthreads();
+  if (wv < 2) {
+    const bool is_v = wv == 0;
+    if ((is_v && Me > 0) || (!is_v && Ms > 0)) {
+      const int len = is_v ? DH : LF;
+      float x[NV];
+      bool act[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int d = lane + 64 * i;
+        act[i] = d < len;
+        x[i] = act[i] ? (is_v ? ve[d] : ke[lf + d]) : 0.f;
+      }
+      wave_unit<T, NV>(x, act);
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) (is_v ? vnrm : knrm)[lane + 64 * i] = x[i];
+    }
+  }
+  __syncthreads();
+  if (wv < 2 && Me > 0) {
+    const T* en = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + h) * Me * DH;
+    wave_dots<T, 16>(
+        Me, DH, wv, 2, lane, [&](int it) { return en + (int64_t)it * DH; }, [&](int) { return (const float*)vnrm; },
+        [&](int it, float v) { out_e[it] = v; });
+  }
+  if (wv >= 2 && Ms > 0) {
+    const T* sn = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + h) * Ms * LF;
+    wave_dots<T, 16>(
+        Ms, LF, wv - 2, 2, lane, [&](int it) { return sn + (int64_t)it * LF; },
+        [&](int) { return (const float*)knrm; }, [&](int it, float v) { out_s[it] = v; });
+  }
 }
 
 // Host launcher of decode_route_kernel (defined with the bank kernels).

@@ -124,67 +124,24 @@ __global__ __launch_bounds__(512) void decode_write_kernel(const coda_bank_desc 
   if (t == 0) commit_decode_meta(s, b, dec, j, pos_e, g_new[b]);
 }
 
-// First kernel of the two-kernel decode step: one workgroup per (head h,
-// sequence b) normalises head h of the evicted ring row and takes its
-// cosine dots with head h's norm caches; the h == 0 workgroup also
-// snapshots the sequence's bank metadata before any update.
+// Routing kernel of the decode step: one workgroup per (head h, sequence
+// b) takes head h's routing dots for evicting ring slot j; the h == 0
+// workgroup also snapshots the sequence's bank metadata before any update.
 template <typename T, int DH>
 __global__ __launch_bounds__(256) void decode_route_kernel(const coda_bank_desc s, int j, float* ws) {
-  using E = Elt<T>;
-  constexpr int NV = (DH + 63) / 64;
   __shared__ __attribute__((aligned(16))) float ke[DH], ve[DH], vnrm[DH], knrm[DH];
-  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, lf = s.lf, LF = DH - lf;
-  const int Lbuf = W + Me + Ms;
+  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms;
   DStepWs w = dstep_ws(ws, b, Hkv, Me, Ms);
-  const T* kr = (const T*)s.k_buf + (((int64_t)b * Hkv + h) * Lbuf + j) * DH;
-  const T* vr = (const T*)s.v_buf + (((int64_t)b * Hkv + h) * Lbuf + j) * DH;
   if (h == 0) {
-    const uint8_t* al = s.allowed + (int64_t)b * Lbuf;
+    const uint8_t* al = s.allowed + (int64_t)b * (W + Me + Ms);
     for (int m = t; m < Me + Ms; m += 256) w.used[m] = al[W + m];
     for (int m = t; m < Me; m += 256) w.last[m] = s.mem_last[(int64_t)b * Me + m];
     if (t == 0) *w.g_e = s.g_recent[(int64_t)b * W + j];
   }
-  for (int d = t; d < DH; d += 256) {
-    ke[d] = E::ld(kr[d]);
-    ve[d] = E::ld(vr[d]);
-  }
-  __syncthreads();
-  if (wv < 2) {
-    const bool is_v = wv == 0;
-    if ((is_v && Me > 0) || (!is_v && Ms > 0)) {
-      const int len = is_v ? DH : LF;
-      float x[NV];
-      bool act[NV];
-#pragma unroll
-      for (int i = 0; i < NV; ++i) {
-        const int d = lane + 64 * i;
-        act[i] = d < len;
-        x[i] = act[i] ? (is_v ? ve[d] : ke[lf + d]) : 0.f;
-      }
-      wave_unit<T, NV>(x, act);
-#pragma unroll
-      for (int i = 0; i < NV; ++i)
-        if (act[i]) (is_v ? vnrm : knrm)[lane + 64 * i] = x[i];
-    }
-  }
-  __syncthreads();
   // dots layout: exact [Hkv][Me] then summary [Hkv][Ms]
-  float* out_e = w.dots + (int64_t)h * Me;
-  float* out_s = w.dots + (int64_t)Hkv * Me + (int64_t)h * Ms;
-  // waves 0-1: exact rows, waves 2-3: summary rows
-  if (wv < 2 && Me > 0) {
-    const T* en = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + h) * Me * DH;
-    wave_dots<T, 16>(
-        Me, DH, wv, 2, lane, [&](int it) { return en + (int64_t)it * DH; }, [&](int) { return (const float*)vnrm; },
-        [&](int it, float v) { out_e[it] = v; });
-  }
-  if (wv >= 2 && Ms > 0) {
-    const T* sn = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + h) * Ms * LF;
-    wave_dots<T, 16>(
-        Ms, LF, wv - 2, 2, lane, [&](int it) { return sn + (int64_t)it * LF; },
-        [&](int) { return (const float*)knrm; }, [&](int it, float v) { out_s[it] = v; });
-  }
+  route_head_dots<T, DH>(s, b, h, j, ke, ve, vnrm, knrm, w.dots + (int64_t)h * Me,
+                         w.dots + (int64_t)Hkv * Me + (int64_t)h * Ms);
 }
 
 // ------------------------------------------------------------ block plan

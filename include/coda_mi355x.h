@@ -204,9 +204,17 @@ int coda_decode_write(const coda_bank_desc* s, const void* k_new, const void* v_
  * cache (the reference's default step order, write then attend).  `a`
  * describes that attention: Lq = 1, prefix = the state cache of `s`
  * (Lp = Lbuf, contiguous), no block keys.  With a full ring and bf16 the
- * update is spread over (head, sequence) workgroups: a routing kernel takes
- * the per-head cosine dots and the attention kernel applies its own head's
- * rows before attending (two launches); otherwise coda_decode_write then
+ * update is spread over (head, sequence) workgroups of the attention kernel:
+ * each recomputes the sequence's decision from a routing record (per-head
+ * cosine dots of the evicted row + metadata snapshot), applies its own
+ * head's rows, attends, and then writes the routing record of the next
+ * token against the updated banks.  The workspace holds two records, picked
+ * by the parity of `pos`.  routed (in/out, may be NULL): on entry nonzero
+ * when the record for this call was left by the previous call on the same
+ * state and workspace with nothing else modifying the state in between
+ * (then the call is one launch; otherwise a routing kernel runs first); on
+ * return 1 when this call left the record of the next token, else 0.  Other
+ * shapes (ring filling, fp32, key split): coda_decode_write then
  * coda_diff_attn_fwd.  workspace >= coda_decode_step_workspace_bytes().
  * Replaces: CoDAGQALandmarkPerf2.step after its projections
  *   (src/coda_gqa_l/attention.py:526-536 -> memory_banks.py:183-432 and
@@ -214,7 +222,7 @@ int coda_decode_write(const coda_bank_desc* s, const void* k_new, const void* v_
 int coda_decode_step_workspace_bytes(const coda_bank_desc* s, const coda_attn_desc* a, size_t* bytes);
 int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new, const void* v_new,
                      int64_t nb_sb, int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled,
-                     int64_t pos, void* workspace, size_t workspace_bytes, void* stream);
+                     int64_t pos, void* workspace, size_t workspace_bytes, int* routed, void* stream);
 
 /* Candidate plan of a chunked prefill: for every chunk c (block_size
  * tokens, last one ragged) and sequence b, the evicted-token indices picked

@@ -289,3 +289,63 @@ def test_decode_step_matches_oracle_large_batch(dtype):
         torch.cuda.synchronize()
         assert_close(hp.permute(0, 2, 1, 3), ho, dtype, f"decode_step {t} heads")
         compare_states(st_p, st_o, dtype, W, Me, f"decode_step {t}")
+
+
+def _clone_state(st):
+    from coda_gqa_l import CoDAGQALandmarkStatePerf2
+    c = lambda t: None if t is None else t.clone()
+    return CoDAGQALandmarkStatePerf2(
+        k_buf=c(st.k_buf), v_buf=c(st.v_buf), allowed=c(st.allowed), g_recent=c(st.g_recent),
+        recent_idx=st.recent_idx, recent_filled=st.recent_filled, mem_last_exact=c(st.mem_last_exact),
+        pos=st.pos, active_exact=st.active_exact, active_summary=st.active_summary,
+        _exact_v_norm=c(st._exact_v_norm), _sum_lf_k_norm=c(st._sum_lf_k_norm),
+        metrics=None if st.metrics is None else dict(st.metrics))
+
+
+def _assert_same_state(a, b, what):
+    for f in ("k_buf", "v_buf", "allowed", "g_recent", "mem_last_exact", "_exact_v_norm", "_sum_lf_k_norm"):
+        assert torch.equal(getattr(a, f), getattr(b, f)), f"{what}: {f} differs"
+    assert (a.pos, a.recent_idx, a.recent_filled) == (b.pos, b.recent_idx, b.recent_filled), what
+
+
+@torch.no_grad()
+def test_decode_step_carried_routing_matches_fresh_routing():
+    """bf16 fused decode: a state stepped on its own reuses the routing
+    record each step leaves for the next; a copy of that state stepped once
+    from scratch routes with the routing kernel.  Outputs and states must be
+    bit-identical, also after an in-place torch edit of the cache and after a
+    prefill chunk between decode steps (both force a fresh routing)."""
+    _need_gpu()
+    import coda_gqa_l
+    print("[decode_step carried routing]", flush=True)
+    dt = torch.bfloat16
+    torch.manual_seed(11)
+    m = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=256, num_heads=8, num_kv_heads=2, window=32,
+                                        num_landmarks_exact=16, num_landmarks_summary=16).to(dt).to(DEV).eval()
+    # a second module with the same weights steps the fresh copies, so the
+    # routing record m keeps for its own state is never displaced
+    m2 = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=256, num_heads=8, num_kv_heads=2, window=32,
+                                         num_landmarks_exact=16, num_landmarks_summary=16).to(dt).to(DEV).eval()
+    m2.load_state_dict(m.state_dict())
+    B = 256
+    st = m.init_state(batch_size=B, device=DEV, dtype=dt)
+    g = torch.Generator(device=DEV).manual_seed(12)
+    m.prefill_chunked(torch.randn(B, 70, 256, generator=g, device=DEV, dtype=dt), st, block_size=32,
+                      return_outputs=False)
+    for t in range(14):
+        if t == 6:
+            st.v_buf[:, :, m.window + 3] *= -1          # in-place edit: version counter moves
+            st._exact_v_norm[:, :, 3] *= -1
+        if t == 10:
+            m.prefill_chunked(torch.randn(B, 5, 256, generator=g, device=DEV, dtype=dt), st, block_size=32,
+                              return_outputs=False)
+        x = torch.randn(B, 1, 256, generator=g, device=DEV, dtype=dt)
+        fresh = _clone_state(st)
+        carried = m.__dict__.get("_route_tag") is not None
+        y1, _ = m.step(x, st)
+        y2, _ = m2.step(x, fresh)
+        torch.cuda.synchronize()
+        if t not in (0, 6, 10):
+            assert carried, f"step {t}: routing record was not carried over"
+        assert torch.equal(y1, y2), f"step {t}: outputs differ"
+        _assert_same_state(st, fresh, f"step {t}")
