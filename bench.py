@@ -47,6 +47,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the configs[2] prefill figure")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="before timing, run 5 device-to-device copies of this many MiB (a plain copy kernel of "
+                         "known size that scales the FETCH_SIZE / WRITE_SIZE counters of a --pmc run)")
     return ap.parse_args()
 
 
@@ -55,6 +58,22 @@ def layer(torch, coda, dtype, dev):
     m = coda.CoDAGQALandmarkPerf2(embed_dim=4096, num_heads=32, num_kv_heads=8, window=256,
                                   num_landmarks_exact=64, num_landmarks_summary=64, rope_base=1e4)
     return m.to(dtype=dtype).to(dev).eval()
+
+
+def profile_traffic(label):
+    """HBM bytes per launch of `label` from the committed rocprofv3 --pmc
+    summaries (FETCH_SIZE / WRITE_SIZE scaled by a plain copy of known size),
+    or None when no summary covers it."""
+    d = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(d):
+        return None
+    for f in sorted(os.listdir(d)):
+        if not f.startswith("traffic_"):
+            continue
+        for line in open(os.path.join(d, f)):
+            if line.startswith("traffic_bytes ") and line[len("traffic_bytes "):].rsplit(" ", 1)[0] == label:
+                return int(float(line.rsplit(" ", 1)[1]))
+    return None
 
 
 def decode_bytes(m, B, e=2):
@@ -121,6 +140,13 @@ def main():
     torch.cuda.synchronize()
 
     stream = torch.cuda.current_stream()
+    if a.copy_calib_mib > 0:
+        src = torch.empty(a.copy_calib_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     def run_step(i, ev=None):
         # one library call: routing kernel, then the decode attention kernel
@@ -166,9 +192,10 @@ def main():
                 % a.prefill_tokens,
         "config": {"workload": "configs[1] decode: hidden 4096, H32/Hkv8/Dh128, W256/Me64/Ms64, bf16",
                    "batch": B, "prefilled_tokens": a.prefill_tokens, "Lbuf": m.Lbuf},
-        "roofline": {"bound": "hbm", "kernel": "decode step: decode_route_kernel + attn_rows_bf16<APPLY>",
+        "roofline": {"bound": "hbm", "kernel": "attn_rows_bf16<128,true> (fused decode step: bank update + attention, one launch per token)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profile_traffic("decode_step_b%d attn_rows_bf16<128,true>" % B),
                      "bytes_per_launch": attn_bytes + bank_bytes, "avg_launch_ms": round(step_gpu_ms, 5)},
         "step_bytes": attn_bytes + bank_bytes,
         "step_hbm_frac": round((attn_bytes + bank_bytes) / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -179,9 +206,8 @@ def main():
     # ---------------------------------------------------------------- prefill
     if not a.no_prefill:
         out["prefill"] = bench_prefill(torch, coda, m, a)
-
-    # ---------------------------------------------------------------- CPU baseline
         print(f"# prefill: {out['prefill']['value']:.0f} tok/s", file=sys.stderr, flush=True)
+    # ---------------------------------------------------------------- CPU baseline
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a)
     print(json.dumps(out), flush=True)
@@ -239,6 +265,7 @@ def bench_prefill(torch, coda, m, a):
             "roofline": {"bound": "mfma", "kernel": "attn_tile_bf16", "achieved": round(tflops, 2),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                          "flops_per_launch": flops, "avg_launch_ms": round(attn_ms, 5),
+                         "traffic": profile_traffic("prefill_chunk_b%d attn_tile_bf16<128,4>" % B),
                          "valid_prefix_slots": n_prefix}}
 
 
