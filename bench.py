@@ -192,7 +192,7 @@ def main():
                 % a.prefill_tokens,
         "config": {"workload": "configs[1] decode: hidden 4096, H32/Hkv8/Dh128, W256/Me64/Ms64, bf16",
                    "batch": B, "prefilled_tokens": a.prefill_tokens, "Lbuf": m.Lbuf},
-        "roofline": {"bound": "hbm", "kernel": "attn_rows_bf16<128,true> (fused decode step: bank update + attention, one launch per token)",
+        "roofline": {"bound": "hbm", "kernel": "decode step: decode_bank_kernel + attn_rows_bf16<128> (bank update from the carried routing record, then attention)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profile_traffic("decode_step_b%d attn_rows_bf16<128,true>" % B),

@@ -415,187 +415,11 @@ __device__ __forceinline__ void store_vt(char* base, int kg, int d0, const uint4
 // Workgroup = (split, KV head, batch); 4 waves take 16-key tiles in turn.
 // Partial (m, l, O) of the 4 waves merge in LDS; with nsplit > 1 each
 // workgroup leaves its merged partial in `ws` for attn_rows_merge.
-// Bank update applied by the decode attention kernel itself (fused decode
-// step): each (head, sequence) workgroup recomputes the sequence's decision
-// from the routing record `ws` (per-head dots and metadata snapshot, written
-// by decode_route_kernel or by the previous step), writes its own head's
-// modified rows and attends over the updated cache.  With `ws_next` it then
-// writes the routing record of the next step (which evicts ring slot
-// (j + 1) % W) against the updated banks, so steady-state decoding needs
-// one launch per token.
-struct DecodeApply {
-  coda_bank_desc s;
-  const void* k_new;
-  const void* v_new;
-  int64_t nb_sb, nb_sh;
-  const float* g_new;
-  int j;
-  int64_t pos;
-  float* ws;
-  float* ws_next;
-  int staged;  // the norm caches of a head fit the merge buffer (staged in LDS)
-};
-
-// s_waitcnt lgkmcnt(0) + a code-motion barrier: LDS writes of this wave are
-// visible to its other lanes
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_wave_barrier();
-}
-
-// Copy nbytes (a multiple of 16) from global memory to LDS with direct
-// global->LDS loads: one wave instruction moves 1 KiB, lane l the bytes
-// [16 l, 16 l + 16) of it.  The loads count in vmcnt like any other.
-__device__ __forceinline__ void wave_copy_to_lds(const void* src, void* dst, int nbytes, int lane) {
-  for (int c = 0; c < nbytes; c += 1024)
-    if (c + 16 * lane < nbytes)
-      __builtin_amdgcn_global_load_lds((const char*)src + c + 16 * lane,
-                                       (__attribute__((address_space(3))) void*)((char*)dst + c), 16, 0, 0);
-}
-
-// The bank wave of the fused decode step (one wave, before the workgroup
-// barrier that releases the bank tiles to the attention waves):
-//   - the routing record of this step comes to LDS (`rec`, same layout as
-//     in the workspace), and with `stage` head hk's norm caches too;
-//   - the sequence's exact / summary decision, this head's row writes
-//     (exact slot, summary slot, ring slot j), the visibility bytes of the
-//     written slots in the workgroup's LDS copy, and (head 0) the sequence
-//     metadata;
-//   - with ap.ws_next, the routing record of the next step, which evicts
-//     ring slot jn = (j + 1) % W, against the updated banks: the staged
-//     norm rows are patched with the rows the update rewrote, so the dots
-//     equal the routing kernel's (same per-row arithmetic as
-//     route_head_dots, bit for bit).
-template <int DH>
-__device__ __forceinline__ void bank_wave(const DecodeApply& ap, int b, int hk, float* rec, float* rows,
-                                          DecodeDecision& dec, uint8_t* al_lds, bf16_t* stage, int lane) {
-  using E = Elt<bf16_t>;
-  constexpr int NV = (DH + 63) / 64;
-  const coda_bank_desc& bs = ap.s;
-  const int Me = bs.Me, Ms = bs.Ms, W = bs.W, Hkv = bs.Hkv, lf = bs.lf, LF = DH - lf;
-  const int Lbuf = W + Me + Ms, MM = Me + Ms;
-  const int words = dstep_words(Hkv, Me, Ms);
-  const DStepWs L = dstep_ws(rec, 0, Hkv, Me, Ms);
-  float* ke = rows;
-  float* ve = ke + DH;
-  float* vnrm = ve + DH;
-  float* knrm = vnrm + DH;
-  const bool route = ap.ws_next != nullptr;
-  const int j = ap.j, jn = ap.j + 1 == W ? 0 : ap.j + 1;
-  const int64_t plane = ((int64_t)b * Hkv + hk) * Lbuf;
-  const bf16_t* en_g = Me > 0 ? (const bf16_t*)bs.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH : nullptr;
-  const bf16_t* sn_g = Ms > 0 ? (const bf16_t*)bs.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF : nullptr;
-
-  // every independent load first: record and norm caches to LDS, the
-  // evicted row j, the new token, and the row evicted next
-  wave_copy_to_lds(ap.ws + (int64_t)b * words, rec, words * 4, lane);
-  if (route && stage) {
-    if (Me > 0) wave_copy_to_lds(en_g, stage, Me * DH * 2, lane);
-    if (Ms > 0) wave_copy_to_lds(sn_g, stage + Me * DH, Ms * LF * 2, lane);
-  }
-  const bf16_t* kr = (const bf16_t*)bs.k_buf + (plane + j) * DH;
-  const bf16_t* vr = (const bf16_t*)bs.v_buf + (plane + j) * DH;
-  const bf16_t* kn_row = (const bf16_t*)ap.k_new + b * ap.nb_sb + hk * ap.nb_sh;
-  const bf16_t* vn_row = (const bf16_t*)ap.v_new + b * ap.nb_sb + hk * ap.nb_sh;
-  // slot jn after this step's update: the new token when jn == j (W == 1)
-  const bf16_t* kx = jn == j ? kn_row : (const bf16_t*)bs.k_buf + (plane + jn) * DH;
-  const bf16_t* vx = jn == j ? vn_row : (const bf16_t*)bs.v_buf + (plane + jn) * DH;
-  float xke[NV], xve[NV], xk[NV], xv[NV];
-  bool av[NV], ak[NV];
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int d = lane + 64 * i;
-    av[i] = d < DH;
-    ak[i] = d < LF;
-    const int dc = av[i] ? d : 0;
-    xke[i] = E::ld(kr[dc]);
-    xve[i] = E::ld(vr[dc]);
-    xv[i] = av[i] ? E::ld(vx[dc]) : 0.f;
-    xk[i] = ak[i] ? E::ld(kx[lf + (ak[i] ? d : 0)]) : 0.f;
-  }
-#pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (av[i]) {
-      ke[lane + 64 * i] = xke[i];
-      ve[lane + 64 * i] = xve[i];
-    }
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the LDS copies have landed
-  wave_lds_sync();
-  const float g_e = *L.g_e;
-  if (Me > 0) decide_exact<bf16_t>(bs, L.dots, L.used, L.last, g_e, dec, hk == 0, lane);
-  if (Ms > 0) decide_summary<bf16_t>(bs, L.dots + Hkv * Me, L.used + Me, g_e, dec, hk == 0, lane);
-  wave_lds_sync();
-  const bool patch = route && stage != nullptr;
-  apply_head<bf16_t, DH>(bs, b, hk, dec, ke, ve, kn_row, vn_row, j, g_e, lane,
-                         patch && Me > 0 ? stage + dec.idx_e * DH : nullptr,
-                         patch && Ms > 0 ? stage + Me * DH + dec.idx_s * LF : nullptr);
-  if (lane == 0) {
-    // the written slots are visible regardless of when another head's
-    // workgroup committed `allowed`
-    if (Me > 0 && dec.ow_e) al_lds[W + dec.idx_e] = 1;
-    if (Ms > 0 && dec.keep_s) al_lds[W + Me + dec.idx_s] = 1;
-    if (hk == 0) commit_decode_meta(bs, b, dec, j, ap.pos - W, ap.g_new[b]);
-    // metadata snapshot of the next record
-    if (Me > 0 && dec.ow_e) L.used[dec.idx_e] = 1;
-    if (Me > 0 && dec.keep_e) L.last[dec.idx_e] = ap.pos - W;
-    if (Ms > 0 && dec.keep_s) L.used[Me + dec.idx_s] = 1;
-  }
-  if (!route) return;
-  wave_lds_sync();
-  const DStepWs wn = dstep_ws(ap.ws_next, b, Hkv, Me, Ms);
-  if (hk == 0) {
-    for (int i = lane; i < MM; i += 64) wn.used[i] = L.used[i];
-    for (int i = lane; i < Me; i += 64) wn.last[i] = L.last[i];
-    if (lane == 0) *wn.g_e = jn == j ? ap.g_new[b] : bs.g_recent[(int64_t)b * W + jn];
-  }
-  if (Me > 0) {
-    wave_unit<bf16_t, NV>(xv, av);
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (av[i]) vnrm[lane + 64 * i] = xv[i];
-  }
-  if (Ms > 0) {
-    wave_unit<bf16_t, NV>(xk, ak);
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (ak[i]) knrm[lane + 64 * i] = xk[i];
-  }
-  wave_lds_sync();
-  float* out_e = wn.dots + (int64_t)hk * Me;
-  float* out_s = wn.dots + (int64_t)Hkv * Me + (int64_t)hk * Ms;
-  auto put_e = [&](int it, float v) { out_e[it] = v; };
-  auto put_s = [&](int it, float v) { out_s[it] = v; };
-  auto vecv = [&](int) { return (const float*)vnrm; };
-  auto veck = [&](int) { return (const float*)knrm; };
-  if (stage) {
-    const bf16_t* es = stage;
-    const bf16_t* ss = stage + Me * DH;
-    if (Me > 0) wave_dots<bf16_t, 4>(Me, DH, 0, 1, lane, [&](int it) { return es + it * DH; }, vecv, put_e);
-    if (Ms > 0) wave_dots<bf16_t, 4>(Ms, LF, 0, 1, lane, [&](int it) { return ss + it * LF; }, veck, put_s);
-  } else {
-    // rows read back from memory (this wave's own stores above come first)
-    if (Me > 0)
-      wave_dots<bf16_t, 4>(Me, DH, 0, 1, lane, [&](int it) { return en_g + (int64_t)it * DH; }, vecv, put_e);
-    if (Ms > 0)
-      wave_dots<bf16_t, 4>(Ms, LF, 0, 1, lane, [&](int it) { return sn_g + (int64_t)it * LF; }, veck, put_s);
-  }
-}
-
 // Workgroup = (split, KV head, batch); 4 attention waves take 16-key tiles
 // in turn and merge their partial (m, l, O) in LDS; with nsplit > 1 each
 // workgroup leaves its merged partial in `ws` for attn_rows_merge.
-// APPLY (fused decode step, nsplit = 1): a fifth wave, the bank wave, runs
-// the bank update while the attention waves take the tiles that lie wholly
-// in the ring (which the update does not touch: ring slot j, rewritten with
-// the new token, is read from the token itself); after a workgroup barrier
-// the attention waves take the bank tiles and the bank wave writes the next
-// step's routing record.
-// (APPLY: two 5-wave workgroups per CU need 3 waves per SIMD, i.e. at most
-// 168 VGPRs)
-template <int DH, bool APPLY>
-__global__ __launch_bounds__(APPLY ? 320 : 256) __attribute__((amdgpu_waves_per_eu(APPLY ? 3 : 1)))
-void attn_rows_bf16(const coda_attn_desc a, int keys_per_split,
-                                                                   float* ws, const DecodeApply ap) {
+template <int DH>
+__global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, int keys_per_split, float* ws) {
   constexpr int NC = DH / 32, NM = DH / 16, NW = 4;
   __shared__ __attribute__((aligned(16))) char vt_smem[NW][VtLayout<DH>::kTileBytes];
   __shared__ float red_m[NW][16], red_l[NW][16];
@@ -621,11 +445,6 @@ void attn_rows_bf16(const coda_attn_desc a, int keys_per_split,
   // Lp <= kMaxRowsPrefix, so the tile loop reads them from LDS without a branch
   for (int i = threadIdx.x; i < a.Lp; i += blockDim.x)
     al_lds[i] = a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1;
-  // LDS of the bank wave: the routing record (workspace layout) | ke, ve,
-  // vnrm, knrm [DH] each
-  extern __shared__ __attribute__((aligned(16))) float ap_smem[];
-  __shared__ DecodeDecision dec;
-  const coda_bank_desc& bs = ap.s;
   __syncthreads();
   // query fragments (B operand of S^T): row n, channels 32c + 8 g4 + j
   bf16x8_t qf[NC];
@@ -644,7 +463,7 @@ void attn_rows_bf16(const coda_attn_desc a, int keys_per_split,
   f32x4 o[NM];
 #pragma unroll
   for (int i = 0; i < NM; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  char* vt = vt_smem[wv < NW ? wv : NW - 1];
+  char* vt = vt_smem[wv];
   // V load roles: lane -> (key group kgl, 8-channel chunk dcl)
   constexpr int DCH = DH / 8;
   const int kgl = lane / DCH, dcl = lane % DCH;
@@ -799,53 +618,22 @@ void attn_rows_bf16(const coda_attn_desc a, int keys_per_split,
   };
   const int kbeg = split * keys_per_split;
   const int kend = min(a.Lp + a.Lb, kbeg + keys_per_split);
-  if constexpr (APPLY) {
-    // one split over the state cache (Lp = Lbuf, no block keys)
+  // prefix keys [0, Lp) then block keys [Lp, Lp + Lb), each clipped to
+  // this split's [kbeg, kend)
+  if (a.Lp > 0 && kbeg < a.Lp) {
     const Src sp = make_src(a.kp, a.vp, a.p_sb, a.p_sh, a.p_sl, a.Lp, 0, true);
-    const int j = ap.j;
-    // phase 1: tiles wholly inside the ring, which the bank update does not
-    // touch except at ring slot j (rewritten with the new token: masked here)
-    const int ta = min((a.Lp + 15) / 16, bs.W / 16);
-    const Vis v1{0, 16 * ta, j, -1};
-    if (wv < NW) {
-      run_tiles(sp, ta, [&](int t) { return 16 * t; }, v1, v1);
-    } else {
-      // the merge buffer is idle until the attention waves finish phase 2
-      bf16_t* stage = ap.staged ? reinterpret_cast<bf16_t*>(&red_o[0][0][0]) : nullptr;
-      bank_wave<DH>(ap, b, hk, ap_smem, ap_smem + dstep_words(bs.Hkv, bs.Me, bs.Ms), dec, al_lds, stage, lane);
-    }
-    // (workgroup barrier: its release / acquire fences at workgroup scope
-    // order the bank wave's row stores and LDS writes before the loads
-    // below; all waves of the workgroup share one CU and its L1)
-    __syncthreads();
-    // phase 2: the remaining tiles (banks, a ring tail shorter than a tile)
-    // plus, as the last tile, slot j alone when phase 1 masked it
-    if (wv < NW) {
-      const int n2 = (a.Lp - 16 * ta + 15) / 16;
-      const bool jt = j < 16 * ta;
-      const Vis v2{16 * ta, a.Lp, -1, -1};
-      const Vis vj{j, j + 1, -1, j};
-      run_tiles(sp, n2 + (jt ? 1 : 0), [&](int t) { return t < n2 ? 16 * (ta + t) : 16 * (j / 16); }, v2,
-                jt ? vj : v2);
-    }
-  } else {
-    // prefix keys [0, Lp) then block keys [Lp, Lp + Lb), each clipped to
-    // this split's [kbeg, kend)
-    if (a.Lp > 0 && kbeg < a.Lp) {
-      const Src sp = make_src(a.kp, a.vp, a.p_sb, a.p_sh, a.p_sl, a.Lp, 0, true);
-      const int e = min(kend, a.Lp);
-      const Vis vs{kbeg, e, -1, -1};
-      run_tiles(sp, (e - kbeg + 15) / 16, [&](int t) { return kbeg + 16 * t; }, vs, vs);
-    }
-    if (a.Lb > 0 && kend > a.Lp) {
-      const Src sb = make_src(a.kb, a.vb, a.b_sb, a.b_sh, a.b_sl, a.Lb, a.Lp, false);
-      const int s0 = max(kbeg, a.Lp);
-      const Vis vs{s0, kend, -1, -1};
-      run_tiles(sb, (kend - s0 + 15) / 16, [&](int t) { return s0 + 16 * t; }, vs, vs);
-    }
+    const int e = min(kend, a.Lp);
+    const Vis vs{kbeg, e, -1, -1};
+    run_tiles(sp, (e - kbeg + 15) / 16, [&](int t) { return kbeg + 16 * t; }, vs, vs);
+  }
+  if (a.Lb > 0 && kend > a.Lp) {
+    const Src sb = make_src(a.kb, a.vb, a.b_sb, a.b_sh, a.b_sl, a.Lb, a.Lp, false);
+    const int s0 = max(kbeg, a.Lp);
+    const Vis vs{s0, kend, -1, -1};
+    run_tiles(sb, (kend - s0 + 15) / 16, [&](int t) { return s0 + 16 * t; }, vs, vs);
   }
   // merge the 4 attention waves
-  if (wv < NW) {
+  {
     if (g4 == 0) { red_m[wv][n] = m_i; red_l[wv][n] = l_i; }
 #pragma unroll
     for (int mt = 0; mt < NM; ++mt)
@@ -878,7 +666,6 @@ void attn_rows_bf16(const coda_attn_desc a, int keys_per_split,
     return;
   }
   // single split: merge + epilogue, one wave per (head, query) output row
-  if (wv >= NW) return;
   constexpr int NV = (DH + 63) / 64;
   for (int orow = wv; orow < GL; orow += NW) {
     const int g = orow / a.Lq, qi = orow % a.Lq, h = hk * G + g;
@@ -1203,8 +990,8 @@ static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
       if (!d->workspace || d->workspace_bytes < need)
         return fail(CODA_ESMALL, "coda_diff_attn_fwd: workspace %zu < %zu bytes", d->workspace_bytes, need);
     }
-    hipLaunchKernelGGL((attn_rows_bf16<DH, false>), dim3(ns_eff > 0 ? ns_eff : 1, d->Hkv, d->B), dim3(256), 0, st,
-                       *d, per, (float*)d->workspace, DecodeApply{});
+    hipLaunchKernelGGL((attn_rows_bf16<DH>), dim3(ns_eff > 0 ? ns_eff : 1, d->Hkv, d->B), dim3(256), 0, st, *d, per,
+                       (float*)d->workspace);
     int rc = check_launch("attn_rows_bf16");
     if (rc || ns_eff <= 1) return rc;
     hipLaunchKernelGGL((attn_rows_merge<DH>), dim3(d->Hkv, d->B), dim3(256), 0, st, *d, ns_eff,
@@ -1236,26 +1023,18 @@ extern "C" int coda_diff_attn_fwd(const coda_attn_desc* d, void* stream) {
 }
 
 // ------------------------------------------------------------ decode step
-static bool step_fused(const coda_bank_desc* s, const coda_attn_desc* a, int ring_filled) {
-  return s->dtype == CODA_BF16 && ring_filled >= s->W && use_rows(a) && rows_nsplit(a) == 1;
+// Full ring (the steady state): the bank update runs from a routing record
+// (decode_bank_kernel, one workgroup per (head, sequence)), which also
+// writes the record of the next token, then the attention kernel reads the
+// updated cache.  The workspace holds two records, picked by the parity of
+// the token position, followed by the attention kernel's scratch.
+static bool step_routed(const coda_bank_desc* s, int ring_filled) {
+  return ring_filled >= s->W && (s->Me > 0 || s->Ms > 0);
 }
 
-static size_t step_apply_lds(const coda_bank_desc* s) {
-  return sizeof(float) * ((size_t)dstep_words(s->Hkv, s->Me, s->Ms) + 4 * (size_t)s->Dh);
-}
-
-// head hk's norm caches fit the decode kernel's merge buffer
-// (red_o: 4 waves x 16 rows x (Dh + 4) floats) and move in 16-byte pieces
-static int step_staged(const coda_bank_desc* s) {
-  const int LF = s->Dh - s->lf;
-  const size_t need = 2 * ((size_t)s->Me * s->Dh + (size_t)s->Ms * LF);
-  return need <= (size_t)4 * 16 * (s->Dh + 4) * sizeof(float) && LF % 8 == 0;
-}
-
-// bytes of one routing record (all sequences); the fused step keeps two,
-// selected by the parity of the token position
+// bytes of one routing record (all sequences), 256-byte aligned
 static size_t route_record_bytes(const coda_bank_desc* s) {
-  return sizeof(float) * (size_t)s->B * dstep_words(s->Hkv, s->Me, s->Ms);
+  return (sizeof(float) * (size_t)s->B * dstep_words(s->Hkv, s->Me, s->Ms) + 255) & ~(size_t)255;
 }
 
 static int validate_step(const coda_bank_desc* s, const coda_attn_desc* a) {
@@ -1279,8 +1058,7 @@ extern "C" int coda_decode_step_workspace_bytes(const coda_bank_desc* s, const c
   size_t att = 0;
   rc = coda_attn_workspace_bytes(a, &att);
   if (rc) return rc;
-  const size_t fused = 2 * route_record_bytes(s);
-  *bytes = att > fused ? att : fused;
+  *bytes = 2 * route_record_bytes(s) + att;
   return CODA_OK;
 }
 
@@ -1291,12 +1069,13 @@ extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a
   if (rc) return rc;
   const int have_route = routed != nullptr && *routed != 0;
   if (routed) *routed = 0;
-  if (!step_fused(s, a, ring_filled)) {
-    // ring still filling, fp32, key split or a shape outside the decode
-    // tile: bank kernel, then the attention kernel
+  hipStream_t st = (hipStream_t)stream;
+  const size_t rec = route_record_bytes(s);
+  coda_attn_desc d = *a;
+  if (!step_routed(s, ring_filled)) {
+    // ring still filling (or no banks): bank kernel, then the attention kernel
     rc = coda_decode_write(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, stream);
     if (rc) return rc;
-    coda_attn_desc d = *a;
     d.workspace = workspace;
     d.workspace_bytes = workspace_bytes;
     return coda_diff_attn_fwd(&d, stream);
@@ -1306,33 +1085,25 @@ extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a
   CODA_REQUIRE(s->k_buf && s->v_buf && s->allowed && s->g_recent, "coda_decode_step: state buffers missing");
   CODA_REQUIRE(s->Me == 0 || (s->mem_last && s->exact_v_norm), "coda_decode_step: exact bank buffers missing");
   CODA_REQUIRE(s->Ms == 0 || (s->sum_lf_k_norm && s->eta_logit), "coda_decode_step: summary bank buffers missing");
-  const size_t rec = route_record_bytes(s);
-  if (!workspace || workspace_bytes < 2 * rec)
-    return fail(CODA_ESMALL, "coda_decode_step: workspace %zu < %zu bytes", workspace_bytes, 2 * rec);
+  CODA_REQUIRE(s->lf > 0 && s->lf < s->Dh && (s->Dh - s->lf) % 8 == 0, "coda_decode_step: lf %d unsupported",
+               s->lf);
+  size_t att = 0;
+  rc = coda_attn_workspace_bytes(a, &att);
+  if (rc) return rc;
+  if (!workspace || workspace_bytes < 2 * rec + att)
+    return fail(CODA_ESMALL, "coda_decode_step: workspace %zu < %zu bytes", workspace_bytes, 2 * rec + att);
   if (s->B == 0) return CODA_OK;
-  hipStream_t st = (hipStream_t)stream;
   float* rec_in = (float*)((char*)workspace + (pos & 1) * rec);
   float* rec_out = (float*)((char*)workspace + ((pos + 1) & 1) * rec);
   if (!have_route) {
     rc = launch_decode_route(s, ring_idx, rec_in, st);
     if (rc) return rc;
   }
-  DecodeApply ap{*s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, step_staged(s)};
-  const size_t lds = step_apply_lds(s);
-  const int Lk = a->Lp;
-  // four attention waves + the bank wave
-  const dim3 grid(1, a->Hkv, a->B), block(320);
-  switch (a->Dh) {
-    case 32:
-      hipLaunchKernelGGL((attn_rows_bf16<32, true>), grid, block, lds, st, *a, Lk, nullptr, ap);
-      break;
-    case 64:
-      hipLaunchKernelGGL((attn_rows_bf16<64, true>), grid, block, lds, st, *a, Lk, nullptr, ap);
-      break;
-    default:
-      hipLaunchKernelGGL((attn_rows_bf16<128, true>), grid, block, lds, st, *a, Lk, nullptr, ap);
-  }
-  rc = check_launch("attn_rows_bf16<apply>");
+  rc = launch_decode_bank(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st);
+  if (rc) return rc;
+  d.workspace = (char*)workspace + 2 * rec;
+  d.workspace_bytes = workspace_bytes - 2 * rec;
+  rc = coda_diff_attn_fwd(&d, stream);
   if (rc == CODA_OK && routed) *routed = 1;
   return rc;
 }

@@ -436,7 +436,10 @@ __device__ __forceinline__ void route_head_dots(const coda_bank_desc& s, int b, 
   }
 }
 
-// Host launcher of decode_route_kernel (defined with the bank kernels).
+// Host launchers of decode_route_kernel and decode_bank_kernel (defined
+// with the bank kernels).
 int launch_decode_route(const coda_bank_desc* s, int j, float* ws, hipStream_t st);
+int launch_decode_bank(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
+                       const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st);
 
 }  // namespace coda

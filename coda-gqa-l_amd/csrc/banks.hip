@@ -144,6 +144,131 @@ __global__ __launch_bounds__(256) void decode_route_kernel(const coda_bank_desc 
                          w.dots + (int64_t)Hkv * Me + (int64_t)h * Ms);
 }
 
+// Bank update of one decode token from its routing record, spread over
+// (head hk, sequence b) workgroups of 4 waves, followed by the routing
+// record of the next token (which evicts ring slot jn = (j + 1) % W):
+//   1. every load the workgroup needs is issued at once: the record of
+//      sequence b, head hk's norm caches (staged in LDS), the evicted row j,
+//      and the row evicted next (the new token itself when W == 1);
+//   2. wave 0 takes the exact decision, wave 1 the summary decision (each
+//      workgroup of a sequence recomputes the same decision from the same
+//      record, so no cross-workgroup barrier is needed); waves 2-3 form the
+//      unit vectors of the next evicted row;
+//   3. wave 0 writes head hk's rows (exact slot, summary slot, ring slot j)
+//      and patches the staged norm rows it rewrote; workgroup hk == 0 also
+//      writes the sequence metadata;
+//   4. all waves take the next record's dots against the staged (updated)
+//      norm rows, with the per-row arithmetic of the routing kernel.
+// LDS: record [words] f32 | norm stage [Me*DH + Ms*LF] T | ke, ve, vnrm, knrm [DH] f32.
+__host__ __device__ __forceinline__ size_t dbank_stage_elems(int DH, int Me, int Ms, int lf) {
+  return ((size_t)Me * DH + (size_t)Ms * (DH - lf) + 7) & ~(size_t)7;
+}
+__host__ __device__ __forceinline__ size_t dbank_lds(const coda_bank_desc& s) {
+  const size_t es = s.dtype == CODA_BF16 ? 2 : 4;
+  return sizeof(float) * (size_t)dstep_words(s.Hkv, s.Me, s.Ms) + es * dbank_stage_elems(s.Dh, s.Me, s.Ms, s.lf) +
+         sizeof(float) * 4 * (size_t)s.Dh;
+}
+
+// 16-byte copy of nbytes (a multiple of 16) global -> LDS by the workgroup.
+__device__ __forceinline__ void wg_copy16(void* dst, const void* src, int nbytes) {
+  for (int c = threadIdx.x * 16; c < nbytes; c += blockDim.x * 16)
+    *reinterpret_cast<uint4*>((char*)dst + c) = *reinterpret_cast<const uint4*>((const char*)src + c);
+}
+
+template <typename T, int DH>
+__global__ __launch_bounds__(256) void decode_bank_kernel(const coda_bank_desc s, const T* __restrict__ k_new,
+                                                          const T* __restrict__ v_new, int64_t nb_sb, int64_t nb_sh,
+                                                          const float* __restrict__ g_new, int j, int64_t pos,
+                                                          const float* __restrict__ rec_in,
+                                                          float* __restrict__ rec_out) {
+  using E = Elt<T>;
+  constexpr int NV = (DH + 63) / 64;
+  extern __shared__ __attribute__((aligned(16))) float dsm[];
+  __shared__ DecodeDecision dec;
+  const int hk = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, lf = s.lf, LF = DH - lf;
+  const int Lbuf = W + Me + Ms;
+  const int words = dstep_words(Hkv, Me, Ms);
+  const int jn = j + 1 == W ? 0 : j + 1;
+  float* rec = dsm;
+  T* stage = reinterpret_cast<T*>(rec + words);
+  float* ke = reinterpret_cast<float*>(stage + dbank_stage_elems(DH, Me, Ms, lf));
+  float* ve = ke + DH;
+  float* vnrm = ve + DH;
+  float* knrm = vnrm + DH;
+  const DStepWs L = dstep_ws(rec, 0, Hkv, Me, Ms);
+  const int64_t plane = ((int64_t)b * Hkv + hk) * Lbuf;
+  const T* kn_row = k_new + b * nb_sb + hk * nb_sh;
+  const T* vn_row = v_new + b * nb_sb + hk * nb_sh;
+
+  // ---- 1. loads
+  wg_copy16(rec, rec_in + (int64_t)b * words, words * 4);
+  if (Me > 0) wg_copy16(stage, (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH, Me * DH * (int)sizeof(T));
+  if (Ms > 0)
+    wg_copy16(stage + Me * DH, (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF,
+              Ms * LF * (int)sizeof(T));
+  const T* kr = (const T*)s.k_buf + (plane + j) * DH;
+  const T* vr = (const T*)s.v_buf + (plane + j) * DH;
+  for (int d = t; d < DH; d += 256) {
+    ke[d] = E::ld(kr[d]);
+    ve[d] = E::ld(vr[d]);
+  }
+  // the row evicted next: waves 2 (V, full) and 3 (K, LF band) hold it in registers
+  const T* kx = jn == j ? kn_row : (const T*)s.k_buf + (plane + jn) * DH;
+  const T* vx = jn == j ? vn_row : (const T*)s.v_buf + (plane + jn) * DH;
+  float xn[NV];
+  bool an[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int d = lane + 64 * i;
+    an[i] = wv == 2 ? d < DH : d < LF;
+    const int dc = an[i] ? d : 0;
+    xn[i] = (wv >= 2 && an[i]) ? E::ld(wv == 2 ? vx[dc] : kx[lf + dc]) : 0.f;
+  }
+  __syncthreads();
+  // ---- 2. decisions / next unit vectors
+  const float g_e = *L.g_e;
+  if (wv == 0 && Me > 0) decide_exact<T>(s, L.dots, L.used, L.last, g_e, dec, hk == 0, lane);
+  if (wv == 1 && Ms > 0) decide_summary<T>(s, L.dots + Hkv * Me, L.used + Me, g_e, dec, hk == 0, lane);
+  if ((wv == 2 && Me > 0) || (wv == 3 && Ms > 0)) {
+    wave_unit<T, NV>(xn, an);
+    float* dst = wv == 2 ? vnrm : knrm;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (an[i]) dst[lane + 64 * i] = xn[i];
+  }
+  __syncthreads();
+  // ---- 3. row writes of head hk, metadata
+  if (wv == 0)
+    apply_head<T, DH>(s, b, hk, dec, ke, ve, kn_row, vn_row, j, g_e, lane, Me > 0 ? stage + dec.idx_e * DH : nullptr,
+                      Ms > 0 ? stage + Me * DH + dec.idx_s * LF : nullptr);
+  if (wv == 1 && hk == 0) {
+    // metadata of the sequence, and the next record's snapshot of it
+    const DStepWs wn = dstep_ws(rec_out, b, Hkv, Me, Ms);
+    const bool ow_e = Me > 0 && dec.ow_e, keep_e = Me > 0 && dec.keep_e, keep_s = Ms > 0 && dec.keep_s;
+    const int ie = Me > 0 ? dec.idx_e : -1, is = Ms > 0 ? dec.idx_s : -1;
+    for (int m = lane; m < Me + Ms; m += 64)
+      wn.used[m] = L.used[m] | ((ow_e && m == ie) || (keep_s && m == Me + is) ? 1 : 0);
+    for (int m = lane; m < Me; m += 64) wn.last[m] = (keep_e && m == ie) ? pos - W : L.last[m];
+    if (lane == 0) {
+      *wn.g_e = jn == j ? g_new[b] : s.g_recent[(int64_t)b * W + jn];
+      commit_decode_meta(s, b, dec, j, pos - W, g_new[b]);
+    }
+  }
+  __syncthreads();
+  // ---- 4. next record: head hk's dots against the updated norm rows
+  float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
+  float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
+  if (Me > 0)
+    wave_dots<T, 4>(
+        Me, DH, wv, 4, lane, [&](int it) { return (const T*)stage + it * DH; }, [&](int) { return (const float*)vnrm; },
+        [&](int it, float v) { out_e[it] = v; });
+  if (Ms > 0)
+    wave_dots<T, 4>(
+        Ms, LF, wv, 4, lane, [&](int it) { return (const T*)stage + Me * DH + it * LF; },
+        [&](int) { return (const float*)knrm; }, [&](int it, float v) { out_s[it] = v; });
+}
+
 // ------------------------------------------------------------ block plan
 // One wave per (chunk, sequence); lane 0 runs the libstdc++-order selection
 // on the chunk's evicted gates staged in LDS.  Gates of the virtual
@@ -847,6 +972,36 @@ int launch_decode_route(const coda_bank_desc* s, int j, float* ws, hipStream_t s
       else hipLaunchKernelGGL((decode_route_kernel<float, 128>), grid, block, 0, st, *s, j, ws);
   }
   return check_launch("decode_route");
+}
+
+template <typename T, int DH>
+static int launch_dbank(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
+                        const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st) {
+  const size_t lds = dbank_lds(*s);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)decode_bank_kernel<T, DH>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return fail(CODA_EHIP, "coda_decode_step: LDS attribute: %s", hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL((decode_bank_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(256), lds, st, *s, (const T*)k_new,
+                     (const T*)v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out);
+  return check_launch("decode_bank");
+}
+
+int launch_decode_bank(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
+                       const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st) {
+  if (dbank_lds(*s) > 160 * 1024)
+    return fail(CODA_EUNSUP, "coda_decode_step: bank of %d + %d rows does not fit one workgroup", s->Me, s->Ms);
+  const bool bf = s->dtype == CODA_BF16;
+#define CODA_DBANK(D)                                                                                     \
+  return bf ? launch_dbank<bf16_t, D>(s, k_new, v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out, st) \
+            : launch_dbank<float, D>(s, k_new, v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out, st)
+  switch (s->Dh) {
+    case 32: CODA_DBANK(32);
+    case 64: CODA_DBANK(64);
+    default: CODA_DBANK(128);
+  }
+#undef CODA_DBANK
 }
 
 static size_t decode_lds(const coda_bank_desc* s) {

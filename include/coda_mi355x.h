@@ -203,18 +203,17 @@ int coda_decode_write(const coda_bank_desc* s, const void* k_new, const void* v_
  * evicted slot followed by attention of the token's query over the updated
  * cache (the reference's default step order, write then attend).  `a`
  * describes that attention: Lq = 1, prefix = the state cache of `s`
- * (Lp = Lbuf, contiguous), no block keys.  With a full ring and bf16 the
- * update is spread over (head, sequence) workgroups of the attention kernel:
- * each recomputes the sequence's decision from a routing record (per-head
- * cosine dots of the evicted row + metadata snapshot), applies its own
- * head's rows, attends, and then writes the routing record of the next
- * token against the updated banks.  The workspace holds two records, picked
- * by the parity of `pos`.  routed (in/out, may be NULL): on entry nonzero
- * when the record for this call was left by the previous call on the same
- * state and workspace with nothing else modifying the state in between
- * (then the call is one launch; otherwise a routing kernel runs first); on
- * return 1 when this call left the record of the next token, else 0.  Other
- * shapes (ring filling, fp32, key split): coda_decode_write then
+ * (Lp = Lbuf, contiguous), no block keys.  With a full ring the bank update
+ * runs from a routing record (per-head cosine dots of the evicted row with
+ * the norm caches + a snapshot of the bank metadata), one workgroup per
+ * (head, sequence), and leaves the routing record of the next token in the
+ * workspace; then the attention kernel runs.  The workspace holds two
+ * records, picked by the parity of `pos`, followed by the attention
+ * kernel's scratch.  routed (in/out, may be NULL): on entry nonzero when the
+ * record for this call was left by the previous call on the same state and
+ * workspace with nothing else modifying the state in between (otherwise a
+ * routing kernel runs first); on return 1 when this call left the record of
+ * the next token, else 0.  Ring still filling: coda_decode_write then
  * coda_diff_attn_fwd.  workspace >= coda_decode_step_workspace_bytes().
  * Replaces: CoDAGQALandmarkPerf2.step after its projections
  *   (src/coda_gqa_l/attention.py:526-536 -> memory_banks.py:183-432 and
