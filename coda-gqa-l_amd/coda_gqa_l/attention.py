@@ -300,6 +300,8 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         H, Dh = self.num_heads, self.head_dim
         if out is None:
             out = torch.empty((B, 1, H, Dh), dtype=q.dtype, device=q.device)
+        if self._decode_step_planned(state, q, k_new, v_new, g_new, lam, rope_cos, rope_sin, out):
+            return out
         self._check_state(state)
         ct, sn = self._theta_tables(q.dtype)
         desc, keep = ops.attention_desc(

@@ -22,7 +22,7 @@ from typing import Optional
 
 import torch
 
-from . import _hip
+from . import _hip, ops
 from .state import CoDAGQALandmarkStatePerf2
 
 METRIC_KEYS = ("exact_hits", "exact_inserts", "exact_overwrites", "exact_fill_ratio", "summary_updates",
@@ -223,6 +223,75 @@ class MemoryBankMixin:
         st.pos += 1
         if routed.value:
             self.__dict__["_route_tag"] = self._route_key(st, ws)
+
+    # ------------------------------------------------------------ decode plan
+    def _plan_key(self, st: CoDAGQALandmarkStatePerf2, q: torch.Tensor):
+        """Everything the cached descriptors of a decode step depend on."""
+        w = self.head_norm.weight if self.head_norm_mode == "full" else None
+        return (id(st), st.k_buf.data_ptr(), st.v_buf.data_ptr(), st.allowed.data_ptr(), st.g_recent.data_ptr(),
+                st.mem_last_exact.data_ptr(), _hip.ptr(st._exact_v_norm), _hip.ptr(st._sum_lf_k_norm),
+                st.active_exact, st.active_summary, q.dtype, q.shape[0], q.device, self.theta._version,
+                None if w is None else w._version, self.summary_eta_logit._version)
+
+    def _decode_step_planned(self, st: CoDAGQALandmarkStatePerf2, q, k_new, v_new, g_new, lam, rope_cos, rope_sin,
+                             out) -> bool:
+        """Steady-state decode step through descriptors cached per state:
+        full ring, no metrics dict, fixed bank sizes.  Per call only the
+        token's pointers change, so the host side is a few field updates and
+        one library call.  Returns False when the general path must run."""
+        if st.metrics is not None or st.recent_filled < self.window or self._expandable() or \
+                (self.Me == 0 and self.Ms == 0):
+            return False
+        plan = self.__dict__.get("_dplan")
+        key = self._plan_key(st, q)
+        if plan is None or plan["key"] != key:
+            self.__dict__["_dplan"] = None
+            self._check_state(st)
+            key = self._plan_key(st, q)
+            dt = q.dtype
+            ct, sn = self._theta_tables(dt)
+            B, H, Dh = q.shape[0], self.num_heads, self.head_dim
+            a, keep = ops.attention_desc(
+                q=q, rope_cos=rope_cos, rope_sin=rope_sin, rope_interleaved=self.rope_interleaved, theta_cos=ct,
+                theta_sin=sn, k_prefix=st.k_buf, v_prefix=st.v_buf,
+                allowed=st.allowed if self.mask_unused_memory else None, k_block=None, v_block=None, lam=lam,
+                rms_weight=self._rms_weight(dt), eps=self._eps, out=out.permute(0, 2, 1, 3))
+            eta = self._eta_logit_f32(q.device) if self.Ms > 0 else None
+            d = self._bank_desc(st, eta, None, None)
+            nb = ctypes.c_size_t(0)
+            _hip.check(_hip.lib().coda_decode_step_workspace_bytes(d, a, nb))
+            ws = self._route_workspace(q.device, nb.value)
+            plan = {"key": key, "attn": a, "bank": d, "keep": (keep, ct, sn, eta, self._rms_weight(dt)),
+                    "ws": ws, "ws_ptr": _hip.ptr(ws), "ws_bytes": nb.value, "routed": ctypes.c_int(0),
+                    "fn": _hip.lib().coda_decode_step}
+            self.__dict__["_dplan"] = plan
+        a = plan["attn"]
+        a.q = q.data_ptr()
+        a.q_sb, a.q_sh, a.q_sl = q.stride()[:3]
+        a.rope_cos, a.rope_sin = rope_cos.data_ptr(), rope_sin.data_ptr()
+        a.lam = lam.data_ptr()
+        a.lam_sb, a.lam_sh, a.lam_sl = lam.stride()
+        a.out = out.data_ptr()
+        ob, ol, oh = out.stride()[:3]
+        a.o_sb, a.o_sh, a.o_sl = ob, oh, ol
+        # (B, Hkv, 1, Dh) or (B, Hkv, Dh): sequence / head strides, unit channel stride
+        kst, vst = k_new.stride(), v_new.stride()
+        if kst[-1] != 1 or kst[:2] != vst[:2] or vst[-1] != 1 or g_new.dtype != torch.float32 or \
+                g_new.stride(-1) != 1 or rope_cos.stride(-1) != 1 or rope_sin.stride(-1) != 1:
+            return False
+        routed = plan["routed"]
+        tag = self._route_key(st, plan["ws"])
+        routed.value = 1 if self.__dict__.get("_route_tag") == tag else 0
+        self.__dict__["_route_tag"] = None
+        _hip.check(plan["fn"](plan["bank"], a, k_new.data_ptr(), v_new.data_ptr(), kst[0], kst[1], g_new.data_ptr(),
+                              int(st.recent_idx), int(st.recent_filled), int(st.pos), plan["ws_ptr"],
+                              plan["ws_bytes"], ctypes.byref(routed), _hip.stream_of(q)))
+        j = int(st.recent_idx)
+        st.recent_idx = 0 if j + 1 == self.window else j + 1
+        st.pos += 1
+        if routed.value:
+            self.__dict__["_route_tag"] = self._route_key(st, plan["ws"])
+        return True
 
     @staticmethod
     def _route_key(st: CoDAGQALandmarkStatePerf2, ws: Optional[torch.Tensor]):

@@ -230,6 +230,27 @@ __device__ __forceinline__ void diff_norm(float (&y)[NV], const float (&os)[NV],
   for (int i = 0; i < NV; ++i) y[i] = act[i] ? E::rnd(E::rnd(y[i] * r) * E::ld(w[dd[i]])) : 0.f;
 }
 
+// diff_norm for bf16 with the weight values of this lane's channels
+// already in registers (w[i] for channel lane + 64 i; null: identity norm).
+template <int NV>
+__device__ __forceinline__ void diff_norm_w(float (&y)[NV], const float (&os)[NV], const float (&on)[NV],
+                                            const bool (&act)[NV], float lam, const float* w, float eps, int Dh) {
+  using E = Elt<bf16_t>;
+  float sq = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const float s = E::rnd(os[i]), n = E::rnd(on[i]);
+    y[i] = E::rnd(s - E::rnd(lam * n));
+    if (act[i]) sq += E::rnd(y[i] * y[i]);
+  }
+  if (!w) return;
+  sq = wave_sum(sq);
+  const float ms = E::rnd(sq / (float)Dh);
+  const float r = E::rnd(1.0f / sqrtf(E::rnd(ms + E::rnd(eps))));
+#pragma unroll
+  for (int i = 0; i < NV; ++i) y[i] = act[i] ? E::rnd(E::rnd(y[i] * r) * w[i]) : 0.f;
+}
+
 // ------------------------------------------------------------ fp32 / VALU
 // Workgroup = (query qi, KV head, batch); rows = 2 streams x G heads.
 template <typename T, int DH>
@@ -427,74 +448,38 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
   const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
   const int nsplit = gridDim.x;
   const int G = a.H / a.Hkv, GL = G * a.Lq, R = 2 * GL;
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g4 = lane >> 4;
   const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
 
-  // queries (roped, rotated) and the allowed row go to LDS once
   __shared__ __attribute__((aligned(16))) bf16_t q_lds[16][DH + 8];
   __shared__ uint8_t al_lds[kMaxRowsPrefix];
-  stage_queries(a, b, R, &q_lds[0][0], DH + 8, [&](int r, int& st, int& h, int& qi) {
-    st = r / GL;
-    const int rem = r % GL;
-    h = hk * G + rem / a.Lq;
-    qi = rem % a.Lq;
-    return true;
-  });
-  // visibility bytes of the prefix (1 where unmasked); the host guarantees
-  // Lp <= kMaxRowsPrefix, so the tile loop reads them from LDS without a branch
-  for (int i = threadIdx.x; i < a.Lp; i += blockDim.x)
-    al_lds[i] = a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1;
-  __syncthreads();
-  // query fragments (B operand of S^T): row n, channels 32c + 8 g4 + j
-  bf16x8_t qf[NC];
-  int row_qi = 0;
-  {
-    const bool live = n < R;
-    const int rem = live ? n % GL : 0;
-    row_qi = rem % a.Lq;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      uint4 u = live ? *reinterpret_cast<const uint4*>(&q_lds[n][32 * c + 8 * g4]) : uint4{0, 0, 0, 0};
-      qf[c] = __builtin_bit_cast(bf16x8_t, u);
-    }
-  }
-  float m_i = -INFINITY, l_i = 0.f;
-  f32x4 o[NM];
-#pragma unroll
-  for (int i = 0; i < NM; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  char* vt = vt_smem[wv];
-  // V load roles: lane -> (key group kgl, 8-channel chunk dcl)
   constexpr int DCH = DH / 8;
+  // V load roles: lane -> (key group kgl, 8-channel chunk dcl)
   const int kgl = lane / DCH, dcl = lane % DCH;
   const bool vload = kgl < 4;
+  char* vt = vt_smem[wv];
 
-  // Tile loads (K fragments straight from memory, V rows for the LDS
-  // transpose, visibility of this lane's 4 keys) are issued one tile ahead
-  // of the MFMA work so the HBM latency overlaps the previous tile.  Keys
-  // come from one source per phase (prefix = state cache, or block keys)
-  // through a raw buffer resource of that (sequence, KV head) plane: one
-  // 32-bit offset per load, rows past the plane read as zero (hardware range
-  // check), so every load is unconditional and no branch splits the loop;
-  // keys outside the phase's range are removed by the visibility mask.
+  // Keys come from two sources, the prefix (state cache, visibility from
+  // `allowed`) and the block (causal), each through a raw buffer resource of
+  // its (sequence, KV head) plane: one 32-bit offset per load, rows past the
+  // plane read as zero (hardware range check), so every load is
+  // unconditional; keys outside a tile's range are removed by its mask.
   struct Src {
     const bf16_t* k;
     const bf16_t* v;
     int nbytes;      // bytes of the (sequence, KV head) plane
     int row0;        // global key index of the source's row 0
     int rb;          // row stride in bytes
-    bool pre;        // prefix (visibility from `allowed`) or block (causal)
   };
-  auto make_src = [&](const void* kbase, const void* vbase, int64_t sb, int64_t sh, int64_t sl, int rows, int row0,
-                      bool pre) {
+  auto make_src = [&](const void* kbase, const void* vbase, int64_t sb, int64_t sh, int64_t sl, int rows, int row0) {
     Src sr;
     const int64_t off = (int64_t)b * sb + (int64_t)hk * sh;
-    sr.k = (const bf16_t*)kbase + off;
-    sr.v = (const bf16_t*)vbase + off;
+    sr.k = rows > 0 ? (const bf16_t*)kbase + off : (const bf16_t*)nullptr;
+    sr.v = rows > 0 ? (const bf16_t*)vbase + off : (const bf16_t*)nullptr;
     sr.nbytes = rows > 0 ? (int)(((int64_t)(rows - 1) * sl + DH) * 2) : 0;
     sr.row0 = row0;
     sr.rb = (int)(sl * 2);
-    sr.pre = pre;
     return sr;
   };
   // buffer resources from wave-uniform values (readfirstlane makes the
@@ -508,40 +493,119 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
                                              __builtin_amdgcn_readfirstlane(nbytes), kBufWord3);
   };
   const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
-  // Visible keys of a tile: [lo, hi) in global key numbering, minus `excl`;
-  // with `only` >= 0 just that key.
-  struct Vis {
-    int lo, hi, excl, only;
-  };
-  auto load_tile = [&](const Src& sr, int kt, const Vis& vs, bf16x8_t (&kf)[NC], uint4 (&vv)[4], int& vmask) {
-    const __amdgpu_buffer_rsrc_t rk = rsrc(sr.k, sr.nbytes), rv = rsrc(sr.v, sr.nbytes);
-    const int koff = (kt + n - sr.row0) * sr.rb + 16 * g4;
+  // this split's keys [kbeg, kend): prefix tiles over [kbeg, pe), then
+  // block tiles over [bs0, kend), 16 keys each
+  const int kbeg = split * keys_per_split;
+  const int kend = min(a.Lp + a.Lb, kbeg + keys_per_split);
+  const int pe = min(kend, a.Lp);
+  const int n1 = (a.Lp > 0 && kbeg < a.Lp) ? (pe - kbeg + 15) / 16 : 0;
+  const int bs0 = max(kbeg, a.Lp);
+  const int n2 = (a.Lb > 0 && kend > a.Lp) ? (kend - bs0 + 15) / 16 : 0;
+  const int n_tiles = n1 + n2;
+  const Src sp = make_src(a.kp, a.vp, a.p_sb, a.p_sh, a.p_sl, a.Lp, 0);
+  const Src sb = make_src(a.kb, a.vb, a.b_sb, a.b_sh, a.b_sl, a.Lb, a.Lp);
+  auto tile_kt = [&](int i) { return i < n1 ? kbeg + 16 * i : bs0 + 16 * (i - n1); };
+  // K fragments straight from memory, V rows for the LDS transpose, of
+  // this wave's i-th tile (tile wv + i * NW; past the end: the last tile
+  // again, masked out by tile_mask)
+  auto issue = [&](int i, bf16x8_t (&kf)[NC], uint4 (&vv)[4]) {
+    int t = wv + i * NW;
+    t = t < n_tiles ? t : n_tiles - 1;
+    const bool pre = t < n1;
+    const int kt = tile_kt(t);
+    const __amdgpu_buffer_rsrc_t rk = rsrc(pre ? sp.k : sb.k, pre ? sp.nbytes : sb.nbytes);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(pre ? sp.v : sb.v, pre ? sp.nbytes : sb.nbytes);
+    const int row0 = pre ? sp.row0 : sb.row0, rb = pre ? sp.rb : sb.rb;
+    const int koff = (kt + n - row0) * rb + 16 * g4;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
       kf[c] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 64 * c, 0, 0));
     // every lane loads (lanes past the 4 key groups re-read group kgl & 3)
     // so the loads stay unconditional; only their LDS store is predicated
-    const int voff = (kt + 4 * (kgl & 3) - sr.row0) * sr.rb + 16 * dcl;
+    const int voff = (kt + 4 * (kgl & 3) - row0) * rb + 16 * dcl;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
-      vv[jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff + jj * sr.rb, 0, 0));
-    // branch-free (bitwise ops and selects only): a branch here would make
-    // the compiler wait for the loads just issued
-    const int pre_i = sr.pre ? 1 : 0;
-    const int any_only = vs.only < 0 ? 1 : 0;
+      vv[jj] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff + jj * rb, 0, 0));
+  };
+  int row_qi = 0;
+  // visibility of this lane's 4 keys (kt + 4 g4 + j) for query row n in
+  // this wave's i-th tile; branch-free (a branch would make the compiler
+  // wait for loads in flight)
+  auto tile_mask = [&](int i) {
+    const int t = wv + i * NW;
+    const bool live = t < n_tiles;
+    const bool pre = t < n1;
+    const int kt = tile_kt(live ? t : 0);
+    const int lo = live ? (pre ? kbeg : bs0) : 0, hi = live ? (pre ? pe : kend) : 0;
+    const int pre_i = pre ? 1 : 0;
     int m4 = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kk = kt + 4 * g4 + j;
-      const int in = (kk >= vs.lo) & (kk < vs.hi) & (kk != vs.excl) & (any_only | (kk == vs.only));
-      const int kc = in ? kk : vs.lo;
+      const int in = (kk >= lo) & (kk < hi);
+      const int kc = in ? kk : lo;
       const int al_ok = al_lds[pre_i ? kc : 0] != 0;
       const int blk_ok = (a.causal == 0) | ((kc - a.Lp) <= row_qi + coff);
-      const int ok = pre_i ? al_ok : blk_ok;
-      m4 |= (in & ok) << j;
+      m4 |= (in & (pre_i ? al_ok : blk_ok)) << j;
     }
-    vmask = m4;
+    return m4;
   };
+  const int nt_w = (n_tiles + NW - 1) / NW;
+  bf16x8_t kf0[NC], kf1[NC];
+  uint4 vv0[4], vv1[4];
+  int vm0 = 0, vm1 = 0;
+  // the first tile loads while the queries are staged
+  if (n_tiles > 0) issue(0, kf0, vv0);
+  // epilogue operands of this wave's output rows (single split), early
+  constexpr int NV = (DH + 63) / 64;
+  float lam_pf[2] = {0.f, 0.f}, w_pf[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) w_pf[i] = 1.f;
+  if (nsplit == 1) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int orow = wv + r * NW;
+      if (orow < GL) {
+        const int g = orow / a.Lq, qi = orow % a.Lq, h = hk * G + g;
+        lam_pf[r] = bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + qi * a.lam_sl]);
+      }
+    }
+    if (a.rms_w) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) w_pf[i] = bf2f(((const bf16_t*)a.rms_w)[min(lane + 64 * i, DH - 1)]);
+    }
+  }
+  // queries (roped, rotated) and the visibility bytes of the prefix (1
+  // where unmasked) go to LDS once; the host guarantees Lp <=
+  // kMaxRowsPrefix, so the tile masks read them from LDS without a branch
+  stage_queries(a, b, R, &q_lds[0][0], DH + 8, [&](int r, int& st, int& h, int& qi) {
+    st = r / GL;
+    const int rem = r % GL;
+    h = hk * G + rem / a.Lq;
+    qi = rem % a.Lq;
+    return true;
+  });
+  for (int i = threadIdx.x; i < a.Lp; i += blockDim.x)
+    al_lds[i] = a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1;
+  __syncthreads();
+  // query fragments (B operand of S^T): row n, channels 32c + 8 g4 + j
+  bf16x8_t qf[NC];
+  {
+    const bool live = n < R;
+    const int rem = live ? n % GL : 0;
+    row_qi = rem % a.Lq;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      uint4 u = live ? *reinterpret_cast<const uint4*>(&q_lds[n][32 * c + 8 * g4]) : uint4{0, 0, 0, 0};
+      qf[c] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+  if (n_tiles > 0) vm0 = tile_mask(0);
+  float m_i = -INFINITY, l_i = 0.f;
+  f32x4 o[NM];
+#pragma unroll
+  for (int i = 0; i < NM; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
   // One tile of MFMA + online-softmax work on already-loaded registers.
   auto consume = [&](const bf16x8_t (&kf)[NC], const uint4 (&vv)[4], int vmask) {
     f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -582,55 +646,19 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
     }
     __builtin_amdgcn_wave_barrier();
   };
-  // n_tiles tiles of one source, tile i starting at key tile_kt(i) (wave
-  // uniform), round robin over the attention waves, with ping-pong register
-  // buffers: tile i+1 loads while tile i computes, with no register copies
-  // between iterations (a copy would wait for the loads).  Every wave runs
-  // the same trip count and always prefetches; tiles past n_tiles are
-  // masked out entirely.
-  auto run_tiles = [&](const Src& sr, int n_tiles, auto tile_kt, const Vis& vs, const Vis& vs_last) {
-    if (n_tiles <= 0) return;
-    bf16x8_t kf0[NC], kf1[NC];
-    uint4 vv0[4], vv1[4];
-    int vm0 = 0, vm1 = 0;
-    const int nt_w = (n_tiles + NW - 1) / NW;
-    const Vis none{0, 0, -1, -1};
-    auto ld = [&](int i, bf16x8_t (&kf)[NC], uint4 (&vv)[4], int& vm) {
-      const int t = wv + i * NW;
-      const int tc = t < n_tiles ? t : n_tiles - 1;
-      const bool lastt = t == n_tiles - 1, past = t >= n_tiles;
-      Vis v;
-      v.lo = past ? none.lo : (lastt ? vs_last.lo : vs.lo);
-      v.hi = past ? none.hi : (lastt ? vs_last.hi : vs.hi);
-      v.excl = lastt ? vs_last.excl : vs.excl;
-      v.only = lastt ? vs_last.only : vs.only;
-      load_tile(sr, tile_kt(tc), v, kf, vv, vm);
-    };
-    ld(0, kf0, vv0, vm0);
-    for (int i = 0; i < nt_w; i += 2) {
-      ld(i + 1, kf1, vv1, vm1);
-      __builtin_amdgcn_sched_barrier(0);
-      consume(kf0, vv0, vm0);
-      ld(i + 2, kf0, vv0, vm0);
-      __builtin_amdgcn_sched_barrier(0);
-      consume(kf1, vv1, vm1);
-    }
-  };
-  const int kbeg = split * keys_per_split;
-  const int kend = min(a.Lp + a.Lb, kbeg + keys_per_split);
-  // prefix keys [0, Lp) then block keys [Lp, Lp + Lb), each clipped to
-  // this split's [kbeg, kend)
-  if (a.Lp > 0 && kbeg < a.Lp) {
-    const Src sp = make_src(a.kp, a.vp, a.p_sb, a.p_sh, a.p_sl, a.Lp, 0, true);
-    const int e = min(kend, a.Lp);
-    const Vis vs{kbeg, e, -1, -1};
-    run_tiles(sp, (e - kbeg + 15) / 16, [&](int t) { return kbeg + 16 * t; }, vs, vs);
-  }
-  if (a.Lb > 0 && kend > a.Lp) {
-    const Src sb = make_src(a.kb, a.vb, a.b_sb, a.b_sh, a.b_sl, a.Lb, a.Lp, false);
-    const int s0 = max(kbeg, a.Lp);
-    const Vis vs{s0, kend, -1, -1};
-    run_tiles(sb, (kend - s0 + 15) / 16, [&](int t) { return s0 + 16 * t; }, vs, vs);
+  // this wave's tiles i = 0 .. nt_w-1 (tile wv + i * NW) in ping-pong
+  // register buffers: tile i+1 loads while tile i computes, with no
+  // register copies between iterations (a copy would wait for the loads)
+  for (int i = 0; i < nt_w; i += 2) {
+    issue(i + 1, kf1, vv1);
+    vm1 = tile_mask(i + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(kf0, vv0, vm0);
+    if (i + 1 >= nt_w) break;
+    issue(i + 2, kf0, vv0);
+    vm0 = tile_mask(i + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    consume(kf1, vv1, vm1);
   }
   // merge the 4 attention waves
   {
@@ -666,8 +694,7 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
     return;
   }
   // single split: merge + epilogue, one wave per (head, query) output row
-  constexpr int NV = (DH + 63) / 64;
-  for (int orow = wv; orow < GL; orow += NW) {
+  for (int orow = wv, r_pf = 0; orow < GL; orow += NW, ++r_pf) {
     const int g = orow / a.Lq, qi = orow % a.Lq, h = hk * G + g;
     float os[NV], on[NV], y[NV];
     bool act[NV];
@@ -699,8 +726,10 @@ __global__ __launch_bounds__(256) void attn_rows_bf16(const coda_attn_desc a, in
       os[i] = act[i] ? acc[0] : 0.f;
       on[i] = act[i] ? acc[1] : 0.f;
     }
-    const float lam = bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + qi * a.lam_sl]);
-    diff_norm<bf16_t, NV>(y, os, on, act, lam, (const bf16_t*)a.rms_w, dd, a.eps, DH, true, 0, 0);
+    const float lam = r_pf == 0   ? lam_pf[0]
+                      : r_pf == 1 ? lam_pf[1]
+                                  : bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + qi * a.lam_sl]);
+    diff_norm_w<NV>(y, os, on, act, lam, a.rms_w ? w_pf : nullptr, a.eps, DH);
     bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qi * a.o_sl;
 #pragma unroll
     for (int i = 0; i < NV; ++i)

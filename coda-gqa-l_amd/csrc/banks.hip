@@ -169,10 +169,16 @@ __host__ __device__ __forceinline__ size_t dbank_lds(const coda_bank_desc& s) {
          sizeof(float) * 4 * (size_t)s.Dh;
 }
 
-// 16-byte copy of nbytes (a multiple of 16) global -> LDS by the workgroup.
-__device__ __forceinline__ void wg_copy16(void* dst, const void* src, int nbytes) {
-  for (int c = threadIdx.x * 16; c < nbytes; c += blockDim.x * 16)
-    *reinterpret_cast<uint4*>((char*)dst + c) = *reinterpret_cast<const uint4*>((const char*)src + c);
+// Copy nbytes (a multiple of 16) global -> LDS with direct global->LDS
+// loads, spread over the waves of the workgroup: one wave instruction moves
+// 1 KiB (lane l the bytes [16 l, 16 l + 16) of it).  The loads are
+// asynchronous; they count in vmcnt and land before `s_waitcnt vmcnt(0)`.
+__device__ __forceinline__ void wg_copy_lds(void* dst, const void* src, int nbytes) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  for (int c = wv * 1024; c < nbytes; c += nw * 1024)
+    if (c + 16 * lane < nbytes)
+      __builtin_amdgcn_global_load_lds((const char*)src + c + 16 * lane,
+                                       (__attribute__((address_space(3))) void*)((char*)dst + c), 16, 0, 0);
 }
 
 template <typename T, int DH>
@@ -202,11 +208,12 @@ __global__ __launch_bounds__(256) void decode_bank_kernel(const coda_bank_desc s
   const T* vn_row = v_new + b * nb_sb + hk * nb_sh;
 
   // ---- 1. loads
-  wg_copy16(rec, rec_in + (int64_t)b * words, words * 4);
-  if (Me > 0) wg_copy16(stage, (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH, Me * DH * (int)sizeof(T));
+  wg_copy_lds(rec, rec_in + (int64_t)b * words, words * 4);
+  if (Me > 0)
+    wg_copy_lds(stage, (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH, Me * DH * (int)sizeof(T));
   if (Ms > 0)
-    wg_copy16(stage + Me * DH, (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF,
-              Ms * LF * (int)sizeof(T));
+    wg_copy_lds(stage + Me * DH, (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF,
+                Ms * LF * (int)sizeof(T));
   const T* kr = (const T*)s.k_buf + (plane + j) * DH;
   const T* vr = (const T*)s.v_buf + (plane + j) * DH;
   for (int d = t; d < DH; d += 256) {
@@ -225,6 +232,7 @@ __global__ __launch_bounds__(256) void decode_bank_kernel(const coda_bank_desc s
     const int dc = an[i] ? d : 0;
     xn[i] = (wv >= 2 && an[i]) ? E::ld(wv == 2 ? vx[dc] : kx[lf + dc]) : 0.f;
   }
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the direct LDS loads have landed
   __syncthreads();
   // ---- 2. decisions / next unit vectors
   const float g_e = *L.g_e;
