@@ -325,20 +325,24 @@ __global__ __launch_bounds__(64) void block_plan_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------ block write
-// Two kernels per chunk:
+// Three kernels per chunk:
 //   route  grid (Hkv + 1, B): blocks h < Hkv normalise head h of the
 //          candidate rows and take their cosine dots with the head's norm
 //          caches (staged in LDS); block Hkv snapshots the pre-update bank
 //          metadata of sequence b (used bits, LRU stamps, candidate gates)
 //          and computes the LRU victim order.
-//   update grid (Hkv, B): every head block recomputes the per-sequence
-//          decisions from the dots and snapshots (cheap, deterministic,
-//          identical in every block, so no cross-block barrier is needed),
-//          applies them to its own head's rows, and writes its head of the
-//          ring; block h == 0 also writes the per-sequence metadata.
+//   decide grid (1 + ceil(Ts / 16), B): block 0 takes the exact decisions of
+//          sequence b (and commits its LRU stamps), the others route 16
+//          summary candidates each (head-mean scores, first-occurrence
+//          argmax, token weights).
+//   apply  grid (Hkv, B): every head block applies the decisions to its own
+//          head's rows (exact delta write-back, summary accumulate + EMA,
+//          norm caches) and writes its head of the ring; block h == 0 also
+//          writes the per-sequence metadata.
 // Workspace (4-byte words), TT = max(Te, Ts):
 //   dot_e [B][Hkv][Te][Me] f32, dot_s [B][Hkv][Ts][Ms] f32,
-//   snap  [B][SNAP]: used (Me+Ms) i32 | last (Me) i64 | gate (TT) f32 | lru (Me) i32
+//   snap  [B][SNAP]: used (Me+Ms) i32 | last (Me) i64 | gate (TT) f32 | lru (Me) i32,
+//   dec   [B][DEC]: decisions (block_decide_kernel)
 struct BlockGeom {
   int blk, ring_head, ring_filled, n_ev, Kmax, Te, Ts;
   int64_t pos0;
@@ -355,8 +359,10 @@ __host__ __device__ __forceinline__ size_t ws_dot_s(int B, int Hkv, int Me, int 
 __host__ __device__ __forceinline__ size_t ws_snap(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
   return (ws_dot_s(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * Hkv * Ts * Ms + 1) & ~(size_t)1;  // 8-byte aligned
 }
+__host__ __device__ __forceinline__ int dec_words(int Me, int Te, int Ts);
 __host__ __device__ __forceinline__ size_t ws_total(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
-  return ws_snap(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * snap_words(Me, Ms, Te > Ts ? Te : Ts) + 2;
+  return ws_snap(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * snap_words(Me, Ms, Te > Ts ? Te : Ts) +
+         (size_t)B * dec_words(Me, Te, Ts) + 2;
 }
 #define CODA_WS(fn, s, g) fn((s).B, (s).Hkv, (s).Me, (s).Ms, (g).Te, (g).Ts)
 
@@ -442,41 +448,58 @@ __device__ __forceinline__ void lds_dots(const float* rows, int n_rows, const fl
 }
 
 // Stage `n` rows of `len` elements (row stride `rs` elements) into LDS fp32
-// with row stride `ls` floats; 16-byte loads, all issued before use.
+// with row stride `ls` floats; 16-byte loads, 8 per thread in flight
+// before their stores.
 template <typename T>
 __device__ __forceinline__ void stage_rows(float* dst, int ls, const T* src, int64_t rs, int n, int len) {
-  const int chunks = len >> 3;
-  for (int i = threadIdx.x; i < n * chunks; i += blockDim.x) {
-    const int r = i / chunks, c = i % chunks;
-    float x[8];
-    load8f<T>(src + r * rs + 8 * c, x);
-    float4* d = reinterpret_cast<float4*>(dst + r * ls + 8 * c);
-    d[0] = make_float4(x[0], x[1], x[2], x[3]);
-    d[1] = make_float4(x[4], x[5], x[6], x[7]);
+  const int chunks = len >> 3, nt = blockDim.x, total = n * chunks;
+  for (int base = threadIdx.x; base < total; base += 8 * nt) {
+    float x[8][8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = min(base + u * nt, total - 1);
+      load8f<T>(src + (i / chunks) * rs + 8 * (i % chunks), x[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = base + u * nt;
+      if (i < total) {
+        float4* d = reinterpret_cast<float4*>(dst + (i / chunks) * ls + 8 * (i % chunks));
+        d[0] = make_float4(x[u][0], x[u][1], x[u][2], x[u][3]);
+        d[1] = make_float4(x[u][4], x[u][5], x[u][6], x[u][7]);
+      }
+    }
   }
 }
 
-// Normalised candidate rows (one wave per row) into LDS.
+// Normalised candidate rows into LDS: each wave takes 8 rows at a time,
+// loads all of them, then normalises them one by one.
 template <typename T, int DH>
 __device__ __forceinline__ void stage_cands(float* dst, int ls, const coda_bank_desc& s, const BlockGeom& g,
                                             const T* src_blk, const int32_t* pc, int b, int h, int n, int off,
                                             int len, bool value) {
-  constexpr int NV = (DH + 63) / 64;
+  constexpr int NV = (DH + 63) / 64, RB = 8;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  for (int r = wv; r < n; r += nw) {
-    const T* row = cand_row<T, DH>(s, g, src_blk, b, h, pc[r], value);
-    float x[NV];
-    bool act[NV];
+  bool act[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int d = lane + 64 * i;
-      act[i] = d < len;
-      x[i] = act[i] ? Elt<T>::ld(row[off + d]) : 0.f;
+  for (int i = 0; i < NV; ++i) act[i] = lane + 64 * i < len;
+  for (int r0 = wv * RB; r0 < n; r0 += nw * RB) {
+    float x[RB][NV];
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const int r = min(r0 + u, n - 1);
+      const T* row = cand_row<T, DH>(s, g, src_blk, b, h, pc[r], value);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) x[u][i] = act[i] ? Elt<T>::ld(row[off + lane + 64 * i]) : 0.f;
     }
-    wave_unit<T, NV>(x, act);
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (act[i]) dst[r * ls + lane + 64 * i] = x[i];
+    for (int u = 0; u < RB; ++u) {
+      if (r0 + u >= n) break;
+      wave_unit<T, NV>(x[u], act);
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) dst[(r0 + u) * ls + lane + 64 * i] = x[u][i];
+    }
   }
 }
 
@@ -502,384 +525,628 @@ __global__ __launch_bounds__(256) void block_route_kernel(const coda_bank_desc s
         const bool u = al[W + m] != 0 && m < Ae;
         rk[m] = sel::Item<int64_t>{u ? s.mem_last[(int64_t)b * Me + m] : kNegBig, (int64_t)m};
       }
+      __shared__ int ties;
+      if (t == 0) ties = 0;
       __syncthreads();
       const int n_lru = min(g.Te, Ae);
-      if (t == 0) sel::topk_order<int64_t>(rk, Me, n_lru, false, true);
+      // Keys that reach the first n_lru places with no equal key: the
+      // sorted topk order is their rank order, whatever the algorithm
+      // (the usual case once the bank is full: LRU stamps are distinct).
+      for (int m = t; m < Me; m += blockDim.x) {
+        const int64_t km = rk[m].v;
+        int lt = 0, eq = 0;
+        for (int j = 0; j < Me; ++j) {
+          const int64_t kj = rk[j].v;
+          lt += kj < km;
+          eq += (kj == km) & (j != m);
+        }
+        if (lt < n_lru) {
+          if (eq) atomicOr(&ties, 1);
+          else sn.lru[lt] = m;
+        }
+      }
       __syncthreads();
-      for (int r = t; r < n_lru; r += blockDim.x) sn.lru[r] = (int32_t)rk[r].i;
+      // ties among the leading keys: their order is libstdc++'s
+      if (ties) {
+        if (t == 0) sel::topk_order<int64_t>(rk, Me, n_lru, false, true);
+        __syncthreads();
+        for (int r = t; r < n_lru; r += blockDim.x) sn.lru[r] = (int32_t)rk[r].i;
+      }
     }
     return;
   }
-  if (g.Te > 0) {
-    const int ls = DH + 4;
-    float* nrm = rsm;
-    float* cnd = rsm + Me * ls;
-    stage_rows<T>(nrm, ls, (const T*)s.exact_v_norm + ((int64_t)b * s.Hkv + h) * Me * DH, DH, Me, DH);
-    stage_cands<T, DH>(cnd, ls, s, g, vbk, pc, b, h, g.Te, 0, DH, true);
-    __syncthreads();
-    lds_dots<T>(nrm, Me, cnd, g.Te, DH, ls, ws + (((int64_t)b * s.Hkv + h) * g.Te) * Me);
-    __syncthreads();
-  }
-  if (g.Ts > 0) {
-    const int ls = LF + 4;
-    float* nrm = rsm;
-    float* cnd = rsm + Ms * ls;
-    stage_rows<T>(nrm, ls, (const T*)s.sum_lf_k_norm + ((int64_t)b * s.Hkv + h) * Ms * LF, LF, Ms, LF);
-    stage_cands<T, DH>(cnd, ls, s, g, kbk, pc, b, h, g.Ts, s.lf, LF, false);
-    __syncthreads();
-    lds_dots<T>(nrm, Ms, cnd, g.Ts, LF, ls, ws + CODA_WS(ws_dot_s, s, g) + (((int64_t)b * s.Hkv + h) * g.Ts) * Ms);
+  // LDS: exact norm rows [Me][DH+4] | exact candidates [Te][DH+4] |
+  //      summary norm rows [Ms][LF+4] | summary candidates [Ts][LF+4]
+  const int le = DH + 4, lsum = LF + 4;
+  float* nrm_e = rsm;
+  float* cnd_e = nrm_e + (g.Te > 0 ? Me * le : 0);
+  float* nrm_s = cnd_e + g.Te * le;
+  float* cnd_s = nrm_s + (g.Ts > 0 ? Ms * lsum : 0);
+  if (g.Te > 0) stage_rows<T>(nrm_e, le, (const T*)s.exact_v_norm + ((int64_t)b * s.Hkv + h) * Me * DH, DH, Me, DH);
+  if (g.Ts > 0)
+    stage_rows<T>(nrm_s, lsum, (const T*)s.sum_lf_k_norm + ((int64_t)b * s.Hkv + h) * Ms * LF, LF, Ms, LF);
+  if (g.Te > 0) stage_cands<T, DH>(cnd_e, le, s, g, vbk, pc, b, h, g.Te, 0, DH, true);
+  if (g.Ts > 0) stage_cands<T, DH>(cnd_s, lsum, s, g, kbk, pc, b, h, g.Ts, s.lf, LF, false);
+  __syncthreads();
+  if (g.Te > 0) lds_dots<T>(nrm_e, Me, cnd_e, g.Te, DH, le, ws + (((int64_t)b * s.Hkv + h) * g.Te) * Me);
+  if (g.Ts > 0)
+    lds_dots<T>(nrm_s, Ms, cnd_s, g.Ts, LF, lsum,
+                ws + CODA_WS(ws_dot_s, s, g) + (((int64_t)b * s.Hkv + h) * g.Ts) * Ms);
+}
+
+// Decision record of a chunk, per sequence (4-byte words), written by
+// block_decide_kernel and read by block_apply_kernel:
+//   idx_e [Te] i32 | fl_e [Te] i32 (1 overwrite, 2 touch) | eflag [Me] i32 |
+//   idx_s [Ts] i32 | wtok [Ts] f32
+__host__ __device__ __forceinline__ int dec_words(int Me, int Te, int Ts) { return even_up(2 * Te + Me + 2 * Ts); }
+__host__ __device__ __forceinline__ size_t ws_dec(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
+  return ws_snap(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * snap_words(Me, Ms, Te > Ts ? Te : Ts);
+}
+struct Dec {
+  int32_t* idx_e;
+  int32_t* fl_e;
+  int32_t* eflag;
+  int32_t* idx_s;
+  float* wtok;
+};
+__device__ __forceinline__ Dec dec_of(const coda_bank_desc& s, const BlockGeom& g, float* ws, int b) {
+  int32_t* base = reinterpret_cast<int32_t*>(ws + CODA_WS(ws_dec, s, g)) + (int64_t)b * dec_words(s.Me, g.Te, g.Ts);
+  Dec d;
+  d.idx_e = base;
+  d.fl_e = base + g.Te;
+  d.eflag = base + 2 * g.Te;
+  d.idx_s = base + 2 * g.Te + s.Me;
+  d.wtok = reinterpret_cast<float*>(base + 2 * g.Te + s.Me + g.Ts);
+  return d;
+}
+
+// Summary candidates per decide workgroup.
+static constexpr int kDecideChunk = 16;
+
+// fp32 copy global -> LDS by the workgroup, 16 independent loads per thread
+// in flight before their stores.
+__device__ __forceinline__ void wg_copy_f32(float* dst, const float* src, int n) {
+  const int nt = blockDim.x;
+  for (int base = threadIdx.x; base < n; base += 16 * nt) {
+    float x[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = base + u * nt;
+      x[u] = i < n ? src[i] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int i = base + u * nt;
+      if (i < n) dst[i] = x[u];
+    }
   }
 }
 
-struct UpdLds {
-  int32_t *idx_e, *fl_e, *idx_s, *used, *eflag, *sflag, *best_i, *misc;
-  float *wtok, *cnt, *best, *big;
-};
-__host__ __device__ __forceinline__ size_t upd_small_words(int Me, int Ms, int TT) {
-  return (size_t)6 * TT + (Me + Ms) + Me + 2 * Ms + 8 + Ms;  // + active-slot list
+// Decisions of one chunk (memory_banks.py:640-697 exact, :866-878 summary).
+// Workgroup x == 0: exact decisions of sequence b from the per-head dots
+// and the metadata snapshot (LRU stamps are committed here, the only
+// writer); x >= 1: summary routing of candidates [16 (x-1), 16 x).
+template <typename T>
+__global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc s, BlockGeom g,
+                                                           const int32_t* __restrict__ plan_c, float* ws) {
+  using E = Elt<T>;
+  extern __shared__ __attribute__((aligned(16))) float dsm2[];
+  __shared__ float best[kDecideChunk > 64 ? kDecideChunk : 64];
+  __shared__ int best_i[kDecideChunk > 64 ? kDecideChunk : 64];
+  const int x = blockIdx.x, b = blockIdx.y, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int Me = s.Me, Ms = s.Ms, Hkv = s.Hkv, Te = g.Te, Ts = g.Ts, W = s.W;
+  const Snap sn = snap_of(s, g, ws, b);
+  const Dec dc = dec_of(s, g, ws, b);
+  if (x == 0) {
+    if (Te == 0) return;
+    float* dl = dsm2;                           // [Hkv][Te][Me]
+    float* sc = dl + Hkv * Te * Me;             // [Te][Me]
+    int* used = reinterpret_cast<int*>(sc + Te * Me);  // [Me]
+    int* idx_l = used + Me;                      // [Te]
+    int* fl_l = idx_l + Te;                      // [Te]
+    wg_copy_f32(dl, ws + (int64_t)b * Hkv * Te * Me, Hkv * Te * Me);
+    for (int m = t; m < Me; m += blockDim.x) used[m] = sn.used[m];
+    __syncthreads();
+    for (int i = t; i < Te * Me; i += blockDim.x) {
+      float acc = 0.f;
+      for (int hh = 0; hh < Hkv; ++hh) acc += dl[hh * Te * Me + i];
+      float v = E::rnd(acc / (float)Hkv);
+      const int m = i % Me;
+      if (m >= s.active_exact || used[m] == 0) v = neg_fill<T>();
+      sc[i] = v;
+    }
+    __syncthreads();
+    for (int tt = wv; tt < Te; tt += blockDim.x >> 6) {
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int m = lane; m < Me; m += 64) {
+        const float v = sc[tt * Me + m];
+        if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
+      }
+      wave_argmax(bv, bi);
+      if (lane == 0) { best[tt & 63] = bv; best_i[tt & 63] = bi; }
+    }
+    __syncthreads();
+    __shared__ int any_used_s;
+    if (t == 0) any_used_s = 0;
+    __syncthreads();
+    if (wv == 0) {
+      int u = 0;
+      for (int m = lane; m < Me; m += 64) u |= used[m] != 0;
+      u = wave_or(u);
+      if (lane == 0) any_used_s = u;
+    }
+    __syncthreads();
+    if (t == 0) {
+      const int Ae = s.active_exact;
+      const int any_used = any_used_s;
+      const int n_lru = min(Te, Ae);
+      int rank = -1;
+      int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
+      for (int tt = 0; tt < Te; ++tt) {
+        const bool keep = s.gated ? (sn.gate[tt] >= s.tau_exact) : true;
+        const float bv = best[tt & 63];
+        const bool novel = !any_used || bv < E::rnd(s.tau_novel);
+        const bool hit = any_used && bv >= E::rnd(s.tau_match);
+        const bool nk = novel && keep;
+        if (nk) ++rank;  // cumsum(novel & keep) - 1 at tt
+        const bool cap = nk && rank < Ae;
+        int idx = best_i[tt & 63];
+        if (cap) {
+          int r = rank < 0 ? 0 : rank;
+          if (r > n_lru - 1) r = n_lru - 1;
+          idx = sn.lru[r];
+        }
+        const bool touch = keep && (!novel || cap);
+        const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
+        idx_l[tt] = idx;
+        fl_l[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
+        cnt_ow += ow;
+        cnt_cap += cap;
+        cnt_hit += (hit && keep);
+        cnt_gated += !keep;
+        cnt_fr += (nk && !cap);
+      }
+      if (s.metrics) {
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, cnt_ow);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, cnt_fr);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, cnt_cap);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, cnt_hit);
+        if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, cnt_gated);
+      }
+      if (s.frustrated) atomic_add_i64(s.frustrated + 0, cnt_fr);
+    }
+    __syncthreads();
+    for (int tt = t; tt < Te; tt += blockDim.x) {
+      dc.idx_e[tt] = idx_l[tt];
+      dc.fl_e[tt] = fl_l[tt];
+    }
+    const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
+    for (int m = t; m < Me; m += blockDim.x) {
+      int f = 0;
+      bool tm = false;
+      int64_t pv = kNegBig;
+      for (int tt = 0; tt < Te; ++tt) {
+        if (idx_l[tt] != m) continue;
+        f |= fl_l[tt] & 1;
+        if (fl_l[tt] & 2) {
+          tm = true;
+          const int64_t p = g.pos0 - g.ring_filled + pc[tt];
+          if (p > pv) pv = p;
+        }
+      }
+      dc.eflag[m] = f;
+      if (tm) s.mem_last[(int64_t)b * Me + m] = pv;  // LRU: max pos of the touching tokens
+    }
+    return;
+  }
+  // ---- summary routing of candidates [t0, t0 + nt)
+  const int t0 = (x - 1) * kDecideChunk;
+  const int nt = min(kDecideChunk, Ts - t0);
+  if (nt <= 0) return;
+  float* dl = dsm2;  // [Hkv][nt][Ms]
+  const float* dsd = ws + CODA_WS(ws_dot_s, s, g) + (int64_t)b * Hkv * Ts * Ms;
+  {
+    const int per = nt * Ms, total = Hkv * per, ntr = blockDim.x;
+    for (int base = t; base < total; base += 16 * ntr) {
+      float xv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int i = base + u * ntr;
+        xv[u] = i < total ? dsd[((int64_t)(i / per) * Ts + t0) * Ms + (i % per)] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int i = base + u * ntr;
+        if (i < total) dl[i] = xv[u];
+      }
+    }
+  }
+  __syncthreads();
+  for (int tt = wv; tt < nt; tt += blockDim.x >> 6) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int m = lane; m < Ms; m += 64) {
+      float acc = 0.f;
+      for (int hh = 0; hh < Hkv; ++hh) acc += dl[(hh * nt + tt) * Ms + m];
+      float v = E::rnd(acc / (float)Hkv);
+      if (m >= s.active_summary) v = neg_fill<T>();
+      if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
+    }
+    wave_argmax(bv, bi);
+    if (lane == 0) {
+      dc.idx_s[t0 + tt] = bi;
+      const float gate = sn.gate[t0 + tt];
+      dc.wtok[t0 + tt] = (!s.gated || gate >= s.tau_summary) ? E::rnd(gate) : 0.f;
+    }
+  }
 }
-__host__ __device__ __forceinline__ size_t upd_big_words(int Me, int Ms, int Te, int Ts, int DH, int LF) {
-  const size_t a = (size_t)Te * Me, b2 = (size_t)Ts * Ms, c = (size_t)Ms * (DH + LF);
-  return a > b2 ? (a > c ? a : c) : (b2 > c ? b2 : c);
+
+// Bank writes of head h of sequence b for one chunk, from the decisions
+// (memory_banks.py:707-742 exact write-back, :880-932 summary accumulate +
+// EMA) and the ring write of the surviving block tokens.  8 waves.  Loads
+// are issued in batches before their first use: the block tokens the ring
+// write copies (stored once every evicted ring row of this head has been
+// read), the summary candidate rows, the summary bank rows of head h and
+// the exact candidate rows (to LDS).  Each summary slot keeps the list of its tokens in token
+// order, so one thread per (active slot, channel) sums the slot's weighted
+// tokens in registers (fp32, token order: the scatter_add order) and
+// applies the EMA in the same pass.
+// LDS: summary candidate rows [Ts][DH + LF] T | summary bank rows
+//      [Ms][DH + LF] T (V channels first, then K's LF band) | exact
+//      candidate rows [Te][2 DH] T (K, V) | new LF keys [Ms][LF] f32 |
+//      token lists [Ms][Ts] i32 | small arrays.  Once every evicted ring
+//      row is in LDS the ring write goes out (the stores overlap the rest).
+static constexpr int kApplyThreads = 512;
+static constexpr int kRingPre = 8;   // 16-byte ring-write chunks per thread loaded up front
+
+__host__ __device__ __forceinline__ size_t apply_small_words(int Me, int Ms, int Te, int Ts) {
+  return (size_t)2 * Te + Me + 2 * Ts + (Me + Ms) + 4 * Ms + 8;
+}
+__host__ __device__ __forceinline__ size_t apply_rows_bytes(int n, int DH, int LF, int esz) {
+  return ((size_t)n * (DH + LF) * esz + 15) & ~(size_t)15;
+}
+__host__ __device__ __forceinline__ size_t apply_erows_bytes(int Te, int DH, int esz) {
+  return ((size_t)Te * 2 * DH * esz + 15) & ~(size_t)15;
+}
+__host__ __device__ __forceinline__ size_t apply_lds_bytes(int Me, int Ms, int Te, int Ts, int DH, int LF, int esz) {
+  return apply_rows_bytes(Ts, DH, LF, esz) + apply_rows_bytes(Ms, DH, LF, esz) + apply_erows_bytes(Te, DH, esz) +
+         (size_t)Ms * LF * 4 + (size_t)Ms * Ts * 4 + 4 * apply_small_words(Me, Ms, Te, Ts);
+}
+
+// Eight consecutive elements moved as raw bits: PW 16-byte words.
+template <typename T>
+struct Piece8 {
+  static constexpr int PW = sizeof(T) / 2;
+  uint4 w[PW];
+};
+template <typename T>
+__device__ __forceinline__ Piece8<T> ld8(const T* p) {
+  Piece8<T> x;
+#pragma unroll
+  for (int i = 0; i < Piece8<T>::PW; ++i) x.w[i] = reinterpret_cast<const uint4*>(p)[i];
+  return x;
+}
+template <typename T>
+__device__ __forceinline__ void st8(T* p, const Piece8<T> x) {
+#pragma unroll
+  for (int i = 0; i < Piece8<T>::PW; ++i) reinterpret_cast<uint4*>(p)[i] = x.w[i];
 }
 
 template <typename T, int DH>
-__global__ __launch_bounds__(256) void block_update_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
-                                                           const T* vbk, const float* gb,
-                                                           const int32_t* __restrict__ plan_c, float* ws) {
+__global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
+                                                                    const T* vbk, const float* gb,
+                                                                    const int32_t* __restrict__ plan_c, float* ws) {
   using E = Elt<T>;
-  constexpr int NV = (DH + 63) / 64;
-  extern __shared__ __attribute__((aligned(16))) float usm[];
+  constexpr int NV = (DH + 63) / 64, CH = DH / 8, LF = DH / 2, NCOL = DH + LF, CPR = NCOL / 8;
+  extern __shared__ __attribute__((aligned(16))) float asm_[];
   const int h = blockIdx.x, b = blockIdx.y;
-  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int W = s.W, Me = s.Me, Ms = s.Ms, Hkv = s.Hkv, Te = g.Te, Ts = g.Ts, lf = s.lf, LF = DH - lf;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6, NT = blockDim.x, NW = NT >> 6;
+  const int W = s.W, Me = s.Me, Ms = s.Ms, Hkv = s.Hkv, Te = g.Te, Ts = g.Ts, lf = s.lf;
   const int Lbuf = W + Me + Ms;
-  const int TT = max(Te, Ts);
   const bool lead = h == 0;
-  // LDS carve-up
-  UpdLds L;
-  {
-    int32_t* p = reinterpret_cast<int32_t*>(usm);
-    L.big = usm;  // union: scores, then summary accumulators
-    p += upd_big_words(Me, Ms, Te, Ts, DH, LF);
-    L.idx_e = p; p += TT;
-    L.fl_e = p; p += TT;
-    L.idx_s = p; p += TT;
-    L.wtok = reinterpret_cast<float*>(p); p += TT;
-    L.best = reinterpret_cast<float*>(p); p += TT;
-    L.best_i = p; p += TT;
-    L.used = p; p += Me + Ms;
-    L.eflag = p; p += Me;
-    L.sflag = p; p += Ms;
-    L.cnt = reinterpret_cast<float*>(p); p += Ms;
-    L.misc = p;
-  }
-  const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
-  uint8_t* al = s.allowed + (int64_t)b * Lbuf;
   T* kb = (T*)s.k_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
   T* vb = (T*)s.v_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
-  const bool evict = g.n_ev > 0;
-  if (evict) {
-    Snap sn = snap_of(s, g, ws, b);
-    for (int m = t; m < Me + Ms; m += 256) L.used[m] = sn.used[m];
-    for (int m = t; m < Me; m += 256) L.eflag[m] = 0;
-    for (int m = t; m < Ms; m += 256) { L.sflag[m] = 0; L.cnt[m] = 0.f; }
-    if (t < 8) L.misc[t] = 0;
-    __syncthreads();
-    // ---------------- exact decisions (memory_banks.py:640-697)
-    if (Te > 0) {
-      float* sc = L.big;
-      const float* de = ws + (int64_t)b * Hkv * Te * Me;
-      for (int i = t; i < Te * Me; i += 256) {
-        float acc = 0.f;
-        for (int hh = 0; hh < Hkv; ++hh) acc += de[(int64_t)hh * Te * Me + i];
-        float v = E::rnd(acc / (float)Hkv);
-        const int m = i % Me;
-        if (m >= s.active_exact || L.used[m] == 0) v = neg_fill<T>();
-        sc[i] = v;
-      }
-      __syncthreads();
-      for (int tt = wv; tt < Te; tt += 4) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int m = lane; m < Me; m += 64) {
-          const float v = sc[tt * Me + m];
-          if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
-        }
-        wave_argmax(bv, bi);
-        if (lane == 0) { L.best[tt] = bv; L.best_i[tt] = bi; }
-      }
-      __syncthreads();
-      if (t == 0) {
-        const int Ae = s.active_exact;
-        int any_used = 0;
-        for (int m = 0; m < Me; ++m) any_used |= L.used[m] != 0;
-        const int n_lru = min(Te, Ae);
-        int rank = -1;
-        int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
-        for (int tt = 0; tt < Te; ++tt) {
-          const bool keep = s.gated ? (sn.gate[tt] >= s.tau_exact) : true;
-          const float bv = L.best[tt];
-          const bool novel = !any_used || bv < E::rnd(s.tau_novel);
-          const bool hit = any_used && bv >= E::rnd(s.tau_match);
-          const bool nk = novel && keep;
-          if (nk) ++rank;  // cumsum(novel & keep) - 1 at tt
-          const bool cap = nk && rank < Ae;
-          int idx = L.best_i[tt];
-          if (cap) {
-            int r = rank < 0 ? 0 : rank;
-            if (r > n_lru - 1) r = n_lru - 1;
-            idx = sn.lru[r];
-          }
-          const bool touch = keep && (!novel || cap);
-          const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
-          L.idx_e[tt] = idx;
-          L.fl_e[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
-          cnt_ow += ow;
-          cnt_cap += cap;
-          cnt_hit += (hit && keep);
-          cnt_gated += !keep;
-          cnt_fr += (nk && !cap);
-        }
-        if (lead) {
-          if (s.metrics) {
-            atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, cnt_ow);
-            atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, cnt_fr);
-            atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, cnt_cap);
-            atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, cnt_hit);
-            if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, cnt_gated);
-          }
-          if (s.frustrated) atomic_add_i64(s.frustrated + 0, cnt_fr);
-        }
-      }
-      __syncthreads();
-      for (int m = t; m < Me; m += 256) {
-        int f = 0;
-        bool tm = false;
-        int64_t pv = kNegBig;
-        for (int tt = 0; tt < Te; ++tt) {
-          if (L.idx_e[tt] != m) continue;
-          f |= L.fl_e[tt] & 1;
-          if (L.fl_e[tt] & 2) {
-            tm = true;
-            const int64_t p = g.pos0 - g.ring_filled + pc[tt];
-            if (p > pv) pv = p;
-          }
-        }
-        L.eflag[m] = f;
-        if (lead && tm) s.mem_last[(int64_t)b * Me + m] = pv;  // LRU: max pos of the touching tokens
-      }
-      __syncthreads();
-    }
-    // ---------------- summary routing + counts (memory_banks.py:513-528, :866-898)
-    if (Ts > 0) {
-      float* sc = L.big;
-      const float* dsd = ws + CODA_WS(ws_dot_s, s, g) + (int64_t)b * Hkv * Ts * Ms;
-      for (int i = t; i < Ts * Ms; i += 256) {
-        float acc = 0.f;
-        for (int hh = 0; hh < Hkv; ++hh) acc += dsd[(int64_t)hh * Ts * Ms + i];
-        float v = E::rnd(acc / (float)Hkv);
-        if (i % Ms >= s.active_summary) v = neg_fill<T>();
-        sc[i] = v;
-      }
-      __syncthreads();
-      for (int tt = wv; tt < Ts; tt += 4) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int m = lane; m < Ms; m += 64) {
-          const float v = sc[tt * Ms + m];
-          if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
-        }
-        wave_argmax(bv, bi);
-        if (lane == 0) {
-          L.idx_s[tt] = bi;
-          const float gate = sn.gate[tt];
-          L.wtok[tt] = (!s.gated || gate >= s.tau_summary) ? E::rnd(gate) : 0.f;
-        }
-      }
-      __syncthreads();
-      for (int m = t; m < Ms; m += 256) {
-        float c = 0.f;
-        for (int tt = 0; tt < Ts; ++tt)
-          if (L.idx_s[tt] == m) c += L.wtok[tt];  // fp32 accumulation in token order
-        L.cnt[m] = E::rnd(c);
-        const bool active = L.cnt[m] > 0.f;
-        L.sflag[m] = (active ? 1 : 0) | ((active && L.used[Me + m] == 0) ? 2 : 0);
-      }
-      __syncthreads();
-    }
-    // ---------------- exact writeback of head h (memory_banks.py:707-742)
-    if (Te > 0) {
-      for (int m = wv; m < Me; m += 4) {
-        if (!L.eflag[m]) continue;
-        float nv[NV];
-        bool act[NV];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int d = lane + 64 * i;
-          act[i] = d < DH;
-          nv[i] = 0.f;
-          if (!act[i]) continue;
-          T* kr = kb + (int64_t)(W + m) * DH;
-          T* vr = vb + (int64_t)(W + m) * DH;
-          const float mk = E::ld(kr[d]), mv = E::ld(vr[d]);
-          float ak = 0.f, av = 0.f;
-          for (int tt = 0; tt < Te; ++tt) {
-            if (L.idx_e[tt] != m || !(L.fl_e[tt] & 1)) continue;
-            ak += E::rnd(E::ld(cand_row<T, DH>(s, g, kbk, b, h, pc[tt], false)[d]) - mk);
-            av += E::rnd(E::ld(cand_row<T, DH>(s, g, vbk, b, h, pc[tt], true)[d]) - mv);
-          }
-          kr[d] = E::st(mk + E::rnd(ak));
-          nv[i] = E::rnd(mv + E::rnd(av));
-          vr[d] = E::st(nv[i]);
-        }
-        wave_unit<T, NV>(nv, act);
-        T* nr = (T*)s.exact_v_norm + (((int64_t)b * Hkv + h) * Me + m) * DH;
-#pragma unroll
-        for (int i = 0; i < NV; ++i)
-          if (act[i]) nr[lane + 64 * i] = E::st(nv[i]);
-      }
-    }
-    // ---------------- summary accumulate + EMA of head h (memory_banks.py:880-932)
-    if (Ts > 0) {
-      // accumulators [Ms][DH + LF]: V channels then K's LF channels; one
-      // thread per channel walks the tokens in order (fp32 scatter_add order)
-      float* acc = L.big;
-      const int ncol = DH + LF;
-      for (int i = t; i < Ms * ncol; i += 256) acc[i] = 0.f;
-      __syncthreads();
-      for (int col = t; col < ncol; col += 256) {
-        const bool is_v = col < DH;
-        const int d = is_v ? col : lf + (col - DH);
-        const T* src = is_v ? vbk : kbk;
-        // 8 independent row loads in flight, then the in-order accumulation
-        for (int t0 = 0; t0 < Ts; t0 += 8) {
-          float xv[8];
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const int tt = min(t0 + u, Ts - 1);
-            xv[u] = E::ld(cand_row<T, DH>(s, g, src, b, h, pc[tt], is_v)[d]);
-          }
-#pragma unroll
-          for (int u = 0; u < 8; ++u) {
-            const int tt = t0 + u;
-            if (tt < Ts) acc[L.idx_s[tt] * ncol + col] += E::rnd(xv[u] * L.wtok[tt]);
-          }
-        }
-      }
-      __syncthreads();
-      // active slots, compacted (in slot order)
-      int* act_list = L.misc + 8;
-      if (t == 0) {
-        int na = 0;
-        for (int m = 0; m < Ms; ++m)
-          if (L.sflag[m] & 1) act_list[na++] = m;
-        L.misc[0] = na;
-      }
-      __syncthreads();
-      const int n_act = L.misc[0];
-      const float eta_h = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
-#pragma unroll 4
-      for (int it = t; it < n_act * ncol; it += 256) {
-        const int m = act_list[it / ncol], col = it % ncol;
-        const bool is_v = col < DH;
-        const int d = is_v ? col : lf + (col - DH);
-        const int f = L.sflag[m];
-        const float eta = (s.overwrite_on_insert && (f & 2)) ? 1.f : eta_h;
-        const float den = fmaxf(L.cnt[m], eps_r<T>());
-        const float avg = E::rnd(E::rnd(acc[m * ncol + col]) / den);
-        T* row = (is_v ? vb : kb) + (int64_t)(W + Me + m) * DH;
-        const float mem = E::ld(row[d]);
-        if (is_v) {
-          row[d] = E::st(mem + E::rnd(eta * E::rnd(avg - mem)));
-        } else {
-          const float dk = E::rnd(E::rnd(avg * s.energy_scale) - mem);
-          const float nk = E::rnd(mem + E::rnd(eta * dk));
-          row[d] = E::st(nk);
-          acc[m * ncol + col] = nk;  // new LF key, read back for the norm cache
-        }
-      }
-      __syncthreads();
-      for (int m = wv; m < Ms; m += 4) {
-        if (!(L.sflag[m] & 1)) continue;
-        float x[NV];
-        bool act[NV];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-          const int d = lane + 64 * i;
-          act[i] = d < LF;
-          x[i] = act[i] ? acc[m * ncol + DH + d] : 0.f;
-        }
-        wave_unit<T, NV>(x, act);
-        T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + m) * LF;
-#pragma unroll
-        for (int i = 0; i < NV; ++i)
-          if (act[i]) nr[lane + 64 * i] = E::st(x[i]);
-      }
-    }
-    // ---------------- per-sequence metadata (lead block)
-    if (lead) {
-      for (int m = t; m < Me; m += 256)
-        if (L.eflag[m]) al[W + m] = 1;
-      for (int m = t; m < Ms; m += 256)
-        if (L.sflag[m] & 1) al[W + Me + m] = 1;
-      if (Ts > 0 && wv == 0) {
-        int64_t upd = 0, ins = 0;
-        int all_used = 1, any_cnt = 0;
-        for (int m = lane; m < Ms; m += 64) {
-          const int f = L.sflag[m];
-          upd += f & 1;
-          ins += (f >> 1) & 1;
-          if (m < s.active_summary) {
-            if (!(L.used[Me + m] != 0 || (f & 1))) all_used = 0;
-            if (f & 1) any_cnt = 1;
-          }
-        }
-        for (int o = 32; o > 0; o >>= 1) {
-          upd += __shfl_xor(upd, o, 64);
-          ins += __shfl_xor(ins, o, 64);
-        }
-        all_used = wave_and(all_used);
-        any_cnt = wave_or(any_cnt);
-        if (lane == 0) {
-          if (s.metrics) {
-            atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, upd);
-            if (s.overwrite_on_insert) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, ins);
-          }
-          if (s.frustrated) {
-            if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
-            if (any_cnt) atomic_add_i64(s.frustrated + 2, 1);
-          }
-        }
-      }
-    }
-    __syncthreads();
-  }
-  // ---------------- ring write of the surviving block tokens (combined index i >= Lr)
+  uint8_t* al = s.allowed + (int64_t)b * Lbuf;
+  const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
+  auto blk_row = [&](const T* base, int jb) { return base + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl; };
+
+  // ---- ring-write sources (block tokens), loaded now
   const int Lr = g.ring_filled;
   const int first = max(Lr, g.n_ev);
   const int total = Lr + g.blk;
-  const int head = (Lr == W) ? g.ring_head : 0;
-  constexpr int CH = DH / 8;
-  for (int i = t; i < (total - first) * CH; i += 256) {
-    const int r = first + i / CH, c = i % CH;
-    const int slot = (head + r) % W;
-    const int jb = r - Lr;
-    const T* ks = kbk + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl;
-    const T* vs = vbk + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl;
-    if constexpr (sizeof(T) == 2) {
-      *reinterpret_cast<uint4*>(kb + (int64_t)slot * DH + 8 * c) = *reinterpret_cast<const uint4*>(ks + 8 * c);
-      *reinterpret_cast<uint4*>(vb + (int64_t)slot * DH + 8 * c) = *reinterpret_cast<const uint4*>(vs + 8 * c);
-    } else {
+  const int rhead = (Lr == W) ? g.ring_head : 0;
+  const int n_ring = (total - first) * CH;  // pieces of 8 elements per plane (K and V each)
+  Piece8<T> rk[kRingPre], rv[kRingPre];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        reinterpret_cast<float4*>(kb + (int64_t)slot * DH + 8 * c)[j] = reinterpret_cast<const float4*>(ks + 8 * c)[j];
-        reinterpret_cast<float4*>(vb + (int64_t)slot * DH + 8 * c)[j] = reinterpret_cast<const float4*>(vs + 8 * c)[j];
+  for (int u = 0; u < kRingPre; ++u) {
+    const int i = t + u * NT;
+    if (i < n_ring) {
+      const int jb = first + i / CH - Lr, c = i % CH;
+      rk[u] = ld8<T>(blk_row(kbk, jb) + 8 * c);
+      rv[u] = ld8<T>(blk_row(vbk, jb) + 8 * c);
+    }
+  }
+  auto ring_store = [&](int i, Piece8<T> xk, Piece8<T> xv) {
+    const int r = first + i / CH, c = i % CH;
+    const int slot = (rhead + r) % W;
+    st8<T>(kb + (int64_t)slot * DH + 8 * c, xk);
+    st8<T>(vb + (int64_t)slot * DH + 8 * c, xv);
+    if (lead && c == 0) {
+      s.g_recent[(int64_t)b * W + slot] = gb[(int64_t)b * g.g_sb + (r - Lr)];
+      al[slot] = 1;
+    }
+  };
+  auto ring_write = [&]() {
+#pragma unroll
+    for (int u = 0; u < kRingPre; ++u)
+      if (t + u * NT < n_ring) ring_store(t + u * NT, rk[u], rv[u]);
+    for (int i = t + kRingPre * NT; i < n_ring; i += NT) {
+      const int jb = first + i / CH - Lr, c = i % CH;
+      ring_store(i, ld8<T>(blk_row(kbk, jb) + 8 * c), ld8<T>(blk_row(vbk, jb) + 8 * c));
+    }
+  };
+  const bool evict = g.n_ev > 0 && (Te > 0 || Ts > 0);
+  if (!evict) {
+    ring_write();
+    return;
+  }
+  T* cst = reinterpret_cast<T*>(asm_);  // summary candidates [Ts][NCOL]
+  T* bst = reinterpret_cast<T*>(reinterpret_cast<char*>(cst) + apply_rows_bytes(Ts, DH, LF, sizeof(T)));  // [Ms][NCOL]
+  T* est = reinterpret_cast<T*>(reinterpret_cast<char*>(bst) + apply_rows_bytes(Ms, DH, LF, sizeof(T)));  // [Te][2 DH]
+  float* knew = reinterpret_cast<float*>(reinterpret_cast<char*>(est) + apply_erows_bytes(Te, DH, sizeof(T)));
+  int32_t* list = reinterpret_cast<int32_t*>(knew + (size_t)Ms * LF);  // [Ms][Ts]
+  int32_t* p = list + (size_t)Ms * Ts;
+  int32_t* idx_e = p; p += Te;
+  int32_t* fl_e = p; p += Te;
+  int32_t* eflag = p; p += Me;
+  int32_t* idx_s = p; p += Ts;
+  float* wtok = reinterpret_cast<float*>(p); p += Ts;
+  int32_t* used = p; p += Me + Ms;
+  float* cnt = reinterpret_cast<float*>(p); p += Ms;
+  int32_t* sflag = p; p += Ms;
+  int32_t* nlist = p; p += Ms;
+  int32_t* act_list = p; p += Ms;
+  int32_t* misc = p;
+  const Snap sn = snap_of(s, g, ws, b);
+  const Dec dc = dec_of(s, g, ws, b);
+  for (int i = t; i < Te; i += NT) { idx_e[i] = dc.idx_e[i]; fl_e[i] = dc.fl_e[i]; }
+  for (int i = t; i < Me; i += NT) eflag[i] = Te > 0 ? dc.eflag[i] : 0;
+  for (int i = t; i < Ts; i += NT) { idx_s[i] = dc.idx_s[i]; wtok[i] = dc.wtok[i]; }
+  for (int i = t; i < Me + Ms; i += NT) used[i] = sn.used[i];
+  for (int m = t; m < Ms; m += NT) nlist[m] = 0;
+  // every row this workgroup reads goes to LDS in one pass, 8 pieces per
+  // thread in flight: summary candidates (V, then K's LF band), the
+  // summary bank rows of head h, the exact candidates (K, then V)
+  {
+    const int n_c = Ts * CPR, n_b = Ts > 0 ? Ms * CPR : 0, n_e = Te * 2 * CH;
+    const int n_all = n_c + n_b + n_e;
+    for (int base = t; base < n_all; base += 8 * NT) {
+      Piece8<T> xp[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * NT;
+        if (i < n_c) {
+          const int r = i / CPR, c8 = (i % CPR) * 8;
+          const bool is_v = c8 < DH;
+          xp[u] = ld8<T>(cand_row<T, DH>(s, g, is_v ? vbk : kbk, b, h, pc[r], is_v) + (is_v ? c8 : lf + (c8 - DH)));
+        } else if (i < n_c + n_b) {
+          const int ii = i - n_c, r = ii / CPR, c8 = (ii % CPR) * 8;
+          xp[u] = ld8<T>(c8 < DH ? vb + (int64_t)(W + Me + r) * DH + c8 : kb + (int64_t)(W + Me + r) * DH + lf + (c8 - DH));
+        } else if (i < n_all) {
+          const int ii = i - n_c - n_b, r = ii / (2 * CH), c = ii % (2 * CH);
+          const bool is_v = c >= CH;
+          xp[u] = ld8<T>(cand_row<T, DH>(s, g, is_v ? vbk : kbk, b, h, pc[r], is_v) + 8 * (c % CH));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int i = base + u * NT;
+        if (i < n_c) st8<T>(cst + (size_t)i * 8, xp[u]);
+        else if (i < n_c + n_b) st8<T>(bst + (size_t)(i - n_c) * 8, xp[u]);
+        else if (i < n_all) st8<T>(est + (size_t)(i - n_c - n_b) * 8, xp[u]);
       }
     }
-    if (lead && c == 0) {
-      s.g_recent[(int64_t)b * W + slot] = gb[(int64_t)b * g.g_sb + jb];
-      al[slot] = 1;
+  }
+  __syncthreads();
+  // every evicted ring row of this head is in LDS now: the ring write can go
+  ring_write();
+  // ---- per summary slot: its tokens in order (list), count (fp32 in token
+  // order; adding 0 for other slots' tokens leaves the sum unchanged) and
+  // flags; tokens read 16 at a time (same address across threads)
+  for (int m = t; m < Ms; m += NT) {
+    float c = 0.f;
+    int k = 0;
+    for (int t0 = 0; t0 < Ts; t0 += 16) {
+      int iv[16];
+      float wv16[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int tt = min(t0 + u, Ts - 1);
+        iv[u] = t0 + u < Ts ? idx_s[tt] : -1;
+        wv16[u] = wtok[tt];
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const bool on = iv[u] == m;
+        c += on ? wv16[u] : 0.f;
+        if (on) list[m * Ts + k] = t0 + u;
+        k += on ? 1 : 0;
+      }
+    }
+    nlist[m] = k;
+    cnt[m] = E::rnd(c);
+    const bool active = cnt[m] > 0.f;
+    sflag[m] = (active ? 1 : 0) | ((active && used[Me + m] == 0) ? 2 : 0);
+  }
+  // ---- exact write-back of head h (memory_banks.py:707-742): one wave per
+  // written slot, candidates from LDS, deltas summed in token order
+  if (Te > 0) {
+    for (int m = wv; m < Me; m += NW) {
+      if (!eflag[m]) continue;
+      T* kr = kb + (int64_t)(W + m) * DH;
+      T* vr = vb + (int64_t)(W + m) * DH;
+      float mk[NV], mv[NV], ak[NV], av[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int d = min(lane + 64 * i, DH - 1);
+        mk[i] = E::ld(kr[d]);
+        mv[i] = E::ld(vr[d]);
+        ak[i] = 0.f;
+        av[i] = 0.f;
+      }
+      for (int tt = 0; tt < Te; ++tt) {
+        if (idx_e[tt] != m || !(fl_e[tt] & 1)) continue;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int d = min(lane + 64 * i, DH - 1);
+          ak[i] += E::rnd(E::ld(est[(size_t)tt * 2 * DH + d]) - mk[i]);
+          av[i] += E::rnd(E::ld(est[(size_t)tt * 2 * DH + DH + d]) - mv[i]);
+        }
+      }
+      float nv[NV];
+      bool act[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int d = lane + 64 * i;
+        act[i] = d < DH;
+        nv[i] = 0.f;
+        if (act[i]) {
+          kr[d] = E::st(mk[i] + E::rnd(ak[i]));
+          nv[i] = E::rnd(mv[i] + E::rnd(av[i]));
+          vr[d] = E::st(nv[i]);
+        }
+      }
+      wave_unit<T, NV>(nv, act);
+      T* nr = (T*)s.exact_v_norm + (((int64_t)b * Hkv + h) * Me + m) * DH;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) nr[lane + 64 * i] = E::st(nv[i]);
+    }
+  }
+  if (Ts > 0) {
+    __syncthreads();
+    // active slots, compacted in slot order by wave 0 (ballot prefix counts)
+    if (wv == 0) {
+      int na = 0;
+      for (int m0 = 0; m0 < Ms; m0 += 64) {
+        const int m = m0 + lane;
+        const bool on = m < Ms && (sflag[m] & 1);
+        const uint64_t bal = __ballot(on);
+        if (on) act_list[na + __popcll(bal & ((1ull << lane) - 1ull))] = m;
+        na += __popcll(bal);
+      }
+      if (lane == 0) misc[0] = na;
+    }
+    __syncthreads();
+    // ---- accumulate + EMA: thread (group q, channel col) takes the active
+    // slots q, q + NG, ...; 8 slots at a time, their metadata and the
+    // values of their first token read before any arithmetic; further
+    // tokens of a slot (rare) follow in token order (fp32 sum)
+    const int n_act = misc[0];
+    const float eta_h = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
+    constexpr int NG = kApplyThreads / NCOL, SB = 8;
+    const int q = t / NCOL, col = t % NCOL;
+    if (q < NG) {
+      const bool is_v = col < DH;
+      const int d = is_v ? col : lf + (col - DH);
+      T* rbase = (is_v ? vb : kb) + (int64_t)(W + Me) * DH + d;
+      for (int a0 = q; a0 < n_act; a0 += NG * SB) {
+        int mm[SB], nk[SB], fl[SB], t0[SB];
+        float cn[SB];
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+          const int ai = min(a0 + NG * j, n_act - 1);
+          mm[j] = act_list[ai];
+        }
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+          nk[j] = nlist[mm[j]];
+          fl[j] = sflag[mm[j]];
+          cn[j] = cnt[mm[j]];
+          t0[j] = list[mm[j] * Ts];
+        }
+        float x0[SB], w0[SB], mem[SB];
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+          x0[j] = E::ld(cst[(size_t)t0[j] * NCOL + col]);
+          w0[j] = wtok[t0[j]];
+          mem[j] = E::ld(bst[(size_t)mm[j] * NCOL + col]);
+        }
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+          if (a0 + NG * j >= n_act) break;
+          const int m = mm[j];
+          float a = E::rnd(x0[j] * w0[j]);
+          for (int k = 1; k < nk[j]; ++k) {
+            const int tt = list[m * Ts + k];
+            a += E::rnd(E::ld(cst[(size_t)tt * NCOL + col]) * wtok[tt]);
+          }
+          const float eta = (s.overwrite_on_insert && (fl[j] & 2)) ? 1.f : eta_h;
+          const float avg = E::rnd(E::rnd(a) / fmaxf(cn[j], eps_r<T>()));
+          if (is_v) {
+            rbase[(int64_t)m * DH] = E::st(mem[j] + E::rnd(eta * E::rnd(avg - mem[j])));
+          } else {
+            const float dk = E::rnd(E::rnd(avg * s.energy_scale) - mem[j]);
+            const float nkv = E::rnd(mem[j] + E::rnd(eta * dk));
+            rbase[(int64_t)m * DH] = E::st(nkv);
+            knew[m * LF + (col - DH)] = nkv;  // new LF key for the norm cache
+          }
+        }
+      }
+    }
+    __syncthreads();
+    for (int ai = wv; ai < n_act; ai += NW) {
+      const int m = act_list[ai];
+      float x[NV];
+      bool act[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int dd = lane + 64 * i;
+        act[i] = dd < LF;
+        x[i] = act[i] ? knew[m * LF + dd] : 0.f;
+      }
+      wave_unit<T, NV>(x, act);
+      T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + m) * LF;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) nr[lane + 64 * i] = E::st(x[i]);
+    }
+  }
+  // ---- per-sequence metadata (lead workgroup)
+  if (lead) {
+    for (int m = t; m < Me; m += NT)
+      if (eflag[m]) al[W + m] = 1;
+    for (int m = t; m < Ms; m += NT)
+      if (Ts > 0 && (sflag[m] & 1)) al[W + Me + m] = 1;
+    if (Ts > 0 && wv == 0) {
+      int64_t upd = 0, ins = 0;
+      int all_used = 1, any_cnt = 0;
+      for (int m = lane; m < Ms; m += 64) {
+        const int f = sflag[m];
+        upd += f & 1;
+        ins += (f >> 1) & 1;
+        if (m < s.active_summary) {
+          if (!(used[Me + m] != 0 || (f & 1))) all_used = 0;
+          if (f & 1) any_cnt = 1;
+        }
+      }
+      for (int o = 32; o > 0; o >>= 1) {
+        upd += __shfl_xor(upd, o, 64);
+        ins += __shfl_xor(ins, o, 64);
+      }
+      all_used = wave_and(all_used);
+      any_cnt = wave_or(any_cnt);
+      if (lane == 0) {
+        if (s.metrics) {
+          atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, upd);
+          if (s.overwrite_on_insert) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, ins);
+        }
+        if (s.frustrated) {
+          if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
+          if (any_cnt) atomic_add_i64(s.frustrated + 2, 1);
+        }
+      }
     }
   }
 }
@@ -1115,8 +1382,8 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
   const int LF = DH - s->lf;
   const int TT = g.Te > g.Ts ? g.Te : g.Ts;
   if (g.n_ev > 0 && TT > 0) {
-    const size_t lds1 = std::max(std::max(sizeof(float) * (size_t)(s->Me + g.Te) * (DH + 4),
-                                          sizeof(float) * (size_t)(s->Ms + g.Ts) * (LF + 4)),
+    const size_t lds1 = std::max(sizeof(float) * ((g.Te > 0 ? (size_t)(s->Me + g.Te) * (DH + 4) : 0) +
+                                                  (g.Ts > 0 ? (size_t)(s->Ms + g.Ts) * (LF + 4) : 0)),
                                  sizeof(sel::Item<int64_t>) * (size_t)s->Me);
     int rc = ensure_lds(block_route_kernel<T, DH>, lds1, "coda_block_write");
     if (rc) return rc;
@@ -1125,13 +1392,23 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
     rc = check_launch("block_route");
     if (rc) return rc;
   }
-  const size_t lds2 = sizeof(float) * (upd_big_words(s->Me, s->Ms, g.Te, g.Ts, DH, LF) +
-                                       upd_small_words(s->Me, s->Ms, TT));
-  int rc = ensure_lds(block_update_kernel<T, DH>, lds2, "coda_block_write");
+  const int nsc = (g.Ts + kDecideChunk - 1) / kDecideChunk;
+  if (g.n_ev > 0 && TT > 0) {
+    const size_t lds_d = std::max(sizeof(float) * ((size_t)s->Hkv * g.Te * s->Me + (size_t)g.Te * s->Me) +
+                                      sizeof(int) * ((size_t)s->Me + 2 * g.Te),
+                                  sizeof(float) * (size_t)s->Hkv * kDecideChunk * s->Ms);
+    int rc = ensure_lds(block_decide_kernel<T>, lds_d, "coda_block_write");
+    if (rc) return rc;
+    hipLaunchKernelGGL((block_decide_kernel<T>), dim3(1 + nsc, s->B), dim3(256), lds_d, st, *s, g, plan_c, ws);
+    rc = check_launch("block_decide");
+    if (rc) return rc;
+  }
+  const size_t lds_a = apply_lds_bytes(s->Me, s->Ms, g.Te, g.Ts, DH, LF, (int)sizeof(T));
+  int rc = ensure_lds(block_apply_kernel<T, DH>, lds_a, "coda_block_write");
   if (rc) return rc;
-  hipLaunchKernelGGL((block_update_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(256), lds2, st, *s, g, (const T*)kb,
-                     (const T*)vb, gb, plan_c, ws);
-  return check_launch("block_update");
+  hipLaunchKernelGGL((block_apply_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(kApplyThreads), lds_a, st, *s, g,
+                     (const T*)kb, (const T*)vb, gb, plan_c, ws);
+  return check_launch("block_apply");
 }
 
 extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb, int64_t b_sh,
