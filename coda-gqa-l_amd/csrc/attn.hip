@@ -824,6 +824,9 @@ __global__ __launch_bounds__(NW * 64) void attn_tile_bf16(const coda_attn_desc a
 #pragma unroll
     for (int i = 0; i < NM; ++i) o[s][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // visibility bytes of the prefix (the host guarantees Lp <= kMaxRowsPrefix)
+  __shared__ uint8_t al_lds[kMaxRowsPrefix];
+  for (int i = tid; i < a.Lp; i += NW * 64) al_lds[i] = a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1;
   const int Lk = a.Lp + a.Lb;
   // last key any query of this workgroup can see
   const int qlast = min(a.Lq - 1, qb * 16 * NQ + 16 * NQ - 1);
@@ -869,7 +872,12 @@ __global__ __launch_bounds__(NW * 64) void attn_tile_bf16(const coda_attn_desc a
       }
       bool vis[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) vis[j] = key_visible(a, b, qrow, kt + 4 * g4 + j);
+      for (int j = 0; j < 4; ++j) {
+        const int kidx = kt + 4 * g4 + j;
+        const int jb = kidx - a.Lp;
+        vis[j] = kidx < a.Lp ? al_lds[kidx] != 0
+                             : (jb < a.Lb && (!a.causal || jb <= qrow + (a.causal == 2 ? 0 : a.Lb - a.Lq)));
+      }
       short4_t pf[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
@@ -925,6 +933,429 @@ __global__ __launch_bounds__(NW * 64) void attn_tile_bf16(const coda_attn_desc a
     }
   const float lam = qlive ? bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + qrow * a.lam_sl]) : 0.f;
   diff_norm<bf16_t, NV>(y, os, on, act, lam, (const bf16_t*)a.rms_w, dd, a.eps, DH, false, 16, 32);
+  if (qlive) {
+    bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt) {
+      uint2 u;
+      u.x = (uint32_t)f2bf(y[mt * 4 + 0]) | ((uint32_t)f2bf(y[mt * 4 + 1]) << 16);
+      u.y = (uint32_t)f2bf(y[mt * 4 + 2]) | ((uint32_t)f2bf(y[mt * 4 + 3]) << 16);
+      *reinterpret_cast<uint2*>(orow_p + 16 * mt + 4 * g4) = u;
+    }
+  }
+}
+
+// ------------------------------------------------------------ prefill flash tiles
+// attn_fa_bf16: the MFMA path for prefill chunks and unbounded causal
+// attention.  Workgroup = (query block, KV head, batch) as attn_tile_bf16;
+// wave w owns head g = w / NQ and 16 queries (both streams).  Per 64-key
+// tile, double-buffered:
+//   K: loaded straight into LDS (global_load_lds, 16 bytes a lane) in MFMA
+//      fragment order: the 1 KiB chunk (sub-tile st of 16 keys, channel
+//      block c of 32) holds, at lane l = n + 16 g4, K[16 st + n][32 c +
+//      8 g4 .. + 8), so the A fragment of S^T = K Q^T is one contiguous
+//      16-byte LDS read per lane;
+//   V: loaded into registers one tile ahead and written transposed: per
+//      pair of sub-tiles (32 keys), key group g and channel m, 16 bytes =
+//      V[4g .. 4g+3][m] of the pair's first sub-tile then of its second,
+//      which is the A fragment of the k=32 PV MFMA whose B fragment is the
+//      S^T output of the two sub-tiles (keys 4 g4 .. +3 of each).
+// Online softmax per stream with a lazy rescale: the running max moves
+// (and O is rescaled) only when a row's new max exceeds it by more than
+// 2^8, so most tiles skip the rescale; P is rounded to bf16 by the
+// hardware conversion before the PV MFMA and summed as rounded.
+template <int DH>
+struct FaLayout {
+  static constexpr int KT = 64, NST = 4, NC = DH / 32, NM = DH / 16;
+  static constexpr int KBYTES = NST * NC * 1024;
+  static constexpr int GB = DH * 16 + 16;  // key-group stride, padded
+  static constexpr int PB = 4 * GB;        // pair stride
+  static constexpr int VBYTES = 2 * PB;
+  static constexpr int LDS = 2 * KBYTES + 2 * VBYTES;
+};
+
+// 16 bytes per lane global -> LDS (direct load): lane l's bytes land at
+// lds + 16 l (lds wave-uniform); counted in vmcnt
+__device__ __forceinline__ void lds_load16(const void* gsrc, void* lds) {
+  __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// v_exp_f32 (2^x; -inf -> 0)
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t v;
+  v[0] = (__bf16)a;
+  v[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& u, float x[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = bf2f((bf16_t)(w[j] & 0xffffu));
+    x[2 * j + 1] = bf2f((bf16_t)(w[j] >> 16));
+  }
+}
+__device__ __forceinline__ void unpack4(const uint2& u, float x[4]) {
+  x[0] = bf2f((bf16_t)(u.x & 0xffffu));
+  x[1] = bf2f((bf16_t)(u.x >> 16));
+  x[2] = bf2f((bf16_t)(u.y & 0xffffu));
+  x[3] = bf2f((bf16_t)(u.y >> 16));
+}
+
+template <int DH, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_fa_bf16(const coda_attn_desc a, int NQ, int nqb,
+                                                                          int npairs) {
+  using Lay = FaLayout<DH>;
+  constexpr int KT = Lay::KT, NC = Lay::NC, NM = Lay::NM, DCH = DH / 8;
+  constexpr int KCH = Lay::NST * NC;        // K chunks per tile
+  constexpr int KCW = (KCH + NW - 1) / NW;  // per wave
+  extern __shared__ __attribute__((aligned(16))) char fa_smem[];
+  __shared__ uint8_t al_lds[kMaxRowsPrefix];
+  __shared__ uint8_t al32[kMaxRowsPrefix / 32];
+  __shared__ float w_lds[DH];
+  char* kbuf = fa_smem;
+  char* vbuf = fa_smem + 2 * Lay::KBYTES;
+
+  // block -> (query block, KV head, sequence); with a multiple of 8 pairs
+  // the query blocks of one (sequence, KV head) share an XCD (dispatch is
+  // round robin over the 8 XCDs), so its K/V stay in that XCD's L2
+  const int id = blockIdx.x;
+  int qb, pair;
+  if (npairs % 8 == 0) {
+    const int local = id >> 3;
+    pair = (id & 7) + 8 * (local / nqb);
+    qb = local % nqb;
+  } else {
+    pair = id / nqb;
+    qb = id % nqb;
+  }
+  const int hk = pair % a.Hkv, b = pair / a.Hkv;
+  const int G = a.H / a.Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g4 = lane >> 4;
+  const int g = wv / NQ, qsub = wv % NQ, h = hk * G + g;
+  const int q0 = qb * 16 * NQ + 16 * qsub;
+  const int qrow = q0 + n;
+  const bool qlive = qrow < a.Lq;
+  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
+  const int Lk = a.Lp + a.Lb;
+  const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
+  const int q_hi = min(a.Lq - 1, qb * 16 * NQ + 16 * NQ - 1);
+  const int klim = a.causal ? min(Lk, a.Lp + q_hi + coff + 1) : Lk;
+  const int ntile = (klim + KT - 1) / KT;
+  const int wq_hi = min(a.Lq - 1, q0 + 15);
+  const int wklim = a.causal ? min(Lk, a.Lp + wq_hi + coff + 1) : Lk;
+
+  const bf16_t* kpb = a.Lp > 0 ? (const bf16_t*)a.kp + b * a.p_sb + hk * a.p_sh : nullptr;
+  const bf16_t* vpb = a.Lp > 0 ? (const bf16_t*)a.vp + b * a.p_sb + hk * a.p_sh : nullptr;
+  const bf16_t* kbb = a.Lb > 0 ? (const bf16_t*)a.kb + b * a.b_sb + hk * a.b_sh : nullptr;
+  const bf16_t* vbb = a.Lb > 0 ? (const bf16_t*)a.vb + b * a.b_sb + hk * a.b_sh : nullptr;
+  auto krow = [&](int kidx) {
+    return kidx < a.Lp ? kpb + (int64_t)kidx * a.p_sl : kbb + (int64_t)(kidx - a.Lp) * a.b_sl;
+  };
+  auto vrow = [&](int kidx) {
+    return kidx < a.Lp ? vpb + (int64_t)kidx * a.p_sl : vbb + (int64_t)(kidx - a.Lp) * a.b_sl;
+  };
+
+  // K chunks of a tile: straight to LDS buffer bi (keys past Lk read key 0,
+  // a valid row, and are masked)
+  auto kload = [&](int kt0, int bi) {
+#pragma unroll
+    for (int j = 0; j < KCW; ++j) {
+      const int ci = wv + NW * j;
+      if (ci < KCH) {
+        const int st = ci / NC, c = ci % NC;
+        int kidx = kt0 + 16 * st + n;
+        kidx = kidx < Lk ? kidx : 0;
+        lds_load16(krow(kidx) + 32 * c + 8 * g4, kbuf + bi * Lay::KBYTES + ci * 1024);
+      }
+    }
+  };
+  // V rows of a tile into registers (thread: 4 keys x 8 channels)
+  const bool vth = tid < 16 * DCH;
+  const int vkg = tid / DCH, vdc = tid % DCH;
+  uint4 vr[4];
+  auto vload = [&](int kt0) {
+    if (vth) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int kidx = kt0 + 4 * vkg + jj;
+        vr[jj] = kidx < Lk ? *reinterpret_cast<const uint4*>(vrow(kidx) + 8 * vdc) : uint4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto vstore = [&](int bi) {
+    if (vth) {
+      const int st = vkg >> 2, gg = vkg & 3;
+      char* base = vbuf + bi * Lay::VBYTES + (st >> 1) * Lay::PB + gg * Lay::GB + (st & 1) * 8 + 8 * vdc * 16;
+      const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
+      const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+      const uint32_t w2[4] = {vr[2].x, vr[2].y, vr[2].z, vr[2].w};
+      const uint32_t w3[4] = {vr[3].x, vr[3].y, vr[3].z, vr[3].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int sh = (e & 1) * 16, wi = e >> 1;
+        uint2 cell;
+        cell.x = ((w0[wi] >> sh) & 0xffffu) | (((w1[wi] >> sh) & 0xffffu) << 16);
+        cell.y = ((w2[wi] >> sh) & 0xffffu) | (((w3[wi] >> sh) & 0xffffu) << 16);
+        *reinterpret_cast<uint2*>(base + e * 16) = cell;
+      }
+    }
+  };
+  if (ntile > 0) {
+    kload(0, 0);
+    vload(0);
+  }
+
+  // ---- queries of this lane (row qrow, channels 32 c + 8 g4 .. + 8), both
+  // streams; every load first, then the eager-op rounding of RoPE and of
+  // the noise rotation (primitives.py:58-113)
+  bf16x8_t qf[2][NC];
+  float lam = 0.f;
+  {
+    using E = Elt<bf16_t>;
+    constexpr int half = DH / 2;
+    const int qi = qlive ? qrow : 0;
+    const bf16_t* qr = (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
+    const bool rope = a.rope_cos != nullptr, inter = a.rope_interleaved != 0;
+    const bool given_noise = a.q_noise != nullptr;
+    const bf16_t* csr = rope ? (const bf16_t*)a.rope_cos + (int64_t)qi * half : nullptr;
+    const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
+    uint4 uq[NC], up[NC], un[NC], rc[NC], rs[NC];
+    uint2 rc2[NC], rs2[NC], tcs[NC], tsn[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d0 = 32 * c + 8 * g4;
+      uq[c] = *reinterpret_cast<const uint4*>(qr + d0);
+      if (rope && inter) {
+        rc2[c] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
+        rs2[c] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
+      }
+      if (rope && !inter) {
+        const int f0 = d0 < half ? d0 : d0 - half;
+        up[c] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
+        rc[c] = *reinterpret_cast<const uint4*>(csr + f0);
+        rs[c] = *reinterpret_cast<const uint4*>(snr + f0);
+      }
+      if (given_noise) {
+        un[c] = *reinterpret_cast<const uint4*>((const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh +
+                                                (int64_t)qi * a.qn_sl + d0);
+      } else {
+        tcs[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_cos + (int64_t)h * half + d0 / 2);
+        tsn[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_sin + (int64_t)h * half + d0 / 2);
+      }
+    }
+    lam = bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl]);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d0 = 32 * c + 8 * g4;
+      float x[8];
+      unpack8(uq[c], x);
+      if (rope && inter) {
+        // pairs (2p, 2p+1) rotated by angle d0/2 + p
+        float cc[4], ss[4];
+        unpack4(rc2[c], cc);
+        unpack4(rs2[c], ss);
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const float e = x[2 * pp], o = x[2 * pp + 1];
+          x[2 * pp] = E::rnd(E::rnd(e * cc[pp]) - E::rnd(o * ss[pp]));
+          x[2 * pp + 1] = E::rnd(E::rnd(e * ss[pp]) + E::rnd(o * cc[pp]));
+        }
+      }
+      if (rope && !inter) {
+        // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin
+        float cc[8], ss[8], y[8];
+        unpack8(rc[c], cc);
+        unpack8(rs[c], ss);
+        unpack8(up[c], y);
+        const bool lo = d0 < half;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float rot = lo ? -y[j] : y[j];
+          x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rot * ss[j]));
+        }
+      }
+      uint4 u;
+      u.x = pk_bf16(x[0], x[1]);
+      u.y = pk_bf16(x[2], x[3]);
+      u.z = pk_bf16(x[4], x[5]);
+      u.w = pk_bf16(x[6], x[7]);
+      qf[0][c] = __builtin_bit_cast(bf16x8_t, qlive ? u : uint4{0, 0, 0, 0});
+      if (given_noise) {
+        qf[1][c] = __builtin_bit_cast(bf16x8_t, qlive ? un[c] : uint4{0, 0, 0, 0});
+      } else {
+        float tc[4], ts[4], y[8];
+        unpack4(tcs[c], tc);
+        unpack4(tsn[c], ts);
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const float e = x[2 * pp], o = x[2 * pp + 1];
+          y[2 * pp] = E::rnd(E::rnd(e * tc[pp]) - E::rnd(o * ts[pp]));
+          y[2 * pp + 1] = E::rnd(E::rnd(e * ts[pp]) + E::rnd(o * tc[pp]));
+        }
+        uint4 v;
+        v.x = pk_bf16(y[0], y[1]);
+        v.y = pk_bf16(y[2], y[3]);
+        v.z = pk_bf16(y[4], y[5]);
+        v.w = pk_bf16(y[6], y[7]);
+        qf[1][c] = __builtin_bit_cast(bf16x8_t, qlive ? v : uint4{0, 0, 0, 0});
+      }
+    }
+  }
+  // visibility bytes of the prefix, per-32-key "all visible" flags, norm weight
+  for (int i = tid; i < a.Lp; i += NW * 64) al_lds[i] = a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1;
+  if (tid < DH) w_lds[tid] = a.rms_w ? bf2f(((const bf16_t*)a.rms_w)[tid]) : 1.f;
+  __syncthreads();
+  for (int i = tid; i < (a.Lp + 31) / 32; i += NW * 64) {
+    int all = 32 * i + 32 <= a.Lp;
+    for (int j = 0; j < 32 && all; ++j) all = al_lds[32 * i + j] != 0;
+    al32[i] = (uint8_t)all;
+  }
+  if (ntile > 0) vstore(0);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile 0's direct LDS loads have landed
+  __syncthreads();
+
+  float m_s[2] = {-INFINITY, -INFINITY}, l_s[2] = {0.f, 0.f};
+  f32x4 o[2][NM];
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int i = 0; i < NM; ++i) o[s][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int it = 0; it < ntile; ++it) {
+    const int bi = it & 1, kt0 = it * KT;
+    if (it + 1 < ntile) {
+      kload(kt0 + KT, bi ^ 1);
+      vload(kt0 + KT);
+    }
+    const char* kb_t = kbuf + bi * Lay::KBYTES;
+    const char* vb_t = vbuf + bi * Lay::VBYTES;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int pk0 = kt0 + 32 * p;
+      if (pk0 >= wklim) break;
+      f32x4 sa[2][2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub) sa[s][sub] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const bf16x8_t kf = __builtin_bit_cast(
+              bf16x8_t, *reinterpret_cast<const uint4*>(kb_t + ((2 * p + sub) * NC + c) * 1024 + 16 * lane));
+          sa[0][sub] = mfma_k32(kf, qf[0][c], sa[0][sub]);
+          sa[1][sub] = mfma_k32(kf, qf[1][c], sa[1][sub]);
+        }
+      // masks only where a key of the pair may be hidden from a query of this wave
+      const bool need_mask = (pk0 + 32 > Lk) || (pk0 < a.Lp && !al32[pk0 >> 5]) ||
+                             (pk0 + 32 > a.Lp && a.causal && (pk0 + 31 - a.Lp) > q0 + coff);
+      if (need_mask) {
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // branch-free: the visibility byte is read at a clamped index
+            const int kidx = pk0 + 16 * sub + 4 * g4 + j;
+            const int jb = kidx - a.Lp;
+            const bool pre = kidx < a.Lp;
+            const bool al_ok = al_lds[pre ? kidx : 0] != 0;
+            const bool blk_ok = (jb < a.Lb) & ((a.causal == 0) | (jb <= qrow + coff));
+            const bool vis = pre ? al_ok : blk_ok;
+            sa[0][sub][j] = vis ? sa[0][sub][j] : -INFINITY;
+            sa[1][sub][j] = vis ? sa[1][sub][j] : -INFINITY;
+          }
+      }
+      uint4 pb[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        float tmax = -INFINITY;
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, sa[s][sub][j]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        const float tsc = tmax * scale;
+        if (__ballot(tsc > m_s[s] + 8.f)) {
+          const float mnew = fmaxf(m_s[s], tsc);
+          const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s[s] - mnew);
+#pragma unroll
+          for (int i = 0; i < NM; ++i) o[s][i] *= alpha;
+          l_s[s] *= alpha;
+          m_s[s] = mnew;
+        }
+        const float mu = m_s[s] == -INFINITY ? 0.f : m_s[s];
+        float pr[2][4];
+#pragma unroll
+        for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pr[sub][j] = fast_exp2(fmaf(sa[s][sub][j], scale, -mu));
+        pb[s].x = pk_bf16(pr[0][0], pr[0][1]);
+        pb[s].y = pk_bf16(pr[0][2], pr[0][3]);
+        pb[s].z = pk_bf16(pr[1][0], pr[1][1]);
+        pb[s].w = pk_bf16(pr[1][2], pr[1][3]);
+        float pf[8];
+        unpack8(pb[s], pf);
+        float ps = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ps += pf[k];
+        l_s[s] += ps;
+      }
+      const bf16x8_t pf0 = __builtin_bit_cast(bf16x8_t, pb[0]), pf1 = __builtin_bit_cast(bf16x8_t, pb[1]);
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) {
+        const bf16x8_t vf = __builtin_bit_cast(
+            bf16x8_t, *reinterpret_cast<const uint4*>(vb_t + p * Lay::PB + g4 * Lay::GB + (16 * mt + n) * 16));
+        o[0][mt] = mfma_k32(vf, pf0, o[0][mt]);
+        o[1][mt] = mfma_k32(vf, pf1, o[1][mt]);
+      }
+    }
+    if (it + 1 < ntile) vstore(bi ^ 1);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the next tile's direct LDS loads have landed
+    __syncthreads();
+  }
+  // ---- epilogue: lane holds channels 16 mt + 4 g4 + j of row n
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    l_s[s] += __shfl_xor(l_s[s], 16, 64);
+    l_s[s] += __shfl_xor(l_s[s], 32, 64);
+  }
+  constexpr int NV = NM * 4;
+  float y[NV];
+  {
+    using E = Elt<bf16_t>;
+    float sq = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = mt * 4 + j;
+        const float os = l_s[0] > 0.f ? o[0][mt][j] / l_s[0] : 0.f;
+        const float on = l_s[1] > 0.f ? o[1][mt][j] / l_s[1] : 0.f;
+        y[i] = E::rnd(E::rnd(os) - E::rnd(lam * E::rnd(on)));
+        sq += E::rnd(y[i] * y[i]);
+      }
+    if (a.rms_w) {
+      sq += __shfl_xor(sq, 16, 64);
+      sq += __shfl_xor(sq, 32, 64);
+      const float ms = E::rnd(sq / (float)DH);
+      const float r = E::rnd(1.0f / sqrtf(E::rnd(ms + E::rnd(a.eps))));
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = mt * 4 + j;
+          y[i] = E::rnd(E::rnd(y[i] * r) * w_lds[16 * mt + 4 * g4 + j]);
+        }
+    }
+  }
   if (qlive) {
     bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
 #pragma unroll
@@ -1001,6 +1432,26 @@ extern "C" int coda_attn_workspace_bytes(const coda_attn_desc* d, size_t* bytes)
   return CODA_OK;
 }
 
+// flash tiles (MFMA k=32 for both products, K straight to LDS)
+template <int DH, int NW>
+static int launch_fa_nw(const coda_attn_desc* d, hipStream_t st, int NQ, int nblk) {
+  const int npairs = d->B * d->Hkv;
+  const size_t lds = FaLayout<DH>::LDS;
+  hipError_t e = hipFuncSetAttribute((const void*)attn_fa_bf16<DH, NW>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)lds);
+  if (e != hipSuccess) return fail(CODA_EHIP, "coda_diff_attn_fwd: LDS attribute: %s", hipGetErrorString(e));
+  hipLaunchKernelGGL((attn_fa_bf16<DH, NW>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk, npairs);
+  return check_launch("attn_fa_bf16");
+}
+template <int DH>
+static int launch_fa(const coda_attn_desc* d, hipStream_t st, int G, int NQ, int nblk) {
+  if constexpr (DH >= 64) {
+    return G == 8 ? launch_fa_nw<DH, 8>(d, st, NQ, nblk) : launch_fa_nw<DH, 4>(d, st, NQ, nblk);
+  } else {
+    return fail(CODA_EUNSUP, "coda_diff_attn_fwd: flash tiles need head_dim >= 64");
+  }
+}
+
 template <int DH>
 static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
   const int G = d->H / d->Hkv;
@@ -1029,6 +1480,7 @@ static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
   }
   int NQ = G >= 4 ? 1 : 4 / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
+  if (DH >= 64 && (G == 8 || G == 4 || G == 2 || G == 1)) return launch_fa<DH>(d, st, G, NQ, nblk);
   if (G == 8) {
     hipLaunchKernelGGL((attn_tile_bf16<DH, 8>), dim3(nblk, d->Hkv, d->B), dim3(512), 0, st, *d, NQ);
   } else if (G == 4 || G == 2 || G == 1) {

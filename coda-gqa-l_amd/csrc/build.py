@@ -28,6 +28,10 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          # no implicit multiply-add fusion: the reference rounds every product
          # before the add; accumulations that want FMA call fmaf explicitly
          "-ffp-contract=off",
+         # MFMA accumulators in ordinary VGPRs: the online-softmax rescale and
+         # the epilogue read them with VALU instructions, which cannot address
+         # AGPRs (every access would be a copy)
+         "-mllvm", "-amdgpu-mfma-vgpr-form",
          "-Wno-unused-result"]
 
 
