@@ -947,37 +947,78 @@ __global__ __launch_bounds__(NW * 64) void attn_tile_bf16(const coda_attn_desc a
 
 // ------------------------------------------------------------ prefill flash tiles
 // attn_fa_bf16: the MFMA path for prefill chunks and unbounded causal
-// attention.  Workgroup = (query block, KV head, batch) as attn_tile_bf16;
-// wave w owns head g = w / NQ and 16 queries (both streams).  Per 64-key
-// tile, double-buffered:
-//   K: loaded straight into LDS (global_load_lds, 16 bytes a lane) in MFMA
-//      fragment order: the 1 KiB chunk (sub-tile st of 16 keys, channel
-//      block c of 32) holds, at lane l = n + 16 g4, K[16 st + n][32 c +
-//      8 g4 .. + 8), so the A fragment of S^T = K Q^T is one contiguous
-//      16-byte LDS read per lane;
-//   V: loaded into registers one tile ahead and written transposed: per
-//      pair of sub-tiles (32 keys), key group g and channel m, 16 bytes =
-//      V[4g .. 4g+3][m] of the pair's first sub-tile then of its second,
-//      which is the A fragment of the k=32 PV MFMA whose B fragment is the
-//      S^T output of the two sub-tiles (keys 4 g4 .. +3 of each).
+// attention.  Workgroup = (query block, KV head, sequence); wave w owns head
+// g = w / NQ and 16 queries (both streams), so one K/V tile in LDS serves
+// the G heads that share the KV head.  Per 64-key tile, double-buffered,
+// both operands go straight from global memory to LDS (global_load_lds, 16
+// bytes a lane, no register transit):
+//   K in MFMA fragment order: the 1 KiB chunk (sub-tile st of 16 keys,
+//     channel block c of 32) holds, at lane l = n + 16 g4, K[16 st + n][32 c
+//     + 8 g4 .. + 8), so the A fragment of S^T = K Q^T is one contiguous
+//     16-byte read per lane;
+//   V row-major (one key a row) with the 16-byte chunks of row k permuted
+//     by XOR with vswz(k); the A fragment of the k=32 PV MFMA (V^T, keys
+//     4 g4 .. +3 of each of the pair's two 16-key sub-tiles, matching the
+//     S^T accumulator that becomes the B fragment) is two ds_read_b64_tr_b16
+//     transposed reads, whose 16 rows land on distinct bank pairs.
 // Online softmax per stream with a lazy rescale: the running max moves
 // (and O is rescaled) only when a row's new max exceeds it by more than
 // 2^8, so most tiles skip the rescale; P is rounded to bf16 by the
-// hardware conversion before the PV MFMA and summed as rounded.
+// hardware conversion for the PV MFMA.
 template <int DH>
 struct FaLayout {
   static constexpr int KT = 64, NST = 4, NC = DH / 32, NM = DH / 16;
-  static constexpr int KBYTES = NST * NC * 1024;
-  static constexpr int GB = DH * 16 + 16;  // key-group stride, padded
-  static constexpr int PB = 4 * GB;        // pair stride
-  static constexpr int VBYTES = 2 * PB;
+  static constexpr int KBYTES = NST * NC * 1024;  // K tile
+  static constexpr int ROWB = DH * 2;             // V row (one key)
+  static constexpr int VBYTES = KT * ROWB;        // V tile
+  static constexpr int CPR = DH / 8;              // 16-byte chunks per V row
+  static constexpr int RPI = 1024 / ROWB;         // V rows per 1 KiB direct load
   static constexpr int LDS = 2 * KBYTES + 2 * VBYTES;
 };
+// chunk position of V row k is chunk ^ fa_vswz<DH>(k) (even, so the two
+// chunks of a 32-byte channel group stay adjacent)
+template <int DH>
+__device__ __forceinline__ int fa_vswz(int k) {
+  return DH == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3);
+}
 
 // 16 bytes per lane global -> LDS (direct load): lane l's bytes land at
 // lds + 16 l (lds wave-uniform); counted in vmcnt
 __device__ __forceinline__ void lds_load16(const void* gsrc, void* lds) {
   __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element
+// (j & 3) of the 8-byte segments addressed by lanes 4 y + (j & 15) / 4,
+// y = 0..3 (a 4 x 16 -> 16 x 4 transpose of 16-bit elements)
+typedef __bf16 bf16x4v_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
+  const bf16x4v_t t =
+      __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v_t*)lds);
+  return __builtin_bit_cast(uint2, t);
+}
+
+// max / sum of v over lanes l and l ^ 16 (or l ^ 32): the permlane swaps
+// hand each lane the pair {v[l], v[l ^ d]} in the same order on both lanes
+__device__ __forceinline__ float xmax16(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float xmax32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float xsum16(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ __forceinline__ float xsum32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
 // v_exp_f32 (2^x; -inf -> 0)
@@ -1007,12 +1048,13 @@ __device__ __forceinline__ void unpack4(const uint2& u, float x[4]) {
 }
 
 template <int DH, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2))) void attn_fa_bf16(const coda_attn_desc a, int NQ, int nqb,
-                                                                          int npairs) {
+__global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, int NQ, int nqb, int npairs) {
   using Lay = FaLayout<DH>;
-  constexpr int KT = Lay::KT, NC = Lay::NC, NM = Lay::NM, DCH = DH / 8;
-  constexpr int KCH = Lay::NST * NC;        // K chunks per tile
-  constexpr int KCW = (KCH + NW - 1) / NW;  // per wave
+  constexpr int KT = Lay::KT, NC = Lay::NC, NM = Lay::NM;
+  constexpr int KCH = Lay::NST * NC;          // 1 KiB K chunks per tile
+  constexpr int KCW = (KCH + NW - 1) / NW;    // per wave
+  constexpr int VCH = Lay::VBYTES / 1024;     // 1 KiB V pieces per tile
+  constexpr int VCW = (VCH + NW - 1) / NW;    // per wave
   extern __shared__ __attribute__((aligned(16))) char fa_smem[];
   __shared__ uint8_t al_lds[kMaxRowsPrefix];
   __shared__ uint8_t al32[kMaxRowsPrefix / 32];
@@ -1054,62 +1096,73 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
   const bf16_t* vpb = a.Lp > 0 ? (const bf16_t*)a.vp + b * a.p_sb + hk * a.p_sh : nullptr;
   const bf16_t* kbb = a.Lb > 0 ? (const bf16_t*)a.kb + b * a.b_sb + hk * a.b_sh : nullptr;
   const bf16_t* vbb = a.Lb > 0 ? (const bf16_t*)a.vb + b * a.b_sb + hk * a.b_sh : nullptr;
-  auto krow = [&](int kidx) {
-    return kidx < a.Lp ? kpb + (int64_t)kidx * a.p_sl : kbb + (int64_t)(kidx - a.Lp) * a.b_sl;
-  };
-  auto vrow = [&](int kidx) {
-    return kidx < a.Lp ? vpb + (int64_t)kidx * a.p_sl : vbb + (int64_t)(kidx - a.Lp) * a.b_sl;
-  };
 
-  // K chunks of a tile: straight to LDS buffer bi (keys past Lk read key 0,
-  // a valid row, and are masked)
-  auto kload = [&](int kt0, int bi) {
+  // this lane's byte offsets in the direct loads of a tile (K chunk ci =
+  // wv + NW j, V piece vi = wv + NW j), relative to the tile's first row in
+  // the prefix (P) or in the block (B); the launcher checks they fit 31 bits
+  static_assert(KCH % NW == 0 && VCH % NW == 0, "tile pieces split evenly over the waves");
+  const int psl = (int)a.p_sl, bsl = (int)a.b_sl;
+  int k_key[KCW], k_ch[KCW], v_key[VCW], v_ch[VCW];
+  uint32_t kofP[KCW], kofB[KCW], vofP[VCW], vofB[VCW];
 #pragma unroll
-    for (int j = 0; j < KCW; ++j) {
-      const int ci = wv + NW * j;
-      if (ci < KCH) {
-        const int st = ci / NC, c = ci % NC;
-        int kidx = kt0 + 16 * st + n;
-        kidx = kidx < Lk ? kidx : 0;
-        lds_load16(krow(kidx) + 32 * c + 8 * g4, kbuf + bi * Lay::KBYTES + ci * 1024);
-      }
-    }
-  };
-  // V rows of a tile into registers (thread: 4 keys x 8 channels)
-  const bool vth = tid < 16 * DCH;
-  const int vkg = tid / DCH, vdc = tid % DCH;
-  uint4 vr[4];
-  auto vload = [&](int kt0) {
-    if (vth) {
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int kidx = kt0 + 4 * vkg + jj;
-        vr[jj] = kidx < Lk ? *reinterpret_cast<const uint4*>(vrow(kidx) + 8 * vdc) : uint4{0, 0, 0, 0};
-      }
-    }
-  };
-  auto vstore = [&](int bi) {
-    if (vth) {
-      const int st = vkg >> 2, gg = vkg & 3;
-      char* base = vbuf + bi * Lay::VBYTES + (st >> 1) * Lay::PB + gg * Lay::GB + (st & 1) * 8 + 8 * vdc * 16;
-      const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
-      const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
-      const uint32_t w2[4] = {vr[2].x, vr[2].y, vr[2].z, vr[2].w};
-      const uint32_t w3[4] = {vr[3].x, vr[3].y, vr[3].z, vr[3].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int sh = (e & 1) * 16, wi = e >> 1;
-        uint2 cell;
-        cell.x = ((w0[wi] >> sh) & 0xffffu) | (((w1[wi] >> sh) & 0xffffu) << 16);
-        cell.y = ((w2[wi] >> sh) & 0xffffu) | (((w3[wi] >> sh) & 0xffffu) << 16);
-        *reinterpret_cast<uint2*>(base + e * 16) = cell;
-      }
-    }
-  };
-  if (ntile > 0) {
-    kload(0, 0);
-    vload(0);
+  for (int j = 0; j < KCW; ++j) {
+    const int ci = wv + NW * j;
+    k_key[j] = 16 * (ci / NC) + n;
+    k_ch[j] = 32 * (ci % NC) + 8 * g4;
+    kofP[j] = 2u * (uint32_t)(k_key[j] * psl + k_ch[j]);
+    kofB[j] = 2u * (uint32_t)(k_key[j] * bsl + k_ch[j]);
   }
+#pragma unroll
+  for (int j = 0; j < VCW; ++j) {
+    const int vi = wv + NW * j;
+    const int row = Lay::RPI * vi + lane / Lay::CPR;
+    v_key[j] = row;
+    v_ch[j] = 8 * ((lane % Lay::CPR) ^ fa_vswz<DH>(row));
+    vofP[j] = 2u * (uint32_t)(row * psl + v_ch[j]);
+    vofB[j] = 2u * (uint32_t)(row * bsl + v_ch[j]);
+  }
+  // one tile: rows wholly in the prefix or wholly in the block take a
+  // wave-uniform base; a tile across the boundary or the end picks per row
+  // (rows past Lk read row 0, a valid row, and are masked)
+  auto tile_load = [&](int kt0, int bi) {
+    char* kd = kbuf + bi * Lay::KBYTES + wv * 1024;
+    char* vd = vbuf + bi * Lay::VBYTES + wv * 1024;
+    if (kt0 + KT <= a.Lp) {
+      const char* kb0 = (const char*)(kpb + (int64_t)kt0 * a.p_sl);
+      const char* vb0 = (const char*)(vpb + (int64_t)kt0 * a.p_sl);
+#pragma unroll
+      for (int j = 0; j < KCW; ++j) lds_load16(kb0 + kofP[j], kd + NW * j * 1024);
+#pragma unroll
+      for (int j = 0; j < VCW; ++j) lds_load16(vb0 + vofP[j], vd + NW * j * 1024);
+    } else if (kt0 >= a.Lp && kt0 + KT <= Lk) {
+      const char* kb0 = (const char*)(kbb + (int64_t)(kt0 - a.Lp) * a.b_sl);
+      const char* vb0 = (const char*)(vbb + (int64_t)(kt0 - a.Lp) * a.b_sl);
+#pragma unroll
+      for (int j = 0; j < KCW; ++j) lds_load16(kb0 + kofB[j], kd + NW * j * 1024);
+#pragma unroll
+      for (int j = 0; j < VCW; ++j) lds_load16(vb0 + vofB[j], vd + NW * j * 1024);
+    } else {
+#pragma unroll
+      for (int j = 0; j < KCW; ++j) {
+        int kidx = kt0 + k_key[j];
+        kidx = kidx < Lk ? kidx : 0;
+        const bool pre = kidx < a.Lp;
+        const bf16_t* base = pre ? kpb : kbb;
+        const int off = pre ? kidx * psl : (kidx - a.Lp) * bsl;
+        lds_load16(base + off + k_ch[j], kd + NW * j * 1024);
+      }
+#pragma unroll
+      for (int j = 0; j < VCW; ++j) {
+        int kidx = kt0 + v_key[j];
+        kidx = kidx < Lk ? kidx : 0;
+        const bool pre = kidx < a.Lp;
+        const bf16_t* base = pre ? vpb : vbb;
+        const int off = pre ? kidx * psl : (kidx - a.Lp) * bsl;
+        lds_load16(base + off + v_ch[j], vd + NW * j * 1024);
+      }
+    }
+  };
+  if (ntile > 0) tile_load(0, 0);
 
   // ---- queries of this lane (row qrow, channels 32 c + 8 g4 .. + 8), both
   // streams; every load first, then the eager-op rounding of RoPE and of
@@ -1207,16 +1260,25 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
       }
     }
   }
-  // visibility bytes of the prefix, per-32-key "all visible" flags, norm weight
+  // visibility bytes of the prefix, per-32-key "all visible" flags (one
+  // ballot per 64 keys), norm weight
   for (int i = tid; i < a.Lp; i += NW * 64) al_lds[i] = a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1;
   if (tid < DH) w_lds[tid] = a.rms_w ? bf2f(((const bf16_t*)a.rms_w)[tid]) : 1.f;
   __syncthreads();
-  for (int i = tid; i < (a.Lp + 31) / 32; i += NW * 64) {
-    int all = 32 * i + 32 <= a.Lp;
-    for (int j = 0; j < 32 && all; ++j) all = al_lds[32 * i + j] != 0;
-    al32[i] = (uint8_t)all;
+  for (int base = 64 * wv; base < a.Lp; base += 64 * NW) {
+    const int i = base + lane;
+    const uint64_t m = __ballot(i < a.Lp && al_lds[i] != 0);
+    const int e = (base >> 5) + lane;
+    if (lane < 2 && 32 * e < a.Lp) al32[e] = (uint8_t)(((m >> (32 * lane)) & 0xffffffffull) == 0xffffffffull);
   }
-  if (ntile > 0) vstore(0);
+  // V transposed-read addresses: rows 4 g4 + (n >> 2) (+ 16) of a key
+  // pair, channels 16 mt + 4 (n & 3); the row's chunk permutation folds
+  // into a per-lane offset for each mt
+  const int vrow = 4 * g4 + (n >> 2);
+  int v_off[NM];
+#pragma unroll
+  for (int mt = 0; mt < NM; ++mt)
+    v_off[mt] = vrow * Lay::ROWB + 16 * ((2 * mt + ((n & 3) >> 1)) ^ fa_vswz<DH>(vrow)) + 8 * (n & 1);
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile 0's direct LDS loads have landed
   __syncthreads();
 
@@ -1229,10 +1291,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 
   for (int it = 0; it < ntile; ++it) {
     const int bi = it & 1, kt0 = it * KT;
-    if (it + 1 < ntile) {
-      kload(kt0 + KT, bi ^ 1);
-      vload(kt0 + KT);
-    }
+    if (it + 1 < ntile) tile_load(kt0 + KT, bi ^ 1);
     const char* kb_t = kbuf + bi * Lay::KBYTES;
     const char* vb_t = vbuf + bi * Lay::VBYTES;
 #pragma unroll
@@ -1275,13 +1334,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
       uint4 pb[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        float tmax = -INFINITY;
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, sa[s][sub][j]);
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+        float tmax = fmaxf(fmaxf(fmaxf(sa[s][0][0], sa[s][0][1]), fmaxf(sa[s][0][2], sa[s][0][3])),
+                           fmaxf(fmaxf(sa[s][1][0], sa[s][1][1]), fmaxf(sa[s][1][2], sa[s][1][3])));
+        tmax = xmax32(xmax16(tmax));
         const float tsc = tmax * scale;
         if (__ballot(tsc > m_s[s] + 8.f)) {
           const float mnew = fmaxf(m_s[s], tsc);
@@ -1301,50 +1356,44 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
         pb[s].y = pk_bf16(pr[0][2], pr[0][3]);
         pb[s].z = pk_bf16(pr[1][0], pr[1][1]);
         pb[s].w = pk_bf16(pr[1][2], pr[1][3]);
-        float pf[8];
-        unpack8(pb[s], pf);
-        float ps = 0.f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ps += pf[k];
-        l_s[s] += ps;
+        l_s[s] += ((pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3])) + ((pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3]));
       }
       const bf16x8_t pf0 = __builtin_bit_cast(bf16x8_t, pb[0]), pf1 = __builtin_bit_cast(bf16x8_t, pb[1]);
+      const char* vp_t = vb_t + 32 * p * Lay::ROWB;
 #pragma unroll
       for (int mt = 0; mt < NM; ++mt) {
-        const bf16x8_t vf = __builtin_bit_cast(
-            bf16x8_t, *reinterpret_cast<const uint4*>(vb_t + p * Lay::PB + g4 * Lay::GB + (16 * mt + n) * 16));
+        const uint2 lo = lds_read_tr16(vp_t + v_off[mt]);
+        const uint2 hi = lds_read_tr16(vp_t + v_off[mt] + 16 * Lay::ROWB);
+        const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, uint4{lo.x, lo.y, hi.x, hi.y});
         o[0][mt] = mfma_k32(vf, pf0, o[0][mt]);
         o[1][mt] = mfma_k32(vf, pf1, o[1][mt]);
       }
     }
-    if (it + 1 < ntile) vstore(bi ^ 1);
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the next tile's direct LDS loads have landed
     __syncthreads();
   }
   // ---- epilogue: lane holds channels 16 mt + 4 g4 + j of row n
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    l_s[s] += __shfl_xor(l_s[s], 16, 64);
-    l_s[s] += __shfl_xor(l_s[s], 32, 64);
-  }
+  for (int s = 0; s < 2; ++s) l_s[s] = xsum32(xsum16(l_s[s]));
   constexpr int NV = NM * 4;
   float y[NV];
   {
     using E = Elt<bf16_t>;
+    const float inv_s = l_s[0] > 0.f ? 1.f / l_s[0] : 0.f;
+    const float inv_n = l_s[1] > 0.f ? 1.f / l_s[1] : 0.f;
     float sq = 0.f;
 #pragma unroll
     for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int i = mt * 4 + j;
-        const float os = l_s[0] > 0.f ? o[0][mt][j] / l_s[0] : 0.f;
-        const float on = l_s[1] > 0.f ? o[1][mt][j] / l_s[1] : 0.f;
+        const float os = o[0][mt][j] * inv_s;
+        const float on = o[1][mt][j] * inv_n;
         y[i] = E::rnd(E::rnd(os) - E::rnd(lam * E::rnd(on)));
         sq += E::rnd(y[i] * y[i]);
       }
     if (a.rms_w) {
-      sq += __shfl_xor(sq, 16, 64);
-      sq += __shfl_xor(sq, 32, 64);
+      sq = xsum32(xsum16(sq));
       const float ms = E::rnd(sq / (float)DH);
       const float r = E::rnd(1.0f / sqrtf(E::rnd(ms + E::rnd(a.eps))));
 #pragma unroll
@@ -1361,8 +1410,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(1, 2)))
 #pragma unroll
     for (int mt = 0; mt < NM; ++mt) {
       uint2 u;
-      u.x = (uint32_t)f2bf(y[mt * 4 + 0]) | ((uint32_t)f2bf(y[mt * 4 + 1]) << 16);
-      u.y = (uint32_t)f2bf(y[mt * 4 + 2]) | ((uint32_t)f2bf(y[mt * 4 + 3]) << 16);
+      u.x = pk_bf16(y[mt * 4 + 0], y[mt * 4 + 1]);
+      u.y = pk_bf16(y[mt * 4 + 2], y[mt * 4 + 3]);
       *reinterpret_cast<uint2*>(orow_p + 16 * mt + 4 * g4) = u;
     }
   }
@@ -1433,9 +1482,18 @@ extern "C" int coda_attn_workspace_bytes(const coda_attn_desc* d, size_t* bytes)
 }
 
 // flash tiles (MFMA k=32 for both products, K straight to LDS)
+// the flash kernel's per-lane load offsets are 31-bit byte counts from a
+// tile's first row (or from the prefix / block start on a boundary tile)
+static bool fa_offsets_fit(const coda_attn_desc* d) {
+  const int64_t lim = (int64_t)1 << 30;  // elements
+  return (d->Lp == 0 || (d->p_sl >= 0 && ((int64_t)d->Lp + 64) * d->p_sl < lim)) &&
+         (d->Lb == 0 || (d->b_sl >= 0 && ((int64_t)d->Lb + 64) * d->b_sl < lim));
+}
+
 template <int DH, int NW>
 static int launch_fa_nw(const coda_attn_desc* d, hipStream_t st, int NQ, int nblk) {
   const int npairs = d->B * d->Hkv;
+
   const size_t lds = FaLayout<DH>::LDS;
   hipError_t e = hipFuncSetAttribute((const void*)attn_fa_bf16<DH, NW>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
@@ -1480,7 +1538,7 @@ static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
   }
   int NQ = G >= 4 ? 1 : 4 / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
-  if (DH >= 64 && (G == 8 || G == 4 || G == 2 || G == 1)) return launch_fa<DH>(d, st, G, NQ, nblk);
+  if (DH >= 64 && (G == 8 || G == 4 || G == 2 || G == 1) && fa_offsets_fit(d)) return launch_fa<DH>(d, st, G, NQ, nblk);
   if (G == 8) {
     hipLaunchKernelGGL((attn_tile_bf16<DH, 8>), dim3(nblk, d->Hkv, d->B), dim3(512), 0, st, *d, NQ);
   } else if (G == 4 || G == 2 || G == 1) {

@@ -28,11 +28,17 @@ __host__ __device__ __forceinline__ float bf2f(bf16_t h) {
 }
 
 // float -> bfloat16 bits, round to nearest even, NaN -> 0x7FC0 (c10 rule).
+// On the GPU this is the hardware conversion (v_cvt_pk_bf16_f32, round to
+// nearest even; a NaN keeps its sign and the top of its payload, quietened).
 __host__ __device__ __forceinline__ bf16_t f2bf(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(bf16_t, (__bf16)f);
+#else
   uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)0x7FC0;
   u += 0x7fffu + ((u >> 16) & 1u);
   return (bf16_t)(u >> 16);
+#endif
 }
 
 // Element type traits.  `rnd` rounds an fp32 value to the precision of the
