@@ -1021,6 +1021,7 @@ __device__ __forceinline__ float xsum32(float v) {
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
+
 // v_exp_f32 (2^x; -inf -> 0)
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -1030,6 +1031,20 @@ __device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
   v[0] = (__bf16)a;
   v[1] = (__bf16)b;
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// (e, o) -> (e c - o s, e s + o c) for a bf16 pair packed in one word, the
+// angle's cos / sin taken from half `hf` of the words cw / sw: two bf16
+// dot2 (exact products, fp32 sum) and one rounding of each output
+__device__ __forceinline__ uint32_t rot_pair(uint32_t eo, uint32_t cw, uint32_t sw, int hf) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const uint32_t sel = hf ? 0x07060302u : 0x05040100u;
+  const uint32_t cs = __builtin_amdgcn_perm(sw, cw, sel) ^ 0x80000000u;  // (c, -s)
+  const uint32_t sc = __builtin_amdgcn_perm(cw, sw, sel);                // (s, c)
+  const bf16x2_t x = __builtin_bit_cast(bf16x2_t, eo);
+  const float r0 = __builtin_amdgcn_fdot2_f32_bf16(x, __builtin_bit_cast(bf16x2_t, cs), 0.f, false);
+  const float r1 = __builtin_amdgcn_fdot2_f32_bf16(x, __builtin_bit_cast(bf16x2_t, sc), 0.f, false);
+  return pk_bf16(r0, r1);
 }
 
 __device__ __forceinline__ void unpack8(const uint4& u, float x[8]) {
@@ -1079,7 +1094,10 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
   const int G = a.H / a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g4 = lane >> 4;
-  const int g = wv / NQ, qsub = wv % NQ, h = hk * G + g;
+  // wave = (stream, head, 16-query group): waves 2r and 2r + 1 hold the
+  // signal and the noise stream of the same queries
+  const int strm = wv & 1, r = wv >> 1;
+  const int g = r / NQ, qsub = r % NQ, h = hk * G + g;
   const int q0 = qb * 16 * NQ + 16 * qsub;
   const int qrow = q0 + n;
   const bool qlive = qrow < a.Lq;
@@ -1089,96 +1107,114 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
   const int q_hi = min(a.Lq - 1, qb * 16 * NQ + 16 * NQ - 1);
   const int klim = a.causal ? min(Lk, a.Lp + q_hi + coff + 1) : Lk;
   const int ntile = (klim + KT - 1) / KT;
-  const int wq_hi = min(a.Lq - 1, q0 + 15);
-  const int wklim = a.causal ? min(Lk, a.Lp + wq_hi + coff + 1) : Lk;
 
   const bf16_t* kpb = a.Lp > 0 ? (const bf16_t*)a.kp + b * a.p_sb + hk * a.p_sh : nullptr;
   const bf16_t* vpb = a.Lp > 0 ? (const bf16_t*)a.vp + b * a.p_sb + hk * a.p_sh : nullptr;
   const bf16_t* kbb = a.Lb > 0 ? (const bf16_t*)a.kb + b * a.b_sb + hk * a.b_sh : nullptr;
   const bf16_t* vbb = a.Lb > 0 ? (const bf16_t*)a.vb + b * a.b_sb + hk * a.b_sh : nullptr;
 
-  // this lane's byte offsets in the direct loads of a tile (K chunk ci =
-  // wv + NW j, V piece vi = wv + NW j), relative to the tile's first row in
-  // the prefix (P) or in the block (B); the launcher checks they fit 31 bits
-  static_assert(KCH % NW == 0 && VCH % NW == 0, "tile pieces split evenly over the waves");
+  // this lane's byte offsets in the direct loads of a tile, relative to
+  // the tile's first row in the prefix (P) or in the block (B): K chunk
+  // ci = wv + NW j is sub-tile ci / NC, channel block ci % NC; V piece
+  // vi = wv + NW j is rows RPI vi ..; piece j adds a wave-uniform step
+  // (the launcher checks the offsets fit 31 bits)
+  static_assert(KCH % NW == 0 || NW % KCH == 0, "K chunks split evenly over the waves");
+  static_assert(VCH % NW == 0 || NW % VCH == 0, "V pieces split evenly over the waves");
   const int psl = (int)a.p_sl, bsl = (int)a.b_sl;
-  int k_key[KCW], k_ch[KCW], v_key[VCW], v_ch[VCW];
-  uint32_t kofP[KCW], kofB[KCW], vofP[VCW], vofB[VCW];
-#pragma unroll
-  for (int j = 0; j < KCW; ++j) {
-    const int ci = wv + NW * j;
-    k_key[j] = 16 * (ci / NC) + n;
-    k_ch[j] = 32 * (ci % NC) + 8 * g4;
-    kofP[j] = 2u * (uint32_t)(k_key[j] * psl + k_ch[j]);
-    kofB[j] = 2u * (uint32_t)(k_key[j] * bsl + k_ch[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < VCW; ++j) {
-    const int vi = wv + NW * j;
-    const int row = Lay::RPI * vi + lane / Lay::CPR;
-    v_key[j] = row;
-    v_ch[j] = 8 * ((lane % Lay::CPR) ^ fa_vswz<DH>(row));
-    vofP[j] = 2u * (uint32_t)(row * psl + v_ch[j]);
-    vofB[j] = 2u * (uint32_t)(row * bsl + v_ch[j]);
-  }
-  // one tile: rows wholly in the prefix or wholly in the block take a
-  // wave-uniform base; a tile across the boundary or the end picks per row
-  // (rows past Lk read row 0, a valid row, and are masked)
+  const bool kw = KCH >= NW || wv < KCH, vw = VCH >= NW || wv < VCH;  // waves with a K chunk / V piece
+  const int k_key0 = 16 * ((wv % KCH) / NC) + n, k_ch = 32 * (wv % NC) + 8 * g4;
+  const int v_key0 = Lay::RPI * (wv % VCH) + lane / Lay::CPR;
+  const int v_ch = 8 * ((lane % Lay::CPR) ^ fa_vswz<DH>(v_key0));
+  constexpr int KSTEP = 16 * (NW / NC), VSTEP = Lay::RPI * NW;  // rows per piece step
+  const uint32_t kofP = 2u * (uint32_t)(k_key0 * psl + k_ch), kofB = 2u * (uint32_t)(k_key0 * bsl + k_ch);
+  const uint32_t vofP = 2u * (uint32_t)(v_key0 * psl + v_ch), vofB = 2u * (uint32_t)(v_key0 * bsl + v_ch);
+  // rows wholly in the prefix or wholly in the block take a wave-uniform
+  // base; a tile across the boundary or the end picks per row (rows past
+  // Lk read row 0, a valid row, and are masked)
   auto tile_load = [&](int kt0, int bi) {
     char* kd = kbuf + bi * Lay::KBYTES + wv * 1024;
     char* vd = vbuf + bi * Lay::VBYTES + wv * 1024;
     if (kt0 + KT <= a.Lp) {
-      const char* kb0 = (const char*)(kpb + (int64_t)kt0 * a.p_sl);
-      const char* vb0 = (const char*)(vpb + (int64_t)kt0 * a.p_sl);
+      const char* kb0 = (const char*)(kpb + (int64_t)kt0 * a.p_sl) + kofP;
+      const char* vb0 = (const char*)(vpb + (int64_t)kt0 * a.p_sl) + vofP;
+      if (kw) {
 #pragma unroll
-      for (int j = 0; j < KCW; ++j) lds_load16(kb0 + kofP[j], kd + NW * j * 1024);
-#pragma unroll
-      for (int j = 0; j < VCW; ++j) lds_load16(vb0 + vofP[j], vd + NW * j * 1024);
-    } else if (kt0 >= a.Lp && kt0 + KT <= Lk) {
-      const char* kb0 = (const char*)(kbb + (int64_t)(kt0 - a.Lp) * a.b_sl);
-      const char* vb0 = (const char*)(vbb + (int64_t)(kt0 - a.Lp) * a.b_sl);
-#pragma unroll
-      for (int j = 0; j < KCW; ++j) lds_load16(kb0 + kofB[j], kd + NW * j * 1024);
-#pragma unroll
-      for (int j = 0; j < VCW; ++j) lds_load16(vb0 + vofB[j], vd + NW * j * 1024);
-    } else {
-#pragma unroll
-      for (int j = 0; j < KCW; ++j) {
-        int kidx = kt0 + k_key[j];
-        kidx = kidx < Lk ? kidx : 0;
-        const bool pre = kidx < a.Lp;
-        const bf16_t* base = pre ? kpb : kbb;
-        const int off = pre ? kidx * psl : (kidx - a.Lp) * bsl;
-        lds_load16(base + off + k_ch[j], kd + NW * j * 1024);
+        for (int j = 0; j < KCW; ++j) lds_load16(kb0 + (int64_t)j * KSTEP * 2 * psl, kd + NW * j * 1024);
       }
+      if (vw) {
 #pragma unroll
-      for (int j = 0; j < VCW; ++j) {
-        int kidx = kt0 + v_key[j];
-        kidx = kidx < Lk ? kidx : 0;
-        const bool pre = kidx < a.Lp;
-        const bf16_t* base = pre ? vpb : vbb;
-        const int off = pre ? kidx * psl : (kidx - a.Lp) * bsl;
-        lds_load16(base + off + v_ch[j], vd + NW * j * 1024);
+        for (int j = 0; j < VCW; ++j) lds_load16(vb0 + (int64_t)j * VSTEP * 2 * psl, vd + NW * j * 1024);
+      }
+    } else if (kt0 >= a.Lp && kt0 + KT <= Lk) {
+      const char* kb0 = (const char*)(kbb + (int64_t)(kt0 - a.Lp) * a.b_sl) + kofB;
+      const char* vb0 = (const char*)(vbb + (int64_t)(kt0 - a.Lp) * a.b_sl) + vofB;
+      if (kw) {
+#pragma unroll
+        for (int j = 0; j < KCW; ++j) lds_load16(kb0 + (int64_t)j * KSTEP * 2 * bsl, kd + NW * j * 1024);
+      }
+      if (vw) {
+#pragma unroll
+        for (int j = 0; j < VCW; ++j) lds_load16(vb0 + (int64_t)j * VSTEP * 2 * bsl, vd + NW * j * 1024);
+      }
+    } else {
+      if (kw) {
+#pragma unroll
+        for (int j = 0; j < KCW; ++j) {
+          int kidx = kt0 + k_key0 + KSTEP * j;
+          kidx = kidx < Lk ? kidx : 0;
+          const bool pre = kidx < a.Lp;
+          const bf16_t* base = pre ? kpb : kbb;
+          const int off = pre ? kidx * psl : (kidx - a.Lp) * bsl;
+          lds_load16(base + off + k_ch, kd + NW * j * 1024);
+        }
+      }
+      if (vw) {
+#pragma unroll
+        for (int j = 0; j < VCW; ++j) {
+          int kidx = kt0 + v_key0 + VSTEP * j;
+          kidx = kidx < Lk ? kidx : 0;
+          const bool pre = kidx < a.Lp;
+          const bf16_t* base = pre ? vpb : vbb;
+          const int off = pre ? kidx * psl : (kidx - a.Lp) * bsl;
+          lds_load16(base + off + v_ch, vd + NW * j * 1024);
+        }
       }
     }
   };
-  if (ntile > 0) tile_load(0, 0);
 
-  // ---- queries of this lane (row qrow, channels 32 c + 8 g4 .. + 8), both
-  // streams; every load first, then the eager-op rounding of RoPE and of
-  // the noise rotation (primitives.py:58-113)
-  bf16x8_t qf[2][NC];
-  float lam = 0.f;
+  // every global load of the prologue is issued before the first use of
+  // any (the compiler waits for all outstanding loads once direct LDS
+  // loads are in flight): tile 0's K/V, the visibility bytes of the prefix
+  // and the norm weight (into registers, stored to LDS after the query
+  // math), the queries and their tables
+  if (ntile > 0) tile_load(0, 0);
+  constexpr int ALR = kMaxRowsPrefix / (NW * 64);
+  uint8_t al_r[ALR];
+#pragma unroll
+  for (int k = 0; k < ALR; ++k) {
+    const int i = tid + NW * 64 * k;
+    al_r[k] = i < a.Lp ? (a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1) : (uint8_t)0;
+  }
+  const bf16_t w_raw = tid < DH && a.rms_w ? ((const bf16_t*)a.rms_w)[tid] : (bf16_t)0x3f80;
+
+  // ---- queries of this lane (row qrow, channels 32 c + 8 g4 .. + 8) for
+  // this wave's stream: RoPE with the eager-op rounding, then for the
+  // noise stream the per-head rotation (primitives.py:58-113), unless the
+  // noise queries are given
+  bf16x8_t qf[NC];
+  bf16_t lam_raw;
   {
     using E = Elt<bf16_t>;
     constexpr int half = DH / 2;
     const int qi = qlive ? qrow : 0;
-    const bf16_t* qr = (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
-    const bool rope = a.rope_cos != nullptr, inter = a.rope_interleaved != 0;
-    const bool given_noise = a.q_noise != nullptr;
+    const bool given = strm == 1 && a.q_noise != nullptr;
+    const bool rot = strm == 1 && a.q_noise == nullptr;
+    const bf16_t* qr = given ? (const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh + (int64_t)qi * a.qn_sl
+                             : (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
+    const bool rope = a.rope_cos != nullptr && !given, inter = a.rope_interleaved != 0;
     const bf16_t* csr = rope ? (const bf16_t*)a.rope_cos + (int64_t)qi * half : nullptr;
     const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
-    uint4 uq[NC], up[NC], un[NC], rc[NC], rs[NC];
+    uint4 uq[NC], up[NC], rc[NC], rs[NC];
     uint2 rc2[NC], rs2[NC], tcs[NC], tsn[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -1194,76 +1230,60 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
         rc[c] = *reinterpret_cast<const uint4*>(csr + f0);
         rs[c] = *reinterpret_cast<const uint4*>(snr + f0);
       }
-      if (given_noise) {
-        un[c] = *reinterpret_cast<const uint4*>((const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh +
-                                                (int64_t)qi * a.qn_sl + d0);
-      } else {
+      if (rot) {
         tcs[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_cos + (int64_t)h * half + d0 / 2);
         tsn[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_sin + (int64_t)h * half + d0 / 2);
       }
     }
-    lam = bf2f(((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl]);
+    lam_raw = ((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int d0 = 32 * c + 8 * g4;
-      float x[8];
-      unpack8(uq[c], x);
+      if (given) {
+        qf[c] = __builtin_bit_cast(bf16x8_t, qlive ? uq[c] : uint4{0, 0, 0, 0});
+        continue;
+      }
+      uint32_t w[4] = {uq[c].x, uq[c].y, uq[c].z, uq[c].w};
       if (rope && inter) {
-        // pairs (2p, 2p+1) rotated by angle d0/2 + p
-        float cc[4], ss[4];
-        unpack4(rc2[c], cc);
-        unpack4(rs2[c], ss);
+        // pairs (2p, 2p+1) rotated by angle d0/2 + p: one bf16 dot2 per
+        // output (fp32 products and sum, one rounding)
 #pragma unroll
-        for (int pp = 0; pp < 4; ++pp) {
-          const float e = x[2 * pp], o = x[2 * pp + 1];
-          x[2 * pp] = E::rnd(E::rnd(e * cc[pp]) - E::rnd(o * ss[pp]));
-          x[2 * pp + 1] = E::rnd(E::rnd(e * ss[pp]) + E::rnd(o * cc[pp]));
-        }
+        for (int pp = 0; pp < 4; ++pp) w[pp] = rot_pair(w[pp], pp >> 1 ? rc2[c].y : rc2[c].x,
+                                                        pp >> 1 ? rs2[c].y : rs2[c].x, pp & 1);
       }
       if (rope && !inter) {
-        // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin
-        float cc[8], ss[8], y[8];
+        // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin, with
+        // the eager-op rounding of each product and sum
+        float x[8], cc[8], ss[8], y[8];
+        unpack8(uq[c], x);
         unpack8(rc[c], cc);
         unpack8(rs[c], ss);
         unpack8(up[c], y);
         const bool lo = d0 < half;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float rot = lo ? -y[j] : y[j];
-          x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rot * ss[j]));
+          const float rt = lo ? -y[j] : y[j];
+          x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rt * ss[j]));
         }
-      }
-      uint4 u;
-      u.x = pk_bf16(x[0], x[1]);
-      u.y = pk_bf16(x[2], x[3]);
-      u.z = pk_bf16(x[4], x[5]);
-      u.w = pk_bf16(x[6], x[7]);
-      qf[0][c] = __builtin_bit_cast(bf16x8_t, qlive ? u : uint4{0, 0, 0, 0});
-      if (given_noise) {
-        qf[1][c] = __builtin_bit_cast(bf16x8_t, qlive ? un[c] : uint4{0, 0, 0, 0});
-      } else {
-        float tc[4], ts[4], y[8];
-        unpack4(tcs[c], tc);
-        unpack4(tsn[c], ts);
 #pragma unroll
-        for (int pp = 0; pp < 4; ++pp) {
-          const float e = x[2 * pp], o = x[2 * pp + 1];
-          y[2 * pp] = E::rnd(E::rnd(e * tc[pp]) - E::rnd(o * ts[pp]));
-          y[2 * pp + 1] = E::rnd(E::rnd(e * ts[pp]) + E::rnd(o * tc[pp]));
-        }
-        uint4 v;
-        v.x = pk_bf16(y[0], y[1]);
-        v.y = pk_bf16(y[2], y[3]);
-        v.z = pk_bf16(y[4], y[5]);
-        v.w = pk_bf16(y[6], y[7]);
-        qf[1][c] = __builtin_bit_cast(bf16x8_t, qlive ? v : uint4{0, 0, 0, 0});
+        for (int pp = 0; pp < 4; ++pp) w[pp] = pk_bf16(x[2 * pp], x[2 * pp + 1]);
       }
+      if (rot) {
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) w[pp] = rot_pair(w[pp], pp >> 1 ? tcs[c].y : tcs[c].x,
+                                                        pp >> 1 ? tsn[c].y : tsn[c].x, pp & 1);
+      }
+      qf[c] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
     }
   }
   // visibility bytes of the prefix, per-32-key "all visible" flags (one
   // ballot per 64 keys), norm weight
-  for (int i = tid; i < a.Lp; i += NW * 64) al_lds[i] = a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1;
-  if (tid < DH) w_lds[tid] = a.rms_w ? bf2f(((const bf16_t*)a.rms_w)[tid]) : 1.f;
+#pragma unroll
+  for (int k = 0; k < ALR; ++k) {
+    const int i = tid + NW * 64 * k;
+    if (i < a.Lp) al_lds[i] = al_r[k];
+  }
+  if (tid < DH) w_lds[tid] = bf2f(w_raw);
   __syncthreads();
   for (int base = 64 * wv; base < a.Lp; base += 64 * NW) {
     const int i = base + lane;
@@ -1279,129 +1299,144 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
 #pragma unroll
   for (int mt = 0; mt < NM; ++mt)
     v_off[mt] = vrow * Lay::ROWB + 16 * ((2 * mt + ((n & 3) >> 1)) ^ fa_vswz<DH>(vrow)) + 8 * (n & 1);
-  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile 0's direct LDS loads have landed
-  __syncthreads();
 
-  float m_s[2] = {-INFINITY, -INFINITY}, l_s[2] = {0.f, 0.f};
-  f32x4 o[2][NM];
+  float m_s = -INFINITY, l_s = 0.f;
+  f32x4 o[NM];
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int i = 0; i < NM; ++i) o[s][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < NM; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int it = 0; it < ntile; ++it) {
     const int bi = it & 1, kt0 = it * KT;
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it's direct LDS loads have landed
+    __syncthreads();                     // ... for every wave; buffer bi ^ 1 is free
     if (it + 1 < ntile) tile_load(kt0 + KT, bi ^ 1);
     const char* kb_t = kbuf + bi * Lay::KBYTES;
+    // S^T: st[sub][j] = score of key kt0 + 16 sub + 4 g4 + j against query n
+    f32x4 st[4];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const bf16x8_t kf =
+            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(kb_t + (sub * NC + c) * 1024 + 16 * lane));
+        st[sub] = mfma_k32(kf, qf[c], c == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[sub]);
+      }
+    }
+    // hide the keys this wave's queries may not see (only where some may be)
+    bool need = false;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int pk0 = kt0 + 32 * hh;
+      need |= (pk0 + 32 > Lk) || (pk0 < a.Lp && !al32[pk0 >> 5]) ||
+              (pk0 + 32 > a.Lp && a.causal && (pk0 + 31 - a.Lp) > q0 + coff);
+    }
+    if (need) {
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // branch-free: the visibility byte is read at a clamped index
+          const int kidx = kt0 + 16 * sub + 4 * g4 + j;
+          const int jb = kidx - a.Lp;
+          const bool pre = kidx < a.Lp;
+          const bool al_ok = al_lds[pre ? kidx : 0] != 0;
+          const bool blk_ok = (jb < a.Lb) & ((a.causal == 0) | (jb <= qrow + coff));
+          const bool vis = pre ? al_ok : blk_ok;
+          st[sub][j] = vis ? st[sub][j] : -INFINITY;
+        }
+    }
+    float t0 = fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3]));
+    float t1 = fmaxf(fmaxf(st[1][0], st[1][1]), fmaxf(st[1][2], st[1][3]));
+    float t2 = fmaxf(fmaxf(st[2][0], st[2][1]), fmaxf(st[2][2], st[2][3]));
+    float t3 = fmaxf(fmaxf(st[3][0], st[3][1]), fmaxf(st[3][2], st[3][3]));
+    const float tsc = xmax32(xmax16(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)))) * scale;
+    if (__ballot(tsc > m_s + 8.f)) {
+      const float mnew = fmaxf(m_s, tsc);
+      const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s - mnew);
+#pragma unroll
+      for (int i = 0; i < NM; ++i) o[i] *= alpha;
+      l_s *= alpha;
+      m_s = mnew;
+    }
+    const float mu = m_s == -INFINITY ? 0.f : m_s;
+    float pr[4][4];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pr[sub][j] = fast_exp2(fmaf(st[sub][j], scale, -mu));
+    uint4 pb[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      pb[hh].x = pk_bf16(pr[2 * hh][0], pr[2 * hh][1]);
+      pb[hh].y = pk_bf16(pr[2 * hh][2], pr[2 * hh][3]);
+      pb[hh].z = pk_bf16(pr[2 * hh + 1][0], pr[2 * hh + 1][1]);
+      pb[hh].w = pk_bf16(pr[2 * hh + 1][2], pr[2 * hh + 1][3]);
+    }
+    float q4[4];
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) q4[sub] = (pr[sub][0] + pr[sub][1]) + (pr[sub][2] + pr[sub][3]);
+    l_s += (q4[0] + q4[1]) + (q4[2] + q4[3]);
     const char* vb_t = vbuf + bi * Lay::VBYTES;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-      const int pk0 = kt0 + 32 * p;
-      if (pk0 >= wklim) break;
-      f32x4 sa[2][2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub) sa[s][sub] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const bf16x8_t kf = __builtin_bit_cast(
-              bf16x8_t, *reinterpret_cast<const uint4*>(kb_t + ((2 * p + sub) * NC + c) * 1024 + 16 * lane));
-          sa[0][sub] = mfma_k32(kf, qf[0][c], sa[0][sub]);
-          sa[1][sub] = mfma_k32(kf, qf[1][c], sa[1][sub]);
-        }
-      // masks only where a key of the pair may be hidden from a query of this wave
-      const bool need_mask = (pk0 + 32 > Lk) || (pk0 < a.Lp && !al32[pk0 >> 5]) ||
-                             (pk0 + 32 > a.Lp && a.causal && (pk0 + 31 - a.Lp) > q0 + coff);
-      if (need_mask) {
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            // branch-free: the visibility byte is read at a clamped index
-            const int kidx = pk0 + 16 * sub + 4 * g4 + j;
-            const int jb = kidx - a.Lp;
-            const bool pre = kidx < a.Lp;
-            const bool al_ok = al_lds[pre ? kidx : 0] != 0;
-            const bool blk_ok = (jb < a.Lb) & ((a.causal == 0) | (jb <= qrow + coff));
-            const bool vis = pre ? al_ok : blk_ok;
-            sa[0][sub][j] = vis ? sa[0][sub][j] : -INFINITY;
-            sa[1][sub][j] = vis ? sa[1][sub][j] : -INFINITY;
-          }
-      }
-      uint4 pb[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        float tmax = fmaxf(fmaxf(fmaxf(sa[s][0][0], sa[s][0][1]), fmaxf(sa[s][0][2], sa[s][0][3])),
-                           fmaxf(fmaxf(sa[s][1][0], sa[s][1][1]), fmaxf(sa[s][1][2], sa[s][1][3])));
-        tmax = xmax32(xmax16(tmax));
-        const float tsc = tmax * scale;
-        if (__ballot(tsc > m_s[s] + 8.f)) {
-          const float mnew = fmaxf(m_s[s], tsc);
-          const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s[s] - mnew);
-#pragma unroll
-          for (int i = 0; i < NM; ++i) o[s][i] *= alpha;
-          l_s[s] *= alpha;
-          m_s[s] = mnew;
-        }
-        const float mu = m_s[s] == -INFINITY ? 0.f : m_s[s];
-        float pr[2][4];
-#pragma unroll
-        for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) pr[sub][j] = fast_exp2(fmaf(sa[s][sub][j], scale, -mu));
-        pb[s].x = pk_bf16(pr[0][0], pr[0][1]);
-        pb[s].y = pk_bf16(pr[0][2], pr[0][3]);
-        pb[s].z = pk_bf16(pr[1][0], pr[1][1]);
-        pb[s].w = pk_bf16(pr[1][2], pr[1][3]);
-        l_s[s] += ((pr[0][0] + pr[0][1]) + (pr[0][2] + pr[0][3])) + ((pr[1][0] + pr[1][1]) + (pr[1][2] + pr[1][3]));
-      }
-      const bf16x8_t pf0 = __builtin_bit_cast(bf16x8_t, pb[0]), pf1 = __builtin_bit_cast(bf16x8_t, pb[1]);
-      const char* vp_t = vb_t + 32 * p * Lay::ROWB;
+    for (int hh = 0; hh < 2; ++hh) {
+      const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, pb[hh]);
+      const char* vp_t = vb_t + 32 * hh * Lay::ROWB;
 #pragma unroll
       for (int mt = 0; mt < NM; ++mt) {
         const uint2 lo = lds_read_tr16(vp_t + v_off[mt]);
         const uint2 hi = lds_read_tr16(vp_t + v_off[mt] + 16 * Lay::ROWB);
         const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, uint4{lo.x, lo.y, hi.x, hi.y});
-        o[0][mt] = mfma_k32(vf, pf0, o[0][mt]);
-        o[1][mt] = mfma_k32(vf, pf1, o[1][mt]);
+        o[mt] = mfma_k32(vf, pf, o[mt]);
       }
     }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the next tile's direct LDS loads have landed
-    __syncthreads();
   }
-  // ---- epilogue: lane holds channels 16 mt + 4 g4 + j of row n
-#pragma unroll
-  for (int s = 0; s < 2; ++s) l_s[s] = xsum32(xsum16(l_s[s]));
+  // ---- epilogue: lane holds channels 16 mt + 4 g4 + j of row n.  The
+  // noise wave hands rnd(O_noise) (bf16) to its signal wave through LDS
+  // (the K/V buffers, free once every wave has left the loop)
+  l_s = xsum32(xsum16(l_s));
+  const float inv = l_s > 0.f ? 1.f / l_s : 0.f;
   constexpr int NV = NM * 4;
+  uint4* xch = reinterpret_cast<uint4*>(fa_smem) + r * (NV / 8) * 64;
+  __syncthreads();
+  if (strm == 1) {
+#pragma unroll
+    for (int i = 0; i < NV / 8; ++i) {
+      uint4 u;
+      u.x = pk_bf16(o[2 * i][0] * inv, o[2 * i][1] * inv);
+      u.y = pk_bf16(o[2 * i][2] * inv, o[2 * i][3] * inv);
+      u.z = pk_bf16(o[2 * i + 1][0] * inv, o[2 * i + 1][1] * inv);
+      u.w = pk_bf16(o[2 * i + 1][2] * inv, o[2 * i + 1][3] * inv);
+      xch[i * 64 + lane] = u;
+    }
+  }
+  __syncthreads();
+  if (strm == 1) return;
+  const float lam = bf2f(lam_raw);
+  // y = O_signal - lam rnd(O_noise), then the HeadwiseRMSNorm and weight,
+  // in fp32 with one rounding at the store
   float y[NV];
   {
-    using E = Elt<bf16_t>;
-    const float inv_s = l_s[0] > 0.f ? 1.f / l_s[0] : 0.f;
-    const float inv_n = l_s[1] > 0.f ? 1.f / l_s[1] : 0.f;
+    float on[NV];
+#pragma unroll
+    for (int i = 0; i < NV / 8; ++i) unpack8(xch[i * 64 + lane], on + 8 * i);
     float sq = 0.f;
 #pragma unroll
     for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int i = mt * 4 + j;
-        const float os = o[0][mt][j] * inv_s;
-        const float on = o[1][mt][j] * inv_n;
-        y[i] = E::rnd(E::rnd(os) - E::rnd(lam * E::rnd(on)));
-        sq += E::rnd(y[i] * y[i]);
+        y[i] = fmaf(-lam, on[i], o[mt][j] * inv);
+        sq = fmaf(y[i], y[i], sq);
       }
     if (a.rms_w) {
       sq = xsum32(xsum16(sq));
-      const float ms = E::rnd(sq / (float)DH);
-      const float r = E::rnd(1.0f / sqrtf(E::rnd(ms + E::rnd(a.eps))));
+      const float rr = 1.0f / sqrtf(sq / (float)DH + a.eps);
 #pragma unroll
       for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int i = mt * 4 + j;
-          y[i] = E::rnd(E::rnd(y[i] * r) * w_lds[16 * mt + 4 * g4 + j]);
+          y[i] = y[i] * (rr * w_lds[16 * mt + 4 * g4 + j]);
         }
     }
   }
@@ -1504,7 +1539,8 @@ static int launch_fa_nw(const coda_attn_desc* d, hipStream_t st, int NQ, int nbl
 template <int DH>
 static int launch_fa(const coda_attn_desc* d, hipStream_t st, int G, int NQ, int nblk) {
   if constexpr (DH >= 64) {
-    return G == 8 ? launch_fa_nw<DH, 8>(d, st, NQ, nblk) : launch_fa_nw<DH, 4>(d, st, NQ, nblk);
+    // one wave per (stream, head, 16 queries)
+    return G == 8 ? launch_fa_nw<DH, 16>(d, st, NQ, nblk) : launch_fa_nw<DH, 8>(d, st, NQ, nblk);
   } else {
     return fail(CODA_EUNSUP, "coda_diff_attn_fwd: flash tiles need head_dim >= 64");
   }
