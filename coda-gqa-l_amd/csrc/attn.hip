@@ -788,6 +788,389 @@ __global__ __launch_bounds__(256) void attn_rows_merge(const coda_attn_desc a, i
   }
 }
 
+// ------------------------------------------------------------ fused decode step
+// decode_step_bf16: one workgroup per (KV head hk, sequence b) runs the
+// whole decode step of that pair once the ring is full (the same work as
+// decode_bank_kernel followed by attn_rows_bf16):
+//   wave 3     the bank update of head hk for the token evicted from ring
+//              slot j: decisions from the carried routing record, row
+//              writes, metadata, the next step's record;
+//   waves 0-2  meanwhile attend to the ring slots other than j (the update
+//              does not touch them) and to the new token (k_new, v_new: the
+//              row the update writes into slot j);
+//   barrier    the exact / summary rows written by wave 3 are visible;
+//   waves 0-3  attend to the exact and summary slots, merge, epilogue.
+// Tiles of 16 keys as attn_rows_bf16: K straight into MFMA fragments, V
+// through the per-wave LDS transpose, online softmax per wave.
+template <int DH>
+__global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, const coda_bank_desc s,
+                                                        const bf16_t* __restrict__ k_new,
+                                                        const bf16_t* __restrict__ v_new, int64_t nb_sb,
+                                                        int64_t nb_sh, const float* __restrict__ g_new, int j,
+                                                        int64_t pos, const float* __restrict__ rec_in,
+                                                        float* __restrict__ rec_out) {
+  using T = bf16_t;
+  constexpr int NC = DH / 32, NM = DH / 16, NW = 4, NVb = (DH + 63) / 64;
+  __shared__ __attribute__((aligned(16))) char vt_smem[NW][VtLayout<DH>::kTileBytes];
+  __shared__ __attribute__((aligned(16))) bf16_t q_lds[16][DH + 8];
+  __shared__ uint8_t al_lds[kMaxRowsPrefix];
+  __shared__ float red_m[NW][16], red_l[NW][16];
+  __shared__ DecodeDecision dec;
+  // bank stage during the update; the partial outputs of the 4 waves after
+  extern __shared__ __attribute__((aligned(16))) char ds_u[];
+  const int hk = blockIdx.x, b = blockIdx.y;
+  const int G = a.H / a.Hkv, R = 2 * G;
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n = lane & 15, g4 = lane >> 4;
+  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
+  const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, Lbuf = W + Me + Ms;
+  constexpr int DCH = DH / 8;
+  const int kgl = lane / DCH, dcl = lane % DCH;
+  const bool vload = kgl < 4;
+  char* vt = vt_smem[wv];
+  const T* kn_row = k_new + b * nb_sb + hk * nb_sh;
+  const T* vn_row = v_new + b * nb_sb + hk * nb_sh;
+
+  // K / V of the (sequence, head) plane and of the new token through raw
+  // buffer resources (wave-uniform, in SGPRs); rows past the plane read 0
+  auto rsrc = [](const T* p, int nbytes) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0,
+                                             __builtin_amdgcn_readfirstlane(nbytes), kBufWord3);
+  };
+  const int64_t poff = (int64_t)b * a.p_sb + (int64_t)hk * a.p_sh;
+  const __amdgpu_buffer_rsrc_t rk = rsrc((const T*)a.kp + poff, Lbuf * DH * 2);
+  const __amdgpu_buffer_rsrc_t rv = rsrc((const T*)a.vp + poff, Lbuf * DH * 2);
+  const __amdgpu_buffer_rsrc_t rkn = rsrc(kn_row, DH * 2);
+  const __amdgpu_buffer_rsrc_t rvn = rsrc(vn_row, DH * 2);
+  // tile at key kt of the plane, or (nt) the new token in every row
+  auto issue = [&](int kt, bool nt, bf16x8_t (&kf)[NC], uint4 (&vv)[4]) {
+    const int koff = nt ? 16 * g4 : (kt + n) * (DH * 2) + 16 * g4;
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      kf[c] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(nt ? rkn : rk, koff + 64 * c, 0, 0));
+    const int voff = nt ? 16 * dcl : (kt + 4 * (kgl & 3)) * (DH * 2) + 16 * dcl;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+      vv[jj] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(nt ? rvn : rv, voff + (nt ? 0 : jj * DH * 2), 0, 0));
+  };
+  // visibility of this lane's keys kt + 4 g4 + jj: inside [lo, hi) and
+  // allowed; the new-token tile keeps its key 0 only
+  auto tile_mask = [&](int kt, int lo, int hi, bool nt) {
+    int m4 = 0;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int kk = kt + 4 * g4 + jj;
+      const int in = (kk >= lo) & (kk < hi);
+      const int kc = in ? kk : lo;
+      const int ok = nt ? (kk == kt) : (in & (al_lds[kc] != 0));
+      m4 |= ok << jj;
+    }
+    return m4;
+  };
+  // phase 1 tiles of waves 0-2: u < nR ring tile u, u == nR the new token
+  const int nR = (W + 15) / 16, nB = (Me + Ms + 15) / 16;
+  auto p1_kt = [&](int u) { return u < nR ? 16 * u : 0; };
+  const int n1_w = wv < 3 ? (nR + 1 - wv + 2) / 3 : 0;   // tiles u = wv + 3 i
+  // phase 2 tiles: bank tile u of wave (u + 3) % 4
+  const int w2 = (wv + 1) & 3;
+  const int n2_w = nB > w2 ? (nB - w2 + 3) / 4 : 0;      // tiles u = w2 + 4 i
+
+  bf16x8_t kf0[NC], kf1[NC];
+  uint4 vv0[4], vv1[4];
+  int vm0 = 0, vm1 = 0;
+  // ---- prologue: first loads of every wave, then the query staging
+  if (wv < 3 && n1_w > 0) issue(p1_kt(wv), wv == nR, kf0, vv0);
+  // bank wave: record and norm rows straight to LDS, evicted / next rows
+  const int LF = DH - s.lf, words = dstep_words(Hkv, Me, Ms);
+  const int jn = j + 1 == W ? 0 : j + 1;
+  float* rec = reinterpret_cast<float*>(ds_u);
+  T* stage = reinterpret_cast<T*>(rec + words);
+  float* ke = reinterpret_cast<float*>(stage + dbank_stage_elems(DH, Me, Ms, s.lf));
+  float* ve = ke + DH;
+  float* vnrm = ve + DH;
+  float* knrm = vnrm + DH;
+  bf16_t kev[NVb], vev[NVb], xv_r[NVb], xk_r[NVb];
+  bool av[NVb], ak[NVb];
+  if (wv == 3) {
+    wave_copy_lds(rec, rec_in + (int64_t)b * words, words * 4, lane);
+    if (Me > 0)
+      wave_copy_lds(stage, (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH, Me * DH * 2, lane);
+    if (Ms > 0)
+      wave_copy_lds(stage + Me * DH, (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF, Ms * LF * 2,
+                    lane);
+    const int64_t plane = ((int64_t)b * Hkv + hk) * Lbuf;
+    const T* kr = (const T*)s.k_buf + (plane + j) * DH;
+    const T* vr = (const T*)s.v_buf + (plane + j) * DH;
+    const T* kx = jn == j ? kn_row : (const T*)s.k_buf + (plane + jn) * DH;
+    const T* vx = jn == j ? vn_row : (const T*)s.v_buf + (plane + jn) * DH;
+#pragma unroll
+    for (int i = 0; i < NVb; ++i) {
+      const int d = lane + 64 * i;
+      const int dc = d < DH ? d : 0;
+      av[i] = d < DH;
+      ak[i] = d < LF;
+      kev[i] = kr[dc];
+      vev[i] = vr[dc];
+      xv_r[i] = vx[dc];
+      xk_r[i] = kx[s.lf + (ak[i] ? d : 0)];
+    }
+  }
+  // epilogue operands
+  constexpr int NV = (DH + 63) / 64;
+  float lam_pf[2] = {0.f, 0.f}, w_pf[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) w_pf[i] = 1.f;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int orow = wv + r * NW;
+    if (orow < G) lam_pf[r] = bf2f(((const T*)a.lam)[b * a.lam_sb + (hk * G + orow) * a.lam_sh]);
+  }
+  if (a.rms_w) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) w_pf[i] = bf2f(((const T*)a.rms_w)[min(lane + 64 * i, DH - 1)]);
+  }
+  stage_queries(a, b, R, &q_lds[0][0], DH + 8, [&](int r, int& st, int& h, int& qi) {
+    st = r / G;
+    h = hk * G + r % G;
+    qi = 0;
+    return true;
+  });
+  // visibility bytes: ring slot j (the evicted token) hidden; the new token
+  // has its own tile
+  for (int i = threadIdx.x; i < Lbuf; i += blockDim.x)
+    al_lds[i] = i == j ? (uint8_t)0 : (a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1);
+  __syncthreads();
+  bf16x8_t qf[NC];
+  {
+    const bool live = n < R;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      uint4 u = live ? *reinterpret_cast<const uint4*>(&q_lds[n][32 * c + 8 * g4]) : uint4{0, 0, 0, 0};
+      qf[c] = __builtin_bit_cast(bf16x8_t, u);
+    }
+  }
+  float m_i = -INFINITY, l_i = 0.f;
+  f32x4 o[NM];
+#pragma unroll
+  for (int i = 0; i < NM; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](const bf16x8_t (&kf)[NC], const uint4 (&vv)[4], int vmask) {
+    f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) st = mfma_k32(kf[c], qf[c], st);
+    float sv[4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      sv[jj] = ((vmask >> jj) & 1) ? st[jj] * scale : -INFINITY;
+      tmax = fmaxf(tmax, sv[jj]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    const float mnew = fmaxf(m_i, tmax);
+    const float muse = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = exp2f(m_i - muse);
+    float p[4], ps = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      p[jj] = bf2f(f2bf(exp2f(sv[jj] - muse)));
+      ps += p[jj];
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l_i = l_i * alpha + ps;
+    m_i = mnew;
+    const short4_t pf = pack4(p[0], p[1], p[2], p[3]);
+    if (vload) store_vt<DH>(vt, kgl, 8 * dcl, vv);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes of this wave done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt) {
+      const uint2 cell = *reinterpret_cast<const uint2*>(vt + VtLayout<DH>::off(g4, 16 * mt + n));
+      o[mt] *= alpha;
+      o[mt] = mfma_k16(__builtin_bit_cast(short4_t, cell), pf, o[mt]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  // ---- phase 1
+  if (wv < 3) {
+    // ring tiles and the new token, ping-pong register buffers
+    auto mask1 = [&](int i) {
+      const int u = wv + 3 * i;
+      return u < nR ? tile_mask(16 * u, 0, W, false) : (u == nR ? tile_mask(0, 0, 0, true) : 0);
+    };
+    vm0 = n1_w > 0 ? mask1(0) : 0;
+    for (int i = 0; i < n1_w; i += 2) {
+      if (i + 1 < n1_w) {
+        const int u = wv + 3 * (i + 1);
+        issue(p1_kt(u), u == nR, kf1, vv1);
+        vm1 = mask1(i + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      consume(kf0, vv0, vm0);
+      if (i + 1 >= n1_w) break;
+      if (i + 2 < n1_w) {
+        const int u = wv + 3 * (i + 2);
+        issue(p1_kt(u), u == nR, kf0, vv0);
+        vm0 = mask1(i + 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      consume(kf1, vv1, vm1);
+    }
+  } else {
+    // the bank update of head hk (one wave)
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): record, norm rows, evicted / next rows
+    float xv[NVb], xk[NVb];
+#pragma unroll
+    for (int i = 0; i < NVb; ++i) {
+      if (av[i]) {
+        ke[lane + 64 * i] = bf2f(kev[i]);
+        ve[lane + 64 * i] = bf2f(vev[i]);
+      }
+      xv[i] = av[i] ? bf2f(xv_r[i]) : 0.f;
+      xk[i] = ak[i] ? bf2f(xk_r[i]) : 0.f;
+    }
+    // unit rows of the token evicted next (for the next record's dots,
+    // taken by every wave after the barrier)
+    if (Me > 0) {
+      wave_unit<T, NVb>(xv, av);
+#pragma unroll
+      for (int i = 0; i < NVb; ++i)
+        if (av[i]) vnrm[lane + 64 * i] = xv[i];
+    }
+    if (Ms > 0) {
+      wave_unit<T, NVb>(xk, ak);
+#pragma unroll
+      for (int i = 0; i < NVb; ++i)
+        if (ak[i]) knrm[lane + 64 * i] = xk[i];
+    }
+    const DStepWs L = dstep_ws(rec, 0, Hkv, Me, Ms);
+    const float g_e = *L.g_e;
+    if (Me > 0) decide_exact<T>(s, L.dots, L.used, L.last, g_e, dec, hk == 0, lane);
+    if (Ms > 0) decide_summary<T>(s, L.dots + Hkv * Me, L.used + Me, g_e, dec, hk == 0, lane);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the decision (lane 0) and rows are in LDS
+    __builtin_amdgcn_wave_barrier();
+    const DecodeDecision dd = dec;
+    apply_head<T, DH>(s, b, hk, dd, ke, ve, kn_row, vn_row, j, g_e, lane, Me > 0 ? stage + dd.idx_e * DH : nullptr,
+                      Ms > 0 ? stage + Me * DH + dd.idx_s * LF : nullptr);
+    if (hk == 0) {
+      // metadata of the sequence, and the next record's snapshot of it
+      const DStepWs wn = dstep_ws(rec_out, b, Hkv, Me, Ms);
+      const bool ow_e = Me > 0 && dd.ow_e, keep_e = Me > 0 && dd.keep_e, keep_s = Ms > 0 && dd.keep_s;
+      const int ie = Me > 0 ? dd.idx_e : -1, is = Ms > 0 ? dd.idx_s : -1;
+      for (int m = lane; m < Me + Ms; m += 64)
+        wn.used[m] = L.used[m] | ((ow_e && m == ie) || (keep_s && m == Me + is) ? 1 : 0);
+      for (int m = lane; m < Me; m += 64) wn.last[m] = (keep_e && m == ie) ? pos - W : L.last[m];
+      if (lane == 0) {
+        *wn.g_e = jn == j ? g_new[b] : s.g_recent[(int64_t)b * W + jn];
+        commit_decode_meta(s, b, dd, j, pos - W, g_new[b]);
+      }
+    }
+    // the slots this update fills become visible to the bank tiles
+    if (lane == 0) {
+      if (Me > 0 && dd.ow_e) al_lds[W + dd.idx_e] = 1;
+      if (Ms > 0 && dd.keep_s) al_lds[W + Me + dd.idx_s] = 1;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's row writes are done
+  }
+  __syncthreads();  // bank rows and patched norm rows written by wave 3 visible
+
+  // ---- phase 2: exact and summary slots
+  {
+    auto kt2 = [&](int i) { return W + 16 * (w2 + 4 * i); };
+    if (n2_w > 0) {
+      issue(kt2(0), false, kf0, vv0);
+      vm0 = tile_mask(kt2(0), W, Lbuf, false);
+    }
+    // the next step's record while the first bank tile loads: head hk's
+    // dots against the updated norm rows, over the 4 waves
+    float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
+    float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
+    if (Me > 0)
+      wave_dots<T, 4>(
+          Me, DH, wv, NW, lane, [&](int it) { return (const T*)stage + it * DH; },
+          [&](int) { return (const float*)vnrm; }, [&](int it, float v) { out_e[it] = v; });
+    if (Ms > 0)
+      wave_dots<T, 4>(
+          Ms, LF, wv, NW, lane, [&](int it) { return (const T*)stage + Me * DH + it * LF; },
+          [&](int) { return (const float*)knrm; }, [&](int it, float v) { out_s[it] = v; });
+    for (int i = 0; i < n2_w; i += 2) {
+      if (i + 1 < n2_w) {
+        issue(kt2(i + 1), false, kf1, vv1);
+        vm1 = tile_mask(kt2(i + 1), W, Lbuf, false);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      consume(kf0, vv0, vm0);
+      if (i + 1 >= n2_w) break;
+      if (i + 2 < n2_w) {
+        issue(kt2(i + 2), false, kf0, vv0);
+        vm0 = tile_mask(kt2(i + 2), W, Lbuf, false);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      consume(kf1, vv1, vm1);
+    }
+  }
+  // ---- merge the 4 waves (rows r < R), epilogue
+  __syncthreads();  // every wave is done with the bank stage
+  float* red_o = reinterpret_cast<float*>(ds_u);  // [NW][R][DH + 4]
+  if (g4 == 0) {
+    red_m[wv][n] = m_i;
+    red_l[wv][n] = l_i;
+  }
+  if (n < R) {
+#pragma unroll
+    for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) red_o[(wv * R + n) * (DH + 4) + 16 * mt + 4 * g4 + jj] = o[mt][jj];
+  }
+  __syncthreads();
+  for (int orow = wv, r_pf = 0; orow < G; orow += NW, ++r_pf) {
+    const int h = hk * G + orow;
+    float os[NV], on[NV], y[NV];
+    bool act[NV];
+    int dd[NV];
+    float M[2] = {-INFINITY, -INFINITY}, Ls[2] = {0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const int r = st * G + orow;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M[st] = fmaxf(M[st], red_m[w][r]);
+      const float Mu = M[st] == -INFINITY ? 0.f : M[st];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) Ls[st] += red_l[w][r] * exp2f(red_m[w][r] - Mu);
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = lane + 64 * i;
+      act[i] = d < DH;
+      dd[i] = act[i] ? d : 0;
+      float acc[2] = {0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int r = st * G + orow;
+        const float Mu = M[st] == -INFINITY ? 0.f : M[st];
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc[st] += red_o[(w * R + r) * (DH + 4) + dd[i]] * exp2f(red_m[w][r] - Mu);
+        acc[st] = Ls[st] > 0.f ? acc[st] / Ls[st] : 0.f;
+      }
+      os[i] = act[i] ? acc[0] : 0.f;
+      on[i] = act[i] ? acc[1] : 0.f;
+    }
+    const float lam = r_pf == 0   ? lam_pf[0]
+                      : r_pf == 1 ? lam_pf[1]
+                                  : bf2f(((const T*)a.lam)[b * a.lam_sb + h * a.lam_sh]);
+    diff_norm_w<NV>(y, os, on, act, lam, a.rms_w ? w_pf : nullptr, a.eps, DH);
+    T* orow_p = (T*)a.out + b * a.o_sb + h * a.o_sh;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (act[i]) orow_p[dd[i]] = f2bf(y[i]);
+  }
+}
+
 // ------------------------------------------------------------ prefill tiles
 // Workgroup = (query block of 16*NQ, KV head, batch), NW = G*NQ waves;
 // wave w owns head g = w / NQ and queries q0 + 16*(w % NQ) + [0,16) as two
@@ -1626,6 +2009,33 @@ static int validate_step(const coda_bank_desc* s, const coda_attn_desc* a) {
   return CODA_OK;
 }
 
+// the fused decode step kernel: bf16, a full ring, every row of a head's
+// plane in the LDS visibility copy, all query rows in one MFMA tile
+static bool fused_step_ok(const coda_bank_desc* s, const coda_attn_desc* a) {
+  const int G = a->H / a->Hkv;
+  return s->dtype == CODA_BF16 && (s->Dh == 64 || s->Dh == 128) && 2 * G <= 16 && s->W >= 16 &&
+         s->W + s->Me + s->Ms <= kMaxRowsPrefix && a->causal == 0;
+}
+
+template <int DH>
+static int launch_fused_step(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new, const void* v_new,
+                             int64_t nb_sb, int64_t nb_sh, const float* g_new, int j, int64_t pos,
+                             const float* rec_in, float* rec_out, hipStream_t st) {
+  const int R = 2 * (a->H / a->Hkv);
+  size_t lds = dbank_lds(*s);
+  const size_t red = (size_t)4 * R * (DH + 4) * sizeof(float);
+  lds = lds > red ? lds : red;
+  if (lds > 64 * 1024) {
+    if (lds > 120 * 1024) return fail(CODA_EUNSUP, "coda_decode_step: bank of %d + %d rows too large", s->Me, s->Ms);
+    hipError_t e = hipFuncSetAttribute((const void*)decode_step_bf16<DH>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return fail(CODA_EHIP, "coda_decode_step: LDS attribute: %s", hipGetErrorString(e));
+  }
+  hipLaunchKernelGGL((decode_step_bf16<DH>), dim3(s->Hkv, s->B), dim3(256), lds, st, *a, *s, (const bf16_t*)k_new,
+                     (const bf16_t*)v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out);
+  return check_launch("decode_step_bf16");
+}
+
 extern "C" int coda_decode_step_workspace_bytes(const coda_bank_desc* s, const coda_attn_desc* a, size_t* bytes) {
   int rc = validate_step(s, a);
   if (rc) return rc;
@@ -1673,6 +2083,12 @@ extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a
   if (!have_route) {
     rc = launch_decode_route(s, ring_idx, rec_in, st);
     if (rc) return rc;
+  }
+  if (fused_step_ok(s, a)) {
+    rc = s->Dh == 128 ? launch_fused_step<128>(s, a, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st)
+                      : launch_fused_step<64>(s, a, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st);
+    if (rc == CODA_OK && routed) *routed = 1;
+    return rc;
   }
   rc = launch_decode_bank(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st);
   if (rc) return rc;

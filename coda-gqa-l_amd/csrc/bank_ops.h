@@ -381,6 +381,27 @@ __host__ __device__ __forceinline__ DStepWs dstep_ws(float* ws, int b, int Hkv, 
   return w;
 }
 
+// LDS of one (sequence, head) decode bank update: record [words] f32 |
+// norm stage [Me*DH + Ms*LF] T | ke, ve, vnrm, knrm [DH] f32.
+__host__ __device__ __forceinline__ size_t dbank_stage_elems(int DH, int Me, int Ms, int lf) {
+  return ((size_t)Me * DH + (size_t)Ms * (DH - lf) + 7) & ~(size_t)7;
+}
+__host__ __device__ __forceinline__ size_t dbank_lds(const coda_bank_desc& s) {
+  const size_t es = s.dtype == CODA_BF16 ? 2 : 4;
+  return sizeof(float) * (size_t)dstep_words(s.Hkv, s.Me, s.Ms) + es * dbank_stage_elems(s.Dh, s.Me, s.Ms, s.lf) +
+         sizeof(float) * 4 * (size_t)s.Dh;
+}
+
+// Copy nbytes (a multiple of 16) global -> LDS with direct loads by one
+// wave (1 KiB per instruction, lane l the bytes [16 l, 16 l + 16)); the
+// loads count in vmcnt.
+__device__ __forceinline__ void wave_copy_lds(void* dst, const void* src, int nbytes, int lane) {
+  for (int c = 0; c < nbytes; c += 1024)
+    if (c + 16 * lane < nbytes)
+      __builtin_amdgcn_global_load_lds((const char*)src + c + 16 * lane,
+                                       (__attribute__((address_space(3))) void*)((char*)dst + c), 16, 0, 0);
+}
+
 // Routing dots of head h for evicting ring slot j of sequence b, by the
 // 256 threads of a workgroup (every thread must call it): the evicted row
 // (k, v) goes to LDS as floats (ke, ve: DH each), its unit V and unit LF-K

@@ -160,14 +160,6 @@ __global__ __launch_bounds__(256) void decode_route_kernel(const coda_bank_desc 
 //   4. all waves take the next record's dots against the staged (updated)
 //      norm rows, with the per-row arithmetic of the routing kernel.
 // LDS: record [words] f32 | norm stage [Me*DH + Ms*LF] T | ke, ve, vnrm, knrm [DH] f32.
-__host__ __device__ __forceinline__ size_t dbank_stage_elems(int DH, int Me, int Ms, int lf) {
-  return ((size_t)Me * DH + (size_t)Ms * (DH - lf) + 7) & ~(size_t)7;
-}
-__host__ __device__ __forceinline__ size_t dbank_lds(const coda_bank_desc& s) {
-  const size_t es = s.dtype == CODA_BF16 ? 2 : 4;
-  return sizeof(float) * (size_t)dstep_words(s.Hkv, s.Me, s.Ms) + es * dbank_stage_elems(s.Dh, s.Me, s.Ms, s.lf) +
-         sizeof(float) * 4 * (size_t)s.Dh;
-}
 
 // Copy nbytes (a multiple of 16) global -> LDS with direct global->LDS
 // loads, spread over the waves of the workgroup: one wave instruction moves

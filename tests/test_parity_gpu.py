@@ -252,35 +252,43 @@ def test_run_twice_is_bit_identical():
         assert torch.equal(a, b)
 
 
+# (embed_dim, heads, kv heads, batch): head_dim 32 takes the routing kernel +
+# bank kernel + attention kernel; head_dim 64 / 128 in bf16 the fused step
+# kernel (bank update on one wave beside the ring attention)
+STEP_CFGS = {"dh32": (128, 4, 2, 256), "dh128_g2": (512, 4, 2, 64), "dh64_g4": (512, 8, 2, 64),
+             "dh128_g8": (1024, 8, 1, 16)}
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("cfg", list(STEP_CFGS))
 @torch.no_grad()
-def test_decode_step_matches_oracle_large_batch(dtype):
-    """The one-call decode step at a batch large enough for the fused
-    (routing kernel + apply-in-attention) path in bf16; fp32 takes the
-    bank-kernel + attention path.  Teacher-forced per step."""
+def test_decode_step_matches_oracle_large_batch(dtype, cfg):
+    """The one-call decode step (routing record carried between steps) in
+    its bf16 and fp32 paths.  Teacher-forced per step."""
     _need_gpu()
     from coda_oracle import OracleLayer, banks, prims
-    print(f"[decode_step] {dtype}", flush=True)
-    kw = dict(embed_dim=128, num_heads=4, num_kv_heads=2, window=32, num_landmarks_exact=16,
+    E, H, Hkv, B = STEP_CFGS[cfg]
+    Dh = E // H
+    print(f"[decode_step] {dtype} {cfg}", flush=True)
+    kw = dict(embed_dim=E, num_heads=H, num_kv_heads=Hkv, window=32, num_landmarks_exact=16,
               num_landmarks_summary=16)
     case = {"kw": kw}
     torch.manual_seed(5)
     m = OracleLayer(**kw).to(dtype).eval()
     p = product_like(m, case, dtype, DEV)
-    B = 256
     torch.manual_seed(6)
     st_o = m.init_state(batch_size=B, dtype=dtype)
     g = torch.Generator().manual_seed(7)
-    x = torch.randn(B, 80, 128, generator=g).to(dtype)
+    x = torch.randn(B, 80, E, generator=g).to(dtype)
     m.prefill_chunked(x, st_o, block_size=32, return_outputs=False)
     W, Me = m.window, m.Me
     for t in range(12):
-        xt = torch.randn(B, 1, 128, generator=g).to(dtype)
+        xt = torch.randn(B, 1, E, generator=g).to(dtype)
         st_p = to_product_state(st_o, DEV)
         qp = int(st_o.pos)
         kn, vn, gn = m._new_kv(xt, qp)
         banks.write_one(m, st_o, kn, vn, gn)
-        qt = m.q_proj(xt).view(B, 1, 4, 32).transpose(1, 2)
+        qt = m.q_proj(xt).view(B, 1, H, Dh).transpose(1, 2)
         lamt = torch.sigmoid(m.lambda_proj(xt)).transpose(1, 2).unsqueeze(-1)
         ho = m.attend_core(qt, lamt, st_o, qp)
         ct, sn = m.rope_tables(1, qp, dtype)
@@ -308,8 +316,9 @@ def _assert_same_state(a, b, what):
     assert (a.pos, a.recent_idx, a.recent_filled) == (b.pos, b.recent_idx, b.recent_filled), what
 
 
+@pytest.mark.parametrize("E,H", [(256, 8), (512, 4)])
 @torch.no_grad()
-def test_decode_step_carried_routing_matches_fresh_routing():
+def test_decode_step_carried_routing_matches_fresh_routing(E, H):
     """bf16 fused decode: a state stepped on its own reuses the routing
     record each step leaves for the next; a copy of that state stepped once
     from scratch routes with the routing kernel.  Outputs and states must be
@@ -317,29 +326,29 @@ def test_decode_step_carried_routing_matches_fresh_routing():
     prefill chunk between decode steps (both force a fresh routing)."""
     _need_gpu()
     import coda_gqa_l
-    print("[decode_step carried routing]", flush=True)
+    print(f"[decode_step carried routing] E{E} H{H}", flush=True)
     dt = torch.bfloat16
     torch.manual_seed(11)
-    m = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=256, num_heads=8, num_kv_heads=2, window=32,
+    m = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=E, num_heads=H, num_kv_heads=2, window=32,
                                         num_landmarks_exact=16, num_landmarks_summary=16).to(dt).to(DEV).eval()
     # a second module with the same weights steps the fresh copies, so the
     # routing record m keeps for its own state is never displaced
-    m2 = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=256, num_heads=8, num_kv_heads=2, window=32,
+    m2 = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=E, num_heads=H, num_kv_heads=2, window=32,
                                          num_landmarks_exact=16, num_landmarks_summary=16).to(dt).to(DEV).eval()
     m2.load_state_dict(m.state_dict())
-    B = 256
+    B = 256 if E == 256 else 64
     st = m.init_state(batch_size=B, device=DEV, dtype=dt)
     g = torch.Generator(device=DEV).manual_seed(12)
-    m.prefill_chunked(torch.randn(B, 70, 256, generator=g, device=DEV, dtype=dt), st, block_size=32,
+    m.prefill_chunked(torch.randn(B, 70, E, generator=g, device=DEV, dtype=dt), st, block_size=32,
                       return_outputs=False)
     for t in range(14):
         if t == 6:
             st.v_buf[:, :, m.window + 3] *= -1          # in-place edit: version counter moves
             st._exact_v_norm[:, :, 3] *= -1
         if t == 10:
-            m.prefill_chunked(torch.randn(B, 5, 256, generator=g, device=DEV, dtype=dt), st, block_size=32,
+            m.prefill_chunked(torch.randn(B, 5, E, generator=g, device=DEV, dtype=dt), st, block_size=32,
                               return_outputs=False)
-        x = torch.randn(B, 1, 256, generator=g, device=DEV, dtype=dt)
+        x = torch.randn(B, 1, E, generator=g, device=DEV, dtype=dt)
         fresh = _clone_state(st)
         carried = m.__dict__.get("_route_tag") is not None
         y1, _ = m.step(x, st)
