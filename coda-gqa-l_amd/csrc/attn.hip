@@ -788,6 +788,87 @@ __global__ __launch_bounds__(256) void attn_rows_merge(const coda_attn_desc a, i
   }
 }
 
+// ------------------------------------------------------------ gfx950 helpers
+// 16 bytes per lane global -> LDS (direct load): lane l's bytes land at
+// lds + 16 l (lds wave-uniform); counted in vmcnt
+__device__ __forceinline__ void lds_load16(const void* gsrc, void* lds) {
+  __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element
+// (j & 3) of the 8-byte segments addressed by lanes 4 y + (j & 15) / 4,
+// y = 0..3 (a 4 x 16 -> 16 x 4 transpose of 16-bit elements)
+typedef __bf16 bf16x4v_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
+  const bf16x4v_t t =
+      __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v_t*)lds);
+  return __builtin_bit_cast(uint2, t);
+}
+
+// max / sum of v over lanes l and l ^ 16 (or l ^ 32): the permlane swaps
+// hand each lane the pair {v[l], v[l ^ d]} in the same order on both lanes
+__device__ __forceinline__ float xmax16(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float xmax32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
+}
+__device__ __forceinline__ float xsum16(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+__device__ __forceinline__ float xsum32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
+}
+
+
+// v_exp_f32 (2^x; -inf -> 0)
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t v;
+  v[0] = (__bf16)a;
+  v[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// (e, o) -> (e c - o s, e s + o c) for a bf16 pair packed in one word, the
+// angle's cos / sin taken from half `hf` of the words cw / sw: two bf16
+// dot2 (exact products, fp32 sum) and one rounding of each output
+__device__ __forceinline__ uint32_t rot_pair(uint32_t eo, uint32_t cw, uint32_t sw, int hf) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const uint32_t sel = hf ? 0x07060302u : 0x05040100u;
+  const uint32_t cs = __builtin_amdgcn_perm(sw, cw, sel) ^ 0x80000000u;  // (c, -s)
+  const uint32_t sc = __builtin_amdgcn_perm(cw, sw, sel);                // (s, c)
+  const bf16x2_t x = __builtin_bit_cast(bf16x2_t, eo);
+  const float r0 = __builtin_amdgcn_fdot2_f32_bf16(x, __builtin_bit_cast(bf16x2_t, cs), 0.f, false);
+  const float r1 = __builtin_amdgcn_fdot2_f32_bf16(x, __builtin_bit_cast(bf16x2_t, sc), 0.f, false);
+  return pk_bf16(r0, r1);
+}
+
+__device__ __forceinline__ void unpack8(const uint4& u, float x[8]) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = bf2f((bf16_t)(w[j] & 0xffffu));
+    x[2 * j + 1] = bf2f((bf16_t)(w[j] >> 16));
+  }
+}
+__device__ __forceinline__ void unpack4(const uint2& u, float x[4]) {
+  x[0] = bf2f((bf16_t)(u.x & 0xffffu));
+  x[1] = bf2f((bf16_t)(u.x >> 16));
+  x[2] = bf2f((bf16_t)(u.y & 0xffffu));
+  x[3] = bf2f((bf16_t)(u.y >> 16));
+}
+
 // ------------------------------------------------------------ fused decode step
 // decode_step_bf16: one workgroup per (KV head hk, sequence b) runs the
 // whole decode step of that pair once the ring is full (the same work as
@@ -812,10 +893,10 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   using T = bf16_t;
   constexpr int NC = DH / 32, NM = DH / 16, NW = 4, NVb = (DH + 63) / 64;
   __shared__ __attribute__((aligned(16))) char vt_smem[NW][VtLayout<DH>::kTileBytes];
-  __shared__ __attribute__((aligned(16))) bf16_t q_lds[16][DH + 8];
   __shared__ uint8_t al_lds[kMaxRowsPrefix];
   __shared__ float red_m[NW][16], red_l[NW][16];
   __shared__ DecodeDecision dec;
+  __shared__ int dec_ready;
   // bank stage during the update; the partial outputs of the 4 waves after
   extern __shared__ __attribute__((aligned(16))) char ds_u[];
   const int hk = blockIdx.x, b = blockIdx.y;
@@ -857,16 +938,41 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       vv[jj] = __builtin_bit_cast(
           uint4, __builtin_amdgcn_raw_buffer_load_b128(nt ? rvn : rv, voff + (nt ? 0 : jj * DH * 2), 0, 0));
   };
-  // visibility of this lane's keys kt + 4 g4 + jj: inside [lo, hi) and
-  // allowed; the new-token tile keeps its key 0 only
-  auto tile_mask = [&](int kt, int lo, int hi, bool nt) {
+  // visibility of this lane's keys kt + 4 g4 + jj of a bank tile: inside
+  // [W, Lbuf) and allowed (LDS copy with this step's update applied)
+  auto tile_mask = [&](int kt) {
     int m4 = 0;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int kk = kt + 4 * g4 + jj;
-      const int in = (kk >= lo) & (kk < hi);
-      const int kc = in ? kk : lo;
-      const int ok = nt ? (kk == kt) : (in & (al_lds[kc] != 0));
+      const int in = (kk >= W) & (kk < Lbuf);
+      m4 |= (in & (al_lds[in ? kk : W] != 0)) << jj;
+    }
+    return m4;
+  };
+  // ring tile kt: inside [0, W), not slot j (the evicted token), allowed
+  // (bytes loaded with the tile); the new-token tile keeps its key 0 only
+  // (raw bytes, loaded unconditionally with the tile and combined at use:
+  // a use right after the load would wait for every load in flight)
+  const uint8_t* al_row = a.allowed + (int64_t)b * a.al_sb;
+  struct Al4 {
+    uint8_t v[4];
+  };
+  auto ring_al = [&](int kt) {
+    Al4 r;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int kk = kt + 4 * g4 + jj;
+      r.v[jj] = al_row[kk < W ? kk : 0];
+    }
+    return r;
+  };
+  auto ring_mask = [&](int kt, bool nt, const Al4& al) {
+    int m4 = 0;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int kk = kt + 4 * g4 + jj;
+      const int ok = nt ? (kk == kt) : ((kk < W) & (kk != j) & (al.v[jj] != 0));
       m4 |= ok << jj;
     }
     return m4;
@@ -881,10 +987,14 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
 
   bf16x8_t kf0[NC], kf1[NC];
   uint4 vv0[4], vv1[4];
+  Al4 al0, al1;
   int vm0 = 0, vm1 = 0;
-  // ---- prologue: first loads of every wave, then the query staging
-  if (wv < 3 && n1_w > 0) issue(p1_kt(wv), wv == nR, kf0, vv0);
-  // bank wave: record and norm rows straight to LDS, evicted / next rows
+  if (threadIdx.x == 0) dec_ready = 0;
+  __syncthreads();
+  // ---- prologue: every wave's first loads; no workgroup barrier until the
+  // end of phase 1
+  // bank wave: record and norm rows straight to LDS, evicted / next rows,
+  // the visibility bytes of the bank slots
   const int LF = DH - s.lf, words = dstep_words(Hkv, Me, Ms);
   const int jn = j + 1 == W ? 0 : j + 1;
   float* rec = reinterpret_cast<float*>(ds_u);
@@ -895,6 +1005,8 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   float* knrm = vnrm + DH;
   bf16_t kev[NVb], vev[NVb], xv_r[NVb], xk_r[NVb];
   bool av[NVb], ak[NVb];
+  constexpr int kAlBank = 4;  // (Me + Ms) <= 256 bank slots: bytes per lane
+  uint8_t alb[kAlBank];
   if (wv == 3) {
     wave_copy_lds(rec, rec_in + (int64_t)b * words, words * 4, lane);
     if (Me > 0)
@@ -918,39 +1030,106 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       xv_r[i] = vx[dc];
       xk_r[i] = kx[s.lf + (ak[i] ? d : 0)];
     }
-  }
-  // epilogue operands
-  constexpr int NV = (DH + 63) / 64;
-  float lam_pf[2] = {0.f, 0.f}, w_pf[NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) w_pf[i] = 1.f;
+    for (int k = 0; k < kAlBank; ++k) {
+      const int m = lane + 64 * k;
+      alb[k] = al_row[W + (m < Me + Ms ? m : 0)];
+    }
+  }
+  // epilogue operands (raw: a conversion here would wait for every load in
+  // flight)
+  constexpr int NV = (DH + 63) / 64;
+  bf16_t lam_r[2] = {0, 0}, w_r[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) w_r[i] = 0x3f80;  // 1.0
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int orow = wv + r * NW;
-    if (orow < G) lam_pf[r] = bf2f(((const T*)a.lam)[b * a.lam_sb + (hk * G + orow) * a.lam_sh]);
+    if (orow < G) lam_r[r] = ((const T*)a.lam)[b * a.lam_sb + (hk * G + orow) * a.lam_sh];
   }
   if (a.rms_w) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) w_pf[i] = bf2f(((const T*)a.rms_w)[min(lane + 64 * i, DH - 1)]);
+    for (int i = 0; i < NV; ++i) w_r[i] = ((const T*)a.rms_w)[min(lane + 64 * i, DH - 1)];
   }
-  stage_queries(a, b, R, &q_lds[0][0], DH + 8, [&](int r, int& st, int& h, int& qi) {
-    st = r / G;
-    h = hk * G + r % G;
-    qi = 0;
-    return true;
-  });
-  // visibility bytes: ring slot j (the evicted token) hidden; the new token
-  // has its own tile
-  for (int i = threadIdx.x; i < Lbuf; i += blockDim.x)
-    al_lds[i] = i == j ? (uint8_t)0 : (a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1);
-  __syncthreads();
+  // query fragments of every wave (B operand of S^T): row n = stream st,
+  // head g; RoPE and the noise rotation as bf16 dot2 pairs, or given noise
+  // queries; the half-split RoPE with the eager-op rounding
   bf16x8_t qf[NC];
   {
+    using E = Elt<T>;
+    constexpr int half = DH / 2;
     const bool live = n < R;
+    const int st = live ? n / G : 0, h = hk * G + (live ? n % G : 0);
+    const bool given = st == 1 && a.q_noise != nullptr;
+    const bool rot = st == 1 && a.q_noise == nullptr;
+    const T* qr = given ? (const T*)a.q_noise + b * a.qn_sb + h * a.qn_sh : (const T*)a.q + b * a.q_sb + h * a.q_sh;
+    const bool rope = a.rope_cos != nullptr && !given, inter = a.rope_interleaved != 0;
+    const T* csr = (const T*)a.rope_cos;
+    const T* snr = (const T*)a.rope_sin;
+    uint4 uq[NC], up[NC], rc[NC], rs[NC];
+    uint2 rc2[NC], rs2[NC], tcs[NC], tsn[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
-      uint4 u = live ? *reinterpret_cast<const uint4*>(&q_lds[n][32 * c + 8 * g4]) : uint4{0, 0, 0, 0};
-      qf[c] = __builtin_bit_cast(bf16x8_t, u);
+      const int d0 = 32 * c + 8 * g4;
+      if (wv == 3) break;  // wave 3 takes its fragments from wave 0 after phase 1
+      uq[c] = *reinterpret_cast<const uint4*>(qr + d0);
+      if (rope && inter) {
+        rc2[c] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
+        rs2[c] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
+      }
+      if (rope && !inter) {
+        const int f0 = d0 < half ? d0 : d0 - half;
+        up[c] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
+        rc[c] = *reinterpret_cast<const uint4*>(csr + f0);
+        rs[c] = *reinterpret_cast<const uint4*>(snr + f0);
+      }
+      if (rot) {
+        tcs[c] = *reinterpret_cast<const uint2*>((const T*)a.theta_cos + (int64_t)h * half + d0 / 2);
+        tsn[c] = *reinterpret_cast<const uint2*>((const T*)a.theta_sin + (int64_t)h * half + d0 / 2);
+      }
+    }
+    // the first ring tile loads behind the queries
+    if (wv < 3 && n1_w > 0) {
+      issue(p1_kt(wv), wv == nR, kf0, vv0);
+      al0 = ring_al(p1_kt(wv));
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d0 = 32 * c + 8 * g4;
+      if (wv == 3) break;
+      uint32_t w[4] = {uq[c].x, uq[c].y, uq[c].z, uq[c].w};
+      if (rope && inter) {
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp)
+          w[pp] = rot_pair(w[pp], pp >> 1 ? rc2[c].y : rc2[c].x, pp >> 1 ? rs2[c].y : rs2[c].x, pp & 1);
+      }
+      if (rope && !inter) {
+        float x[8], cc[8], ss[8], y[8];
+        unpack8(uq[c], x);
+        unpack8(rc[c], cc);
+        unpack8(rs[c], ss);
+        unpack8(up[c], y);
+        const bool lo = d0 < half;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float rt = lo ? -y[jj] : y[jj];
+          x[jj] = E::rnd(E::rnd(x[jj] * cc[jj]) + E::rnd(rt * ss[jj]));
+        }
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) w[pp] = pk_bf16(x[2 * pp], x[2 * pp + 1]);
+      }
+      if (rot) {
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp)
+          w[pp] = rot_pair(w[pp], pp >> 1 ? tcs[c].y : tcs[c].x, pp >> 1 ? tsn[c].y : tsn[c].x, pp & 1);
+      }
+      qf[c] = __builtin_bit_cast(bf16x8_t, live ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
+    }
+    // wave 0 leaves the fragments for wave 3 in wave 3's (idle) V buffer
+    if (wv == 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        reinterpret_cast<uint4*>(vt_smem[3])[c * 64 + lane] = __builtin_bit_cast(uint4, qf[c]);
     }
   }
   float m_i = -INFINITY, l_i = 0.f;
@@ -999,28 +1178,46 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   // ---- phase 1
   if (wv < 3) {
     // ring tiles and the new token, ping-pong register buffers
-    auto mask1 = [&](int i) {
-      const int u = wv + 3 * i;
-      return u < nR ? tile_mask(16 * u, 0, W, false) : (u == nR ? tile_mask(0, 0, 0, true) : 0);
-    };
-    vm0 = n1_w > 0 ? mask1(0) : 0;
     for (int i = 0; i < n1_w; i += 2) {
+      const int u0 = wv + 3 * i;
       if (i + 1 < n1_w) {
         const int u = wv + 3 * (i + 1);
         issue(p1_kt(u), u == nR, kf1, vv1);
-        vm1 = mask1(i + 1);
+        al1 = ring_al(p1_kt(u));
       }
+      vm0 = ring_mask(p1_kt(u0), u0 == nR, al0);
       __builtin_amdgcn_sched_barrier(0);
       consume(kf0, vv0, vm0);
       if (i + 1 >= n1_w) break;
+      const int u1 = wv + 3 * (i + 1);
       if (i + 2 < n1_w) {
         const int u = wv + 3 * (i + 2);
         issue(p1_kt(u), u == nR, kf0, vv0);
-        vm0 = mask1(i + 2);
+        al0 = ring_al(p1_kt(u));
       }
+      vm1 = ring_mask(p1_kt(u1), u1 == nR, al1);
       __builtin_amdgcn_sched_barrier(0);
       consume(kf1, vv1, vm1);
     }
+    // the next step's record: head hk's dots against the norm rows, over
+    // waves 0-2 once wave 3 has published its decision and the unit rows;
+    // the rows its update rewrites are left to wave 3
+    for (int spin = 0; spin < (1 << 22); ++spin) {
+      if (__atomic_load_n(&dec_ready, __ATOMIC_ACQUIRE) != 0) break;
+      __builtin_amdgcn_s_sleep(2);
+    }
+    const int skip_e = Me > 0 && dec.ow_e ? dec.idx_e : -1;
+    const int skip_s = Ms > 0 && dec.keep_s ? dec.idx_s : -1;
+    float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
+    float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
+    if (Me > 0)
+      wave_dots<T, 4>(
+          Me, DH, wv, 3, lane, [&](int it) { return (const T*)stage + it * DH; },
+          [&](int) { return (const float*)vnrm; }, [&](int it, float v) { if (it != skip_e) out_e[it] = v; });
+    if (Ms > 0)
+      wave_dots<T, 4>(
+          Ms, LF, wv, 3, lane, [&](int it) { return (const T*)stage + Me * DH + it * LF; },
+          [&](int) { return (const float*)knrm; }, [&](int it, float v) { if (it != skip_s) out_s[it] = v; });
   } else {
     // the bank update of head hk (one wave)
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): record, norm rows, evicted / next rows
@@ -1054,6 +1251,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     if (Ms > 0) decide_summary<T>(s, L.dots + Hkv * Me, L.used + Me, g_e, dec, hk == 0, lane);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the decision (lane 0) and rows are in LDS
     __builtin_amdgcn_wave_barrier();
+    if (lane == 0) __atomic_store_n(&dec_ready, 1, __ATOMIC_RELEASE);
     const DecodeDecision dd = dec;
     apply_head<T, DH>(s, b, hk, dd, ke, ve, kn_row, vn_row, j, g_e, lane, Me > 0 ? stage + dd.idx_e * DH : nullptr,
                       Ms > 0 ? stage + Me * DH + dd.idx_s * LF : nullptr);
@@ -1070,52 +1268,63 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
         commit_decode_meta(s, b, dd, j, pos - W, g_new[b]);
       }
     }
-    // the slots this update fills become visible to the bank tiles
-    if (lane == 0) {
-      if (Me > 0 && dd.ow_e) al_lds[W + dd.idx_e] = 1;
-      if (Ms > 0 && dd.keep_s) al_lds[W + Me + dd.idx_s] = 1;
+    // visibility bytes of the bank slots, with the slots this update fills
+#pragma unroll
+    for (int k = 0; k < kAlBank; ++k) {
+      const int m = lane + 64 * k;
+      const bool fill = (Me > 0 && dd.ow_e && m == dd.idx_e) || (Ms > 0 && dd.keep_s && m == Me + dd.idx_s);
+      if (m < Me + Ms) al_lds[W + m] = fill ? (uint8_t)1 : alb[k];
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): rewritten norm rows in LDS
+    __builtin_amdgcn_wave_barrier();
+    // the record dots of the norm rows this update rewrote
+    if (Me > 0 && dd.ow_e) {
+      float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
+      const int ie = dd.idx_e;
+      wave_dots<T, 4>(
+          1, DH, 0, 1, lane, [&](int) { return (const T*)stage + ie * DH; }, [&](int) { return (const float*)vnrm; },
+          [&](int, float v) { out_e[ie] = v; });
+    }
+    if (Ms > 0 && dd.keep_s) {
+      float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
+      const int is = dd.idx_s;
+      wave_dots<T, 4>(
+          1, LF, 0, 1, lane, [&](int) { return (const T*)stage + Me * DH + is * LF; },
+          [&](int) { return (const float*)knrm; }, [&](int, float v) { out_s[is] = v; });
     }
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's row writes are done
   }
   __syncthreads();  // bank rows and patched norm rows written by wave 3 visible
+  if (wv == 3) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qf[c] = __builtin_bit_cast(bf16x8_t, reinterpret_cast<const uint4*>(vt_smem[3])[c * 64 + lane]);
+  }
 
   // ---- phase 2: exact and summary slots
   {
     auto kt2 = [&](int i) { return W + 16 * (w2 + 4 * i); };
     if (n2_w > 0) {
       issue(kt2(0), false, kf0, vv0);
-      vm0 = tile_mask(kt2(0), W, Lbuf, false);
+      vm0 = tile_mask(kt2(0));
     }
-    // the next step's record while the first bank tile loads: head hk's
-    // dots against the updated norm rows, over the 4 waves
-    float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
-    float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
-    if (Me > 0)
-      wave_dots<T, 4>(
-          Me, DH, wv, NW, lane, [&](int it) { return (const T*)stage + it * DH; },
-          [&](int) { return (const float*)vnrm; }, [&](int it, float v) { out_e[it] = v; });
-    if (Ms > 0)
-      wave_dots<T, 4>(
-          Ms, LF, wv, NW, lane, [&](int it) { return (const T*)stage + Me * DH + it * LF; },
-          [&](int) { return (const float*)knrm; }, [&](int it, float v) { out_s[it] = v; });
+
     for (int i = 0; i < n2_w; i += 2) {
       if (i + 1 < n2_w) {
         issue(kt2(i + 1), false, kf1, vv1);
-        vm1 = tile_mask(kt2(i + 1), W, Lbuf, false);
+        vm1 = tile_mask(kt2(i + 1));
       }
       __builtin_amdgcn_sched_barrier(0);
       consume(kf0, vv0, vm0);
       if (i + 1 >= n2_w) break;
       if (i + 2 < n2_w) {
         issue(kt2(i + 2), false, kf0, vv0);
-        vm0 = tile_mask(kt2(i + 2), W, Lbuf, false);
+        vm0 = tile_mask(kt2(i + 2));
       }
       __builtin_amdgcn_sched_barrier(0);
       consume(kf1, vv1, vm1);
     }
   }
-  // ---- merge the 4 waves (rows r < R), epilogue
-  __syncthreads();  // every wave is done with the bank stage
+  // ---- merge the 4 waves (rows r < R), epilogue (the bank stage is free)
   float* red_o = reinterpret_cast<float*>(ds_u);  // [NW][R][DH + 4]
   if (g4 == 0) {
     red_m[wv][n] = m_i;
@@ -1160,9 +1369,10 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       os[i] = act[i] ? acc[0] : 0.f;
       on[i] = act[i] ? acc[1] : 0.f;
     }
-    const float lam = r_pf == 0   ? lam_pf[0]
-                      : r_pf == 1 ? lam_pf[1]
-                                  : bf2f(((const T*)a.lam)[b * a.lam_sb + h * a.lam_sh]);
+    const float lam = bf2f(r_pf == 0 ? lam_r[0] : r_pf == 1 ? lam_r[1] : ((const T*)a.lam)[b * a.lam_sb + h * a.lam_sh]);
+    float w_pf[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) w_pf[i] = bf2f(w_r[i]);
     diff_norm_w<NV>(y, os, on, act, lam, a.rms_w ? w_pf : nullptr, a.eps, DH);
     T* orow_p = (T*)a.out + b * a.o_sb + h * a.o_sh;
 #pragma unroll
@@ -1363,86 +1573,6 @@ struct FaLayout {
 template <int DH>
 __device__ __forceinline__ int fa_vswz(int k) {
   return DH == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3);
-}
-
-// 16 bytes per lane global -> LDS (direct load): lane l's bytes land at
-// lds + 16 l (lds wave-uniform); counted in vmcnt
-__device__ __forceinline__ void lds_load16(const void* gsrc, void* lds) {
-  __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane j receives element
-// (j & 3) of the 8-byte segments addressed by lanes 4 y + (j & 15) / 4,
-// y = 0..3 (a 4 x 16 -> 16 x 4 transpose of 16-bit elements)
-typedef __bf16 bf16x4v_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
-  const bf16x4v_t t =
-      __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v_t*)lds);
-  return __builtin_bit_cast(uint2, t);
-}
-
-// max / sum of v over lanes l and l ^ 16 (or l ^ 32): the permlane swaps
-// hand each lane the pair {v[l], v[l ^ d]} in the same order on both lanes
-__device__ __forceinline__ float xmax16(float v) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, v);
-  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
-}
-__device__ __forceinline__ float xmax32(float v) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, v);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1]));
-}
-__device__ __forceinline__ float xsum16(float v) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, v);
-  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
-}
-__device__ __forceinline__ float xsum32(float v) {
-  const uint32_t u = __builtin_bit_cast(uint32_t, v);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
-}
-
-
-// v_exp_f32 (2^x; -inf -> 0)
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  bf16x2_t v;
-  v[0] = (__bf16)a;
-  v[1] = (__bf16)b;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// (e, o) -> (e c - o s, e s + o c) for a bf16 pair packed in one word, the
-// angle's cos / sin taken from half `hf` of the words cw / sw: two bf16
-// dot2 (exact products, fp32 sum) and one rounding of each output
-__device__ __forceinline__ uint32_t rot_pair(uint32_t eo, uint32_t cw, uint32_t sw, int hf) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  const uint32_t sel = hf ? 0x07060302u : 0x05040100u;
-  const uint32_t cs = __builtin_amdgcn_perm(sw, cw, sel) ^ 0x80000000u;  // (c, -s)
-  const uint32_t sc = __builtin_amdgcn_perm(cw, sw, sel);                // (s, c)
-  const bf16x2_t x = __builtin_bit_cast(bf16x2_t, eo);
-  const float r0 = __builtin_amdgcn_fdot2_f32_bf16(x, __builtin_bit_cast(bf16x2_t, cs), 0.f, false);
-  const float r1 = __builtin_amdgcn_fdot2_f32_bf16(x, __builtin_bit_cast(bf16x2_t, sc), 0.f, false);
-  return pk_bf16(r0, r1);
-}
-
-__device__ __forceinline__ void unpack8(const uint4& u, float x[8]) {
-  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    x[2 * j] = bf2f((bf16_t)(w[j] & 0xffffu));
-    x[2 * j + 1] = bf2f((bf16_t)(w[j] >> 16));
-  }
-}
-__device__ __forceinline__ void unpack4(const uint2& u, float x[4]) {
-  x[0] = bf2f((bf16_t)(u.x & 0xffffu));
-  x[1] = bf2f((bf16_t)(u.x >> 16));
-  x[2] = bf2f((bf16_t)(u.y & 0xffffu));
-  x[3] = bf2f((bf16_t)(u.y >> 16));
 }
 
 template <int DH, int NW>
@@ -2014,7 +2144,7 @@ static int validate_step(const coda_bank_desc* s, const coda_attn_desc* a) {
 static bool fused_step_ok(const coda_bank_desc* s, const coda_attn_desc* a) {
   const int G = a->H / a->Hkv;
   return s->dtype == CODA_BF16 && (s->Dh == 64 || s->Dh == 128) && 2 * G <= 16 && s->W >= 16 &&
-         s->W + s->Me + s->Ms <= kMaxRowsPrefix && a->causal == 0;
+         s->Me + s->Ms <= 256 && s->W + s->Me + s->Ms <= kMaxRowsPrefix && a->causal == 0 && a->allowed != nullptr;
 }
 
 template <int DH>

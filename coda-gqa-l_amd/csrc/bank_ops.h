@@ -26,32 +26,105 @@ __device__ __forceinline__ float neg_fill() {
   return Elt<T>::rnd(-1e9f);
 }
 
+// Wave reductions for order-free combines (max / min with index ties,
+// or, and): DPP within 16-lane rows (xor 1, xor 2, half-row mirror, row
+// mirror), then the gfx950 permlane swaps across rows (16, 32), which
+// hand both lanes of a pair the same two values in the same order.  Every
+// lane ends with the result.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+struct Pair2 {
+  int a, b;
+};
+__device__ __forceinline__ Pair2 swap16(int v) {
+  const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  return Pair2{(int)r[0], (int)r[1]};
+}
+__device__ __forceinline__ Pair2 swap32(int v) {
+  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return Pair2{(int)r[0], (int)r[1]};
+}
+
 // (value, index) arg-max with first-occurrence ties, across a wave.
+__device__ __forceinline__ void argmax_step(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+  argmax_step(v, i, dpp_f<0xB1>(v), dpp_i<0xB1>(i));
+  argmax_step(v, i, dpp_f<0x4E>(v), dpp_i<0x4E>(i));
+  argmax_step(v, i, dpp_f<0x141>(v), dpp_i<0x141>(i));
+  argmax_step(v, i, dpp_f<0x140>(v), dpp_i<0x140>(i));
+  {
+    const Pair2 pv = swap16(__builtin_bit_cast(int, v)), pi = swap16(i);
+    v = __builtin_bit_cast(float, pv.a);
+    i = pi.a;
+    argmax_step(v, i, __builtin_bit_cast(float, pv.b), pi.b);
+  }
+  {
+    const Pair2 pv = swap32(__builtin_bit_cast(int, v)), pi = swap32(i);
+    v = __builtin_bit_cast(float, pv.a);
+    i = pi.a;
+    argmax_step(v, i, __builtin_bit_cast(float, pv.b), pi.b);
   }
 }
+__device__ __forceinline__ void argmin64_step(int64_t& v, int& i, int64_t ov, int oi) {
+  if (ov < v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp_i64(int64_t v) {
+  const int lo = dpp_i<CTRL>((int)(uint32_t)v), hi = dpp_i<CTRL>((int)(v >> 32));
+  return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
 __device__ __forceinline__ void wave_argmin_i64(int64_t& v, int& i) {
+  argmin64_step(v, i, dpp_i64<0xB1>(v), dpp_i<0xB1>(i));
+  argmin64_step(v, i, dpp_i64<0x4E>(v), dpp_i<0x4E>(i));
+  argmin64_step(v, i, dpp_i64<0x141>(v), dpp_i<0x141>(i));
+  argmin64_step(v, i, dpp_i64<0x140>(v), dpp_i<0x140>(i));
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const int64_t ov = __shfl_xor(v, o, 64);
-    const int oi = __shfl_xor(i, o, 64);
-    if (ov < v || (ov == v && oi < i)) { v = ov; i = oi; }
+  for (int st = 0; st < 2; ++st) {
+    const Pair2 lo = st ? swap32((int)(uint32_t)v) : swap16((int)(uint32_t)v);
+    const Pair2 hi = st ? swap32((int)(v >> 32)) : swap16((int)(v >> 32));
+    const Pair2 pi = st ? swap32(i) : swap16(i);
+    v = (int64_t)(((uint64_t)(uint32_t)hi.a << 32) | (uint32_t)lo.a);
+    i = pi.a;
+    argmin64_step(v, i, (int64_t)(((uint64_t)(uint32_t)hi.b << 32) | (uint32_t)lo.b), pi.b);
   }
 }
 __device__ __forceinline__ int wave_or(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
-  return v;
+  v |= dpp_i<0xB1>(v);
+  v |= dpp_i<0x4E>(v);
+  v |= dpp_i<0x141>(v);
+  v |= dpp_i<0x140>(v);
+  Pair2 p = swap16(v);
+  v = p.a | p.b;
+  p = swap32(v);
+  return p.a | p.b;
 }
 __device__ __forceinline__ int wave_and(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v &= __shfl_xor(v, o, 64);
-  return v;
+  v &= dpp_i<0xB1>(v);
+  v &= dpp_i<0x4E>(v);
+  v &= dpp_i<0x141>(v);
+  v &= dpp_i<0x140>(v);
+  Pair2 p = swap16(v);
+  v = p.a & p.b;
+  p = swap32(v);
+  return p.a & p.b;
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = min(v, dpp_i<0xB1>(v));
+  v = min(v, dpp_i<0x4E>(v));
+  v = min(v, dpp_i<0x141>(v));
+  v = min(v, dpp_i<0x140>(v));
+  Pair2 p = swap16(v);
+  v = min(p.a, p.b);
+  p = swap32(v);
+  return min(p.a, p.b);
 }
 
 __device__ __forceinline__ void atomic_add_i64(int64_t* p, int64_t v) {
@@ -107,28 +180,51 @@ __device__ __forceinline__ void wave_dots(int n_items, int len, int wave, int n_
   const int ipw = 64 / lpi;          // items per wave per unrolled slot
   const int grp = lane / lpi, sub = lane % lpi;
   for (int base = wave * ipw * U; base < n_items; base += n_waves * ipw * U) {
-    float x[U][8];
+    // every load unconditional (items past the end re-read the last row,
+    // their result is dropped) and raw, so all of them are in flight before
+    // the first use
+    uint4 xr[U][sizeof(T) / 2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int item = base + u * ipw + grp;
-      if (item < n_items) {
-        load8f<T>(row_ptr(item) + 8 * sub, x[u]);
-      } else {
+      int item = base + u * ipw + grp;
+      item = item < n_items ? item : n_items - 1;
+      const uint4* p = reinterpret_cast<const uint4*>(row_ptr(item) + 8 * sub);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) x[u][j] = 0.f;
-      }
+      for (int k = 0; k < (int)(sizeof(T) / 2); ++k) xr[u][k] = p[k];
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int item = base + u * ipw + grp;
-      float acc = 0.f;
-      if (item < n_items) {
-        const float* v = vec_ptr(item) + 8 * sub;
+      int item = base + u * ipw + grp;
+      const bool live = item < n_items;
+      item = live ? item : n_items - 1;
+      float x[8];
+      if constexpr (sizeof(T) == 2) {
+        const uint32_t w[4] = {xr[u][0].x, xr[u][0].y, xr[u][0].z, xr[u][0].w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc = fmaf(v[j], x[u][j], acc);
+        for (int i = 0; i < 4; ++i) {
+          x[2 * i] = bf2f((bf16_t)(w[i] & 0xffffu));
+          x[2 * i + 1] = bf2f((bf16_t)(w[i] >> 16));
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          x[4 * k] = __builtin_bit_cast(float, xr[u][k].x);
+          x[4 * k + 1] = __builtin_bit_cast(float, xr[u][k].y);
+          x[4 * k + 2] = __builtin_bit_cast(float, xr[u][k].z);
+          x[4 * k + 3] = __builtin_bit_cast(float, xr[u][k].w);
+        }
       }
-      for (int o = lpi >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-      if (item < n_items && sub == 0) out(item, Elt<T>::rnd(acc));
+      const float* v = vec_ptr(item) + 8 * sub;
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf(v[j], x[j], acc);
+      // group sum over the lpi lanes of the item (DPP within the 16-lane
+      // row; every lane of the group ends with the same value)
+      if (lpi >= 2) acc += dpp_f<0xB1>(acc);
+      if (lpi >= 4) acc += dpp_f<0x4E>(acc);
+      if (lpi >= 8) acc += dpp_f<0x141>(acc);
+      if (lpi >= 16) acc += dpp_f<0x140>(acc);
+      if (live && sub == 0) out(item, Elt<T>::rnd(acc));
     }
   }
 }
@@ -169,8 +265,7 @@ __device__ __forceinline__ void decide_exact(const coda_bank_desc& s, const floa
   }
   wave_argmax(bv, bi);
   any_used = wave_or(any_used);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) free_i = min(free_i, __shfl_xor(free_i, o, 64));
+  free_i = wave_min_i(free_i);
   wave_argmin_i64(lv, li);
   if (lane == 0) {
     const bool keep = s.gated ? (g_e >= s.tau_exact) : true;
@@ -266,6 +361,8 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
   T* krs = kb + (int64_t)(W + Me + idx_s) * DH;
   T* vrs = vb + (int64_t)(W + Me + idx_s) * DH;
   float mke[NV], mve[NV], mks[NV], mvs[NV], kn[NV], vn[NV];
+  // every load in one batch (eta's logit included)
+  const float eta_l = Ms > 0 ? s.eta_logit[h] : 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int d = min(lane + 64 * i, DH - 1);
@@ -300,7 +397,7 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
       }
   }
   if (do_s) {
-    float eta = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
+    float eta = E::rnd(1.f / (1.f + expf(-eta_l)));
     if (s.gated) eta = E::rnd(eta * E::rnd(g_e));
     if (s.overwrite_on_insert && dec.new_s) eta = 1.f;
     float nk[NV];
