@@ -897,6 +897,9 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   __shared__ float red_m[NW][16], red_l[NW][16];
   __shared__ DecodeDecision dec;
   __shared__ int dec_ready;
+  // the rows the bank update rewrites: K, V of the exact slot, K, V of the
+  // summary slot (new values, for the bank tiles loaded before the update)
+  __shared__ __attribute__((aligned(16))) T newrows[4][DH];
   // bank stage during the update; the partial outputs of the 4 waves after
   extern __shared__ __attribute__((aligned(16))) char ds_u[];
   const int hk = blockIdx.x, b = blockIdx.y;
@@ -956,7 +959,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   // a use right after the load would wait for every load in flight)
   const uint8_t* al_row = a.allowed + (int64_t)b * a.al_sb;
   struct Al4 {
-    uint8_t v[4];
+    uint32_t v[4];  // 32-bit: byte values packed into one register would need the loads first
   };
   auto ring_al = [&](int kt) {
     Al4 r;
@@ -984,6 +987,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   // phase 2 tiles: bank tile u of wave (u + 3) % 4
   const int w2 = (wv + 1) & 3;
   const int n2_w = nB > w2 ? (nB - w2 + 3) / 4 : 0;      // tiles u = w2 + 4 i
+  auto kt2 = [&](int i) { return W + 16 * (w2 + 4 * i); };
 
   bf16x8_t kf0[NC], kf1[NC];
   uint4 vv0[4], vv1[4];
@@ -1003,17 +1007,19 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   float* ve = ke + DH;
   float* vnrm = ve + DH;
   float* knrm = vnrm + DH;
-  bf16_t kev[NVb], vev[NVb], xv_r[NVb], xk_r[NVb];
+  // raw values in 32-bit registers: packing 16- or 8-bit values would make
+  // the compiler wait for the loads here
+  uint32_t kev[NVb], vev[NVb], xv_r[NVb], xk_r[NVb];
   bool av[NVb], ak[NVb];
   constexpr int kAlBank = 4;  // (Me + Ms) <= 256 bank slots: bytes per lane
-  uint8_t alb[kAlBank];
+  uint32_t alb[kAlBank];
   if (wv == 3) {
-    wave_copy_lds(rec, rec_in + (int64_t)b * words, words * 4, lane);
-    if (Me > 0)
-      wave_copy_lds(stage, (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH, Me * DH * 2, lane);
-    if (Ms > 0)
-      wave_copy_lds(stage + Me * DH, (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF, Ms * LF * 2,
-                    lane);
+    const float* src_r = rec_in + (int64_t)b * words;
+    const T* src_e = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH;
+    const T* src_s = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF;
+    wave_copy_lds(rec, src_r, words * 4, lane);
+    if (Me > 0) wave_copy_lds(stage, src_e, Me * DH * 2, lane);
+    if (Ms > 0) wave_copy_lds(stage + Me * DH, src_s, Ms * LF * 2, lane);
     const int64_t plane = ((int64_t)b * Hkv + hk) * Lbuf;
     const T* kr = (const T*)s.k_buf + (plane + j) * DH;
     const T* vr = (const T*)s.v_buf + (plane + j) * DH;
@@ -1039,18 +1045,19 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   // epilogue operands (raw: a conversion here would wait for every load in
   // flight)
   constexpr int NV = (DH + 63) / 64;
-  bf16_t lam_r[2] = {0, 0}, w_r[NV];
+  uint32_t lam_r[2] = {0, 0}, w_r[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) w_r[i] = 0x3f80;  // 1.0
+  // (unconditional, from clamped valid addresses: a branch would end in a
+  // wait for the loads)
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
-    const int orow = wv + r * NW;
-    if (orow < G) lam_r[r] = ((const T*)a.lam)[b * a.lam_sb + (hk * G + orow) * a.lam_sh];
+    const int orow = min(wv + r * NW, G - 1);
+    lam_r[r] = ((const T*)a.lam)[b * a.lam_sb + (hk * G + orow) * a.lam_sh];
   }
-  if (a.rms_w) {
+  const T* w_src = a.rms_w ? (const T*)a.rms_w : (const T*)a.lam;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) w_r[i] = ((const T*)a.rms_w)[min(lane + 64 * i, DH - 1)];
-  }
+  for (int i = 0; i < NV; ++i) w_r[i] = w_src[a.rms_w ? min(lane + 64 * i, DH - 1) : 0];
   // query fragments of every wave (B operand of S^T): row n = stream st,
   // head g; RoPE and the noise rotation as bf16 dot2 pairs, or given noise
   // queries; the half-split RoPE with the eager-op rounding
@@ -1199,6 +1206,10 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       __builtin_amdgcn_sched_barrier(0);
       consume(kf1, vv1, vm1);
     }
+    // the first two bank tiles load now (a row the bank update rewrites is
+    // replaced from LDS after the barrier)
+    if (n2_w > 0) issue(kt2(0), false, kf0, vv0);
+    if (n2_w > 1) issue(kt2(1), false, kf1, vv1);
     // the next step's record: head hk's dots against the norm rows, over
     // waves 0-2 once wave 3 has published its decision and the unit rows;
     // the rows its update rewrites are left to wave 3
@@ -1225,11 +1236,11 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
 #pragma unroll
     for (int i = 0; i < NVb; ++i) {
       if (av[i]) {
-        ke[lane + 64 * i] = bf2f(kev[i]);
-        ve[lane + 64 * i] = bf2f(vev[i]);
+        ke[lane + 64 * i] = bf2f((bf16_t)kev[i]);
+        ve[lane + 64 * i] = bf2f((bf16_t)vev[i]);
       }
-      xv[i] = av[i] ? bf2f(xv_r[i]) : 0.f;
-      xk[i] = ak[i] ? bf2f(xk_r[i]) : 0.f;
+      xv[i] = av[i] ? bf2f((bf16_t)xv_r[i]) : 0.f;
+      xk[i] = ak[i] ? bf2f((bf16_t)xk_r[i]) : 0.f;
     }
     // unit rows of the token evicted next (for the next record's dots,
     // taken by every wave after the barrier)
@@ -1254,7 +1265,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     if (lane == 0) __atomic_store_n(&dec_ready, 1, __ATOMIC_RELEASE);
     const DecodeDecision dd = dec;
     apply_head<T, DH>(s, b, hk, dd, ke, ve, kn_row, vn_row, j, g_e, lane, Me > 0 ? stage + dd.idx_e * DH : nullptr,
-                      Ms > 0 ? stage + Me * DH + dd.idx_s * LF : nullptr);
+                      Ms > 0 ? stage + Me * DH + dd.idx_s * LF : nullptr, &newrows[0][0]);
     if (hk == 0) {
       // metadata of the sequence, and the next record's snapshot of it
       const DStepWs wn = dstep_ws(rec_out, b, Hkv, Me, Ms);
@@ -1273,8 +1284,12 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     for (int k = 0; k < kAlBank; ++k) {
       const int m = lane + 64 * k;
       const bool fill = (Me > 0 && dd.ow_e && m == dd.idx_e) || (Ms > 0 && dd.keep_s && m == Me + dd.idx_s);
-      if (m < Me + Ms) al_lds[W + m] = fill ? (uint8_t)1 : alb[k];
+      if (m < Me + Ms) al_lds[W + m] = fill ? (uint8_t)1 : (uint8_t)alb[k];
     }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's row writes are done (the ring
+                                         // waves read them after the barrier; its own tiles below)
+    if (n2_w > 0) issue(kt2(0), false, kf0, vv0);
+    if (n2_w > 1) issue(kt2(1), false, kf1, vv1);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): rewritten norm rows in LDS
     __builtin_amdgcn_wave_barrier();
     // the record dots of the norm rows this update rewrote
@@ -1292,9 +1307,8 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
           1, LF, 0, 1, lane, [&](int) { return (const T*)stage + Me * DH + is * LF; },
           [&](int) { return (const float*)knrm; }, [&](int, float v) { out_s[is] = v; });
     }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's row writes are done
   }
-  __syncthreads();  // bank rows and patched norm rows written by wave 3 visible
+  __syncthreads();  // bank rows, new rows and patched norm rows written by wave 3 visible
   if (wv == 3) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) qf[c] = __builtin_bit_cast(bf16x8_t, reinterpret_cast<const uint4*>(vt_smem[3])[c * 64 + lane]);
@@ -1302,15 +1316,32 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
 
   // ---- phase 2: exact and summary slots
   {
-    auto kt2 = [&](int i) { return W + 16 * (w2 + 4 * i); };
+    // the first two bank tiles were loaded before the barrier: rows this
+    // step's update rewrote come from LDS
+    const int re = Me > 0 && dec.ow_e ? W + dec.idx_e : -1;
+    const int rs = Ms > 0 && dec.keep_s ? W + Me + dec.idx_s : -1;
+    auto patch = [&](int kt, bf16x8_t (&kf)[NC], uint4 (&vv)[4]) {
+      const int rk = kt + n;
+      if (rk == re || rk == rs) {
+        const T* src = newrows[rk == re ? 0 : 2];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) kf[c] = *reinterpret_cast<const bf16x8_t*>(src + 32 * c + 8 * g4);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int rv = kt + 4 * (kgl & 3) + jj;
+        if (rv == re || rv == rs) vv[jj] = *reinterpret_cast<const uint4*>(newrows[rv == re ? 1 : 3] + 8 * dcl);
+      }
+    };
     if (n2_w > 0) {
-      issue(kt2(0), false, kf0, vv0);
+      patch(kt2(0), kf0, vv0);
       vm0 = tile_mask(kt2(0));
     }
+    if (n2_w > 1) patch(kt2(1), kf1, vv1);
 
     for (int i = 0; i < n2_w; i += 2) {
       if (i + 1 < n2_w) {
-        issue(kt2(i + 1), false, kf1, vv1);
+        if (i + 1 > 1) issue(kt2(i + 1), false, kf1, vv1);
         vm1 = tile_mask(kt2(i + 1));
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -1369,10 +1400,10 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       os[i] = act[i] ? acc[0] : 0.f;
       on[i] = act[i] ? acc[1] : 0.f;
     }
-    const float lam = bf2f(r_pf == 0 ? lam_r[0] : r_pf == 1 ? lam_r[1] : ((const T*)a.lam)[b * a.lam_sb + h * a.lam_sh]);
+    const float lam = bf2f((bf16_t)(r_pf == 0 ? lam_r[0] : r_pf == 1 ? lam_r[1] : ((const T*)a.lam)[b * a.lam_sb + h * a.lam_sh]));
     float w_pf[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) w_pf[i] = bf2f(w_r[i]);
+    for (int i = 0; i < NV; ++i) w_pf[i] = bf2f((bf16_t)w_r[i]);
     diff_norm_w<NV>(y, os, on, act, lam, a.rms_w ? w_pf : nullptr, a.eps, DH);
     T* orow_p = (T*)a.out + b * a.o_sb + h * a.o_sh;
 #pragma unroll

@@ -346,7 +346,7 @@ template <typename T, int DH>
 __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h, const DecodeDecision& dec,
                                            const float* ke, const float* ve, const T* kn_src, const T* vn_src,
                                            int j, float g_e, int lane, T* patch_e = nullptr,
-                                           T* patch_s = nullptr) {
+                                           T* patch_s = nullptr, T* rows_out = nullptr) {
   using E = Elt<T>;
   constexpr int NV = (DH + 63) / 64;
   const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, lf = s.lf, LF = DH - lf;
@@ -382,9 +382,14 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
       act[i] = d < DH;
       nv[i] = 0.f;
       if (act[i]) {
-        kre[d] = E::st(mke[i] + E::rnd(ke[d] - mke[i]));
+        const T kv = E::st(mke[i] + E::rnd(ke[d] - mke[i]));
+        kre[d] = kv;
         nv[i] = E::rnd(mve[i] + E::rnd(ve[d] - mve[i]));
         vre[d] = E::st(nv[i]);
+        if (rows_out) {
+          rows_out[d] = kv;
+          rows_out[DH + d] = E::st(nv[i]);
+        }
       }
     }
     wave_unit<T, NV>(nv, act);
@@ -408,11 +413,17 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
       act[i] = false;
       nk[i] = 0.f;
       if (d < DH) {
-        vrs[d] = E::st(mvs[i] + E::rnd(eta * E::rnd(ve[d] - mvs[i])));
+        const T vv = E::st(mvs[i] + E::rnd(eta * E::rnd(ve[d] - mvs[i])));
+        vrs[d] = vv;
+        if (rows_out) {
+          rows_out[3 * DH + d] = vv;
+          rows_out[2 * DH + d] = E::st(mks[i]);
+        }
         if (d >= lf) {
           const float dk = E::rnd(E::rnd(ke[d] * s.energy_scale) - mks[i]);
           nk[i] = E::rnd(mks[i] + E::rnd(eta * dk));
           krs[d] = E::st(nk[i]);
+          if (rows_out) rows_out[2 * DH + d] = E::st(nk[i]);
           act[i] = true;
         }
       }
