@@ -205,9 +205,11 @@ int coda_decode_write(const coda_bank_desc* s, const void* k_new, const void* v_
  * describes that attention: Lq = 1, prefix = the state cache of `s`
  * (Lp = Lbuf, contiguous), no block keys.  With a full ring the bank update
  * runs from a routing record (per-head cosine dots of the evicted row with
- * the norm caches + a snapshot of the bank metadata), one workgroup per
- * (head, sequence), and leaves the routing record of the next token in the
- * workspace; then the attention kernel runs.  The workspace holds two
+ * the norm caches + a snapshot of the bank metadata) and leaves the routing
+ * record of the next token in the workspace.  bf16 with head_dim 64 / 128
+ * and G <= 8: one launch, one workgroup per (head, sequence) doing the bank
+ * update and the attention together; otherwise a bank kernel, then the
+ * attention kernel.  The workspace holds two
  * records, picked by the parity of `pos`, followed by the attention
  * kernel's scratch.  routed (in/out, may be NULL): on entry nonzero when the
  * record for this call was left by the previous call on the same state and
