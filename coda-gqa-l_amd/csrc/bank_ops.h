@@ -31,26 +31,6 @@ __device__ __forceinline__ float neg_fill() {
 // mirror), then the gfx950 permlane swaps across rows (16, 32), which
 // hand both lanes of a pair the same two values in the same order.  Every
 // lane ends with the result.
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
-}
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
-}
-struct Pair2 {
-  int a, b;
-};
-__device__ __forceinline__ Pair2 swap16(int v) {
-  const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
-  return Pair2{(int)r[0], (int)r[1]};
-}
-__device__ __forceinline__ Pair2 swap32(int v) {
-  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
-  return Pair2{(int)r[0], (int)r[1]};
-}
-
 // (value, index) arg-max with first-occurrence ties, across a wave.
 __device__ __forceinline__ void argmax_step(float& v, int& i, float ov, int oi) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }

@@ -402,29 +402,28 @@ __device__ __forceinline__ float cand_gate(const coda_bank_desc& s, const BlockG
 
 // Rows x cands dots from LDS, 4 x 4 register blocks, fp32 FMA in channel
 // order; result rounded to the element type (the matmul output dtype).
-template <typename T>
-__device__ __forceinline__ void lds_dots(const float* rows, int n_rows, const float* cands, int n_c, int len,
-                                         int stride, float* out /* [n_c][n_rows] */) {
-  const int nbr = (n_rows + 3) >> 2, nbc = (n_c + 3) >> 2;
+template <typename T, int RB, int CB>
+__device__ __forceinline__ void lds_dots_blk(const float* rows, int n_rows, const float* cands, int n_c, int len,
+                                             int stride, float* out /* [n_c][n_rows] */) {
+  const int nbr = (n_rows + RB - 1) / RB, nbc = (n_c + CB - 1) / CB;
   for (int blk = threadIdx.x; blk < nbr * nbc; blk += blockDim.x) {
-    const int r0 = 4 * (blk % nbr), c0 = 4 * (blk / nbr);
-    float acc[4][4];
+    const int r0 = RB * (blk % nbr), c0 = CB * (blk / nbr);
+    float acc[RB][CB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+      for (int j = 0; j < CB; ++j) acc[i][j] = 0.f;
+#pragma unroll 2
     for (int d = 0; d < len; d += 4) {
-      float4 rv[4], cv[4];
+      float4 rv[RB], cv[CB];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = min(r0 + i, n_rows - 1), c = min(c0 + i, n_c - 1);
-        rv[i] = *reinterpret_cast<const float4*>(rows + r * stride + d);
-        cv[i] = *reinterpret_cast<const float4*>(cands + c * stride + d);
-      }
+      for (int i = 0; i < RB; ++i) rv[i] = *reinterpret_cast<const float4*>(rows + min(r0 + i, n_rows - 1) * stride + d);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < CB; ++j) cv[j] = *reinterpret_cast<const float4*>(cands + min(c0 + j, n_c - 1) * stride + d);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int j = 0; j < CB; ++j) {
           acc[i][j] = fmaf(cv[j].x, rv[i].x, acc[i][j]);
           acc[i][j] = fmaf(cv[j].y, rv[i].y, acc[i][j]);
           acc[i][j] = fmaf(cv[j].z, rv[i].z, acc[i][j]);
@@ -432,11 +431,22 @@ __device__ __forceinline__ void lds_dots(const float* rows, int n_rows, const fl
         }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < CB; ++j)
         if (r0 + i < n_rows && c0 + j < n_c) out[(c0 + j) * n_rows + r0 + i] = Elt<T>::rnd(acc[i][j]);
   }
+}
+// out[c][r] = rnd(dot(cands[c], rows[r])), each an fma chain over the
+// channels in order (the same value whatever the blocking); blocks of
+// 4 x 4 dots per thread when there are enough of them, else 2 x 1
+template <typename T>
+__device__ __forceinline__ void lds_dots(const float* rows, int n_rows, const float* cands, int n_c, int len,
+                                         int stride, float* out /* [n_c][n_rows] */) {
+  if (((n_rows + 3) / 4) * ((n_c + 3) / 4) >= (int)blockDim.x)
+    lds_dots_blk<T, 4, 4>(rows, n_rows, cands, n_c, len, stride, out);
+  else
+    lds_dots_blk<T, 2, 1>(rows, n_rows, cands, n_c, len, stride, out);
 }
 
 // Stage `n` rows of `len` elements (row stride `rs` elements) into LDS fp32
@@ -491,6 +501,53 @@ __device__ __forceinline__ void stage_cands(float* dst, int ls, const coda_bank_
 #pragma unroll
       for (int i = 0; i < NV; ++i)
         if (act[i]) dst[(r0 + u) * ls + lane + 64 * i] = x[u][i];
+    }
+  }
+}
+
+// The chunk's candidates of head h, normalised (F.normalize, rounded as the
+// reference) into LDS: the first Te as exact V rows (all DH channels) into
+// dst_e, all Ts as summary LF-K bands (channels lf ..) into dst_s.  Every
+// wave takes rows r = wv + nw u of the concatenated list; all plan indices
+// of a pass load first, then all candidate rows, then the normalisation.
+template <typename T, int DH>
+__device__ __forceinline__ void stage_cands_both(float* dst_e, int le, float* dst_s, int lsum, const coda_bank_desc& s,
+                                                 const BlockGeom& g, const T* vbk, const T* kbk, const int32_t* pc,
+                                                 int b, int h) {
+  constexpr int NV = (DH + 63) / 64, RB = 12;
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int Te = g.Te, n = g.Te + g.Ts, lf = s.lf, LF = DH - lf;
+  for (int r0 = 0; r0 < n; r0 += nw * RB) {
+    int idx[RB];
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const int r = min(r0 + wv + nw * u, n - 1);
+      idx[u] = pc[r < Te ? r : r - Te];
+    }
+    float x[RB][NV];
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const int r = min(r0 + wv + nw * u, n - 1);
+      const bool ex = r < Te;
+      const T* row = cand_row<T, DH>(s, g, ex ? vbk : kbk, b, h, idx[u], ex) + (ex ? 0 : lf);
+      const int len = ex ? DH : LF;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) x[u][i] = lane + 64 * i < len ? Elt<T>::ld(row[lane + 64 * i]) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < RB; ++u) {
+      const int r = r0 + wv + nw * u;
+      if (r >= n) break;
+      const bool ex = r < Te;
+      const int len = ex ? DH : LF;
+      bool act[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) act[i] = lane + 64 * i < len;
+      wave_unit<T, NV>(x[u], act);
+      float* dst = ex ? dst_e + r * le : dst_s + (r - Te) * lsum;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) dst[lane + 64 * i] = x[u][i];
     }
   }
 }
@@ -557,8 +614,7 @@ __global__ __launch_bounds__(256) void block_route_kernel(const coda_bank_desc s
   if (g.Te > 0) stage_rows<T>(nrm_e, le, (const T*)s.exact_v_norm + ((int64_t)b * s.Hkv + h) * Me * DH, DH, Me, DH);
   if (g.Ts > 0)
     stage_rows<T>(nrm_s, lsum, (const T*)s.sum_lf_k_norm + ((int64_t)b * s.Hkv + h) * Ms * LF, LF, Ms, LF);
-  if (g.Te > 0) stage_cands<T, DH>(cnd_e, le, s, g, vbk, pc, b, h, g.Te, 0, DH, true);
-  if (g.Ts > 0) stage_cands<T, DH>(cnd_s, lsum, s, g, kbk, pc, b, h, g.Ts, s.lf, LF, false);
+  stage_cands_both<T, DH>(cnd_e, le, cnd_s, lsum, s, g, vbk, kbk, pc, b, h);
   __syncthreads();
   if (g.Te > 0) lds_dots<T>(nrm_e, Me, cnd_e, g.Te, DH, le, ws + (((int64_t)b * s.Hkv + h) * g.Te) * Me);
   if (g.Ts > 0)

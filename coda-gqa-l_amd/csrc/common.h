@@ -57,15 +57,51 @@ template <> struct Elt<bf16_t> {
 };
 
 // ----------------------------------------------------------------- wave64
+// Cross-lane moves without LDS traffic: DPP within 16-lane rows, the gfx950
+// permlane swaps across rows (each hands both lanes of a pair the same two
+// values in the same order).
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, dpp_i<CTRL>(__builtin_bit_cast(int, v)));
+}
+struct Pair2 {
+  int a, b;
+};
+__device__ __forceinline__ Pair2 swap16(int v) {
+  const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+  return Pair2{(int)r[0], (int)r[1]};
+}
+__device__ __forceinline__ Pair2 swap32(int v) {
+  const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+  return Pair2{(int)r[0], (int)r[1]};
+}
+
+// Sum over the wave, the same value in every lane: pairs at distance 1 and
+// 2 (quad permutes), then quad pairs (half-row mirror), 8-lane halves (row
+// mirror), rows (swap16), half waves (swap32).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
+  Pair2 p = swap16(__builtin_bit_cast(int, v));
+  v = __builtin_bit_cast(float, p.a) + __builtin_bit_cast(float, p.b);
+  p = swap32(__builtin_bit_cast(int, v));
+  return __builtin_bit_cast(float, p.a) + __builtin_bit_cast(float, p.b);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  Pair2 p = swap16(__builtin_bit_cast(int, v));
+  v = fmaxf(__builtin_bit_cast(float, p.a), __builtin_bit_cast(float, p.b));
+  p = swap32(__builtin_bit_cast(int, v));
+  return fmaxf(__builtin_bit_cast(float, p.a), __builtin_bit_cast(float, p.b));
 }
 
 }  // namespace coda
