@@ -384,7 +384,11 @@ __device__ __forceinline__ const T* cand_row(const coda_bank_desc& s, const Bloc
                                              int h, int e, bool value) {
   const int Lbuf = s.W + s.Me + s.Ms;
   if (e < g.ring_filled) {
-    const int slot = (g.ring_filled == s.W) ? (g.ring_head + e) % s.W : e;
+    int slot = e;
+    if (g.ring_filled == s.W) {  // circular ring: e < W and ring_head < W, one wrap at most
+      slot = g.ring_head + e;
+      slot -= slot >= s.W ? s.W : 0;
+    }
     const T* buf = (const T*)(value ? s.v_buf : s.k_buf);
     return buf + (((int64_t)b * s.Hkv + h) * Lbuf + slot) * DH;
   }
@@ -394,7 +398,11 @@ __device__ __forceinline__ const T* cand_row(const coda_bank_desc& s, const Bloc
 __device__ __forceinline__ float cand_gate(const coda_bank_desc& s, const BlockGeom& g, const float* gb, int b,
                                            int e) {
   if (e < g.ring_filled) {
-    const int slot = (g.ring_filled == s.W) ? (g.ring_head + e) % s.W : e;
+    int slot = e;
+    if (g.ring_filled == s.W) {
+      slot = g.ring_head + e;
+      slot -= slot >= s.W ? s.W : 0;
+    }
     return s.g_recent[(int64_t)b * s.W + slot];
   }
   return gb[(int64_t)b * g.g_sb + (e - g.ring_filled)];
