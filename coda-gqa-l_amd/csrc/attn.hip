@@ -36,6 +36,7 @@
 #include "common.h"
 
 #include <math.h>
+#include <type_traits>
 #include <stdlib.h>
 
 namespace coda {
@@ -829,6 +830,13 @@ __device__ __forceinline__ float xsum32(float v) {
 }
 
 
+// chunk position of V row k is chunk ^ fa_vswz<DH>(k) (even, so the two
+// chunks of a 32-byte channel group stay adjacent)
+template <int DH>
+__device__ __forceinline__ int fa_vswz(int k) {
+  return DH == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3);
+}
+
 // v_exp_f32 (2^x; -inf -> 0)
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -870,19 +878,23 @@ __device__ __forceinline__ void unpack4(const uint2& u, float x[4]) {
 }
 
 // ------------------------------------------------------------ fused decode step
+static constexpr int kFusedMaxBank = 256;  // exact + summary slots of the fused step
 // decode_step_bf16: one workgroup per (KV head hk, sequence b) runs the
 // whole decode step of that pair once the ring is full (the same work as
 // decode_bank_kernel followed by attn_rows_bf16):
 //   wave 3     the bank update of head hk for the token evicted from ring
 //              slot j: decisions from the carried routing record, row
-//              writes, metadata, the next step's record;
+//              writes, metadata, the dots of the norm rows it rewrites;
 //   waves 0-2  meanwhile attend to the ring slots other than j (the update
 //              does not touch them) and to the new token (k_new, v_new: the
-//              row the update writes into slot j);
-//   barrier    the exact / summary rows written by wave 3 are visible;
-//   waves 0-3  attend to the exact and summary slots, merge, epilogue.
-// Tiles of 16 keys as attn_rows_bf16: K straight into MFMA fragments, V
-// through the per-wave LDS transpose, online softmax per wave.
+//              row the update writes into slot j), then take the next
+//              step's routing record (dots of head hk's norm rows);
+//   barrier    the decision and the rows rewritten by wave 3 are in LDS;
+//   waves 0-3  attend to the exact and summary slots (tiles loaded before
+//              the barrier, the rewritten rows taken from LDS in every
+//              tile), merge; epilogue.
+// Tiles of 16 keys: K straight into MFMA fragments, V through a row-major
+// LDS copy read back transposed, online softmax per wave.
 template <int DH>
 __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, const coda_bank_desc s,
                                                         const bf16_t* __restrict__ k_new,
@@ -896,10 +908,13 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   __shared__ uint8_t al_lds[kMaxRowsPrefix];
   __shared__ float red_m[NW][16], red_l[NW][16];
   __shared__ DecodeDecision dec;
-  __shared__ int dec_ready;
   // the rows the bank update rewrites: K, V of the exact slot, K, V of the
   // summary slot (new values, for the bank tiles loaded before the update)
   __shared__ __attribute__((aligned(16))) T newrows[4][DH];
+  // the next record's dots of head hk (exact slots, then summary slots),
+  // and the dots of the two norm rows this update rewrites
+  __shared__ float dots_lds[kFusedMaxBank];
+  __shared__ float fix_lds[2];
   // bank stage during the update; the partial outputs of the 4 waves after
   extern __shared__ __attribute__((aligned(16))) char ds_u[];
   const int hk = blockIdx.x, b = blockIdx.y;
@@ -961,49 +976,57 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   struct Al4 {
     uint32_t v[4];  // 32-bit: byte values packed into one register would need the loads first
   };
+  // (a buffer resource over the W ring bytes: bytes past the ring read 0
+  // without a memory access)
+  const __amdgpu_buffer_rsrc_t ral = [&]() {
+    const uint64_t v = (uint64_t)al_row;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, W, kBufWord3);
+  }();
   auto ring_al = [&](int kt) {
     Al4 r;
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int kk = kt + 4 * g4 + jj;
-      r.v[jj] = al_row[kk < W ? kk : 0];
-    }
+    for (int jj = 0; jj < 4; ++jj) r.v[jj] = __builtin_amdgcn_raw_buffer_load_b8(ral, kt + 4 * g4 + jj, 0, 0);
     return r;
   };
   auto ring_mask = [&](int kt, bool nt, const Al4& al) {
+    const int ntm = -(int)nt;  // all ones for the new-token tile
     int m4 = 0;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      const int kk = kt + 4 * g4 + jj;
-      const int ok = nt ? (kk == kt) : ((kk < W) & (kk != j) & (al.v[jj] != 0));
-      m4 |= ok << jj;
+      const int ok_r = (al.v[jj] != 0) & (kt + 4 * g4 + jj != j);
+      const int ok_n = 4 * g4 + jj == 0;
+      m4 |= ((ok_n & ntm) | (ok_r & ~ntm)) << jj;
     }
     return m4;
   };
   // phase 1 tiles of waves 0-2: u < nR ring tile u, u == nR the new token
   const int nR = (W + 15) / 16, nB = (Me + Ms + 15) / 16;
-  auto p1_kt = [&](int u) { return u < nR ? 16 * u : 0; };
+  // (u > nR: past the plane, so the buffer loads return 0 without touching
+  // memory; issued anyway, which keeps every path's loads alike)
+  auto p1_kt = [&](int u) { return u < nR ? 16 * u : u == nR ? 0 : Lbuf; };
   const int n1_w = wv < 3 ? (nR + 1 - wv + 2) / 3 : 0;   // tiles u = wv + 3 i
-  // phase 2 tiles: bank tile u of wave (u + 3) % 4
-  const int w2 = (wv + 1) & 3;
-  const int n2_w = nB > w2 ? (nB - w2 + 3) / 4 : 0;      // tiles u = w2 + 4 i
-  auto kt2 = [&](int i) { return W + 16 * (w2 + 4 * i); };
+  // phase 2 tiles: bank tile u of wave u % 4
+  const int n2_w = nB > wv ? (nB - wv + 3) / 4 : 0;  // tiles u = wv + 4 i
+  // (i >= n2_w: past the plane, so the buffer loads return 0 without
+  // touching memory; issued anyway, which keeps every path's loads alike)
+  auto kt2 = [&](int i) { return i < n2_w ? W + 16 * (wv + 4 * i) : Lbuf; };
 
   bf16x8_t kf0[NC], kf1[NC];
   uint4 vv0[4], vv1[4];
   Al4 al0, al1;
   int vm0 = 0, vm1 = 0;
-  if (threadIdx.x == 0) dec_ready = 0;
-  __syncthreads();
   // ---- prologue: every wave's first loads; no workgroup barrier until the
   // end of phase 1
-  // bank wave: record and norm rows straight to LDS, evicted / next rows,
-  // the visibility bytes of the bank slots
+  // bank wave: the record straight to LDS, evicted / next rows, the
+  // visibility bytes of the bank slots
   const int LF = DH - s.lf, words = dstep_words(Hkv, Me, Ms);
   const int jn = j + 1 == W ? 0 : j + 1;
   float* rec = reinterpret_cast<float*>(ds_u);
-  T* stage = reinterpret_cast<T*>(rec + words);
-  float* ke = reinterpret_cast<float*>(stage + dbank_stage_elems(DH, Me, Ms, s.lf));
+  T* nnorm_e = reinterpret_cast<T*>(rec + words);  // norm rows the update rewrites
+  T* nnorm_s = nnorm_e + DH;
+  float* ke = reinterpret_cast<float*>(nnorm_s + DH);
   float* ve = ke + DH;
   float* vnrm = ve + DH;
   float* knrm = vnrm + DH;
@@ -1015,11 +1038,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   uint32_t alb[kAlBank];
   if (wv == 3) {
     const float* src_r = rec_in + (int64_t)b * words;
-    const T* src_e = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH;
-    const T* src_s = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF;
     wave_copy_lds(rec, src_r, words * 4, lane);
-    if (Me > 0) wave_copy_lds(stage, src_e, Me * DH * 2, lane);
-    if (Ms > 0) wave_copy_lds(stage + Me * DH, src_s, Ms * LF * 2, lane);
     const int64_t plane = ((int64_t)b * Hkv + hk) * Lbuf;
     const T* kr = (const T*)s.k_buf + (plane + j) * DH;
     const T* vr = (const T*)s.v_buf + (plane + j) * DH;
@@ -1095,10 +1114,12 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
         tsn[c] = *reinterpret_cast<const uint2*>((const T*)a.theta_sin + (int64_t)h * half + d0 / 2);
       }
     }
-    // the first ring tile loads behind the queries
-    if (wv < 3 && n1_w > 0) {
+    // the first two ring tiles load behind the queries
+    if (wv < 3) {
       issue(p1_kt(wv), wv == nR, kf0, vv0);
       al0 = ring_al(p1_kt(wv));
+      issue(p1_kt(wv + 3), wv + 3 == nR, kf1, vv1);
+      al1 = ring_al(p1_kt(wv + 3));
     }
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -1143,6 +1164,15 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   f32x4 o[NM];
 #pragma unroll
   for (int i = 0; i < NM; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // V of a tile goes row-major into the wave's LDS buffer (rows padded to
+  // 2 DH + 32 bytes, which spreads the 4 rows of a transposed read over
+  // distinct banks) and comes back through transposed reads: lane (n, g4)
+  // gets channel 16 mt + n of keys 4 g4 .. 4 g4 + 3, the A operand of the
+  // PV product
+  constexpr int VRB = 2 * DH + 32;
+  static_assert(16 * VRB <= VtLayout<DH>::kTileBytes, "V tile fits the wave's LDS buffer");
+  const int v_rd = (4 * g4 + (n >> 2)) * VRB + 8 * (n & 3);
+  const int v_wr = 4 * (kgl & 3) * VRB + 16 * dcl;
   auto consume = [&](const bf16x8_t (&kf)[NC], const uint4 (&vv)[4], int vmask) {
     f32x4 st = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1154,29 +1184,36 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       sv[jj] = ((vmask >> jj) & 1) ? st[jj] * scale : -INFINITY;
       tmax = fmaxf(tmax, sv[jj]);
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    // max and sum over the 4 lane groups through permlane swaps (no LDS)
+    tmax = xmax32(xmax16(tmax));
     const float mnew = fmaxf(m_i, tmax);
     const float muse = mnew == -INFINITY ? 0.f : mnew;
-    const float alpha = exp2f(m_i - muse);
+    const float alpha = fast_exp2(m_i - muse);
+    // the accumulators need rescaling only where a running max moved
+    const bool grow = __builtin_amdgcn_ballot_w64(mnew != m_i) != 0;
     float p[4], ps = 0.f;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      p[jj] = bf2f(f2bf(exp2f(sv[jj] - muse)));
+      p[jj] = bf2f(f2bf(fast_exp2(sv[jj] - muse)));
       ps += p[jj];
     }
-    ps += __shfl_xor(ps, 16, 64);
-    ps += __shfl_xor(ps, 32, 64);
+    ps = xsum32(xsum16(ps));
     l_i = l_i * alpha + ps;
     m_i = mnew;
     const short4_t pf = pack4(p[0], p[1], p[2], p[3]);
-    if (vload) store_vt<DH>(vt, kgl, 8 * dcl, vv);
+    if (vload) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) *reinterpret_cast<uint4*>(vt + v_wr + jj * VRB) = vv[jj];
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): LDS writes of this wave done
     __builtin_amdgcn_wave_barrier();
+    if (grow) {
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) o[mt] *= alpha;
+    }
 #pragma unroll
     for (int mt = 0; mt < NM; ++mt) {
-      const uint2 cell = *reinterpret_cast<const uint2*>(vt + VtLayout<DH>::off(g4, 16 * mt + n));
-      o[mt] *= alpha;
+      const uint2 cell = lds_read_tr16(vt + v_rd + 32 * mt);
       o[mt] = mfma_k16(__builtin_bit_cast(short4_t, cell), pf, o[mt]);
     }
     __builtin_amdgcn_wave_barrier();
@@ -1184,51 +1221,116 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
 
   // ---- phase 1
   if (wv < 3) {
-    // ring tiles and the new token, ping-pong register buffers
+    // ring tiles and the new token, ping-pong register buffers, two in
+    // flight: a buffer is refilled as soon as it has been consumed
     for (int i = 0; i < n1_w; i += 2) {
       const int u0 = wv + 3 * i;
-      if (i + 1 < n1_w) {
-        const int u = wv + 3 * (i + 1);
-        issue(p1_kt(u), u == nR, kf1, vv1);
-        al1 = ring_al(p1_kt(u));
-      }
       vm0 = ring_mask(p1_kt(u0), u0 == nR, al0);
       __builtin_amdgcn_sched_barrier(0);
       consume(kf0, vv0, vm0);
+      issue(p1_kt(u0 + 6), u0 + 6 == nR, kf0, vv0);
+      al0 = ring_al(p1_kt(u0 + 6));
       if (i + 1 >= n1_w) break;
-      const int u1 = wv + 3 * (i + 1);
-      if (i + 2 < n1_w) {
-        const int u = wv + 3 * (i + 2);
-        issue(p1_kt(u), u == nR, kf0, vv0);
-        al0 = ring_al(p1_kt(u));
-      }
+      const int u1 = u0 + 3;
       vm1 = ring_mask(p1_kt(u1), u1 == nR, al1);
       __builtin_amdgcn_sched_barrier(0);
       consume(kf1, vv1, vm1);
+      issue(p1_kt(u1 + 6), u1 + 6 == nR, kf1, vv1);
+      al1 = ring_al(p1_kt(u1 + 6));
     }
-    // the first two bank tiles load now (a row the bank update rewrites is
-    // replaced from LDS after the barrier)
-    if (n2_w > 0) issue(kt2(0), false, kf0, vv0);
-    if (n2_w > 1) issue(kt2(1), false, kf1, vv1);
-    // the next step's record: head hk's dots against the norm rows, over
-    // waves 0-2 once wave 3 has published its decision and the unit rows;
-    // the rows its update rewrites are left to wave 3
-    for (int spin = 0; spin < (1 << 22); ++spin) {
-      if (__atomic_load_n(&dec_ready, __ATOMIC_ACQUIRE) != 0) break;
-      __builtin_amdgcn_s_sleep(2);
+    // the next step's record: head hk's dots against its norm rows (the
+    // rows this step's update rewrites are redone by wave 3).  Each 16-byte
+    // load covers 8 channels of one norm row (LP lanes per row, 64 / LP rows
+    // per load "slot"); exact slots then summary slots, the wave taking a
+    // third of them.  Loads first: slot j+1's rows (this wave's own unit
+    // rows), the first KD slots, then this wave's first two bank tiles (a
+    // row the update rewrites is replaced from LDS after the barrier)
+    {
+      constexpr int KD = 8, LPE = DH / 8, IPE = 64 / LPE, LPS = DH / 16, IPS = 64 / LPS;
+      const int nSe = (Me + IPE - 1) / IPE, nSs = (Ms + IPS - 1) / IPS, nS = nSe + nSs;
+      const int per = (nS + 2) / 3, qa = min(wv * per, nS), qb = min(qa + per, nS);
+      const T* en = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH;
+      const T* sn = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF;
+      const int64_t plane = ((int64_t)b * Hkv + hk) * Lbuf;
+      const T* kx = jn == j ? kn_row : (const T*)s.k_buf + (plane + jn) * DH;
+      const T* vx = jn == j ? vn_row : (const T*)s.v_buf + (plane + jn) * DH;
+      uint32_t nv_r[NVb], nk_r[NVb];
+#pragma unroll
+      for (int i = 0; i < NVb; ++i) {
+        nv_r[i] = vx[min(lane + 64 * i, DH - 1)];
+        nk_r[i] = kx[s.lf + min(lane + 64 * i, LF - 1)];
+      }
+      auto load_batch = [&](int qs, uint4 (&xr)[KD]) {
+#pragma unroll
+        for (int k = 0; k < KD; ++k) {
+          const int q = min(qs + k, qb - 1);
+          const T* p = q < nSe ? en + min(q * IPE + lane / LPE, Me - 1) * DH + 8 * (lane % LPE)
+                               : sn + min((q - nSe) * IPS + lane / LPS, Ms - 1) * LF + 8 * (lane % LPS);
+          xr[k] = *reinterpret_cast<const uint4*>(p);
+        }
+      };
+      uint4 xr[KD];
+      if (qa < qb) load_batch(qa, xr);
+      issue(kt2(0), false, kf0, vv0);
+      issue(kt2(1), false, kf1, vv1);
+      // unit rows of slot j+1 through the wave's (idle) V buffer: lane reads
+      // back the 8 channels of its slots
+      float* un = reinterpret_cast<float*>(vt);
+      {
+        float xv[NVb], xk[NVb];
+        bool av2[NVb], ak2[NVb];
+#pragma unroll
+        for (int i = 0; i < NVb; ++i) {
+          av2[i] = lane + 64 * i < DH;
+          ak2[i] = lane + 64 * i < LF;
+          xv[i] = av2[i] ? bf2f((bf16_t)nv_r[i]) : 0.f;
+          xk[i] = ak2[i] ? bf2f((bf16_t)nk_r[i]) : 0.f;
+        }
+        wave_unit<T, NVb>(xv, av2);
+        wave_unit<T, NVb>(xk, ak2);
+#pragma unroll
+        for (int i = 0; i < NVb; ++i) {
+          if (av2[i]) un[lane + 64 * i] = xv[i];
+          if (ak2[i]) un[DH + lane + 64 * i] = xk[i];
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
+      float uv[8], uk[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        uv[jj] = un[8 * (lane % LPE) + jj];
+        uk[jj] = un[DH + 8 * (lane % LPS) + jj];
+      }
+      // the fp32 dot of each row in channel order, the group sum in the
+      // order of wave_dots (pairs, quads, half rows, rows), rounded to T
+      auto use_batch = [&](int qs, const uint4 (&xr)[KD]) {
+#pragma unroll
+        for (int k = 0; k < KD; ++k) {
+          const int q = qs + k;
+          const bool ex = q < nSe;
+          float x[8];
+          unpack8(xr[k], x);
+          float acc = 0.f;
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) acc = fmaf(ex ? uv[jj] : uk[jj], x[jj], acc);
+          acc += dpp_f<0xB1>(acc);
+          acc += dpp_f<0x4E>(acc);
+          float t = dpp_f<0x141>(acc);
+          acc = (ex ? LPE >= 8 : LPS >= 8) ? acc + t : acc;
+          t = dpp_f<0x140>(acc);
+          acc = (ex ? LPE >= 16 : LPS >= 16) ? acc + t : acc;
+          const int row = ex ? q * IPE + lane / LPE : (q - nSe) * IPS + lane / LPS;
+          const int sub = ex ? lane % LPE : lane % LPS;
+          if (q < qb && row < (ex ? Me : Ms) && sub == 0) dots_lds[ex ? row : Me + row] = Elt<T>::rnd(acc);
+        }
+      };
+      if (qa < qb) use_batch(qa, xr);
+      for (int qs = qa + KD; qs < qb; qs += KD) {
+        load_batch(qs, xr);
+        use_batch(qs, xr);
+      }
     }
-    const int skip_e = Me > 0 && dec.ow_e ? dec.idx_e : -1;
-    const int skip_s = Ms > 0 && dec.keep_s ? dec.idx_s : -1;
-    float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
-    float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
-    if (Me > 0)
-      wave_dots<T, 4>(
-          Me, DH, wv, 3, lane, [&](int it) { return (const T*)stage + it * DH; },
-          [&](int) { return (const float*)vnrm; }, [&](int it, float v) { if (it != skip_e) out_e[it] = v; });
-    if (Ms > 0)
-      wave_dots<T, 4>(
-          Ms, LF, wv, 3, lane, [&](int it) { return (const T*)stage + Me * DH + it * LF; },
-          [&](int) { return (const float*)knrm; }, [&](int it, float v) { if (it != skip_s) out_s[it] = v; });
   } else {
     // the bank update of head hk (one wave)
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): record, norm rows, evicted / next rows
@@ -1260,12 +1362,10 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     const float g_e = *L.g_e;
     if (Me > 0) decide_exact<T>(s, L.dots, L.used, L.last, g_e, dec, hk == 0, lane);
     if (Ms > 0) decide_summary<T>(s, L.dots + Hkv * Me, L.used + Me, g_e, dec, hk == 0, lane);
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the decision (lane 0) and rows are in LDS
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the decision (lane 0) is in LDS
     __builtin_amdgcn_wave_barrier();
-    if (lane == 0) __atomic_store_n(&dec_ready, 1, __ATOMIC_RELEASE);
     const DecodeDecision dd = dec;
-    apply_head<T, DH>(s, b, hk, dd, ke, ve, kn_row, vn_row, j, g_e, lane, Me > 0 ? stage + dd.idx_e * DH : nullptr,
-                      Ms > 0 ? stage + Me * DH + dd.idx_s * LF : nullptr, &newrows[0][0]);
+    apply_head<T, DH>(s, b, hk, dd, ke, ve, kn_row, vn_row, j, g_e, lane, nnorm_e, nnorm_s, &newrows[0][0]);
     if (hk == 0) {
       // metadata of the sequence, and the next record's snapshot of it
       const DStepWs wn = dstep_ws(rec_out, b, Hkv, Me, Ms);
@@ -1286,38 +1386,35 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       const bool fill = (Me > 0 && dd.ow_e && m == dd.idx_e) || (Ms > 0 && dd.keep_s && m == Me + dd.idx_s);
       if (m < Me + Ms) al_lds[W + m] = fill ? (uint8_t)1 : (uint8_t)alb[k];
     }
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's row writes are done (the ring
-                                         // waves read them after the barrier; its own tiles below)
-    if (n2_w > 0) issue(kt2(0), false, kf0, vv0);
-    if (n2_w > 1) issue(kt2(1), false, kf1, vv1);
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): rewritten norm rows in LDS
     __builtin_amdgcn_wave_barrier();
     // the record dots of the norm rows this update rewrote
     if (Me > 0 && dd.ow_e) {
-      float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
-      const int ie = dd.idx_e;
       wave_dots<T, 4>(
-          1, DH, 0, 1, lane, [&](int) { return (const T*)stage + ie * DH; }, [&](int) { return (const float*)vnrm; },
-          [&](int, float v) { out_e[ie] = v; });
+          1, DH, 0, 1, lane, [&](int) { return (const T*)nnorm_e; }, [&](int) { return (const float*)vnrm; },
+          [&](int, float v) { fix_lds[0] = v; });
     }
     if (Ms > 0 && dd.keep_s) {
-      float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
-      const int is = dd.idx_s;
       wave_dots<T, 4>(
-          1, LF, 0, 1, lane, [&](int) { return (const T*)stage + Me * DH + is * LF; },
-          [&](int) { return (const float*)knrm; }, [&](int, float v) { out_s[is] = v; });
+          1, LF, 0, 1, lane, [&](int) { return (const T*)nnorm_s; },
+          [&](int) { return (const float*)knrm; }, [&](int, float v) { fix_lds[1] = v; });
     }
   }
-  __syncthreads();  // bank rows, new rows and patched norm rows written by wave 3 visible
+  if (wv == 3) {
+    // the bank wave's two bank tiles (rows the update rewrote are replaced
+    // from LDS after the barrier)
+    issue(kt2(0), false, kf0, vv0);
+    issue(kt2(1), false, kf1, vv1);
+  }
+  __syncthreads();  // the decision, new rows, bank visibility bytes and record dots in LDS
   if (wv == 3) {
 #pragma unroll
     for (int c = 0; c < NC; ++c) qf[c] = __builtin_bit_cast(bf16x8_t, reinterpret_cast<const uint4*>(vt_smem[3])[c * 64 + lane]);
   }
 
-  // ---- phase 2: exact and summary slots
+  // ---- phase 2: exact and summary slots; rows this step's update rewrote
+  // come from LDS in every tile
   {
-    // the first two bank tiles were loaded before the barrier: rows this
-    // step's update rewrote come from LDS
     const int re = Me > 0 && dec.ow_e ? W + dec.idx_e : -1;
     const int rs = Ms > 0 && dec.keep_s ? W + Me + dec.idx_s : -1;
     auto patch = [&](int kt, bf16x8_t (&kf)[NC], uint4 (&vv)[4]) {
@@ -1333,26 +1430,18 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
         if (rv == re || rv == rs) vv[jj] = *reinterpret_cast<const uint4*>(newrows[rv == re ? 1 : 3] + 8 * dcl);
       }
     };
-    if (n2_w > 0) {
-      patch(kt2(0), kf0, vv0);
-      vm0 = tile_mask(kt2(0));
-    }
-    if (n2_w > 1) patch(kt2(1), kf1, vv1);
-
+    auto step2 = [&](int i, bf16x8_t (&kf)[NC], uint4 (&vv)[4]) {
+      const int kt = kt2(i);
+      patch(kt, kf, vv);
+      const int vm = tile_mask(kt);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(kf, vv, vm);
+      issue(kt2(i + 2), false, kf, vv);
+    };
     for (int i = 0; i < n2_w; i += 2) {
-      if (i + 1 < n2_w) {
-        if (i + 1 > 1) issue(kt2(i + 1), false, kf1, vv1);
-        vm1 = tile_mask(kt2(i + 1));
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      consume(kf0, vv0, vm0);
+      step2(i, kf0, vv0);
       if (i + 1 >= n2_w) break;
-      if (i + 2 < n2_w) {
-        issue(kt2(i + 2), false, kf0, vv0);
-        vm0 = tile_mask(kt2(i + 2));
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      consume(kf1, vv1, vm1);
+      step2(i + 1, kf1, vv1);
     }
   }
   // ---- merge the 4 waves (rows r < R), epilogue (the bank stage is free)
@@ -1368,6 +1457,17 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       for (int jj = 0; jj < 4; ++jj) red_o[(wv * R + n) * (DH + 4) + 16 * mt + 4 * g4 + jj] = o[mt][jj];
   }
   __syncthreads();
+  // the next record's dots of head hk; the rewritten rows' from the bank wave
+  {
+    float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
+    float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
+    const int ie = Me > 0 && dec.ow_e ? dec.idx_e : -1;
+    const int is = Ms > 0 && dec.keep_s ? dec.idx_s : -1;
+    for (int m = threadIdx.x; m < Me + Ms; m += blockDim.x) {
+      if (m < Me) out_e[m] = m == ie ? fix_lds[0] : dots_lds[m];
+      else out_s[m - Me] = m - Me == is ? fix_lds[1] : dots_lds[m];
+    }
+  }
   for (int orow = wv, r_pf = 0; orow < G; orow += NW, ++r_pf) {
     const int h = hk * G + orow;
     float os[NV], on[NV], y[NV];
@@ -1599,12 +1699,6 @@ struct FaLayout {
   static constexpr int RPI = 1024 / ROWB;         // V rows per 1 KiB direct load
   static constexpr int LDS = 2 * KBYTES + 2 * VBYTES;
 };
-// chunk position of V row k is chunk ^ fa_vswz<DH>(k) (even, so the two
-// chunks of a 32-byte channel group stay adjacent)
-template <int DH>
-__device__ __forceinline__ int fa_vswz(int k) {
-  return DH == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3);
-}
 
 template <int DH, int NW>
 __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, int NQ, int nqb, int npairs) {
@@ -2175,7 +2269,8 @@ static int validate_step(const coda_bank_desc* s, const coda_attn_desc* a) {
 static bool fused_step_ok(const coda_bank_desc* s, const coda_attn_desc* a) {
   const int G = a->H / a->Hkv;
   return s->dtype == CODA_BF16 && (s->Dh == 64 || s->Dh == 128) && 2 * G <= 16 && s->W >= 16 &&
-         s->Me + s->Ms <= 256 && s->W + s->Me + s->Ms <= kMaxRowsPrefix && a->causal == 0 && a->allowed != nullptr;
+         s->Me + s->Ms <= kFusedMaxBank && s->W + s->Me + s->Ms <= kMaxRowsPrefix && 2 * s->lf == s->Dh &&
+         a->causal == 0 && a->allowed != nullptr;
 }
 
 template <int DH>
@@ -2183,7 +2278,8 @@ static int launch_fused_step(const coda_bank_desc* s, const coda_attn_desc* a, c
                              int64_t nb_sb, int64_t nb_sh, const float* g_new, int j, int64_t pos,
                              const float* rec_in, float* rec_out, hipStream_t st) {
   const int R = 2 * (a->H / a->Hkv);
-  size_t lds = dbank_lds(*s);
+  // record, two rewritten norm rows, ke / ve / vnrm / knrm; then the merge
+  size_t lds = sizeof(float) * (size_t)dstep_words(s->Hkv, s->Me, s->Ms) + 2 * 2 * (size_t)DH + 4 * sizeof(float) * DH;
   const size_t red = (size_t)4 * R * (DH + 4) * sizeof(float);
   lds = lds > red ? lds : red;
   if (lds > 64 * 1024) {

@@ -309,6 +309,16 @@ __device__ __forceinline__ void decide_summary(const coda_bank_desc& s, const fl
   }
 }
 
+// One element loaded into a 32-bit register as raw bits, and its value.
+__device__ __forceinline__ uint32_t raw_ld(const bf16_t* p) { return *p; }
+__device__ __forceinline__ uint32_t raw_ld(const float* p) { return __builtin_bit_cast(uint32_t, *p); }
+template <typename T>
+__device__ __forceinline__ float raw_f(uint32_t u);
+template <>
+__device__ __forceinline__ float raw_f<bf16_t>(uint32_t u) { return bf2f((bf16_t)u); }
+template <>
+__device__ __forceinline__ float raw_f<float>(uint32_t u) { return __builtin_bit_cast(float, u); }
+
 // Bank writes of one head for one evicted token, by one wave; every old
 // row this head needs (exact slot, summary slot) and the new token are
 // loaded together, then:
@@ -341,17 +351,33 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
   T* krs = kb + (int64_t)(W + Me + idx_s) * DH;
   T* vrs = vb + (int64_t)(W + Me + idx_s) * DH;
   float mke[NV], mve[NV], mks[NV], mvs[NV], kn[NV], vn[NV];
-  // every load in one batch (eta's logit included)
+  // every load in one batch (eta's logit included), unconditional from
+  // valid rows (the new token's where a bank row is not rewritten) and raw:
+  // a conditional load, or a conversion next to the load, waits for it
   const float eta_l = Ms > 0 ? s.eta_logit[h] : 0.f;
+  const T* lke = do_e ? kre : kn_src;
+  const T* lve = do_e ? vre : vn_src;
+  const T* lks = do_s ? krs : kn_src;
+  const T* lvs = do_s ? vrs : vn_src;
+  uint32_t r_ke[NV], r_ve[NV], r_ks[NV], r_vs[NV], r_kn[NV], r_vn[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int d = min(lane + 64 * i, DH - 1);
-    mke[i] = do_e ? E::ld(kre[d]) : 0.f;
-    mve[i] = do_e ? E::ld(vre[d]) : 0.f;
-    mks[i] = do_s ? E::ld(krs[d]) : 0.f;
-    mvs[i] = do_s ? E::ld(vrs[d]) : 0.f;
-    kn[i] = E::ld(kn_src[d]);
-    vn[i] = E::ld(vn_src[d]);
+    r_ke[i] = raw_ld(lke + d);
+    r_ve[i] = raw_ld(lve + d);
+    r_ks[i] = raw_ld(lks + d);
+    r_vs[i] = raw_ld(lvs + d);
+    r_kn[i] = raw_ld(kn_src + d);
+    r_vn[i] = raw_ld(vn_src + d);
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    mke[i] = do_e ? raw_f<T>(r_ke[i]) : 0.f;
+    mve[i] = do_e ? raw_f<T>(r_ve[i]) : 0.f;
+    mks[i] = do_s ? raw_f<T>(r_ks[i]) : 0.f;
+    mvs[i] = do_s ? raw_f<T>(r_vs[i]) : 0.f;
+    kn[i] = raw_f<T>(r_kn[i]);
+    vn[i] = raw_f<T>(r_vn[i]);
   }
   if (do_e) {
     float nv[NV];
