@@ -47,6 +47,7 @@ def parse():
     ap.add_argument("--block", type=int, default=256)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the configs[2] prefill figure")
+    ap.add_argument("--no-unbounded", action="store_true", help="skip the configs[3] unbounded attention figure")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="before timing, run 5 device-to-device copies of this many MiB (a plain copy kernel of "
@@ -209,6 +210,11 @@ def main():
     if not a.no_prefill:
         out["prefill"] = bench_prefill(torch, coda, m, a)
         print(f"# prefill: {out['prefill']['value']:.0f} tok/s", file=sys.stderr, flush=True)
+    # ---------------------------------------------------------------- unbounded
+    if not a.no_unbounded:
+        out["unbounded"] = bench_unbounded(torch, coda)
+        print(f"# unbounded: {out['unbounded']['value']:.0f} tok/s, "
+              f"{out['unbounded']['roofline']['achieved']:.0f} TFLOP/s", file=sys.stderr, flush=True)
     # ---------------------------------------------------------------- CPU baseline
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a)
@@ -269,6 +275,44 @@ def bench_prefill(torch, coda, m, a):
                          "flops_per_launch": flops, "avg_launch_ms": round(attn_ms, 5),
                          "traffic": profile_traffic("prefill_chunk_b%d attn_fa_bf16<128,8>" % B),
                          "valid_prefix_slots": n_prefix}}
+
+
+def bench_unbounded(torch, coda, B=2, L=8192, H=32, Hkv=8, Dh=128, reps=5):
+    """unbounded causal differential attention (CoDAGQA,
+    reference baseline.py:95-147) through the diff_flash_attn seam: q, k, v ~
+    N(0,1), lambda ~ U(0.1, 0.9), q_noise = q R with R a random orthogonal
+    128x128 rotation per head, bf16.  Attention kernel only (the projections
+    are outside the path); FLOPs over the visible (query, key) pairs."""
+    dev = "cuda:0"
+    dt = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(3)
+    with torch.no_grad():
+        q = torch.randn(B, H, L, Dh, generator=g, device=dev, dtype=torch.float32)
+        rot = torch.linalg.qr(torch.randn(H, Dh, Dh, generator=g, device=dev, dtype=torch.float32))[0]
+        q_noise = torch.matmul(q, rot.unsqueeze(0)).to(dt)
+        q = q.to(dt)
+        k = torch.randn(B, Hkv, L, Dh, generator=g, device=dev, dtype=dt)
+        v = torch.randn(B, Hkv, L, Dh, generator=g, device=dev, dtype=dt)
+        lam = (0.1 + 0.8 * torch.rand(B, H, L, 1, generator=g, device=dev, dtype=torch.float32)).to(dt)
+        w = torch.ones(Dh, dtype=dt, device=dev)
+        for _ in range(2):
+            coda.ops.diff_flash_attn(q, q_noise, k, v, lam, rms_weight=w, is_causal=True)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            coda.ops.diff_flash_attn(q, q_noise, k, v, lam, rms_weight=w, is_causal=True)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    flops = 8.0 * Dh * B * H * L * (L + 1) / 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"metric": "unbounded causal diff-attention tok/s (configs[3])", "value": round(B * L / (ms * 1e-3), 1),
+            "unit": "tok/s", "batch": B, "seq_len": L, "ms": round(ms, 4),
+            "roofline": {"bound": "mfma", "kernel": "attn_fa_bf16<128,8> (causal)", "achieved": round(tflops, 2),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                         "flops_per_launch": flops, "avg_launch_ms": round(ms, 5)}}
 
 
 def cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a):
