@@ -5,6 +5,7 @@ state dataclass and operator seams); compute runs in the hand-written HIP
 kernels of libcoda_mi355x.so (C ABI: include/coda_mi355x.h).
 """
 
+from .adapters import EveCoDAAdapter, LlamaCoDAAdapter, Qwen3CoDAAdapter
 from .attention import CoDAGQALandmarkPerf2
 from .baseline import CoDAGQA
 from .memory_banks import MemoryBankMixin
@@ -16,6 +17,9 @@ __all__ = [
     "CoDAGQALandmarkPerf2",
     "CoDAGQALandmarkStatePerf2",
     "CoDAGQA",
+    "LlamaCoDAAdapter",
+    "Qwen3CoDAAdapter",
+    "EveCoDAAdapter",
     "MemoryBankMixin",
     "HeadwiseRMSNorm",
     "RotaryEmbedding",

@@ -358,3 +358,127 @@ def test_decode_step_carried_routing_matches_fresh_routing(E, H):
             assert carried, f"step {t}: routing record was not carried over"
         assert torch.equal(y1, y2), f"step {t}: outputs differ"
         _assert_same_state(st, fresh, f"step {t}")
+
+
+@torch.no_grad()
+def test_saved_state_decodes_like_the_original(tmp_path):
+    """save_state -> load_state -> state_to_device of a bf16 state in the
+    middle of decoding, then the same decode steps on the original and on the
+    restored copy (which starts from a fresh routing record): identical
+    outputs and states."""
+    _need_gpu()
+    import coda_gqa_l
+    from coda_gqa_l.state_io import load_state, save_state, state_to_device
+    print("[state save/load round trip]", flush=True)
+    dt = torch.bfloat16
+    torch.manual_seed(21)
+    kw = dict(embed_dim=512, num_heads=8, num_kv_heads=2, window=32, num_landmarks_exact=16,
+              num_landmarks_summary=16)
+    m = coda_gqa_l.CoDAGQALandmarkPerf2(**kw).to(dt).to(DEV).eval()
+    m2 = coda_gqa_l.CoDAGQALandmarkPerf2(**kw).to(dt).to(DEV).eval()
+    m2.load_state_dict(m.state_dict())
+    B = 8
+    g = torch.Generator(device=DEV).manual_seed(22)
+    st = m.init_state(batch_size=B, device=DEV, dtype=dt)
+    m.prefill_chunked(torch.randn(B, 100, 512, generator=g, device=DEV, dtype=dt), st, block_size=32,
+                      return_outputs=False)
+    for _ in range(3):
+        m.step(torch.randn(B, 1, 512, generator=g, device=DEV, dtype=dt), st)
+    path = tmp_path / "state.pt"
+    save_state({"states": {0: st}, "metadata": {"tokens": 103}}, path)
+    loaded = load_state(path)
+    assert loaded["metadata"] == {"tokens": 103}
+    st2 = state_to_device(loaded["states"][0], DEV, dt)
+    _assert_same_state(st, st2, "after restore")
+    for t in range(5):
+        x = torch.randn(B, 1, 512, generator=g, device=DEV, dtype=dt)
+        y1, _ = m.step(x, st)
+        y2, _ = m2.step(x, st2)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), f"step {t}: outputs differ"
+        _assert_same_state(st, st2, f"step {t}")
+
+
+def _rel_err(a, b):
+    a, b = a.float(), b.float()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-6)).item()
+
+
+@pytest.mark.filterwarnings("ignore:LlamaCoDAAdapter")
+@torch.no_grad()
+def test_llama_adapter_bounded_equals_unbounded_when_window_covers():
+    """A tiny random-init HF Llama (bf16, GQA 4:2, head_dim 64, biases on the
+    projections) with its attention swapped for the adapters: with a window
+    longer than the sequence nothing is evicted, so the bounded layers
+    (chunked prefill, then decode steps) must give the logits of the
+    unbounded layers over the whole sequence (README.md:263-269)."""
+    _need_gpu()
+    transformers = pytest.importorskip("transformers")
+    import coda_gqa_l
+    print("[llama adapter bounded vs unbounded]", flush=True)
+    cfg = transformers.LlamaConfig(hidden_size=256, num_attention_heads=4, num_key_value_heads=2, head_dim=64,
+                                   num_hidden_layers=2, vocab_size=97, intermediate_size=512, rope_theta=5e5,
+                                   attention_bias=True)
+    torch.manual_seed(0)
+    base = transformers.LlamaForCausalLM(cfg).eval()
+    models = {}
+    for bounded in (True, False):
+        mdl = transformers.LlamaForCausalLM(cfg).eval()
+        mdl.load_state_dict(base.state_dict())
+        coda_gqa_l.LlamaCoDAAdapter.swap_llama_layers(mdl, bounded=bounded, window=512, num_landmarks_exact=16,
+                                                      num_landmarks_summary=16, block_size=64)
+        models[bounded] = mdl.to(torch.bfloat16).to(DEV).eval()
+    # the layers' own parameters (rotation angles, lambda projection) as well
+    for lb_, lu_ in zip(models[True].model.layers, models[False].model.layers):
+        ub = lu_.self_attn.coda.state_dict()
+        for k, v in lb_.self_attn.coda.state_dict().items():
+            if k in ub and ub[k].shape == v.shape:
+                ub[k].copy_(v)
+    ids = torch.randint(0, 97, (2, 203), generator=torch.Generator().manual_seed(5)).to(DEV)
+    lb = models[True](input_ids=ids[:, :200], use_cache=False).logits
+    lu = models[False](input_ids=ids[:, :200], use_cache=False).logits
+    assert _rel_err(lb, lu) < 3e-2, f"prefill logits {_rel_err(lb, lu):.3e}"
+    for t in range(200, 203):
+        lb = models[True](input_ids=ids[:, t:t + 1], use_cache=False).logits[:, -1]
+        lu = models[False](input_ids=ids[:, :t + 1], use_cache=False).logits[:, -1]
+        assert _rel_err(lb, lu) < 3e-2, f"decode {t} logits {_rel_err(lb, lu):.3e}"
+
+
+@torch.no_grad()
+def test_eve_adapter_bounded_equals_unbounded_when_window_covers():
+    """Eve-2 layout (multi-head, head_dim 64, fused QKV with biases, full head
+    norm, interleaved RoPE) through the adapter: bounded with a window
+    covering the sequence == unbounded, for the prefill and decode steps."""
+    _need_gpu()
+    import torch.nn as nn
+    import coda_gqa_l
+    print("[eve adapter bounded vs unbounded]", flush=True)
+
+    class EveAttention(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.n_embd, self.n_head, self.head_dim = 512, 8, 64
+            self.c_attn = nn.Linear(512, 1536, bias=True)
+            self.c_proj = nn.Linear(512, 512, bias=True)
+
+    torch.manual_seed(2)
+    eve = EveAttention()
+    ads = {}
+    for bounded in (True, False):
+        torch.manual_seed(3)                       # the same theta / lambda / norm parameters in both
+        ad = coda_gqa_l.EveCoDAAdapter.from_eve_attention(eve, bounded=bounded, window=256,
+                                                          num_landmarks_exact=16, num_landmarks_summary=16,
+                                                          block_size=64)
+        ads[bounded] = ad.to(torch.bfloat16).to(DEV).eval()
+    ub = ads[False].coda.state_dict()
+    for k, v in ads[True].coda.state_dict().items():
+        if k in ub and ub[k].shape == v.shape:
+            ub[k].copy_(v)
+    x = torch.randn(2, 153, 512, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(DEV)
+    yb = ads[True](x[:, :150])
+    yu = ads[False](x[:, :150])
+    assert _rel_err(yb, yu) < 2e-2, f"prefill {_rel_err(yb, yu):.3e}"
+    for t in range(150, 153):
+        yb = ads[True](x[:, t:t + 1])
+        yu = ads[False](x[:, :t + 1])[:, -1:]
+        assert _rel_err(yb, yu) < 2e-2, f"decode {t} {_rel_err(yb, yu):.3e}"
