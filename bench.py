@@ -48,6 +48,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the configs[2] prefill figure")
     ap.add_argument("--no-unbounded", action="store_true", help="skip the configs[3] unbounded attention figure")
+    ap.add_argument("--no-c5", action="store_true", help="skip the configs[4] 70B-shaped decode figure")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="before timing, run 5 device-to-device copies of this many MiB (a plain copy kernel of "
@@ -96,6 +97,76 @@ def prefill_chunk_flops(m, B, blk, n_prefix):
     return 8 * m.head_dim * B * m.num_heads * (blk * n_prefix + blk * (blk + 1) / 2)
 
 
+def run_decode(torch, coda, m, B, prefill_tokens, prefill_call, steps, warmup, block, copy_calib_mib=0):
+    """Decode throughput of ``m`` at batch ``B``: the state pre-filled with
+    ``prefill_tokens`` N(0,1) tokens, post-projection inputs of every step
+    resident in HBM, then ``warmup`` + ``steps`` calls of the decode step
+    (one launch of the fused step kernel each).  Returns tok/s, wall ms per
+    step, kernel ms per step (one pair of HIP events on the launch stream
+    around the timed steps), the state and the step inputs."""
+    dev = "cuda:0"
+    dt = torch.bfloat16
+    H, Dh, E = m.num_heads, m.head_dim, m.num_heads * m.head_dim
+    g = torch.Generator(device=dev).manual_seed(1)
+    st = m.init_state(batch_size=B, device=dev, dtype=dt)
+    with torch.no_grad():
+        for t0 in range(0, prefill_tokens, prefill_call):
+            n = min(prefill_call, prefill_tokens - t0)
+            x = torch.randn(B, n, E, generator=g, device=dev, dtype=dt)
+            _, st = m.prefill_chunked(x, st, block_size=block, return_outputs=False)
+            del x
+    torch.cuda.synchronize()
+    n_steps = warmup + steps
+    with torch.no_grad():
+        q_all, k_all, v_all, g_all, lam_all, cs_all = [], [], [], [], [], []
+        p0 = st.pos
+        cos, sin = m.rope(seq_len=n_steps, offset=p0, device=dev, dtype=dt)
+        for i in range(n_steps):
+            x = torch.randn(B, 1, E, generator=g, device=dev, dtype=dt)
+            q_all.append(m._project_q(x))
+            kr, v = m._project_kv_raw(x)
+            k_all.append(coda.apply_rope(kr, cos[i:i + 1], sin[i:i + 1], interleaved=m.rope_interleaved))
+            v_all.append(v)
+            g_all.append(m._write_gate(x).reshape(B).contiguous())
+            lam_all.append(m._lambda(x))
+            cs_all.append((cos[i:i + 1].contiguous(), sin[i:i + 1].contiguous()))
+        heads = torch.empty((B, 1, H, Dh), dtype=dt, device=dev)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    if copy_calib_mib > 0:
+        src = torch.empty(copy_calib_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    def run_step(i):
+        # one library call: one launch of the fused decode step kernel (the
+        # routing record is carried from the previous step)
+        m.decode_step_core(q_all[i], k_all[i], v_all[i], g_all[i], lam_all[i], st, cs_all[i][0], cs_all[i][1],
+                           out=heads)
+
+    with torch.no_grad():
+        for i in range(warmup):
+            run_step(i)
+        torch.cuda.synchronize()
+        # HIP events on the launch stream bracket the timed region: one
+        # kernel launch per step, so their span / steps is the average launch
+        # duration (plus any launch gaps)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for j in range(steps):
+            run_step(warmup + j)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    wall = t1 - t0
+    return (B * steps / wall, wall * 1e3 / steps, e0.elapsed_time(e1) / steps, st, q_all, k_all, v_all, g_all,
+            lam_all)
+
+
 def main():
     a = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -110,71 +181,9 @@ def main():
     dt = torch.bfloat16
     B = a.batch
     m = layer(torch, coda, dt, dev)
-    H, Hkv, Dh = m.num_heads, m.num_kv_heads, m.head_dim
-    g = torch.Generator(device=dev).manual_seed(1)
 
-    # ---------------------------------------------------------------- state
-    st = m.init_state(batch_size=B, device=dev, dtype=dt)
-    with torch.no_grad():
-        for t0 in range(0, a.prefill_tokens, 2048):
-            n = min(2048, a.prefill_tokens - t0)
-            x = torch.randn(B, n, 4096, generator=g, device=dev, dtype=dt)
-            _, st = m.prefill_chunked(x, st, block_size=a.block, return_outputs=False)
-    torch.cuda.synchronize()
-
-    # ---------------------------------------------------------------- inputs
-    n_steps = a.warmup + a.steps
-    with torch.no_grad():
-        xs = torch.randn(n_steps, B, 1, 4096, generator=g, device=dev, dtype=dt)
-        q_all, k_all, v_all, g_all, lam_all, cs_all = [], [], [], [], [], []
-        p0 = st.pos
-        cos, sin = m.rope(seq_len=n_steps, offset=p0, device=dev, dtype=dt)
-        for i in range(n_steps):
-            x = xs[i]
-            q_all.append(m._project_q(x))
-            kr, v = m._project_kv_raw(x)
-            k_all.append(coda.apply_rope(kr, cos[i:i + 1], sin[i:i + 1], interleaved=m.rope_interleaved))
-            v_all.append(v)
-            g_all.append(m._write_gate(x).reshape(B).contiguous())
-            lam_all.append(m._lambda(x))
-            cs_all.append((cos[i:i + 1].contiguous(), sin[i:i + 1].contiguous()))
-        heads = torch.empty((B, 1, H, Dh), dtype=dt, device=dev)
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream()
-    if a.copy_calib_mib > 0:
-        src = torch.empty(a.copy_calib_mib << 20, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
-
-    def run_step(i):
-        # one library call: one launch of the fused decode step kernel (the
-        # routing record is carried from the previous step)
-        m.decode_step_core(q_all[i], k_all[i], v_all[i], g_all[i], lam_all[i], st, cs_all[i][0], cs_all[i][1],
-                           out=heads)
-
-    with torch.no_grad():
-        for i in range(a.warmup):
-            run_step(i)
-        torch.cuda.synchronize()
-        # HIP events on the launch stream bracket the timed region: one
-        # kernel launch per step, so their span / steps is the average launch
-        # duration (plus any launch gaps)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        e0.record(stream)
-        for j in range(a.steps):
-            run_step(a.warmup + j)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-    wall = t1 - t0
-    ms_step = wall * 1e3 / a.steps
-    tok_s = B * a.steps / wall
-    step_gpu_ms = e0.elapsed_time(e1) / a.steps
+    (tok_s, ms_step, step_gpu_ms, st, q_all, k_all, v_all, g_all, lam_all) = run_decode(
+        torch, coda, m, B, a.prefill_tokens, 2048, a.steps, a.warmup, a.block, a.copy_calib_mib)
     attn_bytes, bank_bytes = decode_bytes(m, B)
     achieved = (attn_bytes + bank_bytes) / (step_gpu_ms * 1e-3) / 1e9
 
@@ -215,6 +224,11 @@ def main():
         out["unbounded"] = bench_unbounded(torch, coda)
         print(f"# unbounded: {out['unbounded']['value']:.0f} tok/s, "
               f"{out['unbounded']['roofline']['achieved']:.0f} TFLOP/s", file=sys.stderr, flush=True)
+    # ---------------------------------------------------------------- 70B-shaped decode
+    if not a.no_c5:
+        out["decode_c5"] = bench_decode_c5(torch, coda, a)
+        print(f"# decode configs[4]: {out['decode_c5']['value']:.0f} tok/s, "
+              f"{out['decode_c5']['roofline']['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
     # ---------------------------------------------------------------- CPU baseline
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a)
@@ -275,6 +289,27 @@ def bench_prefill(torch, coda, m, a):
                          "flops_per_launch": flops, "avg_launch_ms": round(attn_ms, 5),
                          "traffic": profile_traffic("prefill_chunk_b%d attn_fa_bf16<128,8>" % B),
                          "valid_prefix_slots": n_prefix}}
+
+
+def bench_decode_c5(torch, coda, a, B=128, steps=50, warmup=10):
+    """configs[4]'s decode: the 70B-shaped layer (hidden 8192, 64 q heads, 8
+    KV heads, head_dim 128, W512 / Me128 / Ms128, Lbuf 768) at its full decode
+    batch of 128 on one GPU (the state is 402 MB), pre-filled with 1024
+    tokens; same timing as the configs[1] line."""
+    dev = "cuda:0"
+    torch.manual_seed(0)
+    m = coda.CoDAGQALandmarkPerf2(embed_dim=8192, num_heads=64, num_kv_heads=8, window=512,
+                                  num_landmarks_exact=128, num_landmarks_summary=128, rope_base=1e4)
+    m = m.to(dtype=torch.bfloat16).to(dev).eval()
+    tok_s, ms_step, gpu_ms = run_decode(torch, coda, m, B, 1024, 256, steps, warmup, a.block)[:3]
+    attn_b, bank_b = decode_bytes(m, B)
+    achieved = (attn_b + bank_b) / (gpu_ms * 1e-3) / 1e9
+    return {"metric": "decode tok/s, 70B-shaped bounded layer (configs[4]), large cache, batch %d" % B,
+            "value": round(tok_s, 1), "unit": "tok/s", "batch": B, "steps": steps, "ms_per_step": round(ms_step, 5),
+            "config": "hidden 8192, H64/Hkv8/Dh128, W512/Me128/Ms128 (Lbuf 768), bf16, 1024 tokens pre-filled",
+            "roofline": {"bound": "hbm", "kernel": "decode_step_bf16<128>", "achieved": round(achieved, 1),
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "bytes_per_launch": attn_b + bank_b, "avg_launch_ms": round(gpu_ms, 5)}}
 
 
 def bench_unbounded(torch, coda, B=2, L=8192, H=32, Hkv=8, Dh=128, reps=5):

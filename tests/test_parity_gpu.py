@@ -256,7 +256,10 @@ def test_run_twice_is_bit_identical():
 # bank kernel + attention kernel; head_dim 64 / 128 in bf16 the fused step
 # kernel (bank update on one wave beside the ring attention)
 STEP_CFGS = {"dh32": (128, 4, 2, 256), "dh128_g2": (512, 4, 2, 64), "dh64_g4": (512, 8, 2, 64),
-             "dh128_g8": (1024, 8, 1, 16)}
+             "dh128_g8": (1024, 8, 1, 16),
+             # configs[4]'s per-KV-head shape (70B: G = 8, head_dim 128, large cache W512 / Me128 /
+             # Ms128, Lbuf 768) at a small batch: (E, H, Hkv, B, W, Me, Ms, prefill tokens)
+             "c5_cache": (1024, 8, 1, 8, 512, 128, 128, 640)}
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
@@ -267,11 +270,12 @@ def test_decode_step_matches_oracle_large_batch(dtype, cfg):
     its bf16 and fp32 paths.  Teacher-forced per step."""
     _need_gpu()
     from coda_oracle import OracleLayer, banks, prims
-    E, H, Hkv, B = STEP_CFGS[cfg]
+    E, H, Hkv, B, *rest = STEP_CFGS[cfg]
+    W_, Me_, Ms_, L_ = rest or (32, 16, 16, 80)
     Dh = E // H
     print(f"[decode_step] {dtype} {cfg}", flush=True)
-    kw = dict(embed_dim=E, num_heads=H, num_kv_heads=Hkv, window=32, num_landmarks_exact=16,
-              num_landmarks_summary=16)
+    kw = dict(embed_dim=E, num_heads=H, num_kv_heads=Hkv, window=W_, num_landmarks_exact=Me_,
+              num_landmarks_summary=Ms_)
     case = {"kw": kw}
     torch.manual_seed(5)
     m = OracleLayer(**kw).to(dtype).eval()
@@ -279,10 +283,10 @@ def test_decode_step_matches_oracle_large_batch(dtype, cfg):
     torch.manual_seed(6)
     st_o = m.init_state(batch_size=B, dtype=dtype)
     g = torch.Generator().manual_seed(7)
-    x = torch.randn(B, 80, E, generator=g).to(dtype)
-    m.prefill_chunked(x, st_o, block_size=32, return_outputs=False)
+    x = torch.randn(B, L_, E, generator=g).to(dtype)
+    m.prefill_chunked(x, st_o, block_size=32 if L_ <= 80 else 256, return_outputs=False)
     W, Me = m.window, m.Me
-    for t in range(12):
+    for t in range(12 if L_ <= 80 else 6):
         xt = torch.randn(B, 1, E, generator=g).to(dtype)
         st_p = to_product_state(st_o, DEV)
         qp = int(st_o.pos)
