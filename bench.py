@@ -284,7 +284,7 @@ def bench_prefill(torch, coda, m, a):
     return {"metric": "chunked-prefill tok/s (configs[2], hot path: attention + banks per chunk)",
             "value": round(B * L / wall, 1), "unit": "tok/s", "batch": B, "seq_len": L, "block": blk,
             "ms_total": round(wall * 1e3, 3),
-            "roofline": {"bound": "mfma", "kernel": "attn_fa_bf16<128,8>", "achieved": round(tflops, 2),
+            "roofline": {"bound": "mfma", "kernel": "attn_fa_bf16<128,8,2,1>", "achieved": round(tflops, 2),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                          "flops_per_launch": flops, "avg_launch_ms": round(attn_ms, 5),
                          "traffic": profile_traffic("prefill_chunk_b%d attn_fa_bf16<128,8>" % B),
@@ -345,7 +345,7 @@ def bench_unbounded(torch, coda, B=2, L=8192, H=32, Hkv=8, Dh=128, reps=5):
     tflops = flops / (ms * 1e-3) / 1e12
     return {"metric": "unbounded causal diff-attention tok/s (configs[3])", "value": round(B * L / (ms * 1e-3), 1),
             "unit": "tok/s", "batch": B, "seq_len": L, "ms": round(ms, 4),
-            "roofline": {"bound": "mfma", "kernel": "attn_fa_bf16<128,8> (causal)", "achieved": round(tflops, 2),
+            "roofline": {"bound": "mfma", "kernel": "attn_fa_bf16<128,8,2,1> (causal)", "achieved": round(tflops, 2),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                          "flops_per_launch": flops, "avg_launch_ms": round(ms, 5)}}
 

@@ -37,6 +37,7 @@
 
 #include <math.h>
 #include <type_traits>
+#include <utility>
 #include <stdlib.h>
 
 namespace coda {
@@ -800,6 +801,40 @@ __device__ __forceinline__ void lds_load16(const void* gsrc, void* lds) {
 // (j & 3) of the 8-byte segments addressed by lanes 4 y + (j & 15) / 4,
 // y = 0..3 (a 4 x 16 -> 16 x 4 transpose of 16-bit elements)
 typedef __bf16 bf16x4v_t __attribute__((ext_vector_type(4)));
+// 32-bit LDS byte address of a pointer into LDS
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+// ds_read_b64_tr_b16 issued by hand, at an immediate byte offset.  The
+// compiler treats the intrinsic as a read that may alias any direct
+// global->LDS load in flight and waits for all of them first, which
+// serialises the next tile's loads with this tile's PV product; here the
+// caller orders the reads (barrier after the tile's loads landed) and waits
+// for the results with lds_wait4_n.
+template <int OFF>
+__device__ __forceinline__ uint2 lds_read_tr16_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  uint2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+// lgkmcnt(N) tied to four raw reads: they have landed once at most N LDS
+// operations issued after them are still outstanding (LDS returns in order)
+template <int N>
+__device__ __forceinline__ void lds_wait4_n(uint2& a, uint2& b, uint2& c, uint2& d) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(N));
+}
+// f(std::integral_constant<int, 0>{}) .. f(..<N - 1>{}): loop indices that
+// are constant expressions (immediate offsets, wait counts)
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 __device__ __forceinline__ uint2 lds_read_tr16(const void* lds) {
   const bf16x4v_t t =
       __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v_t*)lds);
@@ -1689,7 +1724,7 @@ __global__ __launch_bounds__(NW * 64) void attn_tile_bf16(const coda_attn_desc a
 // (and O is rescaled) only when a row's new max exceeds it by more than
 // 2^8, so most tiles skip the rescale; P is rounded to bf16 by the
 // hardware conversion for the PV MFMA.
-template <int DH>
+template <int DH, int NS = 2>
 struct FaLayout {
   static constexpr int KT = 64, NST = 4, NC = DH / 32, NM = DH / 16;
   static constexpr int KBYTES = NST * NC * 1024;  // K tile
@@ -1697,12 +1732,24 @@ struct FaLayout {
   static constexpr int VBYTES = KT * ROWB;        // V tile
   static constexpr int CPR = DH / 8;              // 16-byte chunks per V row
   static constexpr int RPI = 1024 / ROWB;         // V rows per 1 KiB direct load
-  static constexpr int LDS = 2 * KBYTES + 2 * VBYTES;
+  static constexpr int LDS = NS * (KBYTES + VBYTES);  // NS tiles in flight
 };
 
-template <int DH, int NW>
-__global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, int NQ, int nqb, int npairs) {
-  using Lay = FaLayout<DH>;
+// s_waitcnt vmcnt(n) for a run-time n in [0, 15] (the count is an immediate)
+__device__ __forceinline__ void vm_wait(int n) {
+  switch (n) {
+#define CODA_VMW(k) \
+  case k: __builtin_amdgcn_s_waitcnt(((k) & 15) | 0x0f70); break;
+    CODA_VMW(0) CODA_VMW(1) CODA_VMW(2) CODA_VMW(3) CODA_VMW(4) CODA_VMW(5) CODA_VMW(6) CODA_VMW(7)
+    CODA_VMW(8) CODA_VMW(9) CODA_VMW(10) CODA_VMW(11) CODA_VMW(12) CODA_VMW(13) CODA_VMW(14) CODA_VMW(15)
+#undef CODA_VMW
+    default: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+  }
+}
+
+template <int DH, int NW, int NS, int QG>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void attn_fa_bf16(const coda_attn_desc a, int NQ, int nqb, int npairs) {
+  using Lay = FaLayout<DH, NS>;
   constexpr int KT = Lay::KT, NC = Lay::NC, NM = Lay::NM;
   constexpr int KCH = Lay::NST * NC;          // 1 KiB K chunks per tile
   constexpr int KCW = (KCH + NW - 1) / NW;    // per wave
@@ -1713,7 +1760,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
   __shared__ uint8_t al32[kMaxRowsPrefix / 32];
   __shared__ float w_lds[DH];
   char* kbuf = fa_smem;
-  char* vbuf = fa_smem + 2 * Lay::KBYTES;
+  char* vbuf = fa_smem + NS * Lay::KBYTES;
 
   // block -> (query block, KV head, sequence); with a multiple of 8 pairs
   // the query blocks of one (sequence, KV head) share an XCD (dispatch is
@@ -1732,17 +1779,17 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
   const int G = a.H / a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g4 = lane >> 4;
-  // wave = (stream, head, 16-query group): waves 2r and 2r + 1 hold the
-  // signal and the noise stream of the same queries
+  // wave = (stream, head, QG groups of 16 queries): waves 2r and 2r + 1
+  // hold the signal and the noise stream of the same queries; each K / V
+  // fragment read from LDS feeds the QG groups' MFMAs
+  constexpr int QW = 16 * QG;  // queries per wave
   const int strm = wv & 1, r = wv >> 1;
   const int g = r / NQ, qsub = r % NQ, h = hk * G + g;
-  const int q0 = qb * 16 * NQ + 16 * qsub;
-  const int qrow = q0 + n;
-  const bool qlive = qrow < a.Lq;
+  const int q0 = qb * QW * NQ + QW * qsub;
   const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
   const int Lk = a.Lp + a.Lb;
   const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
-  const int q_hi = min(a.Lq - 1, qb * 16 * NQ + 16 * NQ - 1);
+  const int q_hi = min(a.Lq - 1, qb * QW * NQ + QW * NQ - 1);
   const int klim = a.causal ? min(Lk, a.Lp + q_hi + coff + 1) : Lk;
   const int ntile = (klim + KT - 1) / KT;
 
@@ -1835,83 +1882,91 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
   }
   const bf16_t w_raw = tid < DH && a.rms_w ? ((const bf16_t*)a.rms_w)[tid] : (bf16_t)0x3f80;
 
-  // ---- queries of this lane (row qrow, channels 32 c + 8 g4 .. + 8) for
-  // this wave's stream: RoPE with the eager-op rounding, then for the
-  // noise stream the per-head rotation (primitives.py:58-113), unless the
-  // noise queries are given
-  bf16x8_t qf[NC];
-  bf16_t lam_raw;
+  // ---- queries of this lane (row q0 + 16 qg + n, channels 32 c + 8 g4 ..
+  // + 8) for this wave's stream: RoPE with the eager-op rounding, then for
+  // the noise stream the per-head rotation (primitives.py:58-113), unless
+  // the noise queries are given.  All loads go out before any math.
+  bf16x8_t qf[QG][NC];
+  bf16_t lam_raw[QG];
   {
     using E = Elt<bf16_t>;
     constexpr int half = DH / 2;
-    const int qi = qlive ? qrow : 0;
     const bool given = strm == 1 && a.q_noise != nullptr;
     const bool rot = strm == 1 && a.q_noise == nullptr;
-    const bf16_t* qr = given ? (const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh + (int64_t)qi * a.qn_sl
-                             : (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
     const bool rope = a.rope_cos != nullptr && !given, inter = a.rope_interleaved != 0;
-    const bf16_t* csr = rope ? (const bf16_t*)a.rope_cos + (int64_t)qi * half : nullptr;
-    const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
-    uint4 uq[NC], up[NC], rc[NC], rs[NC];
-    uint2 rc2[NC], rs2[NC], tcs[NC], tsn[NC];
+    uint4 uq[QG][NC], up[QG][NC], rc[QG][NC], rs[QG][NC];
+    uint2 rc2[QG][NC], rs2[QG][NC], tcs[NC], tsn[NC];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int d0 = 32 * c + 8 * g4;
-      uq[c] = *reinterpret_cast<const uint4*>(qr + d0);
-      if (rope && inter) {
-        rc2[c] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
-        rs2[c] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
-      }
-      if (rope && !inter) {
-        const int f0 = d0 < half ? d0 : d0 - half;
-        up[c] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
-        rc[c] = *reinterpret_cast<const uint4*>(csr + f0);
-        rs[c] = *reinterpret_cast<const uint4*>(snr + f0);
-      }
-      if (rot) {
-        tcs[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_cos + (int64_t)h * half + d0 / 2);
-        tsn[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_sin + (int64_t)h * half + d0 / 2);
-      }
-    }
-    lam_raw = ((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl];
+    for (int qg = 0; qg < QG; ++qg) {
+      const int qrow = q0 + 16 * qg + n;
+      const int qi = qrow < a.Lq ? qrow : 0;
+      const bf16_t* qr = given ? (const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh + (int64_t)qi * a.qn_sl
+                               : (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
+      const bf16_t* csr = rope ? (const bf16_t*)a.rope_cos + (int64_t)qi * half : nullptr;
+      const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int d0 = 32 * c + 8 * g4;
-      if (given) {
-        qf[c] = __builtin_bit_cast(bf16x8_t, qlive ? uq[c] : uint4{0, 0, 0, 0});
-        continue;
-      }
-      uint32_t w[4] = {uq[c].x, uq[c].y, uq[c].z, uq[c].w};
-      if (rope && inter) {
-        // pairs (2p, 2p+1) rotated by angle d0/2 + p: one bf16 dot2 per
-        // output (fp32 products and sum, one rounding)
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp) w[pp] = rot_pair(w[pp], pp >> 1 ? rc2[c].y : rc2[c].x,
-                                                        pp >> 1 ? rs2[c].y : rs2[c].x, pp & 1);
-      }
-      if (rope && !inter) {
-        // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin, with
-        // the eager-op rounding of each product and sum
-        float x[8], cc[8], ss[8], y[8];
-        unpack8(uq[c], x);
-        unpack8(rc[c], cc);
-        unpack8(rs[c], ss);
-        unpack8(up[c], y);
-        const bool lo = d0 < half;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float rt = lo ? -y[j] : y[j];
-          x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rt * ss[j]));
+      for (int c = 0; c < NC; ++c) {
+        const int d0 = 32 * c + 8 * g4;
+        uq[qg][c] = *reinterpret_cast<const uint4*>(qr + d0);
+        if (rope && inter) {
+          rc2[qg][c] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
+          rs2[qg][c] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
         }
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp) w[pp] = pk_bf16(x[2 * pp], x[2 * pp + 1]);
+        if (rope && !inter) {
+          const int f0 = d0 < half ? d0 : d0 - half;
+          up[qg][c] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
+          rc[qg][c] = *reinterpret_cast<const uint4*>(csr + f0);
+          rs[qg][c] = *reinterpret_cast<const uint4*>(snr + f0);
+        }
+        if (rot && qg == 0) {
+          tcs[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_cos + (int64_t)h * half + d0 / 2);
+          tsn[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_sin + (int64_t)h * half + d0 / 2);
+        }
       }
-      if (rot) {
+      lam_raw[qg] = ((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl];
+    }
 #pragma unroll
-        for (int pp = 0; pp < 4; ++pp) w[pp] = rot_pair(w[pp], pp >> 1 ? tcs[c].y : tcs[c].x,
-                                                        pp >> 1 ? tsn[c].y : tsn[c].x, pp & 1);
+    for (int qg = 0; qg < QG; ++qg) {
+      const bool qlive = q0 + 16 * qg + n < a.Lq;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int d0 = 32 * c + 8 * g4;
+        if (given) {
+          qf[qg][c] = __builtin_bit_cast(bf16x8_t, qlive ? uq[qg][c] : uint4{0, 0, 0, 0});
+          continue;
+        }
+        uint32_t w[4] = {uq[qg][c].x, uq[qg][c].y, uq[qg][c].z, uq[qg][c].w};
+        if (rope && inter) {
+          // pairs (2p, 2p+1) rotated by angle d0/2 + p: one bf16 dot2 per
+          // output (fp32 products and sum, one rounding)
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) w[pp] = rot_pair(w[pp], pp >> 1 ? rc2[qg][c].y : rc2[qg][c].x,
+                                                          pp >> 1 ? rs2[qg][c].y : rs2[qg][c].x, pp & 1);
+        }
+        if (rope && !inter) {
+          // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin, with
+          // the eager-op rounding of each product and sum
+          float x[8], cc[8], ss[8], y[8];
+          unpack8(uq[qg][c], x);
+          unpack8(rc[qg][c], cc);
+          unpack8(rs[qg][c], ss);
+          unpack8(up[qg][c], y);
+          const bool lo = d0 < half;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float rt = lo ? -y[j] : y[j];
+            x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rt * ss[j]));
+          }
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) w[pp] = pk_bf16(x[2 * pp], x[2 * pp + 1]);
+        }
+        if (rot) {
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) w[pp] = rot_pair(w[pp], pp >> 1 ? tcs[c].y : tcs[c].x,
+                                                          pp >> 1 ? tsn[c].y : tsn[c].x, pp & 1);
+        }
+        qf[qg][c] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
       }
-      qf[c] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
     }
   }
   // visibility bytes of the prefix, per-32-key "all visible" flags (one
@@ -1922,7 +1977,15 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
     if (i < a.Lp) al_lds[i] = al_r[k];
   }
   if (tid < DH) w_lds[tid] = bf2f(w_raw);
-  __syncthreads();
+  // tiles 1 .. NS-2 go out now, behind tile 0 (the query math above waited
+  // for every load in flight)
+#pragma unroll
+  for (int t = 1; t < NS - 1; ++t)
+    if (t < ntile) tile_load(t * KT, t);
+  // a bare barrier: the LDS stores above are done (lgkmcnt), the tile loads
+  // stay in flight
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
   for (int base = 64 * wv; base < a.Lp; base += 64 * NW) {
     const int i = base + lane;
     const uint64_t m = __ballot(i < a.Lp && al_lds[i] != 0);
@@ -1938,154 +2001,210 @@ __global__ __launch_bounds__(NW * 64) void attn_fa_bf16(const coda_attn_desc a, 
   for (int mt = 0; mt < NM; ++mt)
     v_off[mt] = vrow * Lay::ROWB + 16 * ((2 * mt + ((n & 3) >> 1)) ^ fa_vswz<DH>(vrow)) + 8 * (n & 1);
 
-  float m_s = -INFINITY, l_s = 0.f;
-  f32x4 o[NM];
+  float m_s[QG], l_s[QG];
+  f32x4 o[QG][NM];
 #pragma unroll
-  for (int i = 0; i < NM; ++i) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int qg = 0; qg < QG; ++qg) {
+    m_s[qg] = -INFINITY;
+    l_s[qg] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NM; ++i) o[qg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
+  // direct loads this wave issues per tile
+  const int lpt = (kw ? KCW : 0) + (vw ? VCW : 0);
   for (int it = 0; it < ntile; ++it) {
-    const int bi = it & 1, kt0 = it * KT;
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it's direct LDS loads have landed
-    __syncthreads();                     // ... for every wave; buffer bi ^ 1 is free
-    if (it + 1 < ntile) tile_load(kt0 + KT, bi ^ 1);
+    const int bi = it % NS, kt0 = it * KT;
+    // tile it's direct loads have landed (the tiles after it may stay in
+    // flight), this wave's reads of tile it - 1 are done; after the bare
+    // barrier the same holds for every wave, so tile it + NS - 1 can go into
+    // the buffer of tile it - 1
+    vm_wait(lpt * (min(ntile - 1, it + NS - 2) - it));
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    if (it + NS - 1 < ntile) tile_load(kt0 + (NS - 1) * KT, (it + NS - 1) % NS);
     const char* kb_t = kbuf + bi * Lay::KBYTES;
-    // S^T: st[sub][j] = score of key kt0 + 16 sub + 4 g4 + j against query n
-    f32x4 st[4];
+    // S^T: st[qg][sub][j] = score of key kt0 + 16 sub + 4 g4 + j against
+    // query q0 + 16 qg + n.  Channel block c at a time over the 4 sub-tiles
+    // (4 independent accumulation chains), block c + 1's fragments read
+    // before block c's products
+    f32x4 st[QG][4];
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const bf16x8_t kf =
             __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(kb_t + (sub * NC + c) * 1024 + 16 * lane));
-        st[sub] = mfma_k32(kf, qf[c], c == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[sub]);
+#pragma unroll
+        for (int qg = 0; qg < QG; ++qg)
+          st[qg][sub] = mfma_k32(kf, qf[qg][c], c == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[qg][sub]);
       }
     }
-    // hide the keys this wave's queries may not see (only where some may be)
-    bool need = false;
+    uint4 pb[QG][2];
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int pk0 = kt0 + 32 * hh;
-      need |= (pk0 + 32 > Lk) || (pk0 < a.Lp && !al32[pk0 >> 5]) ||
-              (pk0 + 32 > a.Lp && a.causal && (pk0 + 31 - a.Lp) > q0 + coff);
-    }
-    if (need) {
+    for (int qg = 0; qg < QG; ++qg) {
+      const int qg0 = q0 + 16 * qg, qrow = qg0 + n;
+      // hide the keys these queries may not see (only where some may be)
+      bool need = false;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int pk0 = kt0 + 32 * hh;
+        need |= (pk0 + 32 > Lk) || (pk0 < a.Lp && !al32[pk0 >> 5]) ||
+                (pk0 + 32 > a.Lp && a.causal && (pk0 + 31 - a.Lp) > qg0 + coff);
+      }
+      if (need) {
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            // branch-free: the visibility byte is read at a clamped index
+            const int kidx = kt0 + 16 * sub + 4 * g4 + j;
+            const int jb = kidx - a.Lp;
+            const bool pre = kidx < a.Lp;
+            const bool al_ok = al_lds[pre ? kidx : 0] != 0;
+            const bool blk_ok = (jb < a.Lb) & ((a.causal == 0) | (jb <= qrow + coff));
+            const bool vis = pre ? al_ok : blk_ok;
+            st[qg][sub][j] = vis ? st[qg][sub][j] : -INFINITY;
+          }
+      }
+      float t0 = fmaxf(fmaxf(st[qg][0][0], st[qg][0][1]), fmaxf(st[qg][0][2], st[qg][0][3]));
+      float t1 = fmaxf(fmaxf(st[qg][1][0], st[qg][1][1]), fmaxf(st[qg][1][2], st[qg][1][3]));
+      float t2 = fmaxf(fmaxf(st[qg][2][0], st[qg][2][1]), fmaxf(st[qg][2][2], st[qg][2][3]));
+      float t3 = fmaxf(fmaxf(st[qg][3][0], st[qg][3][1]), fmaxf(st[qg][3][2], st[qg][3][3]));
+      const float tsc = xmax32(xmax16(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)))) * scale;
+      if (__ballot(tsc > m_s[qg] + 8.f)) {
+        const float mnew = fmaxf(m_s[qg], tsc);
+        const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s[qg] - mnew);
+#pragma unroll
+        for (int i = 0; i < NM; ++i) o[qg][i] *= alpha;
+        l_s[qg] *= alpha;
+        m_s[qg] = mnew;
+      }
+      const float mu = m_s[qg] == -INFINITY ? 0.f : m_s[qg];
+      float pr[4][4];
 #pragma unroll
       for (int sub = 0; sub < 4; ++sub)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          // branch-free: the visibility byte is read at a clamped index
-          const int kidx = kt0 + 16 * sub + 4 * g4 + j;
-          const int jb = kidx - a.Lp;
-          const bool pre = kidx < a.Lp;
-          const bool al_ok = al_lds[pre ? kidx : 0] != 0;
-          const bool blk_ok = (jb < a.Lb) & ((a.causal == 0) | (jb <= qrow + coff));
-          const bool vis = pre ? al_ok : blk_ok;
-          st[sub][j] = vis ? st[sub][j] : -INFINITY;
-        }
-    }
-    float t0 = fmaxf(fmaxf(st[0][0], st[0][1]), fmaxf(st[0][2], st[0][3]));
-    float t1 = fmaxf(fmaxf(st[1][0], st[1][1]), fmaxf(st[1][2], st[1][3]));
-    float t2 = fmaxf(fmaxf(st[2][0], st[2][1]), fmaxf(st[2][2], st[2][3]));
-    float t3 = fmaxf(fmaxf(st[3][0], st[3][1]), fmaxf(st[3][2], st[3][3]));
-    const float tsc = xmax32(xmax16(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)))) * scale;
-    if (__ballot(tsc > m_s + 8.f)) {
-      const float mnew = fmaxf(m_s, tsc);
-      const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s - mnew);
+        for (int j = 0; j < 4; ++j) pr[sub][j] = fast_exp2(fmaf(st[qg][sub][j], scale, -mu));
 #pragma unroll
-      for (int i = 0; i < NM; ++i) o[i] *= alpha;
-      l_s *= alpha;
-      m_s = mnew;
-    }
-    const float mu = m_s == -INFINITY ? 0.f : m_s;
-    float pr[4][4];
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pr[sub][j] = fast_exp2(fmaf(st[sub][j], scale, -mu));
-    uint4 pb[2];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      pb[hh].x = pk_bf16(pr[2 * hh][0], pr[2 * hh][1]);
-      pb[hh].y = pk_bf16(pr[2 * hh][2], pr[2 * hh][3]);
-      pb[hh].z = pk_bf16(pr[2 * hh + 1][0], pr[2 * hh + 1][1]);
-      pb[hh].w = pk_bf16(pr[2 * hh + 1][2], pr[2 * hh + 1][3]);
-    }
-    float q4[4];
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub) q4[sub] = (pr[sub][0] + pr[sub][1]) + (pr[sub][2] + pr[sub][3]);
-    l_s += (q4[0] + q4[1]) + (q4[2] + q4[3]);
-    const char* vb_t = vbuf + bi * Lay::VBYTES;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, pb[hh]);
-      const char* vp_t = vb_t + 32 * hh * Lay::ROWB;
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt) {
-        const uint2 lo = lds_read_tr16(vp_t + v_off[mt]);
-        const uint2 hi = lds_read_tr16(vp_t + v_off[mt] + 16 * Lay::ROWB);
-        const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, uint4{lo.x, lo.y, hi.x, hi.y});
-        o[mt] = mfma_k32(vf, pf, o[mt]);
+      for (int hh = 0; hh < 2; ++hh) {
+        pb[qg][hh].x = pk_bf16(pr[2 * hh][0], pr[2 * hh][1]);
+        pb[qg][hh].y = pk_bf16(pr[2 * hh][2], pr[2 * hh][3]);
+        pb[qg][hh].z = pk_bf16(pr[2 * hh + 1][0], pr[2 * hh + 1][1]);
+        pb[qg][hh].w = pk_bf16(pr[2 * hh + 1][2], pr[2 * hh + 1][3]);
       }
+      float q4[4];
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) q4[sub] = (pr[sub][0] + pr[sub][1]) + (pr[sub][2] + pr[sub][3]);
+      l_s[qg] += (q4[0] + q4[1]) + (q4[2] + q4[3]);
     }
+    // PV: the tile's NM pairs of (hh, mt, mt + 1) products, each fed by
+    // four transposed reads; two pairs' reads in flight (three rotating
+    // register sets), each pair waits only for its own reads
+    const uint32_t vt_a = lds_addr(vbuf + bi * Lay::VBYTES);
+    constexpr int NP = NM;  // 2 halves x NM / 2 pairs
+    uint2 rd[3][4];
+    auto pv_issue = [&](auto p_c) {
+      constexpr int p = decltype(p_c)::value;
+      if constexpr (p < NP) {
+        constexpr int hh = p / (NM / 2), mt = 2 * (p % (NM / 2));
+        constexpr int HOFF = 32 * hh * Lay::ROWB, ROW16 = 16 * Lay::ROWB;
+        const uint32_t a0 = vt_a + v_off[mt], a1 = vt_a + v_off[mt + 1];
+        rd[p % 3][0] = lds_read_tr16_at<HOFF>(a0);
+        rd[p % 3][1] = lds_read_tr16_at<HOFF + ROW16>(a0);
+        rd[p % 3][2] = lds_read_tr16_at<HOFF>(a1);
+        rd[p % 3][3] = lds_read_tr16_at<HOFF + ROW16>(a1);
+      }
+    };
+    pv_issue(std::integral_constant<int, 0>{});
+    pv_issue(std::integral_constant<int, 1>{});
+    static_for<NP>([&](auto p_c) {
+      constexpr int p = decltype(p_c)::value;
+      constexpr int hh = p / (NM / 2), mt = 2 * (p % (NM / 2)), b3 = p % 3;
+      lds_wait4_n<(p + 1 < NP) ? 4 : 0>(rd[b3][0], rd[b3][1], rd[b3][2], rd[b3][3]);
+      const bf16x8_t va0 = __builtin_bit_cast(bf16x8_t, uint4{rd[b3][0].x, rd[b3][0].y, rd[b3][1].x, rd[b3][1].y});
+      const bf16x8_t va1 = __builtin_bit_cast(bf16x8_t, uint4{rd[b3][2].x, rd[b3][2].y, rd[b3][3].x, rd[b3][3].y});
+#pragma unroll
+      for (int qg = 0; qg < QG; ++qg) {
+        const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, pb[qg][hh]);
+        o[qg][mt] = mfma_k32(va0, pf, o[qg][mt]);
+        o[qg][mt + 1] = mfma_k32(va1, pf, o[qg][mt + 1]);
+      }
+      // pair p + 2's reads go out after pair p's products (into the set
+      // pair p - 1 used), then nothing crosses into the next pair
+      __builtin_amdgcn_sched_barrier(0);
+      pv_issue(std::integral_constant<int, p + 2>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
   }
-  // ---- epilogue: lane holds channels 16 mt + 4 g4 + j of row n.  The
-  // noise wave hands rnd(O_noise) (bf16) to its signal wave through LDS
-  // (the K/V buffers, free once every wave has left the loop)
-  l_s = xsum32(xsum16(l_s));
-  const float inv = l_s > 0.f ? 1.f / l_s : 0.f;
+  // ---- epilogue: lane holds channels 16 mt + 4 g4 + j of row q0 + 16 qg
+  // + n.  The noise wave hands rnd(O_noise) (bf16) to its signal wave
+  // through LDS (the K/V buffers, free once every wave has left the loop)
   constexpr int NV = NM * 4;
-  uint4* xch = reinterpret_cast<uint4*>(fa_smem) + r * (NV / 8) * 64;
+  float inv[QG];
+#pragma unroll
+  for (int qg = 0; qg < QG; ++qg) {
+    const float l = xsum32(xsum16(l_s[qg]));
+    inv[qg] = l > 0.f ? 1.f / l : 0.f;
+  }
+  uint4* xch = reinterpret_cast<uint4*>(fa_smem) + r * QG * (NV / 8) * 64;
   __syncthreads();
   if (strm == 1) {
 #pragma unroll
-    for (int i = 0; i < NV / 8; ++i) {
-      uint4 u;
-      u.x = pk_bf16(o[2 * i][0] * inv, o[2 * i][1] * inv);
-      u.y = pk_bf16(o[2 * i][2] * inv, o[2 * i][3] * inv);
-      u.z = pk_bf16(o[2 * i + 1][0] * inv, o[2 * i + 1][1] * inv);
-      u.w = pk_bf16(o[2 * i + 1][2] * inv, o[2 * i + 1][3] * inv);
-      xch[i * 64 + lane] = u;
-    }
+    for (int qg = 0; qg < QG; ++qg)
+#pragma unroll
+      for (int i = 0; i < NV / 8; ++i) {
+        uint4 u;
+        u.x = pk_bf16(o[qg][2 * i][0] * inv[qg], o[qg][2 * i][1] * inv[qg]);
+        u.y = pk_bf16(o[qg][2 * i][2] * inv[qg], o[qg][2 * i][3] * inv[qg]);
+        u.z = pk_bf16(o[qg][2 * i + 1][0] * inv[qg], o[qg][2 * i + 1][1] * inv[qg]);
+        u.w = pk_bf16(o[qg][2 * i + 1][2] * inv[qg], o[qg][2 * i + 1][3] * inv[qg]);
+        xch[(qg * (NV / 8) + i) * 64 + lane] = u;
+      }
   }
   __syncthreads();
   if (strm == 1) return;
-  const float lam = bf2f(lam_raw);
-  // y = O_signal - lam rnd(O_noise), then the HeadwiseRMSNorm and weight,
-  // in fp32 with one rounding at the store
-  float y[NV];
-  {
-    float on[NV];
 #pragma unroll
-    for (int i = 0; i < NV / 8; ++i) unpack8(xch[i * 64 + lane], on + 8 * i);
-    float sq = 0.f;
+  for (int qg = 0; qg < QG; ++qg) {
+    const int qrow = q0 + 16 * qg + n;
+    const float lam = bf2f(lam_raw[qg]);
+    // y = O_signal - lam rnd(O_noise), then the HeadwiseRMSNorm and weight,
+    // in fp32 with one rounding at the store
+    float y[NV];
+    {
+      float on[NV];
 #pragma unroll
-    for (int mt = 0; mt < NM; ++mt)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = mt * 4 + j;
-        y[i] = fmaf(-lam, on[i], o[mt][j] * inv);
-        sq = fmaf(y[i], y[i], sq);
-      }
-    if (a.rms_w) {
-      sq = xsum32(xsum16(sq));
-      const float rr = 1.0f / sqrtf(sq / (float)DH + a.eps);
+      for (int i = 0; i < NV / 8; ++i) unpack8(xch[(qg * (NV / 8) + i) * 64 + lane], on + 8 * i);
+      float sq = 0.f;
 #pragma unroll
       for (int mt = 0; mt < NM; ++mt)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int i = mt * 4 + j;
-          y[i] = y[i] * (rr * w_lds[16 * mt + 4 * g4 + j]);
+          y[i] = fmaf(-lam, on[i], o[qg][mt][j] * inv[qg]);
+          sq = fmaf(y[i], y[i], sq);
         }
-    }
-  }
-  if (qlive) {
-    bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
+      if (a.rms_w) {
+        sq = xsum32(xsum16(sq));
+        const float rr = 1.0f / sqrtf(sq / (float)DH + a.eps);
 #pragma unroll
-    for (int mt = 0; mt < NM; ++mt) {
-      uint2 u;
-      u.x = pk_bf16(y[mt * 4 + 0], y[mt * 4 + 1]);
-      u.y = pk_bf16(y[mt * 4 + 2], y[mt * 4 + 3]);
-      *reinterpret_cast<uint2*>(orow_p + 16 * mt + 4 * g4) = u;
+        for (int mt = 0; mt < NM; ++mt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int i = mt * 4 + j;
+            y[i] = y[i] * (rr * w_lds[16 * mt + 4 * g4 + j]);
+          }
+      }
+    }
+    if (qrow < a.Lq) {
+      bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
+#pragma unroll
+      for (int mt = 0; mt < NM; ++mt) {
+        uint2 u;
+        u.x = pk_bf16(y[mt * 4 + 0], y[mt * 4 + 1]);
+        u.y = pk_bf16(y[mt * 4 + 2], y[mt * 4 + 3]);
+        *reinterpret_cast<uint2*>(orow_p + 16 * mt + 4 * g4) = u;
+      }
     }
   }
 }
@@ -2163,22 +2282,25 @@ static bool fa_offsets_fit(const coda_attn_desc* d) {
          (d->Lb == 0 || (d->b_sl >= 0 && ((int64_t)d->Lb + 64) * d->b_sl < lim));
 }
 
-template <int DH, int NW>
-static int launch_fa_nw(const coda_attn_desc* d, hipStream_t st, int NQ, int nblk) {
+template <int DH, int NW, int NS, int QG>
+static int launch_fa_nw(const coda_attn_desc* d, hipStream_t st, int G) {
   const int npairs = d->B * d->Hkv;
-
-  const size_t lds = FaLayout<DH>::LDS;
-  hipError_t e = hipFuncSetAttribute((const void*)attn_fa_bf16<DH, NW>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)lds);
+  const int NQ = NW / (2 * G);  // waves = 2 streams x G heads x NQ
+  const int nblk = (d->Lq + 16 * QG * NQ - 1) / (16 * QG * NQ);
+  const size_t lds = FaLayout<DH, NS>::LDS;
+  hipError_t e = hipFuncSetAttribute((const void*)attn_fa_bf16<DH, NW, NS, QG>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return fail(CODA_EHIP, "coda_diff_attn_fwd: LDS attribute: %s", hipGetErrorString(e));
-  hipLaunchKernelGGL((attn_fa_bf16<DH, NW>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk, npairs);
+  hipLaunchKernelGGL((attn_fa_bf16<DH, NW, NS, QG>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk,
+                     npairs);
   return check_launch("attn_fa_bf16");
 }
 template <int DH>
-static int launch_fa(const coda_attn_desc* d, hipStream_t st, int G, int NQ, int nblk) {
+static int launch_fa(const coda_attn_desc* d, hipStream_t st, int G) {
   if constexpr (DH >= 64) {
-    // one wave per (stream, head, 16 queries)
-    return G == 8 ? launch_fa_nw<DH, 16>(d, st, NQ, nblk) : launch_fa_nw<DH, 8>(d, st, NQ, nblk);
+    // one wave per (stream, head, 16 queries): 16 waves for G = 8, else 8
+    if (G == 8) return launch_fa_nw<DH, 16, 2, 1>(d, st, G);
+    return launch_fa_nw<DH, 8, 2, 1>(d, st, G);
   } else {
     return fail(CODA_EUNSUP, "coda_diff_attn_fwd: flash tiles need head_dim >= 64");
   }
@@ -2210,9 +2332,9 @@ static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
                        (const float*)d->workspace);
     return check_launch("attn_rows_merge");
   }
-  int NQ = G >= 4 ? 1 : 4 / G;
+  if (DH >= 64 && (G == 8 || G == 4 || G == 2 || G == 1) && fa_offsets_fit(d)) return launch_fa<DH>(d, st, G);
+  const int NQ = G >= 4 ? 1 : 4 / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
-  if (DH >= 64 && (G == 8 || G == 4 || G == 2 || G == 1) && fa_offsets_fit(d)) return launch_fa<DH>(d, st, G, NQ, nblk);
   if (G == 8) {
     hipLaunchKernelGGL((attn_tile_bf16<DH, 8>), dim3(nblk, d->Hkv, d->B), dim3(512), 0, st, *d, NQ);
   } else if (G == 4 || G == 2 || G == 1) {
