@@ -514,18 +514,22 @@ __device__ __forceinline__ void stage_cands(float* dst, int ls, const coda_bank_
 }
 
 // The chunk's candidates of head h, normalised (F.normalize, rounded as the
-// reference) into LDS: the first Te as exact V rows (all DH channels) into
-// dst_e, all Ts as summary LF-K bands (channels lf ..) into dst_s.  Every
-// wave takes rows r = wv + nw u of the concatenated list; all plan indices
-// of a pass load first, then all candidate rows, then the normalisation.
+// reference) into LDS, rows [r_lo, r_hi) of the concatenated list (the Te
+// exact candidates, then the Ts summary candidates): exact candidates as V
+// rows (all DH channels) into dst_e from candidate e_lo = min(r_lo, Te) on,
+// summary candidates as LF-K bands (channels lf ..) into dst_s from
+// candidate max(r_lo - Te, 0) on.  Every wave takes rows r_lo + wv + nw u;
+// all plan indices of a pass load first, then all candidate rows, then the
+// normalisation.
 template <typename T, int DH>
 __device__ __forceinline__ void stage_cands_both(float* dst_e, int le, float* dst_s, int lsum, const coda_bank_desc& s,
                                                  const BlockGeom& g, const T* vbk, const T* kbk, const int32_t* pc,
-                                                 int b, int h) {
+                                                 int b, int h, int r_lo, int r_hi) {
   constexpr int NV = (DH + 63) / 64, RB = 12;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  const int Te = g.Te, n = g.Te + g.Ts, lf = s.lf, LF = DH - lf;
-  for (int r0 = 0; r0 < n; r0 += nw * RB) {
+  const int Te = g.Te, n = r_hi, lf = s.lf, LF = DH - lf;
+  const int e_lo = min(r_lo, Te), s_lo = max(r_lo - Te, 0);
+  for (int r0 = r_lo; r0 < n; r0 += nw * RB) {
     int idx[RB];
 #pragma unroll
     for (int u = 0; u < RB; ++u) {
@@ -552,7 +556,7 @@ __device__ __forceinline__ void stage_cands_both(float* dst_e, int le, float* ds
 #pragma unroll
       for (int i = 0; i < NV; ++i) act[i] = lane + 64 * i < len;
       wave_unit<T, NV>(x[u], act);
-      float* dst = ex ? dst_e + r * le : dst_s + (r - Te) * lsum;
+      float* dst = ex ? dst_e + (r - e_lo) * le : dst_s + (r - Te - s_lo) * lsum;
 #pragma unroll
       for (int i = 0; i < NV; ++i)
         if (act[i]) dst[lane + 64 * i] = x[u][i];
@@ -565,10 +569,11 @@ __global__ __launch_bounds__(256) void block_route_kernel(const coda_bank_desc s
                                                           const T* vbk, const float* gb,
                                                           const int32_t* __restrict__ plan_c, float* ws) {
   extern __shared__ __attribute__((aligned(16))) float rsm[];
-  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int h = blockIdx.x, b = blockIdx.y, z = blockIdx.z, t = threadIdx.x;
   const int Me = s.Me, Ms = s.Ms, W = s.W, LF = DH - s.lf;
   const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
   if (h == s.Hkv) {
+    if (z != 0) return;
     Snap sn = snap_of(s, g, ws, b);
     const uint8_t* al = s.allowed + (int64_t)b * (W + Me + Ms);
     for (int m = t; m < Me + Ms; m += blockDim.x) sn.used[m] = al[W + m];
@@ -612,22 +617,31 @@ __global__ __launch_bounds__(256) void block_route_kernel(const coda_bank_desc s
     }
     return;
   }
-  // LDS: exact norm rows [Me][DH+4] | exact candidates [Te][DH+4] |
-  //      summary norm rows [Ms][LF+4] | summary candidates [Ts][LF+4]
+  // workgroup z takes rows [r_lo, r_hi) of the concatenated candidate list
+  // (exact then summary), so the dots of one (sequence, head) spread over
+  // gridDim.z workgroups; each dot is formed as with one workgroup
+  const int n = g.Te + g.Ts, per = (n + (int)gridDim.z - 1) / (int)gridDim.z;
+  const int r_lo = z * per, r_hi = min(n, r_lo + per);
+  if (r_lo >= r_hi) return;
+  const int e_lo = min(r_lo, g.Te), ne = min(r_hi, g.Te) - e_lo;
+  const int s_lo = max(r_lo - g.Te, 0), ns = max(r_hi - g.Te, 0) - s_lo;
+  // LDS: exact norm rows [Me][DH+4] | exact candidates [ne][DH+4] |
+  //      summary norm rows [Ms][LF+4] | summary candidates [ns][LF+4]
   const int le = DH + 4, lsum = LF + 4;
   float* nrm_e = rsm;
-  float* cnd_e = nrm_e + (g.Te > 0 ? Me * le : 0);
-  float* nrm_s = cnd_e + g.Te * le;
-  float* cnd_s = nrm_s + (g.Ts > 0 ? Ms * lsum : 0);
-  if (g.Te > 0) stage_rows<T>(nrm_e, le, (const T*)s.exact_v_norm + ((int64_t)b * s.Hkv + h) * Me * DH, DH, Me, DH);
-  if (g.Ts > 0)
+  float* cnd_e = nrm_e + (ne > 0 ? Me * le : 0);
+  float* nrm_s = cnd_e + ne * le;
+  float* cnd_s = nrm_s + (ns > 0 ? Ms * lsum : 0);
+  if (ne > 0) stage_rows<T>(nrm_e, le, (const T*)s.exact_v_norm + ((int64_t)b * s.Hkv + h) * Me * DH, DH, Me, DH);
+  if (ns > 0)
     stage_rows<T>(nrm_s, lsum, (const T*)s.sum_lf_k_norm + ((int64_t)b * s.Hkv + h) * Ms * LF, LF, Ms, LF);
-  stage_cands_both<T, DH>(cnd_e, le, cnd_s, lsum, s, g, vbk, kbk, pc, b, h);
+  stage_cands_both<T, DH>(cnd_e, le, cnd_s, lsum, s, g, vbk, kbk, pc, b, h, r_lo, r_hi);
   __syncthreads();
-  if (g.Te > 0) lds_dots<T>(nrm_e, Me, cnd_e, g.Te, DH, le, ws + (((int64_t)b * s.Hkv + h) * g.Te) * Me);
-  if (g.Ts > 0)
-    lds_dots<T>(nrm_s, Ms, cnd_s, g.Ts, LF, lsum,
-                ws + CODA_WS(ws_dot_s, s, g) + (((int64_t)b * s.Hkv + h) * g.Ts) * Ms);
+  if (ne > 0)
+    lds_dots<T>(nrm_e, Me, cnd_e, ne, DH, le, ws + (((int64_t)b * s.Hkv + h) * g.Te + e_lo) * Me);
+  if (ns > 0)
+    lds_dots<T>(nrm_s, Ms, cnd_s, ns, LF, lsum,
+                ws + CODA_WS(ws_dot_s, s, g) + (((int64_t)b * s.Hkv + h) * g.Ts + s_lo) * Ms);
 }
 
 // Decision record of a chunk, per sequence (4-byte words), written by
@@ -1438,12 +1452,19 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
   const int LF = DH - s->lf;
   const int TT = g.Te > g.Ts ? g.Te : g.Ts;
   if (g.n_ev > 0 && TT > 0) {
-    const size_t lds1 = std::max(sizeof(float) * ((g.Te > 0 ? (size_t)(s->Me + g.Te) * (DH + 4) : 0) +
-                                                  (g.Ts > 0 ? (size_t)(s->Ms + g.Ts) * (LF + 4) : 0)),
+    // candidate rows split over nz workgroups per (sequence, head): about
+    // 256 workgroups in all, at least 32 rows each
+    const int n = g.Te + g.Ts, pairs = s->B * s->Hkv;
+    int nz = (256 + pairs - 1) / pairs;
+    nz = std::max(1, std::min(nz, (n + 31) / 32));
+    const int per = (n + nz - 1) / nz;
+    const size_t ne = (size_t)std::min(per, g.Te), ns = (size_t)std::min(per, g.Ts);
+    const size_t lds1 = std::max(sizeof(float) * ((ne > 0 ? (s->Me + ne) * (DH + 4) : 0) +
+                                                  (ns > 0 ? (s->Ms + ns) * (LF + 4) : 0)),
                                  sizeof(sel::Item<int64_t>) * (size_t)s->Me);
     int rc = ensure_lds(block_route_kernel<T, DH>, lds1, "coda_block_write");
     if (rc) return rc;
-    hipLaunchKernelGGL((block_route_kernel<T, DH>), dim3(s->Hkv + 1, s->B), dim3(256), lds1, st, *s, g,
+    hipLaunchKernelGGL((block_route_kernel<T, DH>), dim3(s->Hkv + 1, s->B, nz), dim3(256), lds1, st, *s, g,
                        (const T*)kb, (const T*)vb, gb, plan_c, ws);
     rc = check_launch("block_route");
     if (rc) return rc;
