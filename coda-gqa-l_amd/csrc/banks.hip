@@ -852,36 +852,25 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
   }
 }
 
-// Bank writes of head h of sequence b for one chunk, from the decisions
-// (memory_banks.py:707-742 exact write-back, :880-932 summary accumulate +
-// EMA) and the ring write of the surviving block tokens.  8 waves.  Loads
-// are issued in batches before their first use: the block tokens the ring
-// write copies (stored once every evicted ring row of this head has been
-// read), the summary candidate rows, the summary bank rows of head h and
-// the exact candidate rows (to LDS).  Each summary slot keeps the list of its tokens in token
+// Bank writes of one chunk from the decisions (memory_banks.py:707-742
+// exact write-back, :880-932 summary accumulate + EMA).  Workgroup (h, b, z)
+// owns the exact slots [z pe, (z + 1) pe) and the summary slots [z PS,
+// (z + 1) PS) of head h, so one (sequence, head) spreads over gridDim.z
+// workgroups; candidate values are read where they lie (ring slots or block
+// rows, not yet overwritten: the ring write is block_ring_kernel, launched
+// after this one).  Each summary slot keeps the list of its tokens in token
 // order, so one thread per (active slot, channel) sums the slot's weighted
 // tokens in registers (fp32, token order: the scatter_add order) and
-// applies the EMA in the same pass.
-// LDS: summary candidate rows [Ts][DH + LF] T | summary bank rows
-//      [Ms][DH + LF] T (V channels first, then K's LF band) | exact
-//      candidate rows [Te][2 DH] T (K, V) | new LF keys [Ms][LF] f32 |
-//      token lists [Ms][Ts] i32 | small arrays.  Once every evicted ring
-//      row is in LDS the ring write goes out (the stores overlap the rest).
+// applies the EMA in the same pass.  Workgroup (0, b, 0) also writes the
+// per-sequence metadata (visibility bytes of written slots, counters).
+// LDS (4-byte words): idx_e, fl_e [Te] | idx_s, wtok [Ts] | token lists
+//      [PS][Ts] | nlist, cnt, sflag, act_list [PS] | new LF keys [PS][LF] |
+//      summary flags of every slot [Ms] | misc [8].
 static constexpr int kApplyThreads = 512;
 static constexpr int kRingPre = 8;   // 16-byte ring-write chunks per thread loaded up front
 
-__host__ __device__ __forceinline__ size_t apply_small_words(int Me, int Ms, int Te, int Ts) {
-  return (size_t)2 * Te + Me + 2 * Ts + (Me + Ms) + 4 * Ms + 8;
-}
-__host__ __device__ __forceinline__ size_t apply_rows_bytes(int n, int DH, int LF, int esz) {
-  return ((size_t)n * (DH + LF) * esz + 15) & ~(size_t)15;
-}
-__host__ __device__ __forceinline__ size_t apply_erows_bytes(int Te, int DH, int esz) {
-  return ((size_t)Te * 2 * DH * esz + 15) & ~(size_t)15;
-}
-__host__ __device__ __forceinline__ size_t apply_lds_bytes(int Me, int Ms, int Te, int Ts, int DH, int LF, int esz) {
-  return apply_rows_bytes(Ts, DH, LF, esz) + apply_rows_bytes(Ms, DH, LF, esz) + apply_erows_bytes(Te, DH, esz) +
-         (size_t)Ms * LF * 4 + (size_t)Ms * Ts * 4 + 4 * apply_small_words(Me, Ms, Te, Ts);
+__host__ __device__ __forceinline__ size_t apply_lds_bytes(int Ms, int Te, int Ts, int PS, int LF) {
+  return 4 * ((size_t)2 * Te + 2 * Ts + (size_t)PS * Ts + 4 * PS + (size_t)PS * LF + Ms + 8);
 }
 
 // Eight consecutive elements moved as raw bits: PW 16-byte words.
@@ -905,155 +894,79 @@ __device__ __forceinline__ void st8(T* p, const Piece8<T> x) {
 
 template <typename T, int DH>
 __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
-                                                                    const T* vbk, const float* gb,
-                                                                    const int32_t* __restrict__ plan_c, float* ws) {
+                                                                    const T* vbk, const int32_t* __restrict__ plan_c,
+                                                                    float* ws) {
   using E = Elt<T>;
-  constexpr int NV = (DH + 63) / 64, CH = DH / 8, LF = DH / 2, NCOL = DH + LF, CPR = NCOL / 8;
+  constexpr int NV = (DH + 63) / 64, LF = DH / 2, NCOL = DH + LF;
   extern __shared__ __attribute__((aligned(16))) float asm_[];
-  const int h = blockIdx.x, b = blockIdx.y;
+  const int h = blockIdx.x, b = blockIdx.y, z = blockIdx.z, nz = gridDim.z;
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6, NT = blockDim.x, NW = NT >> 6;
   const int W = s.W, Me = s.Me, Ms = s.Ms, Hkv = s.Hkv, Te = g.Te, Ts = g.Ts, lf = s.lf;
   const int Lbuf = W + Me + Ms;
-  const bool lead = h == 0;
   T* kb = (T*)s.k_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
   T* vb = (T*)s.v_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
   uint8_t* al = s.allowed + (int64_t)b * Lbuf;
   const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
-  auto blk_row = [&](const T* base, int jb) { return base + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl; };
-
-  // ---- ring-write sources (block tokens), loaded now
-  const int Lr = g.ring_filled;
-  const int first = max(Lr, g.n_ev);
-  const int total = Lr + g.blk;
-  const int rhead = (Lr == W) ? g.ring_head : 0;
-  const int n_ring = (total - first) * CH;  // pieces of 8 elements per plane (K and V each)
-  Piece8<T> rk[kRingPre], rv[kRingPre];
-#pragma unroll
-  for (int u = 0; u < kRingPre; ++u) {
-    const int i = t + u * NT;
-    if (i < n_ring) {
-      const int jb = first + i / CH - Lr, c = i % CH;
-      rk[u] = ld8<T>(blk_row(kbk, jb) + 8 * c);
-      rv[u] = ld8<T>(blk_row(vbk, jb) + 8 * c);
-    }
-  }
-  auto ring_store = [&](int i, Piece8<T> xk, Piece8<T> xv) {
-    const int r = first + i / CH, c = i % CH;
-    const int slot = (rhead + r) % W;
-    st8<T>(kb + (int64_t)slot * DH + 8 * c, xk);
-    st8<T>(vb + (int64_t)slot * DH + 8 * c, xv);
-    if (lead && c == 0) {
-      s.g_recent[(int64_t)b * W + slot] = gb[(int64_t)b * g.g_sb + (r - Lr)];
-      al[slot] = 1;
-    }
-  };
-  auto ring_write = [&]() {
-#pragma unroll
-    for (int u = 0; u < kRingPre; ++u)
-      if (t + u * NT < n_ring) ring_store(t + u * NT, rk[u], rv[u]);
-    for (int i = t + kRingPre * NT; i < n_ring; i += NT) {
-      const int jb = first + i / CH - Lr, c = i % CH;
-      ring_store(i, ld8<T>(blk_row(kbk, jb) + 8 * c), ld8<T>(blk_row(vbk, jb) + 8 * c));
-    }
-  };
-  const bool evict = g.n_ev > 0 && (Te > 0 || Ts > 0);
-  if (!evict) {
-    ring_write();
-    return;
-  }
-  T* cst = reinterpret_cast<T*>(asm_);  // summary candidates [Ts][NCOL]
-  T* bst = reinterpret_cast<T*>(reinterpret_cast<char*>(cst) + apply_rows_bytes(Ts, DH, LF, sizeof(T)));  // [Ms][NCOL]
-  T* est = reinterpret_cast<T*>(reinterpret_cast<char*>(bst) + apply_rows_bytes(Ms, DH, LF, sizeof(T)));  // [Te][2 DH]
-  float* knew = reinterpret_cast<float*>(reinterpret_cast<char*>(est) + apply_erows_bytes(Te, DH, sizeof(T)));
-  int32_t* list = reinterpret_cast<int32_t*>(knew + (size_t)Ms * LF);  // [Ms][Ts]
-  int32_t* p = list + (size_t)Ms * Ts;
-  int32_t* idx_e = p; p += Te;
-  int32_t* fl_e = p; p += Te;
-  int32_t* eflag = p; p += Me;
-  int32_t* idx_s = p; p += Ts;
-  float* wtok = reinterpret_cast<float*>(p); p += Ts;
-  int32_t* used = p; p += Me + Ms;
-  float* cnt = reinterpret_cast<float*>(p); p += Ms;
-  int32_t* sflag = p; p += Ms;
-  int32_t* nlist = p; p += Ms;
-  int32_t* act_list = p; p += Ms;
-  int32_t* misc = p;
+  const int pe = (Me + nz - 1) / nz, e0 = min(Me, z * pe), e1 = min(Me, e0 + pe);
+  const int PS = (Ms + nz - 1) / nz, s0 = min(Ms, z * PS), s1 = min(Ms, s0 + PS), nsl = s1 - s0;
+  int32_t* idx_e = reinterpret_cast<int32_t*>(asm_);
+  int32_t* fl_e = idx_e + Te;
+  int32_t* idx_s = fl_e + Te;
+  float* wtok = reinterpret_cast<float*>(idx_s + Ts);
+  int32_t* list = reinterpret_cast<int32_t*>(wtok + Ts);  // [PS][Ts]
+  int32_t* nlist = list + (size_t)PS * Ts;
+  float* cnt = reinterpret_cast<float*>(nlist + PS);
+  int32_t* sflag = reinterpret_cast<int32_t*>(cnt + PS);
+  int32_t* act_list = sflag + PS;
+  float* knew = reinterpret_cast<float*>(act_list + PS);  // [PS][LF]
+  int32_t* fl_all = reinterpret_cast<int32_t*>(knew + (size_t)PS * LF);
+  int32_t* misc = fl_all + Ms;
   const Snap sn = snap_of(s, g, ws, b);
   const Dec dc = dec_of(s, g, ws, b);
   for (int i = t; i < Te; i += NT) { idx_e[i] = dc.idx_e[i]; fl_e[i] = dc.fl_e[i]; }
-  for (int i = t; i < Me; i += NT) eflag[i] = Te > 0 ? dc.eflag[i] : 0;
   for (int i = t; i < Ts; i += NT) { idx_s[i] = dc.idx_s[i]; wtok[i] = dc.wtok[i]; }
-  for (int i = t; i < Me + Ms; i += NT) used[i] = sn.used[i];
-  for (int m = t; m < Ms; m += NT) nlist[m] = 0;
-  // every row this workgroup reads goes to LDS in one pass, 8 pieces per
-  // thread in flight: summary candidates (V, then K's LF band), the
-  // summary bank rows of head h, the exact candidates (K, then V)
-  {
-    const int n_c = Ts * CPR, n_b = Ts > 0 ? Ms * CPR : 0, n_e = Te * 2 * CH;
-    const int n_all = n_c + n_b + n_e;
-    for (int base = t; base < n_all; base += 8 * NT) {
-      Piece8<T> xp[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = base + u * NT;
-        if (i < n_c) {
-          const int r = i / CPR, c8 = (i % CPR) * 8;
-          const bool is_v = c8 < DH;
-          xp[u] = ld8<T>(cand_row<T, DH>(s, g, is_v ? vbk : kbk, b, h, pc[r], is_v) + (is_v ? c8 : lf + (c8 - DH)));
-        } else if (i < n_c + n_b) {
-          const int ii = i - n_c, r = ii / CPR, c8 = (ii % CPR) * 8;
-          xp[u] = ld8<T>(c8 < DH ? vb + (int64_t)(W + Me + r) * DH + c8 : kb + (int64_t)(W + Me + r) * DH + lf + (c8 - DH));
-        } else if (i < n_all) {
-          const int ii = i - n_c - n_b, r = ii / (2 * CH), c = ii % (2 * CH);
-          const bool is_v = c >= CH;
-          xp[u] = ld8<T>(cand_row<T, DH>(s, g, is_v ? vbk : kbk, b, h, pc[r], is_v) + 8 * (c % CH));
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int i = base + u * NT;
-        if (i < n_c) st8<T>(cst + (size_t)i * 8, xp[u]);
-        else if (i < n_c + n_b) st8<T>(bst + (size_t)(i - n_c) * 8, xp[u]);
-        else if (i < n_all) st8<T>(est + (size_t)(i - n_c - n_b) * 8, xp[u]);
-      }
-    }
-  }
   __syncthreads();
-  // every evicted ring row of this head is in LDS now: the ring write can go
-  ring_write();
-  // ---- per summary slot: its tokens in order (list), count (fp32 in token
-  // order; adding 0 for other slots' tokens leaves the sum unchanged) and
-  // flags; tokens read 16 at a time (same address across threads)
-  for (int m = t; m < Ms; m += NT) {
+  // tokens of summary slot m in order (into lst when given), their count
+  // k and weight sum (fp32 in token order; adding 0 for other slots'
+  // tokens leaves the sum unchanged); tokens read 16 at a time
+  auto slot_scan = [&](int m, int32_t* lst, int& k) {
     float c = 0.f;
-    int k = 0;
+    k = 0;
     for (int t0 = 0; t0 < Ts; t0 += 16) {
       int iv[16];
-      float wv16[16];
+      float w16[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         const int tt = min(t0 + u, Ts - 1);
         iv[u] = t0 + u < Ts ? idx_s[tt] : -1;
-        wv16[u] = wtok[tt];
+        w16[u] = wtok[tt];
       }
 #pragma unroll
       for (int u = 0; u < 16; ++u) {
         const bool on = iv[u] == m;
-        c += on ? wv16[u] : 0.f;
-        if (on) list[m * Ts + k] = t0 + u;
+        c += on ? w16[u] : 0.f;
+        if (on && lst) lst[k] = t0 + u;
         k += on ? 1 : 0;
       }
     }
-    nlist[m] = k;
-    cnt[m] = E::rnd(c);
-    const bool active = cnt[m] > 0.f;
-    sflag[m] = (active ? 1 : 0) | ((active && used[Me + m] == 0) ? 2 : 0);
+    return E::rnd(c);
+  };
+  if (Ts > 0) {
+    for (int j = t; j < nsl; j += NT) {
+      const int m = s0 + j;
+      int k;
+      const float c = slot_scan(m, list + (size_t)j * Ts, k);
+      nlist[j] = k;
+      cnt[j] = c;
+      const bool active = c > 0.f;
+      sflag[j] = (active ? 1 : 0) | ((active && sn.used[Me + m] == 0) ? 2 : 0);
+    }
   }
-  // ---- exact write-back of head h (memory_banks.py:707-742): one wave per
-  // written slot, candidates from LDS, deltas summed in token order
+  // ---- exact write-back of this workgroup's slots (memory_banks.py:707-742):
+  // one wave per written slot, deltas summed in token order
   if (Te > 0) {
-    for (int m = wv; m < Me; m += NW) {
-      if (!eflag[m]) continue;
+    for (int m = e0 + wv; m < e1; m += NW) {
+      if (!dc.eflag[m]) continue;
       T* kr = kb + (int64_t)(W + m) * DH;
       T* vr = vb + (int64_t)(W + m) * DH;
       float mk[NV], mv[NV], ak[NV], av[NV];
@@ -1067,11 +980,13 @@ __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_b
       }
       for (int tt = 0; tt < Te; ++tt) {
         if (idx_e[tt] != m || !(fl_e[tt] & 1)) continue;
+        const T* ck = cand_row<T, DH>(s, g, kbk, b, h, pc[tt], false);
+        const T* cv = cand_row<T, DH>(s, g, vbk, b, h, pc[tt], true);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
           const int d = min(lane + 64 * i, DH - 1);
-          ak[i] += E::rnd(E::ld(est[(size_t)tt * 2 * DH + d]) - mk[i]);
-          av[i] += E::rnd(E::ld(est[(size_t)tt * 2 * DH + DH + d]) - mv[i]);
+          ak[i] += E::rnd(E::ld(ck[d]) - mk[i]);
+          av[i] += E::rnd(E::ld(cv[d]) - mv[i]);
         }
       }
       float nv[NV];
@@ -1099,11 +1014,11 @@ __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_b
     // active slots, compacted in slot order by wave 0 (ballot prefix counts)
     if (wv == 0) {
       int na = 0;
-      for (int m0 = 0; m0 < Ms; m0 += 64) {
-        const int m = m0 + lane;
-        const bool on = m < Ms && (sflag[m] & 1);
+      for (int j0 = 0; j0 < nsl; j0 += 64) {
+        const int j = j0 + lane;
+        const bool on = j < nsl && (sflag[j] & 1);
         const uint64_t bal = __ballot(on);
-        if (on) act_list[na + __popcll(bal & ((1ull << lane) - 1ull))] = m;
+        if (on) act_list[na + __popcll(bal & ((1ull << lane) - 1ull))] = j;
         na += __popcll(bal);
       }
       if (lane == 0) misc[0] = na;
@@ -1121,36 +1036,35 @@ __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_b
       const bool is_v = col < DH;
       const int d = is_v ? col : lf + (col - DH);
       T* rbase = (is_v ? vb : kb) + (int64_t)(W + Me) * DH + d;
+      // token tt's value at this channel: V (channel col) or K (channel lf + col - DH)
+      auto tok = [&](int tt) { return E::ld(cand_row<T, DH>(s, g, is_v ? vbk : kbk, b, h, pc[tt], is_v)[d]); };
       for (int a0 = q; a0 < n_act; a0 += NG * SB) {
-        int mm[SB], nk[SB], fl[SB], t0[SB];
+        int jj[SB], nk[SB], fl[SB], t0[SB];
         float cn[SB];
 #pragma unroll
-        for (int j = 0; j < SB; ++j) {
-          const int ai = min(a0 + NG * j, n_act - 1);
-          mm[j] = act_list[ai];
-        }
+        for (int j = 0; j < SB; ++j) jj[j] = act_list[min(a0 + NG * j, n_act - 1)];
 #pragma unroll
         for (int j = 0; j < SB; ++j) {
-          nk[j] = nlist[mm[j]];
-          fl[j] = sflag[mm[j]];
-          cn[j] = cnt[mm[j]];
-          t0[j] = list[mm[j] * Ts];
+          nk[j] = nlist[jj[j]];
+          fl[j] = sflag[jj[j]];
+          cn[j] = cnt[jj[j]];
+          t0[j] = list[(size_t)jj[j] * Ts];
         }
         float x0[SB], w0[SB], mem[SB];
 #pragma unroll
         for (int j = 0; j < SB; ++j) {
-          x0[j] = E::ld(cst[(size_t)t0[j] * NCOL + col]);
+          x0[j] = tok(t0[j]);
           w0[j] = wtok[t0[j]];
-          mem[j] = E::ld(bst[(size_t)mm[j] * NCOL + col]);
+          mem[j] = E::ld(rbase[(int64_t)(s0 + jj[j]) * DH]);
         }
 #pragma unroll
         for (int j = 0; j < SB; ++j) {
           if (a0 + NG * j >= n_act) break;
-          const int m = mm[j];
+          const int jl = jj[j], m = s0 + jl;
           float a = E::rnd(x0[j] * w0[j]);
           for (int k = 1; k < nk[j]; ++k) {
-            const int tt = list[m * Ts + k];
-            a += E::rnd(E::ld(cst[(size_t)tt * NCOL + col]) * wtok[tt]);
+            const int tt = list[(size_t)jl * Ts + k];
+            a += E::rnd(tok(tt) * wtok[tt]);
           }
           const float eta = (s.overwrite_on_insert && (fl[j] & 2)) ? 1.f : eta_h;
           const float avg = E::rnd(E::rnd(a) / fmaxf(cn[j], eps_r<T>()));
@@ -1160,21 +1074,21 @@ __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_b
             const float dk = E::rnd(E::rnd(avg * s.energy_scale) - mem[j]);
             const float nkv = E::rnd(mem[j] + E::rnd(eta * dk));
             rbase[(int64_t)m * DH] = E::st(nkv);
-            knew[m * LF + (col - DH)] = nkv;  // new LF key for the norm cache
+            knew[jl * LF + (col - DH)] = nkv;  // new LF key for the norm cache
           }
         }
       }
     }
     __syncthreads();
     for (int ai = wv; ai < n_act; ai += NW) {
-      const int m = act_list[ai];
+      const int jl = act_list[ai], m = s0 + jl;
       float x[NV];
       bool act[NV];
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int dd = lane + 64 * i;
         act[i] = dd < LF;
-        x[i] = act[i] ? knew[m * LF + dd] : 0.f;
+        x[i] = act[i] ? knew[jl * LF + dd] : 0.f;
       }
       wave_unit<T, NV>(x, act);
       T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + m) * LF;
@@ -1183,41 +1097,97 @@ __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_b
         if (act[i]) nr[lane + 64 * i] = E::st(x[i]);
     }
   }
-  // ---- per-sequence metadata (lead workgroup)
-  if (lead) {
+  // ---- per-sequence metadata (one workgroup per sequence)
+  if (h == 0 && z == 0) {
     for (int m = t; m < Me; m += NT)
-      if (eflag[m]) al[W + m] = 1;
-    for (int m = t; m < Ms; m += NT)
-      if (Ts > 0 && (sflag[m] & 1)) al[W + Me + m] = 1;
-    if (Ts > 0 && wv == 0) {
-      int64_t upd = 0, ins = 0;
-      int all_used = 1, any_cnt = 0;
-      for (int m = lane; m < Ms; m += 64) {
-        const int f = sflag[m];
-        upd += f & 1;
-        ins += (f >> 1) & 1;
-        if (m < s.active_summary) {
-          if (!(used[Me + m] != 0 || (f & 1))) all_used = 0;
-          if (f & 1) any_cnt = 1;
-        }
+      if (Te > 0 && dc.eflag[m]) al[W + m] = 1;
+    if (Ts > 0) {
+      for (int m = t; m < Ms; m += NT) {
+        int k;
+        const bool active = slot_scan(m, nullptr, k) > 0.f;
+        fl_all[m] = (active ? 1 : 0) | ((active && sn.used[Me + m] == 0) ? 2 : 0);
+        if (active) al[W + Me + m] = 1;
       }
-      for (int o = 32; o > 0; o >>= 1) {
-        upd += __shfl_xor(upd, o, 64);
-        ins += __shfl_xor(ins, o, 64);
-      }
-      all_used = wave_and(all_used);
-      any_cnt = wave_or(any_cnt);
-      if (lane == 0) {
-        if (s.metrics) {
-          atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, upd);
-          if (s.overwrite_on_insert) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, ins);
+      __syncthreads();
+      if (wv == 0) {
+        int64_t upd = 0, ins = 0;
+        int all_used = 1, any_cnt = 0;
+        for (int m = lane; m < Ms; m += 64) {
+          const int f = fl_all[m];
+          upd += f & 1;
+          ins += (f >> 1) & 1;
+          if (m < s.active_summary) {
+            if (!(sn.used[Me + m] != 0 || (f & 1))) all_used = 0;
+            if (f & 1) any_cnt = 1;
+          }
         }
-        if (s.frustrated) {
-          if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
-          if (any_cnt) atomic_add_i64(s.frustrated + 2, 1);
+        for (int o = 32; o > 0; o >>= 1) {
+          upd += __shfl_xor(upd, o, 64);
+          ins += __shfl_xor(ins, o, 64);
+        }
+        all_used = wave_and(all_used);
+        any_cnt = wave_or(any_cnt);
+        if (lane == 0) {
+          if (s.metrics) {
+            atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, upd);
+            if (s.overwrite_on_insert) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, ins);
+          }
+          if (s.frustrated) {
+            if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
+            if (any_cnt) atomic_add_i64(s.frustrated + 2, 1);
+          }
         }
       }
     }
+  }
+}
+
+// Ring write of the chunk's surviving block tokens (memory_banks.py:135-177)
+// for head h of sequence b, after the bank writes have read the evicted
+// ring rows; the lead head also writes the ring gates and visibility bytes.
+// Workgroup z takes the 16-byte pieces [z per, (z + 1) per) of the copy.
+template <typename T, int DH>
+__global__ __launch_bounds__(kApplyThreads) void block_ring_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
+                                                                   const T* vbk, const float* gb) {
+  constexpr int CH = DH / 8;
+  const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, NT = blockDim.x;
+  const int W = s.W, Lbuf = W + s.Me + s.Ms;
+  const bool lead = h == 0;
+  T* kb = (T*)s.k_buf + ((int64_t)b * s.Hkv + h) * Lbuf * DH;
+  T* vb = (T*)s.v_buf + ((int64_t)b * s.Hkv + h) * Lbuf * DH;
+  uint8_t* al = s.allowed + (int64_t)b * Lbuf;
+  auto blk_row = [&](const T* base, int jb) { return base + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl; };
+  const int Lr = g.ring_filled;
+  const int first = max(Lr, g.n_ev);
+  const int total = Lr + g.blk;
+  const int rhead = (Lr == W) ? g.ring_head : 0;
+  const int n_all = (total - first) * CH;  // pieces of 8 elements per plane (K and V each)
+  const int per = (n_all + (int)gridDim.z - 1) / (int)gridDim.z;
+  const int p0 = min(n_all, (int)blockIdx.z * per), n_ring = min(n_all, p0 + per);
+  auto ring_store = [&](int i, Piece8<T> xk, Piece8<T> xv) {
+    const int r = first + i / CH, c = i % CH;
+    const int slot = (rhead + r) % W;
+    st8<T>(kb + (int64_t)slot * DH + 8 * c, xk);
+    st8<T>(vb + (int64_t)slot * DH + 8 * c, xv);
+    if (lead && c == 0) {
+      s.g_recent[(int64_t)b * W + slot] = gb[(int64_t)b * g.g_sb + (r - Lr)];
+      al[slot] = 1;
+    }
+  };
+  for (int base = p0 + t; base < n_ring; base += kRingPre * NT) {
+    Piece8<T> rk[kRingPre], rv[kRingPre];
+#pragma unroll
+    for (int u = 0; u < kRingPre; ++u) {
+      const int i = base + u * NT;
+      if (i < n_ring) {
+        const int jb = first + i / CH - Lr, c = i % CH;
+        rk[u] = ld8<T>(blk_row(kbk, jb) + 8 * c);
+        rv[u] = ld8<T>(blk_row(vbk, jb) + 8 * c);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRingPre; ++u)
+      if (base + u * NT < n_ring) ring_store(base + u * NT, rk[u], rv[u]);
   }
 }
 
@@ -1480,12 +1450,30 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
     rc = check_launch("block_decide");
     if (rc) return rc;
   }
-  const size_t lds_a = apply_lds_bytes(s->Me, s->Ms, g.Te, g.Ts, DH, LF, (int)sizeof(T));
-  int rc = ensure_lds(block_apply_kernel<T, DH>, lds_a, "coda_block_write");
-  if (rc) return rc;
-  hipLaunchKernelGGL((block_apply_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(kApplyThreads), lds_a, st, *s, g,
-                     (const T*)kb, (const T*)vb, gb, plan_c, ws);
-  return check_launch("block_apply");
+  if (g.n_ev > 0 && TT > 0) {
+    // bank slots split over nz workgroups per (sequence, head): about 256
+    // workgroups in all
+    const int pairs = s->B * s->Hkv;
+    int nz = (256 + pairs - 1) / pairs;
+    nz = std::max(1, std::min(nz, std::max(s->Me, s->Ms)));
+    const int PS = (s->Ms + nz - 1) / nz;
+    const size_t lds_a = apply_lds_bytes(s->Ms, g.Te, g.Ts, PS, LF);
+    int rc = ensure_lds(block_apply_kernel<T, DH>, lds_a, "coda_block_write");
+    if (rc) return rc;
+    hipLaunchKernelGGL((block_apply_kernel<T, DH>), dim3(s->Hkv, s->B, nz), dim3(kApplyThreads), lds_a, st, *s, g,
+                       (const T*)kb, (const T*)vb, plan_c, ws);
+    rc = check_launch("block_apply");
+    if (rc) return rc;
+  }
+  {
+    // at most two 16-byte pieces per thread and plane in each workgroup
+    const int first = std::max(g.ring_filled, g.n_ev);
+    const int n_all = (g.ring_filled + g.blk - first) * (DH / 8);
+    const int nzr = std::max(1, (n_all + 2 * kApplyThreads - 1) / (2 * kApplyThreads));
+    hipLaunchKernelGGL((block_ring_kernel<T, DH>), dim3(s->Hkv, s->B, nzr), dim3(kApplyThreads), 0, st, *s, g,
+                       (const T*)kb, (const T*)vb, gb);
+  }
+  return check_launch("block_ring");
 }
 
 extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb, int64_t b_sh,
