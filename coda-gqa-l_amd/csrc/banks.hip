@@ -726,57 +726,65 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
       sc[i] = v;
     }
     __syncthreads();
-    for (int tt = wv; tt < Te; tt += blockDim.x >> 6) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int m = lane; m < Me; m += 64) {
-        const float v = sc[tt * Me + m];
-        if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
-      }
-      wave_argmax(bv, bi);
-      if (lane == 0) { best[tt & 63] = bv; best_i[tt & 63] = bi; }
-    }
-    __syncthreads();
     __shared__ int any_used_s;
-    if (t == 0) any_used_s = 0;
-    __syncthreads();
     if (wv == 0) {
       int u = 0;
       for (int m = lane; m < Me; m += 64) u |= used[m] != 0;
       u = wave_or(u);
       if (lane == 0) any_used_s = u;
     }
-    __syncthreads();
-    if (t == 0) {
-      const int Ae = s.active_exact;
-      const int any_used = any_used_s;
-      const int n_lru = min(Te, Ae);
-      int rank = -1;
-      int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
-      for (int tt = 0; tt < Te; ++tt) {
-        const bool keep = s.gated ? (sn.gate[tt] >= s.tau_exact) : true;
-        const float bv = best[tt & 63];
-        const bool novel = !any_used || bv < E::rnd(s.tau_novel);
-        const bool hit = any_used && bv >= E::rnd(s.tau_match);
-        const bool nk = novel && keep;
-        if (nk) ++rank;  // cumsum(novel & keep) - 1 at tt
-        const bool cap = nk && rank < Ae;
-        int idx = best_i[tt & 63];
-        if (cap) {
-          int r = rank < 0 ? 0 : rank;
-          if (r > n_lru - 1) r = n_lru - 1;
-          idx = sn.lru[r];
+    // candidates 64 at a time: the best slot of each (one wave per
+    // candidate), then thread 0 walks them in token order, its rank and
+    // counters carried from chunk to chunk
+    const int Ae = s.active_exact;
+    const int n_lru = min(Te, Ae);
+    int rank = -1;
+    int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
+    for (int c0 = 0; c0 < Te; c0 += 64) {
+      const int cn = min(64, Te - c0);
+      for (int k = wv; k < cn; k += blockDim.x >> 6) {
+        const int tt = c0 + k;
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int m = lane; m < Me; m += 64) {
+          const float v = sc[tt * Me + m];
+          if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
         }
-        const bool touch = keep && (!novel || cap);
-        const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
-        idx_l[tt] = idx;
-        fl_l[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
-        cnt_ow += ow;
-        cnt_cap += cap;
-        cnt_hit += (hit && keep);
-        cnt_gated += !keep;
-        cnt_fr += (nk && !cap);
+        wave_argmax(bv, bi);
+        if (lane == 0) { best[k] = bv; best_i[k] = bi; }
       }
+      __syncthreads();
+      if (t == 0) {
+        const int any_used = any_used_s;
+        for (int k = 0; k < cn; ++k) {
+          const int tt = c0 + k;
+          const bool keep = s.gated ? (sn.gate[tt] >= s.tau_exact) : true;
+          const float bv = best[k];
+          const bool novel = !any_used || bv < E::rnd(s.tau_novel);
+          const bool hit = any_used && bv >= E::rnd(s.tau_match);
+          const bool nk = novel && keep;
+          if (nk) ++rank;  // cumsum(novel & keep) - 1 at tt
+          const bool cap = nk && rank < Ae;
+          int idx = best_i[k];
+          if (cap) {
+            int r = rank < 0 ? 0 : rank;
+            if (r > n_lru - 1) r = n_lru - 1;
+            idx = sn.lru[r];
+          }
+          const bool touch = keep && (!novel || cap);
+          const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
+          idx_l[tt] = idx;
+          fl_l[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
+          cnt_ow += ow;
+          cnt_cap += cap;
+          cnt_hit += (hit && keep);
+          cnt_gated += !keep;
+          cnt_fr += (nk && !cap);
+        }
+      }
+      __syncthreads();
+    }
+    if (t == 0) {
       if (s.metrics) {
         atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, cnt_ow);
         atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, cnt_fr);

@@ -56,6 +56,15 @@ CASES = {
 }
 
 
+# Cases checked only as HIP path vs oracle on the GPU (no reference
+# fixture): more than 64 exact candidates per block, so the chunk's exact
+# decisions span several 64-candidate passes.
+GPU_CASES = {
+    "tiny_cand_many": _case(TINY, B=2, L=512, block=128, seed=180, exact_candidates_per_block=80,
+                            summary_candidates_per_block=70),
+}
+
+
 def make_inputs(case):
     """(x_prefill (B,L,D), [x_t (B,1,D)] * steps) in the case dtype."""
     dtype = getattr(torch, case["dtype"])

@@ -8,7 +8,7 @@ import os
 import numpy as np
 import torch
 
-from cases import CASES, make_inputs
+from cases import CASES, GPU_CASES, make_inputs
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
@@ -57,7 +57,7 @@ def trace_events(trace):
 
 def build_oracle(name):
     from coda_oracle import OracleLayer
-    case = CASES[name]
+    case = CASES[name] if name in CASES else GPU_CASES[name]
     dtype = getattr(torch, case["dtype"])
     torch.manual_seed(case["seed_model"])
     m = OracleLayer(**case["kw"]).to(dtype=dtype).eval()

@@ -100,7 +100,8 @@ def test_rope_bit_exact(dtype, interleaved):
 # ------------------------------------------------------------------ bounded layer
 CORE_CASES = ["tiny_f32", "tiny_bf16", "tiny_b2_f32", "tiny_b3_bf16", "tiny_policy_none", "tiny_refresh",
               "tiny_no_overwrite", "tiny_zeros", "tiny_nomask", "tiny_me0", "tiny_ms0", "tiny_w1", "tiny_llama",
-              "tiny_mha", "tiny_expand", "tiny_metrics_bf16", "tiny_bigblock", "tiny_cand", "c1_f32", "c1_bf16"]
+              "tiny_mha", "tiny_expand", "tiny_metrics_bf16", "tiny_bigblock", "tiny_cand", "tiny_cand_many",
+              "c1_f32", "c1_bf16"]
 
 
 def _oracle_case(name):
