@@ -1431,10 +1431,10 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
   const int TT = g.Te > g.Ts ? g.Te : g.Ts;
   if (g.n_ev > 0 && TT > 0) {
     // candidate rows split over nz workgroups per (sequence, head): about
-    // 512 workgroups in all, at least 16 rows each
+    // 512 workgroups in all, at least 8 rows each
     const int n = g.Te + g.Ts, pairs = s->B * s->Hkv;
     int nz = (512 + pairs - 1) / pairs;
-    nz = std::max(1, std::min(nz, (n + 15) / 16));
+    nz = std::max(1, std::min(nz, (n + 7) / 8));
     const int per = (n + nz - 1) / nz;
     const size_t ne = (size_t)std::min(per, g.Te), ns = (size_t)std::min(per, g.Ts);
     const size_t lds1 = std::max(sizeof(float) * ((ne > 0 ? (s->Me + ne) * (DH + 4) : 0) +
