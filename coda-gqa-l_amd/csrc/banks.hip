@@ -671,7 +671,7 @@ __device__ __forceinline__ Dec dec_of(const coda_bank_desc& s, const BlockGeom& 
 }
 
 // Summary candidates per decide workgroup.
-static constexpr int kDecideChunk = 16;
+static constexpr int kDecideChunk = 8;
 
 // fp32 copy global -> LDS by the workgroup, 16 independent loads per thread
 // in flight before their stores.
@@ -695,7 +695,7 @@ __device__ __forceinline__ void wg_copy_f32(float* dst, const float* src, int n)
 // Decisions of one chunk (memory_banks.py:640-697 exact, :866-878 summary).
 // Workgroup x == 0: exact decisions of sequence b from the per-head dots
 // and the metadata snapshot (LRU stamps are committed here, the only
-// writer); x >= 1: summary routing of candidates [16 (x-1), 16 x).
+// writer); x >= 1: summary routing of candidates [8 (x-1), 8 x).
 template <typename T>
 __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc s, BlockGeom g,
                                                            const int32_t* __restrict__ plan_c, float* ws) {
