@@ -1,0 +1,120 @@
+"""Parity of the HIP path with the CPU oracle at the benchmark's own shapes.
+
+Head_dim 128 with the per-KV-head geometry of the 7B layer (G = 4, W256 /
+Me64 / Ms64, Lbuf 384) and of the 70B layer (G = 8, W512 / Me128 / Ms128,
+Lbuf 768), blocks of 256 and 128, and batches large enough that the bank
+kernels run one workgroup per (sequence, KV head) (B * Hkv >= 512).
+
+Free-running: the oracle and the HIP path each keep their own state through
+a chunked prefill, a second ragged prefill call and then decode steps (the
+HIP decode carries its routing record from step to step, as in the bench);
+the states are compared after every call and every step.  Inputs are seeded
+on the CPU at the post-projection boundary and copied to the device.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from parity_util import assert_close, compare_states, product_like, to_product_state
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+# name: (H, Hkv, Dh, W, Me, Ms, B, L, block, gates, decode steps, dtype)
+SHAPES = {
+    # configs[1] / configs[2] per-KV-head shape (7B: 32 / 8 heads -> G = 4)
+    "c2_g4_b4_blk256": (8, 2, 128, 256, 64, 64, 4, 1536, 256, "random", 6, torch.bfloat16),
+    "c2_g4_b4_blk128": (8, 2, 128, 256, 64, 64, 4, 1152, 128, "const", 6, torch.bfloat16),
+    "c2_g4_b64_blk256": (8, 2, 128, 256, 64, 64, 64, 1024, 256, "random", 4, torch.bfloat16),
+    "c2_g4_b4_f32": (8, 2, 128, 256, 64, 64, 4, 768, 256, "random", 4, torch.float32),
+    # the 7B layer itself at the decode bench's batch: B * Hkv = 512, so the
+    # routing and write-back kernels run one workgroup per (sequence, head)
+    "c2_full_b64_blk256": (32, 8, 128, 256, 64, 64, 64, 640, 256, "const", 4, torch.bfloat16),
+    # configs[4] per-KV-head shape (70B: 64 / 8 heads -> G = 8), large cache
+    "c5_g8_b4_blk256": (16, 2, 128, 512, 128, 128, 4, 2048, 256, "random", 4, torch.bfloat16),
+    "c5_full_b2_blk256": (64, 8, 128, 512, 128, 128, 2, 1280, 256, "const", 4, torch.bfloat16),
+    # small rows, B * Hkv = 512 (one workgroup per (sequence, head) again)
+    "tiny_b256": (4, 2, 32, 32, 16, 16, 256, 200, 48, "random", 6, torch.bfloat16),
+}
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+
+
+def _gates(kind, B, L, g):
+    if kind == "const":
+        # the layer's own gate at init: sigmoid(write_proj(x)) with zero
+        # weights and bias -2, in bf16 -> one value for every token (all ties)
+        v = torch.sigmoid(torch.tensor(-2.0, dtype=torch.bfloat16)).float()
+        return v.expand(B, L).contiguous()
+    return torch.sigmoid(torch.randn(B, L, generator=g) * 1.5 - 2.0)
+
+
+def _inputs(m, B, L, dtype, kind, g):
+    H, Hkv, Dh = m.num_heads, m.num_kv_heads, m.head_dim
+    q = torch.randn(B, H, L, Dh, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, L, Dh, generator=g).to(dtype)
+    v = torch.randn(B, Hkv, L, Dh, generator=g).to(dtype)
+    lam = torch.sigmoid(torch.randn(B, H, L, 1, generator=g) - 1.0).to(dtype)
+    return q, k, v, _gates(kind, B, L, g), lam
+
+
+def _prefill_both(m, p, st_o, st_p, q, k, v, gate, lam, block, dtype, what):
+    from coda_oracle import prims
+    L = q.shape[2]
+    c, s = m.rope_tables(L, st_o.pos, dtype)
+    q_r = prims.rope(q, c, s, m.rope_interleaved)
+    heads_o = m.prefill_core(q_r, k, v, gate, lam, st_o, block_size=block)
+    heads_p = p.prefill_core(q.to(DEV), k.to(DEV), v.to(DEV), gate.to(DEV), lam.squeeze(-1).to(DEV), c.to(DEV),
+                             s.to(DEV), st_p, block_size=block)
+    torch.cuda.synchronize()
+    assert_close(heads_p.permute(0, 2, 1, 3), heads_o, dtype, f"{what} heads")
+    del heads_o, heads_p
+    compare_states(st_p, st_o, dtype, m.window, m.Me, what)
+
+
+@pytest.mark.parametrize("name", list(SHAPES))
+@torch.no_grad()
+def test_bench_shape_trajectory_matches_oracle(name):
+    _need_gpu()
+    from coda_oracle import OracleLayer, banks
+    H, Hkv, Dh, W, Me, Ms, B, L, block, kind, steps, dtype = SHAPES[name]
+    print(f"[bench shape] {name}: H{H} Hkv{Hkv} Dh{Dh} W{W} Me{Me} Ms{Ms} B{B} L{L} block {block} "
+          f"gates {kind} {dtype}", flush=True)
+    kw = dict(embed_dim=H * Dh, num_heads=H, num_kv_heads=Hkv, window=W, num_landmarks_exact=Me,
+              num_landmarks_summary=Ms, rope_base=1e4)
+    torch.manual_seed(31)
+    m = OracleLayer(**kw).to(dtype).eval()
+    p = product_like(m, {"kw": kw}, dtype, DEV)
+    torch.manual_seed(32)
+    st_o = m.init_state(batch_size=B, dtype=dtype)
+    st_p = to_product_state(st_o, DEV)
+    g = torch.Generator().manual_seed(33)
+    # ---- prefill: the whole sequence in one call, then a ragged second call
+    q, k, v, gate, lam = _inputs(m, B, L, dtype, kind, g)
+    _prefill_both(m, p, st_o, st_p, q, k, v, gate, lam, block, dtype, f"{name} prefill")
+    L2 = block + block // 2 + 3
+    q, k, v, gate, lam = _inputs(m, B, L2, dtype, kind, g)
+    _prefill_both(m, p, st_o, st_p, q, k, v, gate, lam, block, dtype, f"{name} second prefill ({L2} tokens)")
+    del q, k, v, gate, lam
+    # ---- decode, free-running: the HIP side keeps its state (and routing
+    # record) from step to step
+    for t in range(steps):
+        qp = int(st_o.pos)
+        qt = torch.randn(B, H, 1, Dh, generator=g).to(dtype)
+        kn = torch.randn(B, Hkv, 1, Dh, generator=g).to(dtype)
+        vn = torch.randn(B, Hkv, 1, Dh, generator=g).to(dtype)
+        gn = _gates(kind, B, 1, g)
+        lamt = torch.sigmoid(torch.randn(B, H, 1, 1, generator=g) - 1.0).to(dtype)
+        banks.write_one(m, st_o, kn, vn, gn)
+        ho = m.attend_core(qt, lamt, st_o, qp)
+        ct, sn = m.rope_tables(1, qp, dtype)
+        hp = p.decode_step_core(qt.to(DEV), kn.to(DEV), vn.to(DEV), gn.reshape(B).to(DEV), lamt.squeeze(-1).to(DEV),
+                                st_p, ct.to(DEV), sn.to(DEV))
+        torch.cuda.synchronize()
+        assert_close(hp.permute(0, 2, 1, 3), ho, dtype, f"{name} decode step {t} heads")
+        compare_states(st_p, st_o, dtype, W, Me, f"{name} decode step {t}")
