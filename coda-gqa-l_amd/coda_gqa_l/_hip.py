@@ -56,10 +56,10 @@ class BankDesc(ctypes.Structure):
         ("dtype", _i32), ("B", _i32), ("Hkv", _i32), ("Dh", _i32), ("W", _i32), ("Me", _i32), ("Ms", _i32),
         ("lf", _i32), ("active_exact", _i32), ("active_summary", _i32),
         ("k_buf", _vp), ("v_buf", _vp), ("allowed", _vp), ("g_recent", _vp), ("mem_last", _vp),
-        ("exact_v_norm", _vp), ("sum_lf_k_norm", _vp), ("eta_logit", _vp),
+        ("exact_v_norm", _vp), ("sum_lf_k_norm", _vp), ("eta", _vp),
         ("gated", _i32), ("tau_exact", _f32), ("tau_summary", _f32), ("tau_match", _f32), ("tau_novel", _f32),
         ("refresh_on_hit", _i32), ("overwrite_on_insert", _i32), ("energy_scale", _f32),
-        ("metrics", _vp), ("frustrated", _vp),
+        ("metrics", _vp), ("frustrated", _vp), ("trace", _vp),
     ]
 
 

@@ -381,7 +381,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         if write_cache:
             plan, kmax, do_e, do_s = self._plan_candidates(state, g, L, block_size)
             ws = self._block_workspace(state, kmax)
-            eta = self._eta_logit_f32(q.device) if self.Ms > 0 else None
+            eta = self._eta_f32(q.device, state.k_buf.dtype) if self.Ms > 0 else None
         p0 = int(state.pos)
         t = 0
         c = 0

@@ -78,13 +78,22 @@ class MemoryBankMixin:
         cache[(name, key)] = (tag, val)
         return val
 
-    def _eta_logit_f32(self, device) -> torch.Tensor:
+    def _eta_f32(self, device, dtype: torch.dtype) -> torch.Tensor:
+        """sigmoid(summary_eta_logit).to(dtype) per KV head, as float32 on the
+        device (memory_banks.py:394, :902).  The sigmoid is torch's CPU op on
+        the parameter's own dtype, as in the reference's CPU path; it runs
+        once per parameter version (an [Hkv] copy to the host and back)."""
         p = self.summary_eta_logit
-        return self._derived("eta", p, device,
-                             lambda: p.detach().to(device=device, dtype=torch.float32).contiguous())
+
+        def make():
+            eta = torch.sigmoid(p.detach().to("cpu")).to(dtype).to(torch.float32)
+            return eta.to(device).contiguous()
+
+        return self._derived("eta", p, (device, dtype), make)
 
     def _bank_desc(self, st: CoDAGQALandmarkStatePerf2, eta: Optional[torch.Tensor],
-                   metrics: Optional[torch.Tensor], frustrated: Optional[torch.Tensor]) -> _hip.BankDesc:
+                   metrics: Optional[torch.Tensor], frustrated: Optional[torch.Tensor],
+                   trace: Optional[torch.Tensor] = None) -> _hip.BankDesc:
         d = _hip.BankDesc()
         d.dtype = _hip.dtype_code(st.k_buf.dtype)
         d.B = st.k_buf.shape[0]
@@ -96,7 +105,7 @@ class MemoryBankMixin:
             st.mem_last_exact.data_ptr()
         d.exact_v_norm = _hip.ptr(st._exact_v_norm)
         d.sum_lf_k_norm = _hip.ptr(st._sum_lf_k_norm)
-        d.eta_logit = _hip.ptr(eta)
+        d.eta = _hip.ptr(eta)
         d.gated = int(self.write_policy != "none")
         d.tau_exact, d.tau_summary = self.write_gate_threshold_exact, self.write_gate_threshold_summary
         d.tau_match, d.tau_novel = self.exact_match_threshold, self.exact_novelty_threshold
@@ -105,7 +114,40 @@ class MemoryBankMixin:
         d.energy_scale = self.energy_scale
         d.metrics = _hip.ptr(metrics)
         d.frustrated = _hip.ptr(frustrated)
+        d.trace = _hip.ptr(trace)
         return d
+
+    # ------------------------------------------------------------ decision trace
+    # Setting ``layer.decision_trace = []`` makes every bank update append its
+    # slot decisions as device tensors, with the tags and fields of the events
+    # the reference path's decisions are usually inspected by:
+    #   ("exact_one", idx, overwrite, keep), ("summary_one", idx, keep)   decode
+    #   ("select", candidate ids), ("exact_block", idx, overwrite, touch),
+    #   ("summary_block", idx)                                            prefill
+    # (memory_banks.py:290-337, :364-432, :459-510, :690-742, :866-878).
+    # Decode steps then take the general (uncached) launch path.
+    def _tracing(self) -> bool:
+        return self.__dict__.get("decision_trace") is not None
+
+    def _trace_decode(self, tr: Optional[torch.Tensor]) -> None:
+        if tr is None:
+            return
+        out = self.__dict__["decision_trace"]
+        if self.Me > 0:
+            out.append(("exact_one", tr[:, 0].long(), (tr[:, 1] & 1).bool(), (tr[:, 1] & 2).bool()))
+        if self.Ms > 0:
+            out.append(("summary_one", tr[:, 2].long(), (tr[:, 3] & 1).bool()))
+
+    def _trace_block(self, tr: Optional[torch.Tensor], plan_c: torch.Tensor, Te: int, Ts: int) -> None:
+        if tr is None:
+            return
+        out = self.__dict__["decision_trace"]
+        out.append(("select", plan_c[:, :max(Te, Ts)].long()))
+        if Te > 0:
+            out.append(("exact_block", tr[:, :Te].long(), (tr[:, Te:2 * Te] & 1).bool(),
+                        (tr[:, Te:2 * Te] & 2).bool()))
+        if Ts > 0:
+            out.append(("summary_block", tr[:, 2 * Te:2 * Te + Ts].long()))
 
     def _aux_buffers(self, st, device):
         metrics = torch.zeros(_hip.NUM_COUNTERS, dtype=torch.int64, device=device) if st.metrics is not None \
@@ -161,8 +203,9 @@ class MemoryBankMixin:
         g = g_new.reshape(B).to(torch.float32).contiguous()
         evict = st.recent_filled >= self.window
         metrics, fr = self._aux_buffers(st, dev) if evict else (None, None)
-        eta = self._eta_logit_f32(dev) if self.Ms > 0 else None
-        d = self._bank_desc(st, eta, metrics, fr)
+        eta = self._eta_f32(dev, st.k_buf.dtype) if self.Ms > 0 else None
+        tr = torch.full((B, 4), -1, dtype=torch.int32, device=dev) if evict and self._tracing() else None
+        d = self._bank_desc(st, eta, metrics, fr, tr)
         _hip.check(_hip.lib().coda_decode_write(
             d, kn.data_ptr(), vn.data_ptr(), kn.stride(0), kn.stride(1), g.data_ptr(), int(st.recent_idx),
             int(st.recent_filled), int(st.pos), _hip.stream_of(kn)))
@@ -170,6 +213,7 @@ class MemoryBankMixin:
             st.recent_filled += 1
         else:
             j = int(st.recent_idx)
+            self._trace_decode(tr)
             self._fold_metrics(st, metrics, 1, self.Me > 0, self.Ms > 0)
             self._expand_from(st, fr, False, self.Me > 0, self.Ms > 0)
             st.recent_idx = (j + 1) % self.window
@@ -196,8 +240,9 @@ class MemoryBankMixin:
         g = g_new.reshape(B).to(torch.float32).contiguous()
         evict = st.recent_filled >= self.window
         metrics, fr = self._aux_buffers(st, dev) if evict else (None, None)
-        eta = self._eta_logit_f32(dev) if self.Ms > 0 else None
-        d = self._bank_desc(st, eta, metrics, fr)
+        eta = self._eta_f32(dev, st.k_buf.dtype) if self.Ms > 0 else None
+        tr = torch.full((B, 4), -1, dtype=torch.int32, device=dev) if evict and self._tracing() else None
+        d = self._bank_desc(st, eta, metrics, fr, tr)
         L = _hip.lib()
         wkey = (B, attn_desc.H, st.k_buf.shape[2], st.k_buf.dtype)
         sizes = self.__dict__.setdefault("_step_ws_bytes", {})
@@ -217,6 +262,7 @@ class MemoryBankMixin:
             st.recent_filled += 1
         else:
             j = int(st.recent_idx)
+            self._trace_decode(tr)
             self._fold_metrics(st, metrics, 1, self.Me > 0, self.Ms > 0)
             self._expand_from(st, fr, False, self.Me > 0, self.Ms > 0)
             st.recent_idx = (j + 1) % self.window
@@ -240,7 +286,7 @@ class MemoryBankMixin:
         token's pointers change, so the host side is a few field updates and
         one library call.  Returns False when the general path must run."""
         if st.metrics is not None or st.recent_filled < self.window or self._expandable() or \
-                (self.Me == 0 and self.Ms == 0):
+                (self.Me == 0 and self.Ms == 0) or self._tracing():
             return False
         plan = self.__dict__.get("_dplan")
         key = self._plan_key(st, q)
@@ -256,7 +302,7 @@ class MemoryBankMixin:
                 theta_sin=sn, k_prefix=st.k_buf, v_prefix=st.v_buf,
                 allowed=st.allowed if self.mask_unused_memory else None, k_block=None, v_block=None, lam=lam,
                 rms_weight=self._rms_weight(dt), eps=self._eps, out=out.permute(0, 2, 1, 3))
-            eta = self._eta_logit_f32(q.device) if self.Ms > 0 else None
+            eta = self._eta_f32(q.device, st.k_buf.dtype) if self.Ms > 0 else None
             d = self._bank_desc(st, eta, None, None)
             nb = ctypes.c_size_t(0)
             _hip.check(_hip.lib().coda_decode_step_workspace_bytes(d, a, nb))
@@ -360,7 +406,10 @@ class MemoryBankMixin:
         Te = min(self.exact_candidates_per_block, n_ev) if do_e else 0
         Ts = min(self.summary_candidates_per_block, n_ev) if do_s else 0
         metrics, fr = self._aux_buffers(st, k_blk.device) if n_ev > 0 else (None, None)
-        d = self._bank_desc(st, eta, metrics, fr)
+        tr = None
+        if n_ev > 0 and (Te > 0 or Ts > 0) and self._tracing():
+            tr = torch.full((B, 2 * Te + Ts), -1, dtype=torch.int32, device=k_blk.device)
+        d = self._bank_desc(st, eta, metrics, fr, tr)
         ws_ptr, ws_bytes = (workspace.data_ptr(), workspace.numel()) if workspace is not None else (None, 0)
         if k_blk.stride() != v_blk.stride():
             v_blk = v_blk.contiguous()
@@ -370,6 +419,7 @@ class MemoryBankMixin:
             g_blk.data_ptr(), g_blk.stride(0), blk, ring_head, ring_filled, int(pos0), _hip.ptr(plan_c), kmax,
             Te, Ts, ws_ptr, ws_bytes, _hip.stream_of(k_blk)))
         if n_ev > 0:
+            self._trace_block(tr, plan_c, Te, Ts)
             self._fold_metrics(st, metrics, n_ev, Te > 0, Ts > 0)
             self._expand_from(st, fr, True, Te > 0, Ts > 0)
         head = ring_head if ring_filled == W else 0

@@ -1274,16 +1274,13 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       al1 = ring_al(p1_kt(u1 + 6));
     }
     // the next step's record: head hk's dots against its norm rows (the
-    // rows this step's update rewrites are redone by wave 3).  Each 16-byte
-    // load covers 8 channels of one norm row (LP lanes per row, 64 / LP rows
-    // per load "slot"); exact slots then summary slots, the wave taking a
-    // third of them.  Loads first: slot j+1's rows (this wave's own unit
-    // rows), the first KD slots, then this wave's first two bank tiles (a
-    // row the update rewrites is replaced from LDS after the barrier)
+    // rows this step's update rewrites are redone by wave 3).  One lane per
+    // norm row, each dot a sequential chain in the CPU matmul order
+    // (lane_dot_cpu_order): exact rows on lanes 0 .. Me-1 of the waves in
+    // order, then summary rows.  Loads first: slot j+1's rows (this wave's
+    // own unit rows), then this wave's first two bank tiles (a row the
+    // update rewrites is replaced from LDS after the barrier)
     {
-      constexpr int KD = 8, LPE = DH / 8, IPE = 64 / LPE, LPS = DH / 16, IPS = 64 / LPS;
-      const int nSe = (Me + IPE - 1) / IPE, nSs = (Ms + IPS - 1) / IPS, nS = nSe + nSs;
-      const int per = (nS + 2) / 3, qa = min(wv * per, nS), qb = min(qa + per, nS);
       const T* en = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + hk) * Me * DH;
       const T* sn = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + hk) * Ms * LF;
       const int64_t plane = ((int64_t)b * Hkv + hk) * Lbuf;
@@ -1295,21 +1292,9 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
         nv_r[i] = vx[min(lane + 64 * i, DH - 1)];
         nk_r[i] = kx[s.lf + min(lane + 64 * i, LF - 1)];
       }
-      auto load_batch = [&](int qs, uint4 (&xr)[KD]) {
-#pragma unroll
-        for (int k = 0; k < KD; ++k) {
-          const int q = min(qs + k, qb - 1);
-          const T* p = q < nSe ? en + min(q * IPE + lane / LPE, Me - 1) * DH + 8 * (lane % LPE)
-                               : sn + min((q - nSe) * IPS + lane / LPS, Ms - 1) * LF + 8 * (lane % LPS);
-          xr[k] = *reinterpret_cast<const uint4*>(p);
-        }
-      };
-      uint4 xr[KD];
-      if (qa < qb) load_batch(qa, xr);
       issue(kt2(0), false, kf0, vv0);
       issue(kt2(1), false, kf1, vv1);
-      // unit rows of slot j+1 through the wave's (idle) V buffer: lane reads
-      // back the 8 channels of its slots
+      // unit rows of slot j+1 through the wave's (idle) V buffer
       float* un = reinterpret_cast<float*>(vt);
       {
         float xv[NVb], xk[NVb];
@@ -1331,39 +1316,11 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       __builtin_amdgcn_wave_barrier();
-      float uv[8], uk[8];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        uv[jj] = un[8 * (lane % LPE) + jj];
-        uk[jj] = un[DH + 8 * (lane % LPS) + jj];
-      }
-      // the fp32 dot of each row in channel order, the group sum in the
-      // order of wave_dots (pairs, quads, half rows, rows), rounded to T
-      auto use_batch = [&](int qs, const uint4 (&xr)[KD]) {
-#pragma unroll
-        for (int k = 0; k < KD; ++k) {
-          const int q = qs + k;
-          const bool ex = q < nSe;
-          float x[8];
-          unpack8(xr[k], x);
-          float acc = 0.f;
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) acc = fmaf(ex ? uv[jj] : uk[jj], x[jj], acc);
-          acc += dpp_f<0xB1>(acc);
-          acc += dpp_f<0x4E>(acc);
-          float t = dpp_f<0x141>(acc);
-          acc = (ex ? LPE >= 8 : LPS >= 8) ? acc + t : acc;
-          t = dpp_f<0x140>(acc);
-          acc = (ex ? LPE >= 16 : LPS >= 16) ? acc + t : acc;
-          const int row = ex ? q * IPE + lane / LPE : (q - nSe) * IPS + lane / LPS;
-          const int sub = ex ? lane % LPE : lane % LPS;
-          if (q < qb && row < (ex ? Me : Ms) && sub == 0) dots_lds[ex ? row : Me + row] = Elt<T>::rnd(acc);
-        }
-      };
-      if (qa < qb) use_batch(qa, xr);
-      for (int qs = qa + KD; qs < qb; qs += KD) {
-        load_batch(qs, xr);
-        use_batch(qs, xr);
+      for (int r = 64 * wv + lane; r < Me + Ms; r += 192) {
+        const bool ex = r < Me;
+        const float acc = ex ? lane_dot_cpu_order<T>(en + (int64_t)r * DH, un, DH)
+                             : lane_dot_cpu_order<T>(sn + (int64_t)(r - Me) * LF, un + DH, LF);
+        dots_lds[r] = Elt<T>::rnd(acc);
       }
     }
   } else {
@@ -1423,16 +1380,13 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): rewritten norm rows in LDS
     __builtin_amdgcn_wave_barrier();
-    // the record dots of the norm rows this update rewrote
-    if (Me > 0 && dd.ow_e) {
-      wave_dots<T, 4>(
-          1, DH, 0, 1, lane, [&](int) { return (const T*)nnorm_e; }, [&](int) { return (const float*)vnrm; },
-          [&](int, float v) { fix_lds[0] = v; });
-    }
-    if (Ms > 0 && dd.keep_s) {
-      wave_dots<T, 4>(
-          1, LF, 0, 1, lane, [&](int) { return (const T*)nnorm_s; },
-          [&](int) { return (const float*)knrm; }, [&](int, float v) { fix_lds[1] = v; });
+    // the record dots of the norm rows this update rewrote: exact row on
+    // lane 0, summary row on lane 1
+    if (lane < 2) {
+      const bool ex = lane == 0;
+      if (ex ? (Me > 0 && dd.ow_e) : (Ms > 0 && dd.keep_s))
+        fix_lds[lane] = Elt<T>::rnd(ex ? lane_dot_cpu_order<T>(nnorm_e, vnrm, DH)
+                                       : lane_dot_cpu_order<T>(nnorm_s, knrm, LF));
     }
   }
   if (wv == 3) {
@@ -2448,9 +2402,8 @@ extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a
   CODA_REQUIRE(ring_idx >= 0 && ring_idx < s->W, "coda_decode_step: ring_idx %d outside [0, %d)", ring_idx, s->W);
   CODA_REQUIRE(s->k_buf && s->v_buf && s->allowed && s->g_recent, "coda_decode_step: state buffers missing");
   CODA_REQUIRE(s->Me == 0 || (s->mem_last && s->exact_v_norm), "coda_decode_step: exact bank buffers missing");
-  CODA_REQUIRE(s->Ms == 0 || (s->sum_lf_k_norm && s->eta_logit), "coda_decode_step: summary bank buffers missing");
-  CODA_REQUIRE(s->lf > 0 && s->lf < s->Dh && (s->Dh - s->lf) % 8 == 0, "coda_decode_step: lf %d unsupported",
-               s->lf);
+  CODA_REQUIRE(s->Ms == 0 || (s->sum_lf_k_norm && s->eta), "coda_decode_step: summary bank buffers missing");
+  CODA_REQUIRE(2 * s->lf == s->Dh, "coda_decode_step: lf %d unsupported (must be Dh/2)", s->lf);
   size_t att = 0;
   rc = coda_attn_workspace_bytes(a, &att);
   if (rc) return rc;

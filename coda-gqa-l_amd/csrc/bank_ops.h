@@ -111,25 +111,60 @@ __device__ __forceinline__ void atomic_add_i64(int64_t* p, int64_t v) {
   if (p && v) atomicAdd(reinterpret_cast<unsigned long long*>(p), (unsigned long long)v);
 }
 
+// Sum of squares of one row held by one wave (lane owns channels lane + 64 i,
+// i < NV; the channels with act set are the contiguous range [LO, LO + len),
+// LO a multiple of 8), summed in the order of torch's CPU last-dim 2-norm on
+// x86 (ATen ReduceOpsKernel.cpp, norm_two_reduce_step into one 8-wide fp32
+// accumulator vector): row channels r < nv = len - len % VW (VW = 8 fp32 /
+// 16 bf16 elements per input vector) go to accumulator r % 8 in increasing
+// order with fused multiply-adds, the eight accumulators are added in
+// order, then each remaining channel adds its rounded square.  Every lane
+// gets the sum.
+template <typename T, int NV, int LO = 0>
+__device__ __forceinline__ float wave_sumsq_cpu_order(const float (&x)[NV], const bool (&act)[NV]) {
+  static_assert(LO % 8 == 0 && LO < 64 * NV, "band offset must be a multiple of 8 inside the row");
+  constexpr int VW = sizeof(T) == 2 ? 16 : 8;
+  int len = 0;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) len += __popcll(__ballot(act[i]));
+  const int nv = len - len % VW;
+  const int j = threadIdx.x & 7;
+  // accumulator j on lanes j, j + 8, ... (lane j's copy is read); row
+  // channel r0 + j lives in register (LO + r0) / 64, lane (LO + r0) % 64 + j
+  float acc = 0.f;
+#pragma unroll
+  for (int r0 = 0; r0 < 64 * NV - LO; r0 += 8) {
+    const float v = __shfl(x[(LO + r0) >> 6], ((LO + r0) & 63) + j, 64);
+    if (r0 + j < nv) acc = fmaf(v, v, acc);
+  }
+  float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
+#pragma unroll
+  for (int q = 1; q < 8; ++q)
+    ss = ss + __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), q));
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int k0 = max(LO + nv, 64 * i), k1 = min(LO + len, 64 * i + 64);
+    for (int k = k0; k < k1; ++k) {
+      const float v = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[i]), k - 64 * i));
+      ss = ss + v * v;
+    }
+  }
+  return ss;
+}
+
 // F.normalize(x, dim=-1, eps=1e-6) of one row held by one wave (lane owns
-// channels lane + 64 i, i < NV): fp32 sum of squares, norm rounded to the
-// element type, clamp_min(eps), rounded division.
-template <typename T, int NV>
+// channels lane + 64 i, i < NV; active channels [LO, LO + len)): fp32 sum of
+// squares in the CPU order above, norm rounded to the element type,
+// clamp_min(eps), rounded division.
+template <typename T, int NV, int LO = 0>
 __device__ __forceinline__ void wave_unit(float (&x)[NV], const bool (&act)[NV]) {
   using E = Elt<T>;
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (act[i]) ss = fmaf(x[i], x[i], ss);
-  ss = wave_sum(ss);
+  const float ss = wave_sumsq_cpu_order<T, NV, LO>(x, act);
   const float den = fmaxf(E::rnd(sqrtf(ss)), eps_r<T>());
 #pragma unroll
   for (int i = 0; i < NV; ++i) x[i] = act[i] ? E::rnd(x[i] / den) : 0.f;
 }
 
-// Dots of rows of a [rows][len] device matrix (element T) against one fp32
-// vector in LDS, cooperatively by a wave: `len/8` lanes per row, 8 channels
-// per lane (one 16-byte load), group reduction by xor shuffles.
 template <typename T>
 __device__ __forceinline__ void load8f(const T* p, float x[8]) {
   if constexpr (sizeof(T) == 2) {
@@ -148,65 +183,50 @@ __device__ __forceinline__ void load8f(const T* p, float x[8]) {
   }
 }
 
-// out[item] = rnd(dot(vec(item), mat_row(item))), items enumerated by the
-// caller through `row_ptr(item)` / `vec_ptr(item)`; len in {16,32,64,128}.
-// Each lane owns 8 channels of one row (len/8 lanes per row); a wave issues
-// the 16-byte loads of U rows per lane before reducing any of them, so U
-// loads are in flight per lane (the dot phase is latency bound otherwise).
-template <typename T, int U = 8, typename RowF, typename VecF, typename OutF>
+// One step of a routing dot in torch's CPU bf16 matmul order (oneDNN on
+// AVX512-BF16 hosts, the x86 VDPBF16PS accumulation): channel pairs (2i,
+// 2i+1) in increasing i, the odd channel's product added first; bf16
+// products are exact in fp32, so each add is one fused multiply-add.
+__device__ __forceinline__ float dot_pair(float acc, float u0, float x0, float u1, float x1) {
+  acc = fmaf(u1, x1, acc);
+  return fmaf(u0, x0, acc);
+}
+__device__ __forceinline__ float dot8_pairs(float acc, const float* u, const float (&x)[8]) {
+  const float4 a = *reinterpret_cast<const float4*>(u);
+  const float4 c = *reinterpret_cast<const float4*>(u + 4);
+  acc = dot_pair(acc, a.x, x[0], a.y, x[1]);
+  acc = dot_pair(acc, a.z, x[2], a.w, x[3]);
+  acc = dot_pair(acc, c.x, x[4], c.y, x[5]);
+  return dot_pair(acc, c.z, x[6], c.w, x[7]);
+}
+
+// dot(u, row) by one lane over len channels (a multiple of 8): row of T in
+// device memory, u fp32 (16-byte aligned, LDS or registers' backing).
+// Loads run PF 16-byte pieces ahead of the chain.  Unrounded.
+template <typename T, int PF = 4>
+__device__ __forceinline__ float lane_dot_cpu_order(const T* row, const float* u, int len) {
+  float acc = 0.f;
+  const int n8 = len >> 3;
+  for (int c0 = 0; c0 < n8; c0 += PF) {
+    float x[PF][8];
+#pragma unroll
+    for (int k = 0; k < PF; ++k) load8f<T>(row + 8 * min(c0 + k, n8 - 1), x[k]);
+#pragma unroll
+    for (int k = 0; k < PF; ++k)
+      if (c0 + k < n8) acc = dot8_pairs(acc, u + 8 * (c0 + k), x[k]);
+  }
+  return acc;
+}
+
+// out[item] = rnd(dot(vec(item), mat_row(item))) for items enumerated by the
+// caller through `row_ptr(item)` / `vec_ptr(item)`; len a multiple of 8.
+// One lane per item (the chain is sequential in the CPU order), items
+// wave * 64 + lane + 64 n_waves k.
+template <typename T, typename RowF, typename VecF, typename OutF>
 __device__ __forceinline__ void wave_dots(int n_items, int len, int wave, int n_waves, int lane, RowF row_ptr,
                                           VecF vec_ptr, OutF out) {
-  const int lpi = len >> 3;          // lanes per item
-  const int ipw = 64 / lpi;          // items per wave per unrolled slot
-  const int grp = lane / lpi, sub = lane % lpi;
-  for (int base = wave * ipw * U; base < n_items; base += n_waves * ipw * U) {
-    // every load unconditional (items past the end re-read the last row,
-    // their result is dropped) and raw, so all of them are in flight before
-    // the first use
-    uint4 xr[U][sizeof(T) / 2];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int item = base + u * ipw + grp;
-      item = item < n_items ? item : n_items - 1;
-      const uint4* p = reinterpret_cast<const uint4*>(row_ptr(item) + 8 * sub);
-#pragma unroll
-      for (int k = 0; k < (int)(sizeof(T) / 2); ++k) xr[u][k] = p[k];
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      int item = base + u * ipw + grp;
-      const bool live = item < n_items;
-      item = live ? item : n_items - 1;
-      float x[8];
-      if constexpr (sizeof(T) == 2) {
-        const uint32_t w[4] = {xr[u][0].x, xr[u][0].y, xr[u][0].z, xr[u][0].w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x[2 * i] = bf2f((bf16_t)(w[i] & 0xffffu));
-          x[2 * i + 1] = bf2f((bf16_t)(w[i] >> 16));
-        }
-      } else {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-          x[4 * k] = __builtin_bit_cast(float, xr[u][k].x);
-          x[4 * k + 1] = __builtin_bit_cast(float, xr[u][k].y);
-          x[4 * k + 2] = __builtin_bit_cast(float, xr[u][k].z);
-          x[4 * k + 3] = __builtin_bit_cast(float, xr[u][k].w);
-        }
-      }
-      const float* v = vec_ptr(item) + 8 * sub;
-      float acc = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc = fmaf(v[j], x[j], acc);
-      // group sum over the lpi lanes of the item (DPP within the 16-lane
-      // row; every lane of the group ends with the same value)
-      if (lpi >= 2) acc += dpp_f<0xB1>(acc);
-      if (lpi >= 4) acc += dpp_f<0x4E>(acc);
-      if (lpi >= 8) acc += dpp_f<0x141>(acc);
-      if (lpi >= 16) acc += dpp_f<0x140>(acc);
-      if (live && sub == 0) out(item, Elt<T>::rnd(acc));
-    }
-  }
+  for (int item = wave * 64 + lane; item < n_items; item += 64 * n_waves)
+    out(item, Elt<T>::rnd(lane_dot_cpu_order<T>(row_ptr(item), vec_ptr(item), len)));
 }
 
 // ------------------------------------------------------------ decode decision
@@ -324,7 +344,7 @@ __device__ __forceinline__ float raw_f<float>(uint32_t u) { return __builtin_bit
 // loaded together, then:
 //   exact  : new = mem + w * (k_e - mem), w = one-hot(idx) * overwrite,
 //            V-norm cache row refreshed
-//   summary: eta = sigmoid(logit_h) (* gate) (1 if new) * keep;
+//   summary: eta = eta_h (* gate) (1 if new) * keep;
 //            K_LF += eta * (k_e_LF * energy - K_LF), V += eta * (v_e - V),
 //            LF-K-norm cache row refreshed
 //   ring   : slot j <- new token
@@ -351,10 +371,10 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
   T* krs = kb + (int64_t)(W + Me + idx_s) * DH;
   T* vrs = vb + (int64_t)(W + Me + idx_s) * DH;
   float mke[NV], mve[NV], mks[NV], mvs[NV], kn[NV], vn[NV];
-  // every load in one batch (eta's logit included), unconditional from
+  // every load in one batch (eta included), unconditional from
   // valid rows (the new token's where a bank row is not rewritten) and raw:
   // a conditional load, or a conversion next to the load, waits for it
-  const float eta_l = Ms > 0 ? s.eta_logit[h] : 0.f;
+  const float eta_h = Ms > 0 ? s.eta[h] : 0.f;
   const T* lke = do_e ? kre : kn_src;
   const T* lve = do_e ? vre : vn_src;
   const T* lks = do_s ? krs : kn_src;
@@ -408,7 +428,7 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
       }
   }
   if (do_s) {
-    float eta = E::rnd(1.f / (1.f + expf(-eta_l)));
+    float eta = eta_h;
     if (s.gated) eta = E::rnd(eta * E::rnd(g_e));
     if (s.overwrite_on_insert && dec.new_s) eta = 1.f;
     float nk[NV];
@@ -434,7 +454,7 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
         }
       }
     }
-    wave_unit<T, NV>(nk, act);
+    wave_unit<T, NV, DH / 2>(nk, act);  // the LF band: channels [lf, DH), lf = DH / 2
     T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + idx_s) * LF;
 #pragma unroll
     for (int i = 0; i < NV; ++i)
@@ -454,7 +474,8 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
 }
 
 // Per-sequence metadata after a decode update (one thread): used bits of
-// the written slots, the LRU stamp, the ring gate.
+// the written slots, the LRU stamp, the ring gate, and the decision record
+// when the caller asked for one.
 __device__ __forceinline__ void commit_decode_meta(const coda_bank_desc& s, int b, const DecodeDecision& dec, int j,
                                                    int64_t pos_e, float g_new) {
   const int W = s.W, Me = s.Me, Ms = s.Ms;
@@ -465,6 +486,13 @@ __device__ __forceinline__ void commit_decode_meta(const coda_bank_desc& s, int 
   }
   if (Ms > 0 && dec.keep_s) al[W + Me + dec.idx_s] = 1;
   s.g_recent[(int64_t)b * W + j] = g_new;
+  if (s.trace) {
+    int32_t* tr = s.trace + 4 * (int64_t)b;
+    tr[0] = Me > 0 ? dec.idx_e : -1;
+    tr[1] = Me > 0 ? ((dec.ow_e ? 1 : 0) | (dec.keep_e ? 2 : 0)) : 0;
+    tr[2] = Ms > 0 ? dec.idx_s : -1;
+    tr[3] = Ms > 0 ? ((dec.keep_s ? 1 : 0) | (dec.new_s ? 2 : 0)) : 0;
+  }
 }
 
 // Routing record of one decode step, per sequence (4-byte words):
@@ -559,13 +587,13 @@ __device__ __forceinline__ void route_head_dots(const coda_bank_desc& s, int b, 
   __syncthreads();
   if (wv < 2 && Me > 0) {
     const T* en = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + h) * Me * DH;
-    wave_dots<T, 16>(
+    wave_dots<T>(
         Me, DH, wv, 2, lane, [&](int it) { return en + (int64_t)it * DH; }, [&](int) { return (const float*)vnrm; },
         [&](int it, float v) { out_e[it] = v; });
   }
   if (wv >= 2 && Ms > 0) {
     const T* sn = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + h) * Ms * LF;
-    wave_dots<T, 16>(
+    wave_dots<T>(
         Ms, LF, wv - 2, 2, lane, [&](int it) { return sn + (int64_t)it * LF; },
         [&](int) { return (const float*)knrm; }, [&](int it, float v) { out_s[it] = v; });
   }

@@ -104,13 +104,13 @@ __global__ __launch_bounds__(512) void decode_write_kernel(const coda_bank_desc 
   // per-head cosine dots against the norm caches
   if (Me > 0) {
     const T* en = (const T*)s.exact_v_norm + (int64_t)b * Hkv * Me * DH;
-    wave_dots<T, 16>(
+    wave_dots<T>(
         Hkv * Me, DH, wv, NWV, lane, [&](int it) { return en + (int64_t)it * DH; },
         [&](int it) { return (const float*)(vnrm + (it / Me) * DH); }, [&](int it, float v) { de[it] = v; });
   }
   if (Ms > 0) {
     const T* sn = (const T*)s.sum_lf_k_norm + (int64_t)b * Hkv * Ms * LF;
-    wave_dots<T, 16>(
+    wave_dots<T>(
         Hkv * Ms, LF, wv, NWV, lane, [&](int it) { return sn + (int64_t)it * LF; },
         [&](int it) { return (const float*)(knrm + (it / Ms) * LF); }, [&](int it, float v) { dsum[it] = v; });
   }
@@ -259,13 +259,14 @@ __global__ __launch_bounds__(256) void decode_bank_kernel(const coda_bank_desc s
   // ---- 4. next record: head hk's dots against the updated norm rows
   float* out_e = rec_out + (int64_t)b * words + (int64_t)hk * Me;
   float* out_s = rec_out + (int64_t)b * words + (int64_t)Hkv * Me + (int64_t)hk * Ms;
-  if (Me > 0)
-    wave_dots<T, 4>(
-        Me, DH, wv, 4, lane, [&](int it) { return (const T*)stage + it * DH; }, [&](int) { return (const float*)vnrm; },
+  // (one lane per dot: exact rows on waves 0-1, summary rows on waves 2-3)
+  if (Me > 0 && wv < 2)
+    wave_dots<T>(
+        Me, DH, wv, 2, lane, [&](int it) { return (const T*)stage + it * DH; }, [&](int) { return (const float*)vnrm; },
         [&](int it, float v) { out_e[it] = v; });
-  if (Ms > 0)
-    wave_dots<T, 4>(
-        Ms, LF, wv, 4, lane, [&](int it) { return (const T*)stage + Me * DH + it * LF; },
+  if (Ms > 0 && wv >= 2)
+    wave_dots<T>(
+        Ms, LF, wv - 2, 2, lane, [&](int it) { return (const T*)stage + Me * DH + it * LF; },
         [&](int) { return (const float*)knrm; }, [&](int it, float v) { out_s[it] = v; });
 }
 
@@ -408,8 +409,10 @@ __device__ __forceinline__ float cand_gate(const coda_bank_desc& s, const BlockG
   return gb[(int64_t)b * g.g_sb + (e - g.ring_filled)];
 }
 
-// Rows x cands dots from LDS, 4 x 4 register blocks, fp32 FMA in channel
-// order; result rounded to the element type (the matmul output dtype).
+// Rows x cands dots from LDS, 4 x 4 register blocks, each a chain of fused
+// multiply-adds in the CPU matmul order (dot_pair: channel pairs in
+// increasing order, odd channel first); result rounded to the element type
+// (the matmul output dtype).
 template <typename T, int RB, int CB>
 __device__ __forceinline__ void lds_dots_blk(const float* rows, int n_rows, const float* cands, int n_c, int len,
                                              int stride, float* out /* [n_c][n_rows] */) {
@@ -432,10 +435,8 @@ __device__ __forceinline__ void lds_dots_blk(const float* rows, int n_rows, cons
       for (int i = 0; i < RB; ++i)
 #pragma unroll
         for (int j = 0; j < CB; ++j) {
-          acc[i][j] = fmaf(cv[j].x, rv[i].x, acc[i][j]);
-          acc[i][j] = fmaf(cv[j].y, rv[i].y, acc[i][j]);
-          acc[i][j] = fmaf(cv[j].z, rv[i].z, acc[i][j]);
-          acc[i][j] = fmaf(cv[j].w, rv[i].w, acc[i][j]);
+          acc[i][j] = dot_pair(acc[i][j], cv[j].x, rv[i].x, cv[j].y, rv[i].y);
+          acc[i][j] = dot_pair(acc[i][j], cv[j].z, rv[i].z, cv[j].w, rv[i].w);
         }
     }
 #pragma unroll
@@ -446,7 +447,7 @@ __device__ __forceinline__ void lds_dots_blk(const float* rows, int n_rows, cons
   }
 }
 // out[c][r] = rnd(dot(cands[c], rows[r])), each an fma chain over the
-// channels in order (the same value whatever the blocking); blocks of
+// channel pairs in order (the same value whatever the blocking); blocks of
 // 4 x 4 dots per thread when there are enough of them, else 2 x 1
 template <typename T>
 __device__ __forceinline__ void lds_dots(const float* rows, int n_rows, const float* cands, int n_c, int len,
@@ -795,9 +796,14 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
       if (s.frustrated) atomic_add_i64(s.frustrated + 0, cnt_fr);
     }
     __syncthreads();
+    int32_t* tr = s.trace ? s.trace + (int64_t)b * (2 * Te + Ts) : nullptr;
     for (int tt = t; tt < Te; tt += blockDim.x) {
       dc.idx_e[tt] = idx_l[tt];
       dc.fl_e[tt] = fl_l[tt];
+      if (tr) {
+        tr[tt] = idx_l[tt];
+        tr[Te + tt] = fl_l[tt];
+      }
     }
     const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
     for (int m = t; m < Me; m += blockDim.x) {
@@ -854,6 +860,7 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
     wave_argmax(bv, bi);
     if (lane == 0) {
       dc.idx_s[t0 + tt] = bi;
+      if (s.trace) s.trace[(int64_t)b * (2 * Te + Ts) + 2 * Te + t0 + tt] = bi;
       const float gate = sn.gate[t0 + tt];
       dc.wtok[t0 + tt] = (!s.gated || gate >= s.tau_summary) ? E::rnd(gate) : 0.f;
     }
@@ -1037,7 +1044,7 @@ __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_b
     // values of their first token read before any arithmetic; further
     // tokens of a slot (rare) follow in token order (fp32 sum)
     const int n_act = misc[0];
-    const float eta_h = E::rnd(1.f / (1.f + expf(-s.eta_logit[h])));
+    const float eta_h = s.eta[h];
     constexpr int NG = kApplyThreads / NCOL, SB = 8;
     const int q = t / NCOL, col = t % NCOL;
     if (q < NG) {
@@ -1274,7 +1281,7 @@ static int validate_bank(const coda_bank_desc* s, const char* who) {
   if (rc) return rc;
   CODA_REQUIRE(s->k_buf && s->v_buf && s->allowed && s->g_recent, "%s: state buffers missing", who);
   CODA_REQUIRE(s->Me == 0 || (s->mem_last && s->exact_v_norm), "%s: exact bank buffers missing", who);
-  CODA_REQUIRE(s->Ms == 0 || (s->sum_lf_k_norm && s->eta_logit), "%s: summary bank buffers missing", who);
+  CODA_REQUIRE(s->Ms == 0 || (s->sum_lf_k_norm && s->eta), "%s: summary bank buffers missing", who);
   return CODA_OK;
 }
 

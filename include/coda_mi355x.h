@@ -157,8 +157,17 @@ int coda_rope_fwd(int dtype, void* out, int64_t o_sb, int64_t o_sh, int64_t o_sl
  *   mem_last      (B, Me) int64
  *   exact_v_norm  (B, Hkv, Me, Dh) dtype       (NULL iff Me == 0)
  *   sum_lf_k_norm (B, Hkv, Ms, Dh - lf) dtype  (NULL iff Ms == 0)
- *   eta_logit     (Hkv,) float (sigmoid taken on device, cast to dtype)
+ *   eta           (Hkv,) float: sigmoid(summary_eta_logit) rounded to dtype,
+ *                 taken by the caller (the reference's torch op, on the host)
  * metrics: optional (CODA_NUM_COUNTERS,) int64 device counters, or NULL.
+ * trace: optional int32 device buffer, or NULL; when set, the entry point
+ *   records its slot decisions per sequence b:
+ *     coda_decode_write / coda_decode_step (evicting steps only), 4 words at
+ *       trace + 4 b: exact idx, exact flags (1 overwrite | 2 keep),
+ *       summary idx, summary flags (1 keep | 2 new slot); -1 for an empty bank;
+ *     coda_block_write (chunks that evict), 2 Te + Ts words at
+ *       trace + (2 Te + Ts) b: exact idx [Te], exact flags [Te]
+ *       (1 overwrite | 2 touch), summary idx [Ts].
  * ---------------------------------------------------------------------- */
 enum {
   CODA_CNT_EXACT_HITS = 0, CODA_CNT_EXACT_INSERTS, CODA_CNT_EXACT_OVERWRITES,
@@ -177,7 +186,7 @@ typedef struct {
   int64_t* mem_last;
   void* exact_v_norm;
   void* sum_lf_k_norm;
-  const float* eta_logit;
+  const float* eta;
   int gated;                          /* write_policy == "gated" */
   float tau_exact, tau_summary;       /* gate thresholds (fp32 compare) */
   float tau_match, tau_novel;         /* exact-bank cosine thresholds */
@@ -185,6 +194,7 @@ typedef struct {
   float energy_scale;                 /* sqrt(Dh / (Dh - lf)) */
   int64_t* metrics;
   int64_t* frustrated;                /* (2,) device int64 or NULL: exact, summary */
+  int32_t* trace;                     /* decision record or NULL (above) */
 } coda_bank_desc;
 
 /* One decode token per sequence: ring FIFO write; when the ring is full the

@@ -6,7 +6,9 @@ GPU-only and differ in semantics, so they are not restated.
 
 All functions take the layer ``m`` (an OracleLayer: thresholds, sizes,
 parameters) and the mutable state ``st`` and mutate ``st`` in place exactly
-like the reference mixin does.
+like the reference mixin does.  With a ``trace`` list they append their slot
+decisions (the fields the golden vectors hold), followed by the masked
+routing scores the decision was taken from (for margins in the tests).
 """
 
 from __future__ import annotations
@@ -151,7 +153,7 @@ def exact_one(m, st, k_e, v_e, pos_e, gate, trace=None):
     st.mem_last_exact = last
 
     if trace is not None:
-        trace.append(("exact_one", idx.clone(), ow.clone(), keep.clone()))
+        trace.append(("exact_one", idx.clone(), ow.clone(), keep.clone(), sc.clone()))
 
     frustrated = int((novel & keep & ~free_exists).any().item())
     if frustrated > 0 and not m.training:
@@ -198,7 +200,7 @@ def summary_one(m, st, k_e, v_e, pos_e, gate, trace=None):
     st._sum_lf_k_norm = unit(new_k[..., lf:])
 
     if trace is not None:
-        trace.append(("summary_one", idx.clone(), keep.clone()))
+        trace.append(("summary_one", idx.clone(), keep.clone(), sc.clone()))
 
     frustrated = int((new_used[:, :As].all() & keep.any()).item())
     if frustrated > 0 and not m.training:
@@ -339,7 +341,7 @@ def exact_block(m, st, k_sel, v_sel, pos_sel, gate_sel, v_sel_norm=None, trace=N
     st._exact_v_norm[:, :, changed, :] = unit(new_v[:, :, changed, :])
 
     if trace is not None:
-        trace.append(("exact_block", idx.clone(), ow.clone(), touch.clone()))
+        trace.append(("exact_block", idx.clone(), ow.clone(), touch.clone(), sc.clone()))
 
     frustrated = int((nk & ~cap).sum().item())
     if frustrated > 0 and not m.training:
@@ -400,7 +402,7 @@ def summary_block(m, st, k_sel, v_sel, pos_sel, w_tok, lf_k_sel_norm=None, trace
         st._sum_lf_k_norm[:, :, touched, :] = unit(new_k[:, :, touched, lf:])
 
     if trace is not None:
-        trace.append(("summary_block", idx.clone()))
+        trace.append(("summary_block", idx.clone(), sc.clone()))
 
     frustrated = int(new_used[:, :As].all().item() and (count[:, :As] > 0).any().item())
     if frustrated > 0 and not m.training:

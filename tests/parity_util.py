@@ -44,12 +44,15 @@ def product_like(oracle, case, dtype, device):
     return m.to(device).eval()
 
 
+def _diff_summary(a: torch.Tensor, b: torch.Tensor) -> str:
+    a, b = a.float(), b.float()
+    n = int((a != b).sum().item())
+    return f"{n} of {b.numel()} elements differ, max abs diff {(a - b).abs().max().item():.3e}"
+
+
 def compare_states(sp, so, dtype, W, Me, what):
-    """Ring and exact bank byte-exact, decisions exact, summary bank and norm
-    caches to rounding (summary EMA uses sigmoid(eta), fp32 normalisation
-    sums in a different order)."""
-    so_k, so_v = so.k_buf, so.v_buf
-    sp_k, sp_v = sp.k_buf.cpu(), sp.v_buf.cpu()
+    """Every state field byte-exact: ring, both banks, both norm caches,
+    visibility bytes, LRU stamps, ring gates and the host ints."""
     assert torch.equal(sp.allowed.cpu(), so.allowed), f"{what}: allowed differs"
     assert torch.equal(sp.mem_last_exact.cpu(), so.mem_last_exact), f"{what}: LRU stamps differ"
     assert torch.equal(sp.g_recent.cpu(), so.g_recent), f"{what}: ring gates differ"
@@ -57,14 +60,49 @@ def compare_states(sp, so, dtype, W, Me, what):
     ints_o = [so.recent_idx, so.recent_filled, so.pos, so.active_exact, so.active_summary]
     assert ints_p == ints_o, f"{what}: ring ints {ints_p} != {ints_o}"
     E = W + Me
-    assert torch.equal(sp_k[:, :, :E], so_k[:, :, :E]), f"{what}: ring/exact K differ"
-    assert torch.equal(sp_v[:, :, :E], so_v[:, :, :E]), f"{what}: ring/exact V differ"
-    st = 1e-5 if dtype == torch.float32 else 8e-3
-    assert_close(sp_k[:, :, E:], so_k[:, :, E:], dtype, f"{what}: summary K", st)
-    assert_close(sp_v[:, :, E:], so_v[:, :, E:], dtype, f"{what}: summary V", st)
+    for f in ("k_buf", "v_buf"):
+        a, b = getattr(sp, f).cpu(), getattr(so, f)
+        for part, sl in (("ring", slice(0, W)), ("exact bank", slice(W, E)), ("summary bank", slice(E, None))):
+            assert torch.equal(a[:, :, sl], b[:, :, sl]), f"{what}: {f} {part}: {_diff_summary(a[:, :, sl], b[:, :, sl])}"
     for f in ("_exact_v_norm", "_sum_lf_k_norm"):
         a, b = getattr(sp, f), getattr(so, f)
         if b is None:
             assert a is None
         else:
-            assert_close(a, b, dtype, f"{what}: {f}", st)
+            a = a.cpu()
+            assert torch.equal(a, b), f"{what}: {f}: {_diff_summary(a, b)}"
+
+
+def _margin(tag, sc, where, m):
+    """Oracle margin of the decision at `where` (tuple index into the
+    decision tensor) from its masked score row."""
+    row = sc[where].float()
+    top = torch.topk(row, k=min(2, row.numel())).values
+    gap = (top[0] - top[1]).item() if top.numel() > 1 else float("inf")
+    msg = f"best {top[0].item():.6g}, gap to second {gap:.3e}"
+    if tag.startswith("exact"):
+        d = min(abs(top[0].item() - m.exact_novelty_threshold), abs(top[0].item() - m.exact_match_threshold))
+        msg += f", distance to a cosine threshold {d:.3e}"
+    return msg
+
+
+def compare_traces(tp, to, m, what):
+    """Decision events of the HIP path (layer.decision_trace) against the
+    oracle's trace: same events in the same order, every decision field
+    equal.  On a difference the message gives the oracle's margin there
+    (score gap between the best two slots, distance to the thresholds)."""
+    tags_p, tags_o = [e[0] for e in tp], [e[0] for e in to]
+    assert tags_p == tags_o, f"{what}: decision events {tags_p[:8]}... != {tags_o[:8]}..."
+    for i, (ep, eo) in enumerate(zip(tp, to)):
+        tag = eo[0]
+        for j in range(1, len(ep)):
+            a, b = ep[j].cpu(), eo[j]
+            if a.shape != b.shape or not torch.equal(a.to(b.dtype), b):
+                msg = f"{what}: event {i} ({tag}) field {j} differs from the oracle"
+                if a.shape == b.shape and tag != "select":
+                    bad = (a.to(b.dtype) != b).nonzero()
+                    where = tuple(bad[0].tolist())
+                    msg += f" at {where} (HIP {a[where].item()}, oracle {b[where].item()}); oracle margin: " + \
+                        _margin(tag, eo[-1], where, m)
+                raise AssertionError(msg)
+    return len(tp)

@@ -17,7 +17,7 @@ from __future__ import annotations
 import pytest
 import torch
 
-from parity_util import assert_close, compare_states, product_like, to_product_state
+from parity_util import assert_close, compare_states, compare_traces, product_like, to_product_state
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -64,17 +64,24 @@ def _inputs(m, B, L, dtype, kind, g):
 
 
 def _prefill_both(m, p, st_o, st_p, q, k, v, gate, lam, block, dtype, what):
+    """One prefill call on each side; heads, slot decisions (every chunk's
+    candidates, exact and summary routing) and the whole state compared."""
     from coda_oracle import prims
     L = q.shape[2]
     c, s = m.rope_tables(L, st_o.pos, dtype)
     q_r = prims.rope(q, c, s, m.rope_interleaved)
-    heads_o = m.prefill_core(q_r, k, v, gate, lam, st_o, block_size=block)
+    tr_o = []
+    p.decision_trace = []
+    heads_o = m.prefill_core(q_r, k, v, gate, lam, st_o, block_size=block, trace=tr_o)
     heads_p = p.prefill_core(q.to(DEV), k.to(DEV), v.to(DEV), gate.to(DEV), lam.squeeze(-1).to(DEV), c.to(DEV),
                              s.to(DEV), st_p, block_size=block)
     torch.cuda.synchronize()
+    n = compare_traces(p.decision_trace, tr_o, m, f"{what} decisions")
+    p.decision_trace = None
     assert_close(heads_p.permute(0, 2, 1, 3), heads_o, dtype, f"{what} heads")
     del heads_o, heads_p
     compare_states(st_p, st_o, dtype, m.window, m.Me, what)
+    return n
 
 
 @pytest.mark.parametrize("name", list(SHAPES))
@@ -102,19 +109,26 @@ def test_bench_shape_trajectory_matches_oracle(name):
     _prefill_both(m, p, st_o, st_p, q, k, v, gate, lam, block, dtype, f"{name} second prefill ({L2} tokens)")
     del q, k, v, gate, lam
     # ---- decode, free-running: the HIP side keeps its state (and routing
-    # record) from step to step
+    # record) from step to step; even steps record their decisions (the
+    # uncached launch path), odd steps run through the cached descriptors
     for t in range(steps):
+        traced = t % 2 == 0
+        tr_o = [] if traced else None
+        p.decision_trace = [] if traced else None
         qp = int(st_o.pos)
         qt = torch.randn(B, H, 1, Dh, generator=g).to(dtype)
         kn = torch.randn(B, Hkv, 1, Dh, generator=g).to(dtype)
         vn = torch.randn(B, Hkv, 1, Dh, generator=g).to(dtype)
         gn = _gates(kind, B, 1, g)
         lamt = torch.sigmoid(torch.randn(B, H, 1, 1, generator=g) - 1.0).to(dtype)
-        banks.write_one(m, st_o, kn, vn, gn)
+        banks.write_one(m, st_o, kn, vn, gn, tr_o)
         ho = m.attend_core(qt, lamt, st_o, qp)
         ct, sn = m.rope_tables(1, qp, dtype)
         hp = p.decode_step_core(qt.to(DEV), kn.to(DEV), vn.to(DEV), gn.reshape(B).to(DEV), lamt.squeeze(-1).to(DEV),
                                 st_p, ct.to(DEV), sn.to(DEV))
         torch.cuda.synchronize()
+        if traced:
+            compare_traces(p.decision_trace, tr_o, m, f"{name} decode step {t} decisions")
+        p.decision_trace = None
         assert_close(hp.permute(0, 2, 1, 3), ho, dtype, f"{name} decode step {t} heads")
         compare_states(st_p, st_o, dtype, W, Me, f"{name} decode step {t}")

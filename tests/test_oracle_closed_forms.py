@@ -194,7 +194,7 @@ def test_exact_route_seam_equals_block_function():
     s2 = _clone(st)
     trace = []
     banks.exact_block(m, s2, k_sel, v_sel, pos_sel, gate, trace=trace)
-    _, idx_b, ow_b, touch_b = trace[-1]
+    _, idx_b, ow_b, touch_b = trace[-1][:4]
     assert torch.equal(idx, idx_b) and torch.equal(ow, ow_b) and torch.equal(touch, touch_b)
     assert torch.equal(last, s2.mem_last_exact)
 
