@@ -18,6 +18,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 namespace coda {
@@ -1529,6 +1530,60 @@ extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const v
       return bf ? launch_block<bf16_t, 128>(s, kb, vb, gb, g, plan_c, ws, st)
                 : launch_block<float, 128>(s, kb, vb, gb, g, plan_c, ws, st);
   }
+}
+
+// ------------------------------------------------------------ no-alloc variant
+// Scratch of coda_block_write_noalloc: one array per GPU, resident until the
+// process ends.  In host code the symbol names a host-side stand-in, never
+// device memory: host code uses only the device address hipGetSymbolAddress
+// returns for the current device, looked up once per device and kept.
+static constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
+static constexpr int kNoAllocMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static int noalloc_scratch(void** out) {
+  static std::mutex mu;
+  static void* per_device[kNoAllocMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(CODA_EHIP, "coda_block_write_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return fail(CODA_EUNSUP, "coda_block_write_noalloc: device %d beyond %d devices", dev, kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lock(mu);
+  if (per_device[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(CODA_EHIP, "coda_block_write_noalloc: scratch address on device %d: %s", dev,
+                  hipGetErrorString(e));
+    per_device[dev] = p;
+  }
+  *out = per_device[dev];
+  return CODA_OK;
+}
+
+extern "C" size_t coda_block_write_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+extern "C" int coda_block_write_noalloc(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb,
+                                        int64_t b_sh, int64_t b_sl, const float* gb, int64_t g_sb, int blk,
+                                        int ring_head, int ring_filled, int64_t pos0, const int32_t* plan_c,
+                                        int Kmax, int Te, int Ts, void* stream) {
+  int rc = validate_bank(s, "coda_block_write_noalloc");
+  if (rc) return rc;
+  CODA_REQUIRE(Te >= 0 && Ts >= 0, "coda_block_write_noalloc: negative candidate counts");
+  const size_t need = block_ws_bytes(s, Te, Ts);
+  CODA_REQUIRE(need <= kNoAllocScratchBytes,
+               "coda_block_write_noalloc: this chunk needs %zu bytes of scratch, more than the %zu bytes the "
+               "library holds per GPU (B * Hkv * (Te * Me + Ts * Ms) fp32 dots dominate); call coda_block_write "
+               "with a workspace instead",
+               need, kNoAllocScratchBytes);
+  // nothing in the scratch needs to start at zero: every word a chunk reads
+  // is written earlier in the same call (dots, metadata snapshot, decisions)
+  void* ws = nullptr;
+  rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  return coda_block_write(s, kb, vb, b_sb, b_sh, b_sl, gb, g_sb, blk, ring_head, ring_filled, pos0, plan_c, Kmax,
+                          Te, Ts, ws, kNoAllocScratchBytes, stream);
 }
 
 extern "C" int coda_ring_rotate(const coda_bank_desc* s, int ring_head, void* workspace, size_t workspace_bytes,

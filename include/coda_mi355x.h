@@ -267,6 +267,25 @@ int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb,
 /* Device scratch for coda_block_write. */
 int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, size_t* bytes);
 
+/* coda_block_write without a workspace argument and without any allocation:
+ * the chunk's scratch (routing dots, metadata snapshot, decisions) lives in a
+ * 16 MiB array of the library's own per GPU (static device memory, held until
+ * the process ends), addressed through hipGetSymbolAddress once per device.
+ * Same arguments, kernels, results and errors as coda_block_write; a chunk
+ * whose scratch (coda_block_workspace_bytes) exceeds
+ * coda_block_write_noalloc_max_bytes() is rejected with CODA_EINVAL before
+ * anything runs.  Calls on one GPU share the array: calls that overlap on one
+ * GPU (different streams, or threads) race, so serialise them.  The stream
+ * must belong to the current device.
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). */
+int coda_block_write_noalloc(const coda_bank_desc* s, const void* kb, const void* vb,
+                             int64_t b_sb, int64_t b_sh, int64_t b_sl, const float* gb, int64_t g_sb,
+                             int blk, int ring_head, int ring_filled, int64_t pos0,
+                             const int32_t* plan_c, int Kmax, int Te, int Ts, void* stream);
+size_t coda_block_write_noalloc_max_bytes(void);
+
 /* Rotate a full circular ring (head != 0) into time order at slots 0..W-1
  * (k_buf, v_buf, g_recent, allowed), as the reference leaves it after every
  * prefill chunk (_set_recent_from_sequence, memory_banks.py:152-177).

@@ -87,6 +87,24 @@ def test_validation_fails_before_any_hip_call():
     assert L.coda_rope_fwd(1, None, 0, 0, 0, None, 0, 0, 0, None, None, 1, 1, 1, 63, 1, None) == 1
 
 
+def test_noalloc_block_write_rejects_chunks_beyond_its_scratch():
+    """coda_block_write_noalloc refuses, before any HIP call, a chunk whose
+    scratch exceeds the library's per-GPU array (16 MiB), naming the limit."""
+    H = _hip()
+    L = H.lib()
+    limit = L.coda_block_write_noalloc_max_bytes()
+    assert limit == 16 << 20
+    b = H.BankDesc()
+    b.dtype, b.B, b.Hkv, b.Dh, b.W, b.Me, b.Ms, b.lf = H.CODA_BF16, 4096, 8, 128, 256, 64, 64, 64
+    b.active_exact, b.active_summary = 64, 64
+    fake = 256  # never dereferenced: the size check comes first
+    b.k_buf = b.v_buf = b.allowed = b.g_recent = b.mem_last = b.exact_v_norm = b.sum_lf_k_norm = b.eta = fake
+    rc = L.coda_block_write_noalloc(b, fake, fake, 0, 0, 0, fake, 0, 256, 0, 256, 0, fake, 64, 8, 64, None)
+    assert rc == 1
+    msg = L.coda_last_error()
+    assert b"16777216" in msg and b"coda_block_write with a workspace" in msg, msg
+
+
 def _topk_host(vals, k, largest, sorted_):
     L = _hip().lib()
     out = np.zeros(k, np.int64)
