@@ -35,6 +35,9 @@
 #include "bank_ops.h"
 #include "common.h"
 
+#include <atomic>
+#include <cstring>
+
 #include <math.h>
 #include <type_traits>
 #include <utility>
@@ -2163,6 +2166,943 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
   }
 }
 
+// ------------------------------------------------------------ prefill flash tiles, 32-row MFMA
+// attn_f2_bf16: the MFMA path for prefill chunks and unbounded attention
+// (head_dim 64 / 128).  Workgroup = (query block, KV head, sequence); wave
+// w owns head g = w / NQ and 16 queries, BOTH streams: the wave's 32 MFMA
+// rows are the 16 signal queries (rows 0-15) and the same 16 queries
+// rotated into the noise stream (rows 16-31).  Every K / V fragment a wave
+// reads from LDS therefore feeds a 32 x 32 x 16 product (twice the FLOPs
+// per LDS byte of a 16-row wave), and the epilogue finds O_noise one
+// permlane swap away (lanes l and l ^ 16).
+//   S^T = K Q^T per 32-key block kb: A = K fragment (32 keys x 16 channels,
+//     lane l: key l % 32, channels 8 (l / 32) ..+8, one contiguous 16-byte
+//     read: K sits in LDS in fragment order), B = Q^T (lane l: row l % 32,
+//     the same channels), D: lane l holds row l % 32 and keys
+//     8 (j / 4) + 4 (l / 32) + j % 4 of the block in register j.
+//   O^T += V^T P^T per 16-key step (kb, ph): B = registers 8 ph .. 8 ph + 7
+//     of S^T block kb (already the B layout, with k-slot i standing for key
+//     16 ph + 8 (i / 4) + 4 (l / 32) + i % 4), A = V^T with the same key
+//     order: two ds_read_b64_tr_b16 of rows 4 (l / 32) + 0..3 and + 8, at
+//     channel 32 db + l % 32.  V is row-major in LDS with 16-byte chunks
+//     XOR-swizzled per row (F2Layout::vchunk) so each transposed read
+//     touches every bank group.
+// Online softmax per row with a lazy rescale (the running max moves only
+// when a tile's max exceeds it by more than 2^8); P rounded to bf16 by the
+// hardware conversion.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma_32x32x16(const bf16x8_t& a, const bf16x8_t& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// ds_read_b128 issued by hand at an immediate offset (see lds_read_tr16_at)
+typedef uint32_t u32x4v_t __attribute__((ext_vector_type(4)));
+template <int OFF>
+__device__ __forceinline__ u32x4v_t lds_read_b128_at(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  u32x4v_t r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+  return r;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait_b128(u32x4v_t& a) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void lds_wait2_n(uint2& a, uint2& b) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+
+template <int DH>
+struct F2Layout {
+  static constexpr int KT = 64;                  // keys per tile
+  static constexpr int NKS = DH / 16;            // 16-channel steps of S^T
+  static constexpr int NDB = DH / 32;            // 32-channel blocks of O^T
+  static constexpr int KBYTES = 2 * NKS * 1024;  // K tile: fragments (kb, ks)
+  static constexpr int ROWB = DH * 2;            // V row (one key)
+  static constexpr int CPR = DH / 8;             // 16-byte chunks per V row
+  static constexpr int VBYTES = KT * ROWB;
+  static constexpr int RPI = 1024 / ROWB;        // V rows per 1 KiB direct load
+  static constexpr int KCH = 2 * NKS, VCH = VBYTES / 1024;
+  static constexpr int LDS = 2 * (KBYTES + VBYTES);  // two tiles in flight
+  // stored chunk of chunk c of V row r (an involution): the 64-byte
+  // segments of the eight rows one transposed read touches land in
+  // distinct bank groups, two rows a group
+  static __host__ __device__ __forceinline__ int vchunk(int r, int c) {
+    return DH == 128 ? (c ^ (4 * (r & 3))) : (c ^ (4 * ((r >> 1) & 1)));
+  }
+};
+
+template <int DH, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_f2_bf16(
+    const coda_attn_desc a, int NQ, int nqb, int npairs) {
+  using Lay = F2Layout<DH>;
+  constexpr int KT = Lay::KT, NKS = Lay::NKS, NDB = Lay::NDB, KCH = Lay::KCH, VCH = Lay::VCH;
+  constexpr int KCW = (KCH + NW - 1) / NW, VCW = (VCH + NW - 1) / NW;
+  extern __shared__ __attribute__((aligned(16))) char f2_smem[];
+  __shared__ uint8_t al_lds[kMaxRowsPrefix];
+  __shared__ uint8_t al32[kMaxRowsPrefix / 32];
+  __shared__ float w_lds[DH];
+  char* kbuf = f2_smem;
+  char* vbuf = f2_smem + 2 * Lay::KBYTES;
+
+  // block -> (query block, KV head, sequence); with a multiple of 8 pairs
+  // the query blocks of one (sequence, KV head) share an XCD (dispatch is
+  // round robin over the 8 XCDs), so its K / V stay in that XCD's L2
+  const int id = blockIdx.x;
+  int qb, pair;
+  if (npairs % 8 == 0) {
+    const int local = id >> 3;
+    pair = (id & 7) + 8 * (local / nqb);
+    qb = local % nqb;
+  } else {
+    pair = id / nqb;
+    qb = id % nqb;
+  }
+  const int hk = pair % a.Hkv, b = pair / a.Hkv;
+  const int G = a.H / a.Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, hl = lane >> 5;  // MFMA row, channel half of a 16-channel step
+  const int strm = n >> 4, qn = n & 15;     // 0 signal / 1 noise, query of the wave
+  const int g = wv / NQ, qsub = wv % NQ, h = hk * G + g;
+  const int q0 = qb * 16 * NQ + 16 * qsub;
+  const int qrow = q0 + qn;
+  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
+  const int Lk = a.Lp + a.Lb;
+  const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
+  const int q_hi = min(a.Lq - 1, qb * 16 * NQ + 16 * NQ - 1);
+  const int klim = a.causal ? min(Lk, a.Lp + q_hi + coff + 1) : Lk;
+  const int ntile = (klim + KT - 1) / KT;
+
+  const bf16_t* kpb = a.Lp > 0 ? (const bf16_t*)a.kp + b * a.p_sb + hk * a.p_sh : nullptr;
+  const bf16_t* vpb = a.Lp > 0 ? (const bf16_t*)a.vp + b * a.p_sb + hk * a.p_sh : nullptr;
+  const bf16_t* kbb = a.Lb > 0 ? (const bf16_t*)a.kb + b * a.b_sb + hk * a.b_sh : nullptr;
+  const bf16_t* vbb = a.Lb > 0 ? (const bf16_t*)a.vb + b * a.b_sb + hk * a.b_sh : nullptr;
+  const int psl = (int)a.p_sl, bsl = (int)a.b_sl;
+
+  // this lane's piece of the direct loads: K fragment ci = (kb, ks) takes
+  // key 32 kb + k_r at channels 16 ks + k_c; V piece vi takes row
+  // RPI vi + v_r at the channels of its stored chunk
+  const int k_r = lane & 31, k_c = 8 * (lane >> 5);
+  const int v_r = lane / Lay::CPR, v_c = 8 * Lay::vchunk(v_r, lane % Lay::CPR);
+  auto row_of = [&](const bf16_t* pb, const bf16_t* bb, int kidx) {
+    kidx = kidx < Lk ? kidx : 0;  // past the end: a valid row, masked later
+    return kidx < a.Lp ? pb + (int64_t)kidx * psl : bb + (int64_t)(kidx - a.Lp) * bsl;
+  };
+  auto tile_load = [&](int kt0, int bi) {
+    char* kd = kbuf + bi * Lay::KBYTES;
+    char* vd = vbuf + bi * Lay::VBYTES;
+#pragma unroll
+    for (int j = 0; j < KCW; ++j) {
+      const int ci = wv + NW * j;
+      if (KCH % NW == 0 || ci < KCH) {
+        const int kb = ci / NKS, ks = ci % NKS;
+        lds_load16(row_of(kpb, kbb, kt0 + 32 * kb + k_r) + 16 * ks + k_c, kd + ci * 1024);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < VCW; ++j) {
+      const int vi = wv + NW * j;
+      if (VCH % NW == 0 || vi < VCH) lds_load16(row_of(vpb, vbb, kt0 + Lay::RPI * vi + v_r) + v_c, vd + vi * 1024);
+    }
+  };
+
+  // ---- prologue: every global load before the first use of any (tile 0,
+  // visibility bytes, norm weight, queries, tables, lambda)
+  if (ntile > 0) tile_load(0, 0);
+  constexpr int ALR = kMaxRowsPrefix / (NW * 64);
+  uint8_t al_r[ALR];
+#pragma unroll
+  for (int k = 0; k < ALR; ++k) {
+    const int i = tid + NW * 64 * k;
+    al_r[k] = i < a.Lp ? (a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1) : (uint8_t)0;
+  }
+  const bf16_t w_raw = tid < DH && a.rms_w ? ((const bf16_t*)a.rms_w)[tid] : (bf16_t)0x3f80;
+
+  // queries of this lane: row n (stream strm of query qrow), channels
+  // 16 ks + 8 hl .. + 8.  RoPE with the eager-op rounding, then for the
+  // noise stream the per-head rotation (primitives.py:58-113), unless the
+  // noise queries are given.
+  bf16x8_t qf[NKS];
+  bf16_t lam_raw;
+  {
+    using E = Elt<bf16_t>;
+    constexpr int half = DH / 2;
+    const bool given = strm == 1 && a.q_noise != nullptr;
+    const bool rot = strm == 1 && a.q_noise == nullptr;
+    const bool rope = a.rope_cos != nullptr && !given, inter = a.rope_interleaved != 0;
+    const bool qlive = qrow < a.Lq;
+    const int qi = qlive ? qrow : 0;
+    const bf16_t* qr = given ? (const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh + (int64_t)qi * a.qn_sl
+                             : (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
+    const bf16_t* csr = rope ? (const bf16_t*)a.rope_cos + (int64_t)qi * half : nullptr;
+    const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
+    uint4 uq[NKS], up[NKS], rc[NKS], rs[NKS];
+    uint2 rc2[NKS], rs2[NKS], tcs[NKS], tsn[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = 16 * ks + 8 * hl;
+      uq[ks] = *reinterpret_cast<const uint4*>(qr + d0);
+      if (rope && inter) {
+        rc2[ks] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
+        rs2[ks] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
+      }
+      if (rope && !inter) {
+        const int f0 = d0 < half ? d0 : d0 - half;
+        up[ks] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
+        rc[ks] = *reinterpret_cast<const uint4*>(csr + f0);
+        rs[ks] = *reinterpret_cast<const uint4*>(snr + f0);
+      }
+      if (rot) {
+        tcs[ks] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_cos + (int64_t)h * half + d0 / 2);
+        tsn[ks] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_sin + (int64_t)h * half + d0 / 2);
+      }
+    }
+    lam_raw = ((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = 16 * ks + 8 * hl;
+      if (given) {
+        qf[ks] = __builtin_bit_cast(bf16x8_t, qlive ? uq[ks] : uint4{0, 0, 0, 0});
+        continue;
+      }
+      uint32_t w[4] = {uq[ks].x, uq[ks].y, uq[ks].z, uq[ks].w};
+      if (rope && inter) {
+        // pairs (2p, 2p+1) rotated by angle d0/2 + p: one bf16 dot2 per
+        // output (fp32 products and sum, one rounding)
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp)
+          w[pp] = rot_pair(w[pp], pp >> 1 ? rc2[ks].y : rc2[ks].x, pp >> 1 ? rs2[ks].y : rs2[ks].x, pp & 1);
+      }
+      if (rope && !inter) {
+        // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin, with
+        // the eager-op rounding of each product and sum
+        float x[8], cc[8], ss[8], y[8];
+        unpack8(uq[ks], x);
+        unpack8(rc[ks], cc);
+        unpack8(rs[ks], ss);
+        unpack8(up[ks], y);
+        const bool lo = d0 < half;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float rt = lo ? -y[j] : y[j];
+          x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rt * ss[j]));
+        }
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) w[pp] = pk_bf16(x[2 * pp], x[2 * pp + 1]);
+      }
+      if (rot) {
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp)
+          w[pp] = rot_pair(w[pp], pp >> 1 ? tcs[ks].y : tcs[ks].x, pp >> 1 ? tsn[ks].y : tsn[ks].x, pp & 1);
+      }
+      qf[ks] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
+    }
+  }
+  // visibility bytes of the prefix, per-32-key "all visible" flags, norm weight
+#pragma unroll
+  for (int k = 0; k < ALR; ++k) {
+    const int i = tid + NW * 64 * k;
+    if (i < a.Lp) al_lds[i] = al_r[k];
+  }
+  if (tid < DH) w_lds[tid] = bf2f(w_raw);
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_s_barrier();
+  for (int base = 64 * wv; base < a.Lp; base += 64 * NW) {
+    const int i = base + lane;
+    const uint64_t m = __ballot(i < a.Lp && al_lds[i] != 0);
+    const int e = (base >> 5) + lane;
+    if (lane < 2 && 32 * e < a.Lp) al32[e] = (uint8_t)(((m >> (32 * lane)) & 0xffffffffull) == 0xffffffffull);
+  }
+
+  // LDS byte addresses: this lane's K fragment word, its V transposed-read
+  // cell for each channel block db (rows 4 hl + (p16 >> 2) of a 16-key step,
+  // channels 32 db + 16 (grp & 1) + 4 (p16 & 3), stored chunk swizzled)
+  const int grp = lane >> 4, p16 = lane & 15;
+  const int vrow = 4 * (grp >> 1) + (p16 >> 2);
+  int v_off[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+    v_off[db] = vrow * Lay::ROWB + 16 * Lay::vchunk(vrow, 4 * db + 2 * (grp & 1) + ((p16 & 3) >> 1)) + 8 * (p16 & 1);
+
+  float m_s = -INFINITY, l_s = 0.f;
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
+
+  for (int it = 0; it < ntile; ++it) {
+    const int bi = it & 1, kt0 = it * KT;
+    // tile it has landed and every wave is done with tile it - 1, whose
+    // buffer now takes tile it + 1
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    if (it + 1 < ntile) tile_load(kt0 + KT, bi ^ 1);
+    // ---- S^T: NKS steps x 2 key blocks, fragment reads four ahead
+    const uint32_t ka = lds_addr(kbuf + bi * Lay::KBYTES) + 16 * lane;
+    f32x16 st[2];
+    {
+      constexpr int NF = 2 * NKS;
+      u32x4v_t kr[4];
+      auto k_issue = [&](auto f_c) {
+        constexpr int f = decltype(f_c)::value;
+        if constexpr (f < NF) {
+          constexpr int ks = f / 2, kb = f % 2;
+          kr[f % 4] = lds_read_b128_at<(kb * NKS + ks) * 1024>(ka);
+        }
+      };
+      k_issue(std::integral_constant<int, 0>{});
+      k_issue(std::integral_constant<int, 1>{});
+      k_issue(std::integral_constant<int, 2>{});
+      static_for<NF>([&](auto f_c) {
+        constexpr int f = decltype(f_c)::value;
+        constexpr int ks = f / 2, kb = f % 2;
+        k_issue(std::integral_constant<int, f + 3>{});
+        lds_wait_b128<(f + 3 < NF) ? 3 : (NF - 1 - f)>(kr[f % 4]);
+        st[kb] = mfma_32x32x16(__builtin_bit_cast(bf16x8_t, kr[f % 4]), qf[ks], ks == 0 ? f32x16{} : st[kb]);
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    }
+    // ---- mask, online softmax, P
+    {
+      bool need = false;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int pk0 = kt0 + 32 * kb;
+        need |= (pk0 + 32 > Lk) || (pk0 < a.Lp && !al32[pk0 >> 5]) ||
+                (pk0 + 32 > a.Lp && a.causal && (pk0 + 31 - a.Lp) > q0 + coff);
+      }
+      if (need) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int kidx = kt0 + 32 * kb + 8 * (j >> 2) + 4 * hl + (j & 3);
+            const int jb = kidx - a.Lp;
+            const bool pre = kidx < a.Lp;
+            const bool al_ok = al_lds[pre ? kidx : 0] != 0;
+            const bool blk_ok = (jb < a.Lb) & ((a.causal == 0) | (jb <= qrow + coff));
+            st[kb][j] = (pre ? al_ok : blk_ok) ? st[kb][j] : -INFINITY;
+          }
+      }
+      float mx = st[0][0];
+#pragma unroll
+      for (int j = 1; j < 16; ++j) mx = fmaxf(mx, st[0][j]);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[1][j]);
+      const float tsc = xmax32(mx) * scale;
+      if (__ballot(tsc > m_s + 8.f)) {
+        const float mnew = fmaxf(m_s, tsc);
+        const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s - mnew);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+        l_s *= alpha;
+        m_s = mnew;
+      }
+      const float mu = m_s == -INFINITY ? 0.f : m_s;
+      float ls = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          st[kb][j] = fast_exp2(fmaf(st[kb][j], scale, -mu));
+          ls += st[kb][j];
+        }
+      l_s += ls;
+    }
+    // ---- O^T += V^T P^T: 4 key steps x NDB channel blocks, each fed by two
+    // transposed reads; two (step, block) read pairs in flight
+    {
+      const uint32_t va = lds_addr(vbuf + bi * Lay::VBYTES);
+      constexpr int NPV = 4 * NDB;
+      uint2 rd[3][2];
+      uint4 pf4[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int kb = p >> 1, ph = p & 1;
+        pf4[p].x = pk_bf16(st[kb][8 * ph + 0], st[kb][8 * ph + 1]);
+        pf4[p].y = pk_bf16(st[kb][8 * ph + 2], st[kb][8 * ph + 3]);
+        pf4[p].z = pk_bf16(st[kb][8 * ph + 4], st[kb][8 * ph + 5]);
+        pf4[p].w = pk_bf16(st[kb][8 * ph + 6], st[kb][8 * ph + 7]);
+      }
+      auto v_issue = [&](auto q_c) {
+        constexpr int q = decltype(q_c)::value;
+        if constexpr (q < NPV) {
+          constexpr int p = q / NDB, db = q % NDB;
+          constexpr int ROW0 = 16 * p * Lay::ROWB, ROW8 = ROW0 + 8 * Lay::ROWB;
+          rd[q % 3][0] = lds_read_tr16_at<ROW0>(va + v_off[db]);
+          rd[q % 3][1] = lds_read_tr16_at<ROW8>(va + v_off[db]);
+        }
+      };
+      v_issue(std::integral_constant<int, 0>{});
+      v_issue(std::integral_constant<int, 1>{});
+      static_for<NPV>([&](auto q_c) {
+        constexpr int q = decltype(q_c)::value;
+        constexpr int p = q / NDB, db = q % NDB, b3 = q % 3;
+        lds_wait2_n<(q + 1 < NPV) ? 2 : 0>(rd[b3][0], rd[b3][1]);
+        const bf16x8_t va8 = __builtin_bit_cast(bf16x8_t, uint4{rd[b3][0].x, rd[b3][0].y, rd[b3][1].x, rd[b3][1].y});
+        o[db] = mfma_32x32x16(va8, __builtin_bit_cast(bf16x8_t, pf4[p]), o[db]);
+        __builtin_amdgcn_sched_barrier(0);
+        v_issue(std::integral_constant<int, q + 2>{});
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    }
+  }
+
+  // ---- epilogue: lane holds row n's channels 32 db + 8 (j / 4) + 4 hl +
+  // j % 4.  Noise lanes (n >= 16) round O_noise to bf16; one permlane swap
+  // hands it to the signal lane l ^ 16; y = O_signal - lam rnd(O_noise),
+  // then the HeadwiseRMSNorm and weight in fp32, one rounding at the store.
+  const float l_tot = xsum32(l_s);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float lam = bf2f(lam_raw);
+  float y[NDB][16];
+  float sq = 0.f;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      const uint32_t mine = pk_bf16(o[db][j] * inv, o[db][j + 1] * inv);
+      const auto r = __builtin_amdgcn_permlane16_swap(mine, mine, false, false);
+      const uint32_t nz = (uint32_t)r[1];  // the odd 16-lane row's value: the noise lane's
+      const float on0 = bf2f((bf16_t)(nz & 0xffffu)), on1 = bf2f((bf16_t)(nz >> 16));
+      y[db][j] = fmaf(-lam, on0, o[db][j] * inv);
+      y[db][j + 1] = fmaf(-lam, on1, o[db][j + 1] * inv);
+      sq = fmaf(y[db][j], y[db][j], sq);
+      sq = fmaf(y[db][j + 1], y[db][j + 1], sq);
+    }
+  if (a.rms_w) {
+    sq = xsum32(sq);
+    const float rr = 1.0f / sqrtf(sq / (float)DH + a.eps);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) y[db][j] *= rr * w_lds[32 * db + 8 * (j >> 2) + 4 * hl + (j & 3)];
+  }
+  if (strm == 0 && qrow < a.Lq) {
+    bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        uint2 u;
+        u.x = pk_bf16(y[db][4 * jq + 0], y[db][4 * jq + 1]);
+        u.y = pk_bf16(y[db][4 * jq + 2], y[db][4 * jq + 3]);
+        *reinterpret_cast<uint2*>(orow_p + 32 * db + 8 * jq + 4 * hl) = u;
+      }
+  }
+}
+
+// ------------------------------------------------------------ prefill flash tiles, pipelined
+// attn_f3_bf16: attn_f2_bf16's tiles (32 MFMA rows per wave: 16 queries x
+// both streams; S^T = K Q^T and O^T += V^T P^T as 32 x 32 x 16 products),
+// software-pipelined so the matrix and vector pipes work at the same time
+// within each wave.  Iteration it, with S(it) already masked and its row
+// max folded into the running max:
+//   phase A: the 16 products of S(it + 1) (tile it + 1's K fragments),
+//            each followed by the exp / row sum / bf16 packing of two of
+//            this lane's 32 entries of P(it);
+//   phase C: the 4 NDB products of O += V(it)^T P(it), each followed by the
+//            mask and running-max work of two entries of S(it + 1);
+//   then the lazy rescale (only when a row max moves by more than 2^8).
+// Four tiles live in LDS (it, it + 1, and it + 2, it + 3 loading), so one
+// barrier per tile suffices and a tile's loads have two iterations to land.
+// Whole tiles inside the prefix or the block load from a wave-uniform base
+// plus per-lane offsets.
+template <int DH, int NW, int QM>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_f3_bf16(
+    const coda_attn_desc a, int NQ, int nqb, int npairs) {
+  using Lay = F2Layout<DH>;
+  constexpr int NS = 4;
+  constexpr int KT = Lay::KT, NKS = Lay::NKS, NDB = Lay::NDB, KCH = Lay::KCH, VCH = Lay::VCH;
+  constexpr int KCW = (KCH + NW - 1) / NW, VCW = (VCH + NW - 1) / NW;
+  static_assert(KCH % NW == 0 && VCH % NW == 0, "tile pieces split evenly over the waves");
+  constexpr int STAGE = Lay::KBYTES + Lay::VBYTES;
+  extern __shared__ __attribute__((aligned(16))) char f3_smem[];
+  __shared__ __attribute__((aligned(16))) uint8_t al_lds[kMaxRowsPrefix];
+  __shared__ __attribute__((aligned(16))) float w_lds[DH];
+
+  const int id = blockIdx.x;
+  int qb, pair;
+  if (npairs % 8 == 0) {
+    const int local = id >> 3;
+    pair = (id & 7) + 8 * (local / nqb);
+    qb = local % nqb;
+  } else {
+    pair = id / nqb;
+    qb = id % nqb;
+  }
+  const int hk = pair % a.Hkv, b = pair / a.Hkv;
+  const int G = a.H / a.Hkv;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, hl = lane >> 5;
+  const int strm = n >> 4, qn = n & 15;
+  const int g = wv / NQ, qsub = wv % NQ, h = hk * G + g;
+  const int q0 = qb * 16 * NQ + 16 * qsub;
+  const int qrow = q0 + qn;
+  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
+  const int Lk = a.Lp + a.Lb;
+  const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
+  const int q_hi = min(a.Lq - 1, qb * 16 * NQ + 16 * NQ - 1);
+  const int klim = a.causal ? min(Lk, a.Lp + q_hi + coff + 1) : Lk;
+  const int ntile = (klim + KT - 1) / KT;
+
+  const bf16_t* kpb = a.Lp > 0 ? (const bf16_t*)a.kp + b * a.p_sb + hk * a.p_sh : nullptr;
+  const bf16_t* vpb = a.Lp > 0 ? (const bf16_t*)a.vp + b * a.p_sb + hk * a.p_sh : nullptr;
+  const bf16_t* kbb = a.Lb > 0 ? (const bf16_t*)a.kb + b * a.b_sb + hk * a.b_sh : nullptr;
+  const bf16_t* vbb = a.Lb > 0 ? (const bf16_t*)a.vb + b * a.b_sb + hk * a.b_sh : nullptr;
+  const int psl = (int)a.p_sl, bsl = (int)a.b_sl;
+
+  // ---- tile loads: K fragment ci = wv + NW j is (kb, ks) = (ci / NKS,
+  // ci % NKS): key 32 kb + k_r, channels 16 ks + k_c; V piece vi = wv + NW j:
+  // row RPI vi + v_r, the channels of its stored chunk.  Per-lane byte
+  // offsets from the tile's first row (31 bits: checked by the launcher).
+  const int k_r = lane & 31, k_c = 8 * (lane >> 5);
+  const int v_r = lane / Lay::CPR, v_c = 8 * Lay::vchunk(v_r, lane % Lay::CPR);
+  const uint32_t kofP = 2u * (uint32_t)(k_r * psl + k_c), kofB = 2u * (uint32_t)(k_r * bsl + k_c);
+  const uint32_t vofP = 2u * (uint32_t)(v_r * psl + v_c), vofB = 2u * (uint32_t)(v_r * bsl + v_c);
+  auto tile_load = [&](int kt0, int bi) {
+    char* kd = f3_smem + bi * STAGE;
+    char* vd = kd + Lay::KBYTES;
+    const bool in_p = kt0 + KT <= a.Lp, in_b = kt0 >= a.Lp && kt0 + KT <= Lk;
+    if (in_p || in_b) {
+      const char* kb0 = in_p ? (const char*)(kpb + (int64_t)kt0 * psl) : (const char*)(kbb + (int64_t)(kt0 - a.Lp) * bsl);
+      const char* vb0 = in_p ? (const char*)(vpb + (int64_t)kt0 * psl) : (const char*)(vbb + (int64_t)(kt0 - a.Lp) * bsl);
+      const int sl2 = 2 * (in_p ? psl : bsl);
+      const uint32_t kof = in_p ? kofP : kofB, vof = in_p ? vofP : vofB;
+#pragma unroll
+      for (int j = 0; j < KCW; ++j) {
+        const int ci = wv + NW * j, kb = ci / NKS, ks = ci % NKS;
+        lds_load16(kb0 + (int64_t)(32 * kb) * sl2 + 32 * ks + kof, kd + ci * 1024);
+      }
+#pragma unroll
+      for (int j = 0; j < VCW; ++j) {
+        const int vi = wv + NW * j;
+        lds_load16(vb0 + (int64_t)(Lay::RPI * vi) * sl2 + vof, vd + vi * 1024);
+      }
+    } else {
+      // a tile across the prefix / block boundary or the end: per row
+      // (rows past Lk read row 0, a valid row, and are masked)
+      auto row_of = [&](const bf16_t* pb, const bf16_t* bb, int kidx) {
+        kidx = kidx < Lk ? kidx : 0;
+        return kidx < a.Lp ? pb + (int64_t)kidx * psl : bb + (int64_t)(kidx - a.Lp) * bsl;
+      };
+#pragma unroll
+      for (int j = 0; j < KCW; ++j) {
+        const int ci = wv + NW * j, kb = ci / NKS, ks = ci % NKS;
+        lds_load16(row_of(kpb, kbb, kt0 + 32 * kb + k_r) + 16 * ks + k_c, kd + ci * 1024);
+      }
+#pragma unroll
+      for (int j = 0; j < VCW; ++j) {
+        const int vi = wv + NW * j;
+        lds_load16(row_of(vpb, vbb, kt0 + Lay::RPI * vi + v_r) + v_c, vd + vi * 1024);
+      }
+    }
+  };
+  constexpr int LPT = KCW + VCW;  // direct loads per wave and tile
+
+  // ---- prologue.  VMEM loads complete in issue order, so the loads the
+  // query math waits for go out first and tiles 0, 1, 2 behind them.  The
+  // compiler cannot tell which LDS bytes a direct global->LDS load writes,
+  // so it makes any LDS access the kernel code issues after one wait for
+  // all of them: the visibility bytes and the norm weight reach LDS before
+  // the tile loads go out, and nothing between those loads and the first
+  // product touches LDS but the hand-issued fragment reads.
+  // Visibility bytes: every wave loads the prefix's bytes (16 a lane, up to
+  // kMaxRowsPrefix), folds them into `allvis` (bit e: the 32 keys [32 e,
+  // 32 e + 32) are all visible, a key past the prefix counting as hidden)
+  // and wave 0 stores them to LDS for the per-entry mask.
+  constexpr int ALC = kMaxRowsPrefix / (16 * 64);  // 16-byte chunks per lane
+  uint4 al_c[ALC];
+  bf16_t w_raw;
+  uint64_t allvis = 0;
+  // queries of this lane: row n (stream strm of query qrow), channels
+  // 16 ks + 8 hl .. + 8: RoPE with the eager-op rounding, then for the noise
+  // stream the per-head rotation (primitives.py:58-113), unless the noise
+  // queries are given.  QM fixes the case at compile time (0: interleaved
+  // RoPE + rotation, 1: half-split RoPE + rotation, 2: given noise queries,
+  // no RoPE, 3: any, decided at run time), so the common cases are
+  // straight-line code: every load unconditional and from a valid address
+  // (the signal and noise lanes of a query read the same row in the same
+  // instruction, one memory access), both streams' math on every lane and
+  // a select, no wait inside a branch.
+  bf16x8_t qf[NKS];
+  bf16_t lam_raw;
+  {
+    using E = Elt<bf16_t>;
+    constexpr int half = DH / 2;
+    const bool noise = strm == 1;
+    const bool given = QM == 2 || (QM == 3 && a.q_noise != nullptr);
+    const bool rope = QM == 0 || QM == 1 || (QM == 3 && a.rope_cos != nullptr);
+    const bool inter = QM == 0 || (QM == 3 && a.rope_interleaved != 0);
+    const bool qlive = qrow < a.Lq;
+    const int qi = qlive ? qrow : 0;
+    const bf16_t* qrow_sig = (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
+    const bf16_t* qr = (given && noise)
+                           ? (const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh + (int64_t)qi * a.qn_sl
+                           : qrow_sig;
+    // RoPE applies to the query rows this lane loads unless they are given
+    // noise queries (QM 3 with both)
+    const bool rope_lane = rope && !(given && noise);
+    const bf16_t* csr = rope ? (const bf16_t*)a.rope_cos + (int64_t)qi * half : nullptr;
+    const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
+    const bf16_t* thc = !given ? (const bf16_t*)a.theta_cos + (int64_t)h * half : nullptr;
+    const bf16_t* ths = !given ? (const bf16_t*)a.theta_sin + (int64_t)h * half : nullptr;
+    uint4 uq[NKS], up[NKS], rc[NKS], rs[NKS];
+    uint2 rc2[NKS], rs2[NKS], tcs[NKS], tsn[NKS];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = 16 * ks + 8 * hl;
+      uq[ks] = *reinterpret_cast<const uint4*>(qr + d0);
+      if (rope && inter) {
+        rc2[ks] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
+        rs2[ks] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
+      }
+      if (rope && !inter) {
+        const int f0 = d0 < half ? d0 : d0 - half;
+        up[ks] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
+        rc[ks] = *reinterpret_cast<const uint4*>(csr + f0);
+        rs[ks] = *reinterpret_cast<const uint4*>(snr + f0);
+      }
+      if (!given) {
+        tcs[ks] = *reinterpret_cast<const uint2*>(thc + d0 / 2);
+        tsn[ks] = *reinterpret_cast<const uint2*>(ths + d0 / 2);
+      }
+    }
+    lam_raw = ((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl];
+    // visibility bytes of the prefix and the norm weight, behind the
+    // queries (without visibility bytes, or past the row, a 16-byte read of
+    // the queries keeps the load unconditional; its value is replaced)
+    {
+      const bool have = a.allowed != nullptr && (a.al_sb % 16) == 0 && ((uintptr_t)a.allowed % 16) == 0 &&
+                        (a.Lp % 16) == 0;
+      const uint8_t* alp = have ? a.allowed + (int64_t)b * a.al_sb : (const uint8_t*)a.q;
+#pragma unroll
+      for (int c = 0; c < ALC; ++c) {
+        const int i0 = 16 * (lane + 64 * c);
+        al_c[c] = *reinterpret_cast<const uint4*>(alp + (have && i0 + 16 <= a.Lp ? i0 : 0));
+      }
+      const bf16_t wl = (a.rms_w ? (const bf16_t*)a.rms_w : (const bf16_t*)a.q)[a.rms_w ? (tid & (DH - 1)) : 0];
+      w_raw = a.rms_w ? wl : (bf16_t)0x3f80;
+      const bool slow = a.allowed != nullptr && !have;
+#pragma unroll
+      for (int c = 0; c < ALC; ++c) {
+        const int i0 = 16 * (lane + 64 * c);
+        uint32_t wd[4] = {al_c[c].x, al_c[c].y, al_c[c].z, al_c[c].w};
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int i = i0 + 4 * q4 + e;
+            uint32_t byte = (wd[q4] >> (8 * e)) & 0xffu;
+            if (a.allowed == nullptr) byte = 1;
+            else if (slow) byte = i < a.Lp ? a.allowed[(int64_t)b * a.al_sb + i] : 0;
+            if (i >= a.Lp) byte = 0;
+            wd[q4] = (wd[q4] & ~(0xffu << (8 * e))) | ((byte ? 1u : 0u) << (8 * e));
+          }
+        }
+        al_c[c] = uint4{wd[0], wd[1], wd[2], wd[3]};
+        const bool all16 = ((wd[0] & wd[1] & wd[2] & wd[3]) == 0x01010101u);
+        const uint64_t m = __ballot(all16);
+        // 16-byte chunk k of this group is lane k: block e of the group is
+        // chunks 2e, 2e + 1
+#pragma unroll
+        for (int e = 0; e < 32; ++e)
+          allvis |= (uint64_t)(((m >> (2 * e)) & 3ull) == 3ull) << (32 * c + e);
+      }
+      if (wv == 0) {
+#pragma unroll
+        for (int c = 0; c < ALC; ++c) {
+          const int i0 = 16 * (lane + 64 * c);
+          if (i0 < a.Lp) *reinterpret_cast<uint4*>(al_lds + i0) = al_c[c];
+        }
+      }
+      if (tid < DH) w_lds[tid] = bf2f(w_raw);
+    }
+    // tiles 0 .. NS-2 behind everything else
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t)
+      if (t < ntile) tile_load(t * KT, t);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const int d0 = 16 * ks + 8 * hl;
+      uint32_t w[4] = {uq[ks].x, uq[ks].y, uq[ks].z, uq[ks].w};
+      if (rope && inter) {
+        // pairs (2p, 2p+1) rotated by angle d0/2 + p: one bf16 dot2 per
+        // output (fp32 products and sum, one rounding)
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const uint32_t r = rot_pair(w[pp], pp >> 1 ? rc2[ks].y : rc2[ks].x, pp >> 1 ? rs2[ks].y : rs2[ks].x, pp & 1);
+          w[pp] = rope_lane ? r : w[pp];
+        }
+      }
+      if (rope && !inter) {
+        // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin
+        float x[8], cc[8], ss[8], y[8];
+        unpack8(uq[ks], x);
+        unpack8(rc[ks], cc);
+        unpack8(rs[ks], ss);
+        unpack8(up[ks], y);
+        const bool lo = d0 < half;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float rt = lo ? -y[j] : y[j];
+          x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rt * ss[j]));
+        }
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) w[pp] = rope_lane ? pk_bf16(x[2 * pp], x[2 * pp + 1]) : w[pp];
+      }
+      if (!given) {
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          const uint32_t r = rot_pair(w[pp], pp >> 1 ? tcs[ks].y : tcs[ks].x, pp >> 1 ? tsn[ks].y : tsn[ks].x, pp & 1);
+          w[pp] = noise ? r : w[pp];
+        }
+      }
+      qf[ks] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
+    }
+  }
+
+  // V transposed-read cells (see attn_f2_bf16)
+  const int grp = lane >> 4, p16 = lane & 15;
+  const int vrow = 4 * (grp >> 1) + (p16 >> 2);
+  int v_off[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+    v_off[db] = vrow * Lay::ROWB + 16 * Lay::vchunk(vrow, 4 * db + 2 * (grp & 1) + ((p16 & 3) >> 1)) + 8 * (p16 & 1);
+  // key kt0 + 32 kb + kk(j) of register j; a block key is visible while
+  // kidx <= thr (causal / end), a prefix key when its byte is set
+  const int thr = min(Lk - 1, a.causal ? a.Lp + qrow + coff : Lk - 1);
+  auto kk = [](int j) { return 8 * (j >> 2) + (j & 3); };
+
+  float m_s = -INFINITY, l_s = 0.f;
+  f32x16 o[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
+
+  // per-entry masking a tile needs: 1 = the end / causal threshold only,
+  // 2 = also hidden prefix slots (visibility bytes), 0 = none
+  auto tile_mask_mode = [&](int kt0) {
+    const bool thr_m = kt0 + KT > Lk || (a.causal && kt0 + KT - 1 > a.Lp + q0 + coff);
+    bool al_m = false;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int pk0 = kt0 + 32 * kb;
+      al_m |= pk0 < a.Lp && !((allvis >> (pk0 >> 5)) & 1);
+    }
+    return al_m ? 2 : thr_m ? 1 : 0;
+  };
+  auto mask_entry = [&](float v, int kt0, int kb, int j, int mode) {
+    const int kidx = kt0 + 32 * kb + 4 * hl + kk(j);
+    if (mode == 1) return kidx <= thr ? v : -INFINITY;
+    const bool pre = kidx < a.Lp;
+    const bool vis = pre ? al_lds[pre ? kidx : 0] != 0 : kidx <= thr;
+    return vis ? v : -INFINITY;
+  };
+  // running-max update from a tile's masked scores (lanes l and l ^ 32
+  // share a row), with the lazy rescale of O and the row sum
+  auto fold_max = [&](float mx) {
+    const float tsc = xmax32(mx) * scale;
+    if (__ballot(tsc > m_s + 8.f)) {
+      const float mnew = fmaxf(m_s, tsc);
+      const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s - mnew);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+      l_s *= alpha;
+      m_s = mnew;
+    }
+  };
+
+  f32x16 st[2][2];  // S of two tiles: [parity][key block]
+  // ---- S(0), masked, max folded
+  if (ntile > 0) {
+    vm_wait(LPT * (min(ntile, NS - 1) - 1));
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    const uint32_t ka = lds_addr(f3_smem) + 16 * lane;
+    u32x4v_t kr[4];
+    auto k_issue = [&](auto f_c) {
+      constexpr int f = decltype(f_c)::value;
+      if constexpr (f < 2 * NKS) kr[f % 4] = lds_read_b128_at<((f % 2) * NKS + f / 2) * 1024>(ka);
+    };
+    k_issue(std::integral_constant<int, 0>{});
+    k_issue(std::integral_constant<int, 1>{});
+    k_issue(std::integral_constant<int, 2>{});
+    static_for<2 * NKS>([&](auto f_c) {
+      constexpr int f = decltype(f_c)::value, ks = f / 2, kb = f % 2;
+      k_issue(std::integral_constant<int, f + 3>{});
+      lds_wait_b128<(f + 3 < 2 * NKS) ? 3 : (2 * NKS - 1 - f)>(kr[f % 4]);
+      st[0][kb] = mfma_32x32x16(__builtin_bit_cast(bf16x8_t, kr[f % 4]), qf[ks], ks == 0 ? f32x16{} : st[0][kb]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    const int mode0 = tile_mask_mode(0);
+    if (mode0) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) st[0][kb][j] = mask_entry(st[0][kb][j], 0, kb, j, mode0);
+    }
+    float mx = st[0][0][0];
+#pragma unroll
+    for (int j = 1; j < 16; ++j) mx = fmaxf(mx, st[0][0][j]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[0][1][j]);
+    fold_max(mx);
+  }
+
+  // one pipelined iteration; PAR = it % 2 selects the S registers
+  auto iteration = [&](auto par_c, int it) {
+    constexpr int PAR = decltype(par_c)::value, NXT = 1 - PAR;
+    const bool has_next = it + 1 < ntile;
+    const int kt0 = it * KT, kt1 = kt0 + KT;
+    // tile it + 1 has landed and every wave has finished iteration it - 1
+    // (so tile it - 1's buffer may take tile it + 2)
+    if (has_next) {
+      vm_wait(it + 2 < ntile ? LPT : 0);
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      __builtin_amdgcn_s_barrier();
+      if (it + 3 < ntile) tile_load(kt1 + 2 * KT, (it + 3) % NS);
+    }
+    const float mu = m_s == -INFINITY ? 0.f : m_s;
+    uint32_t pw[16];  // P(it) as bf16 pairs: word e / 2 holds entries e, e + 1 (e = 16 kb + j)
+    float ls = 0.f;
+    auto p_pair = [&](int e) {
+      const int kb = e >> 4, j = e & 15;
+      const float p0 = fast_exp2(fmaf(st[PAR][kb][j], scale, -mu));
+      const float p1 = fast_exp2(fmaf(st[PAR][kb][j + 1], scale, -mu));
+      ls += p0 + p1;
+      pw[e >> 1] = pk_bf16(p0, p1);
+    };
+    // ---- phase A: S(it + 1) products, each with one pair of P(it)
+    if (has_next) {
+      const uint32_t ka = lds_addr(f3_smem + ((it + 1) % NS) * STAGE) + 16 * lane;
+      u32x4v_t kr[4];
+      auto k_issue = [&](auto f_c) {
+        constexpr int f = decltype(f_c)::value;
+        if constexpr (f < 2 * NKS) kr[f % 4] = lds_read_b128_at<((f % 2) * NKS + f / 2) * 1024>(ka);
+      };
+      k_issue(std::integral_constant<int, 0>{});
+      k_issue(std::integral_constant<int, 1>{});
+      k_issue(std::integral_constant<int, 2>{});
+      static_for<2 * NKS>([&](auto f_c) {
+        constexpr int f = decltype(f_c)::value, ks = f / 2, kb = f % 2;
+        k_issue(std::integral_constant<int, f + 3>{});
+        lds_wait_b128<(f + 3 < 2 * NKS) ? 3 : (2 * NKS - 1 - f)>(kr[f % 4]);
+        st[NXT][kb] = mfma_32x32x16(__builtin_bit_cast(bf16x8_t, kr[f % 4]), qf[ks], ks == 0 ? f32x16{} : st[NXT][kb]);
+        if constexpr (2 * f < 32) p_pair(2 * f);
+        if constexpr (2 * NKS == 8 && 2 * f + 16 < 32) p_pair(2 * f + 16);  // head_dim 64: two pairs a product
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    } else {
+#pragma unroll
+      for (int e = 0; e < 32; e += 2) p_pair(e);
+    }
+    l_s += ls;
+    // ---- S(it + 1)'s mask, where the tile needs one (rare: the tile on the
+    // causal diagonal, the end, hidden prefix slots)
+    if (has_next) {
+      const int mode = tile_mask_mode(kt1);
+      if (mode) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) st[NXT][kb][j] = mask_entry(st[NXT][kb][j], kt1, kb, j, mode);
+      }
+    }
+    // ---- phase C: O += V(it)^T P(it), each product with the running max
+    // of two entries of S(it + 1) (four at head_dim 64; a stale S when
+    // there is no next tile, whose max is then dropped)
+    float mx = -INFINITY;
+    {
+      const uint32_t va = lds_addr(f3_smem + (it % NS) * STAGE + Lay::KBYTES);
+      constexpr int NPV = 4 * NDB;
+      uint2 rd[3][2];
+      auto v_issue = [&](auto q_c) {
+        constexpr int q = decltype(q_c)::value;
+        if constexpr (q < NPV) {
+          constexpr int p = q / NDB, db = q % NDB;
+          constexpr int ROW0 = 16 * p * Lay::ROWB, ROW8 = ROW0 + 8 * Lay::ROWB;
+          rd[q % 3][0] = lds_read_tr16_at<ROW0>(va + v_off[db]);
+          rd[q % 3][1] = lds_read_tr16_at<ROW8>(va + v_off[db]);
+        }
+      };
+      v_issue(std::integral_constant<int, 0>{});
+      v_issue(std::integral_constant<int, 1>{});
+      static_for<NPV>([&](auto q_c) {
+        constexpr int q = decltype(q_c)::value;
+        constexpr int p = q / NDB, db = q % NDB, b3 = q % 3;
+        lds_wait2_n<(q + 1 < NPV) ? 2 : 0>(rd[b3][0], rd[b3][1]);
+        const bf16x8_t va8 = __builtin_bit_cast(bf16x8_t, uint4{rd[b3][0].x, rd[b3][0].y, rd[b3][1].x, rd[b3][1].y});
+        const uint4 pf = uint4{pw[4 * p], pw[4 * p + 1], pw[4 * p + 2], pw[4 * p + 3]};
+        o[db] = mfma_32x32x16(va8, __builtin_bit_cast(bf16x8_t, pf), o[db]);
+        constexpr int PER = 32 / NPV;
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+          constexpr int e0 = PER * q;
+          mx = fmaxf(mx, st[NXT][(e0 + u) >> 4][(e0 + u) & 15]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        v_issue(std::integral_constant<int, q + 2>{});
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    }
+    if (has_next) fold_max(mx);
+  };
+  for (int it = 0; it < ntile; it += 2) {
+    iteration(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntile) iteration(std::integral_constant<int, 1>{}, it + 1);
+  }
+
+  // ---- epilogue (see attn_f2_bf16)
+  const float l_tot = xsum32(l_s);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float lam = bf2f(lam_raw);
+  float y[NDB][16];
+  float sq = 0.f;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db)
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      const uint32_t mine = pk_bf16(o[db][j] * inv, o[db][j + 1] * inv);
+      const auto r = __builtin_amdgcn_permlane16_swap(mine, mine, false, false);
+      const uint32_t nz = (uint32_t)r[1];
+      const float on0 = bf2f((bf16_t)(nz & 0xffffu)), on1 = bf2f((bf16_t)(nz >> 16));
+      y[db][j] = fmaf(-lam, on0, o[db][j] * inv);
+      y[db][j + 1] = fmaf(-lam, on1, o[db][j + 1] * inv);
+      sq = fmaf(y[db][j], y[db][j], sq);
+      sq = fmaf(y[db][j + 1], y[db][j + 1], sq);
+    }
+  if (a.rms_w) {
+    sq = xsum32(sq);
+    const float rr = 1.0f / sqrtf(sq / (float)DH + a.eps);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const float4 wv4 = *reinterpret_cast<const float4*>(w_lds + 32 * db + 8 * jq + 4 * hl);
+        y[db][4 * jq + 0] *= rr * wv4.x;
+        y[db][4 * jq + 1] *= rr * wv4.y;
+        y[db][4 * jq + 2] *= rr * wv4.z;
+        y[db][4 * jq + 3] *= rr * wv4.w;
+      }
+  }
+  if (strm == 0 && qrow < a.Lq) {
+    bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        uint2 u;
+        u.x = pk_bf16(y[db][4 * jq + 0], y[db][4 * jq + 1]);
+        u.y = pk_bf16(y[db][4 * jq + 2], y[db][4 * jq + 3]);
+        *reinterpret_cast<uint2*>(orow_p + 32 * db + 8 * jq + 4 * hl) = u;
+      }
+  }
+}
+
 // ------------------------------------------------------------ host side
 static int rows_nsplit(const coda_attn_desc* d) {
   const int Lk = d->Lp + d->Lb;
@@ -2260,6 +3200,78 @@ static int launch_fa(const coda_attn_desc* d, hipStream_t st, int G) {
   }
 }
 
+// the LDS size attribute of a kernel instance, set once per process
+template <typename K>
+static int set_lds_once(K kern, size_t lds, std::atomic<bool>& done, const char* who) {
+  if (done.load(std::memory_order_acquire)) return CODA_OK;
+  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return fail(CODA_EHIP, "%s: LDS attribute: %s", who, hipGetErrorString(e));
+  done.store(true, std::memory_order_release);
+  return CODA_OK;
+}
+
+// 32-row flash tiles: waves = G heads x NQ groups of 16 queries (both
+// streams in each wave)
+template <int DH, int NW>
+static int launch_f2_nw(const coda_attn_desc* d, hipStream_t st, int G) {
+  static std::atomic<bool> lds_set{false};
+  const int npairs = d->B * d->Hkv;
+  const int NQ = NW / G;
+  const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
+  const size_t lds = F2Layout<DH>::LDS;
+  int rc = set_lds_once(attn_f2_bf16<DH, NW>, lds, lds_set, "coda_diff_attn_fwd");
+  if (rc) return rc;
+  hipLaunchKernelGGL((attn_f2_bf16<DH, NW>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk, npairs);
+  return check_launch("attn_f2_bf16");
+}
+// pipelined 32-row flash tiles: 8 waves, G heads x 8 / G groups of 16
+// queries; QM the query case (see attn_f3_bf16)
+template <int DH, int QM>
+static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G) {
+  constexpr int NW = 8;
+  static std::atomic<bool> lds_set{false};
+  const int npairs = d->B * d->Hkv;
+  const int NQ = NW / G;
+  const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
+  const size_t lds = 4 * (size_t)(F2Layout<DH>::KBYTES + F2Layout<DH>::VBYTES);
+  int rc = set_lds_once(attn_f3_bf16<DH, NW, QM>, lds, lds_set, "coda_diff_attn_fwd");
+  if (rc) return rc;
+  hipLaunchKernelGGL((attn_f3_bf16<DH, NW, QM>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk,
+                     npairs);
+  return check_launch("attn_f3_bf16");
+}
+template <int DH>
+static int launch_f3(const coda_attn_desc* d, hipStream_t st, int G) {
+  if (!d->q_noise && d->rope_cos) return d->rope_interleaved ? launch_f3_qm<DH, 0>(d, st, G)
+                                                             : launch_f3_qm<DH, 1>(d, st, G);
+  if (d->q_noise && !d->rope_cos) return launch_f3_qm<DH, 2>(d, st, G);
+  return launch_f3_qm<DH, 3>(d, st, G);
+}
+// CODA_PREFILL_KERNEL selects the prefill attention kernel for launch-shape
+// tuning: fa16 (16-row flash tiles), f2 / f2q2 (32-row tiles, one / two
+// query groups per head); the default is the pipelined 32-row kernel
+static int prefill_kernel_choice() {
+  static const int choice = [] {
+    const char* e = getenv("CODA_PREFILL_KERNEL");
+    if (e && !strcmp(e, "fa16")) return 1;
+    if (e && !strcmp(e, "f2q2")) return 2;
+    if (e && !strcmp(e, "f2")) return 3;
+    return 0;
+  }();
+  return choice;
+}
+template <int DH>
+static int launch_f2(const coda_attn_desc* d, hipStream_t st, int G) {
+  if (prefill_kernel_choice() == 0) return launch_f3<DH>(d, st, G);
+  const bool q2 = prefill_kernel_choice() == 2;
+  switch (G) {
+    case 8: return launch_f2_nw<DH, 8>(d, st, G);
+    case 4: return q2 ? launch_f2_nw<DH, 8>(d, st, G) : launch_f2_nw<DH, 4>(d, st, G);
+    case 2: return q2 ? launch_f2_nw<DH, 8>(d, st, G) : launch_f2_nw<DH, 4>(d, st, G);
+    default: return launch_f2_nw<DH, 4>(d, st, G);
+  }
+}
+
 template <int DH>
 static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
   const int G = d->H / d->Hkv;
@@ -2286,7 +3298,12 @@ static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
                        (const float*)d->workspace);
     return check_launch("attn_rows_merge");
   }
-  if (DH >= 64 && (G == 8 || G == 4 || G == 2 || G == 1) && fa_offsets_fit(d)) return launch_fa<DH>(d, st, G);
+  if (DH >= 64 && (G == 8 || G == 4 || G == 2 || G == 1) && fa_offsets_fit(d)) {
+    if constexpr (DH >= 64) {
+      if (prefill_kernel_choice() != 1) return launch_f2<DH>(d, st, G);
+    }
+    return launch_fa<DH>(d, st, G);
+  }
   const int NQ = G >= 4 ? 1 : 4 / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
   if (G == 8) {
