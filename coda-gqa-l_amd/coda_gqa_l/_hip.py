@@ -86,6 +86,7 @@ _SIGS = {
     "coda_block_write": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,
                                 _i32, _i64, _vp, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp]),
     "coda_block_workspace_bytes": (_i32, [ctypes.POINTER(BankDesc), _i32, ctypes.POINTER(ctypes.c_size_t)]),
+    "coda_block_sync_timeouts": (_i32, [ctypes.POINTER(ctypes.c_uint)]),
     "coda_block_write_noalloc": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,
                                         _i32, _i64, _vp, _i32, _i32, _i32, _vp]),
     "coda_block_write_noalloc_max_bytes": (ctypes.c_size_t, []),

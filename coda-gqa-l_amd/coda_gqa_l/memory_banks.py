@@ -3,7 +3,8 @@
 The reference implements bank maintenance as ~100 eager torch ops per
 prefill chunk and ~40 per decode token with several host syncs each
 (src/coda_gqa_l/memory_banks.py:183-950).  Here a decode token is one
-kernel (coda_decode_write) and a prefill chunk is three (coda_block_write);
+kernel (coda_decode_write) and a prefill chunk is one (coda_block_write;
+four where a chunk's working set does not fit one CU's LDS);
 the candidate choice of every chunk of a prefill call is planned up front
 by one kernel (coda_block_plan), since the evicted gates depend only on the
 token stream.  Within a prefill call the ring stays circular (head =

@@ -3182,9 +3182,8 @@ static int launch_fa_nw(const coda_attn_desc* d, hipStream_t st, int G) {
   const int NQ = NW / (2 * G);  // waves = 2 streams x G heads x NQ
   const int nblk = (d->Lq + 16 * QG * NQ - 1) / (16 * QG * NQ);
   const size_t lds = FaLayout<DH, NS>::LDS;
-  hipError_t e = hipFuncSetAttribute((const void*)attn_fa_bf16<DH, NW, NS, QG>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return fail(CODA_EHIP, "coda_diff_attn_fwd: LDS attribute: %s", hipGetErrorString(e));
+  const int rc = lds_limit<attn_fa_bf16<DH, NW, NS, QG>>(lds, "coda_diff_attn_fwd");
+  if (rc) return rc;
   hipLaunchKernelGGL((attn_fa_bf16<DH, NW, NS, QG>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk,
                      npairs);
   return check_launch("attn_fa_bf16");
@@ -3200,26 +3199,15 @@ static int launch_fa(const coda_attn_desc* d, hipStream_t st, int G) {
   }
 }
 
-// the LDS size attribute of a kernel instance, set once per process
-template <typename K>
-static int set_lds_once(K kern, size_t lds, std::atomic<bool>& done, const char* who) {
-  if (done.load(std::memory_order_acquire)) return CODA_OK;
-  hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (e != hipSuccess) return fail(CODA_EHIP, "%s: LDS attribute: %s", who, hipGetErrorString(e));
-  done.store(true, std::memory_order_release);
-  return CODA_OK;
-}
-
 // 32-row flash tiles: waves = G heads x NQ groups of 16 queries (both
 // streams in each wave)
 template <int DH, int NW>
 static int launch_f2_nw(const coda_attn_desc* d, hipStream_t st, int G) {
-  static std::atomic<bool> lds_set{false};
   const int npairs = d->B * d->Hkv;
   const int NQ = NW / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
   const size_t lds = F2Layout<DH>::LDS;
-  int rc = set_lds_once(attn_f2_bf16<DH, NW>, lds, lds_set, "coda_diff_attn_fwd");
+  int rc = lds_limit<attn_f2_bf16<DH, NW>>(lds, "coda_diff_attn_fwd");
   if (rc) return rc;
   hipLaunchKernelGGL((attn_f2_bf16<DH, NW>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk, npairs);
   return check_launch("attn_f2_bf16");
@@ -3229,12 +3217,11 @@ static int launch_f2_nw(const coda_attn_desc* d, hipStream_t st, int G) {
 template <int DH, int QM>
 static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G) {
   constexpr int NW = 8;
-  static std::atomic<bool> lds_set{false};
   const int npairs = d->B * d->Hkv;
   const int NQ = NW / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
   const size_t lds = 4 * (size_t)(F2Layout<DH>::KBYTES + F2Layout<DH>::VBYTES);
-  int rc = set_lds_once(attn_f3_bf16<DH, NW, QM>, lds, lds_set, "coda_diff_attn_fwd");
+  int rc = lds_limit<attn_f3_bf16<DH, NW, QM>>(lds, "coda_diff_attn_fwd");
   if (rc) return rc;
   hipLaunchKernelGGL((attn_f3_bf16<DH, NW, QM>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk,
                      npairs);
@@ -3375,12 +3362,9 @@ static int launch_fused_step(const coda_bank_desc* s, const coda_attn_desc* a, c
   size_t lds = sizeof(float) * (size_t)dstep_words(s->Hkv, s->Me, s->Ms) + 2 * 2 * (size_t)DH + 4 * sizeof(float) * DH;
   const size_t red = (size_t)4 * R * (DH + 4) * sizeof(float);
   lds = lds > red ? lds : red;
-  if (lds > 64 * 1024) {
-    if (lds > 120 * 1024) return fail(CODA_EUNSUP, "coda_decode_step: bank of %d + %d rows too large", s->Me, s->Ms);
-    hipError_t e = hipFuncSetAttribute((const void*)decode_step_bf16<DH>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return fail(CODA_EHIP, "coda_decode_step: LDS attribute: %s", hipGetErrorString(e));
-  }
+  if (lds > 120 * 1024) return fail(CODA_EUNSUP, "coda_decode_step: bank of %d + %d rows too large", s->Me, s->Ms);
+  const int rc = lds_limit<decode_step_bf16<DH>>(lds, "coda_decode_step");
+  if (rc) return rc;
   hipLaunchKernelGGL((decode_step_bf16<DH>), dim3(s->Hkv, s->B), dim3(256), lds, st, *a, *s, (const bf16_t*)k_new,
                      (const bf16_t*)v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out);
   return check_launch("decode_step_bf16");

@@ -18,6 +18,8 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <mutex>
 #include <vector>
 
@@ -319,24 +321,29 @@ __global__ __launch_bounds__(64) void block_plan_kernel(const float* __restrict_
 }
 
 // ------------------------------------------------------------ block write
-// Three kernels per chunk:
-//   route  grid (Hkv + 1, B): blocks h < Hkv normalise head h of the
-//          candidate rows and take their cosine dots with the head's norm
-//          caches (staged in LDS); block Hkv snapshots the pre-update bank
-//          metadata of sequence b (used bits, LRU stamps, candidate gates)
-//          and computes the LRU victim order.
-//   decide grid (1 + ceil(Ts / 16), B): block 0 takes the exact decisions of
-//          sequence b (and commits its LRU stamps), the others route 16
-//          summary candidates each (head-mean scores, first-occurrence
-//          argmax, token weights).
-//   apply  grid (Hkv, B): every head block applies the decisions to its own
-//          head's rows (exact delta write-back, summary accumulate + EMA,
-//          norm caches) and writes its head of the ring; block h == 0 also
-//          writes the per-sequence metadata.
+// A chunk is one launch of block_fused_kernel (below) when its working set
+// fits in LDS; otherwise four launches:
+//   route  grid (Hkv + 1, B, nz): workgroups h < Hkv normalise a share of
+//          head h's candidate rows and take their cosine dots with the
+//          head's norm caches (staged in LDS); workgroup Hkv snapshots the
+//          pre-update bank metadata of sequence b (used bits, LRU stamps,
+//          candidate gates) and computes the LRU victim order.
+//   decide grid (1 + ceil(Ts / kDecideChunk), B): workgroup 0 takes the
+//          exact decisions of sequence b (and commits its LRU stamps), the
+//          others route kDecideChunk summary candidates each (head-mean
+//          scores, first-occurrence argmax, token weights).
+//   apply  grid (Hkv, B, nz): workgroup (h, b, z) applies the decisions to
+//          its share of head h's slots (exact delta write-back, summary
+//          accumulate + EMA, norm caches); (0, b, 0) also writes the
+//          per-sequence metadata.
+//   ring   grid (Hkv, B, nzr): the chunk's surviving tokens into the ring,
+//          after the bank writes have read the evicted ring rows.
 // Workspace (4-byte words), TT = max(Te, Ts):
 //   dot_e [B][Hkv][Te][Me] f32, dot_s [B][Hkv][Ts][Ms] f32,
 //   snap  [B][SNAP]: used (Me+Ms) i32 | last (Me) i64 | gate (TT) f32 | lru (Me) i32,
-//   dec   [B][DEC]: decisions (block_decide_kernel)
+//   dec   [B][DEC]: decisions (block_decide_kernel; the fused kernel's
+//         per-token routing),
+//   sync  [B][64] u64: the fused kernel's sync flags.
 struct BlockGeom {
   int blk, ring_head, ring_filled, n_ev, Kmax, Te, Ts;
   int64_t pos0;
@@ -354,9 +361,13 @@ __host__ __device__ __forceinline__ size_t ws_snap(int B, int Hkv, int Me, int M
   return (ws_dot_s(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * Hkv * Ts * Ms + 1) & ~(size_t)1;  // 8-byte aligned
 }
 __host__ __device__ __forceinline__ int dec_words(int Me, int Te, int Ts);
+// sync flags of the fused kernel: 64 64-bit words per sequence, 8-byte aligned
+__host__ __device__ __forceinline__ size_t ws_sync(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
+  return (ws_snap(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * snap_words(Me, Ms, Te > Ts ? Te : Ts) +
+          (size_t)B * dec_words(Me, Te, Ts) + 1) & ~(size_t)1;
+}
 __host__ __device__ __forceinline__ size_t ws_total(int B, int Hkv, int Me, int Ms, int Te, int Ts) {
-  return ws_snap(B, Hkv, Me, Ms, Te, Ts) + (size_t)B * snap_words(Me, Ms, Te > Ts ? Te : Ts) +
-         (size_t)B * dec_words(Me, Te, Ts) + 2;
+  return ws_sync(B, Hkv, Me, Ms, Te, Ts) + 128 * (size_t)B + 2;
 }
 #define CODA_WS(fn, s, g) fn((s).B, (s).Hkv, (s).Me, (s).Ms, (g).Te, (g).Ts)
 
@@ -414,7 +425,7 @@ __device__ __forceinline__ float cand_gate(const coda_bank_desc& s, const BlockG
 // multiply-adds in the CPU matmul order (dot_pair: channel pairs in
 // increasing order, odd channel first); result rounded to the element type
 // (the matmul output dtype).
-template <typename T, int RB, int CB>
+template <typename T, int RB, int CB, bool SC = false>
 __device__ __forceinline__ void lds_dots_blk(const float* rows, int n_rows, const float* cands, int n_c, int len,
                                              int stride, float* out /* [n_c][n_rows] */) {
   const int nbr = (n_rows + RB - 1) / RB, nbc = (n_c + CB - 1) / CB;
@@ -444,19 +455,25 @@ __device__ __forceinline__ void lds_dots_blk(const float* rows, int n_rows, cons
     for (int i = 0; i < RB; ++i)
 #pragma unroll
       for (int j = 0; j < CB; ++j)
-        if (r0 + i < n_rows && c0 + j < n_c) out[(c0 + j) * n_rows + r0 + i] = Elt<T>::rnd(acc[i][j]);
+        if (r0 + i < n_rows && c0 + j < n_c) {
+          if constexpr (SC)  // coherent at agent scope: read by workgroups on other XCDs in this launch
+            __hip_atomic_store(out + (c0 + j) * n_rows + r0 + i, Elt<T>::rnd(acc[i][j]), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+          else
+            out[(c0 + j) * n_rows + r0 + i] = Elt<T>::rnd(acc[i][j]);
+        }
   }
 }
 // out[c][r] = rnd(dot(cands[c], rows[r])), each an fma chain over the
 // channel pairs in order (the same value whatever the blocking); blocks of
 // 4 x 4 dots per thread when there are enough of them, else 2 x 1
-template <typename T>
+template <typename T, bool SC = false>
 __device__ __forceinline__ void lds_dots(const float* rows, int n_rows, const float* cands, int n_c, int len,
                                          int stride, float* out /* [n_c][n_rows] */) {
   if (((n_rows + 3) / 4) * ((n_c + 3) / 4) >= (int)blockDim.x)
-    lds_dots_blk<T, 4, 4>(rows, n_rows, cands, n_c, len, stride, out);
+    lds_dots_blk<T, 4, 4, SC>(rows, n_rows, cands, n_c, len, stride, out);
   else
-    lds_dots_blk<T, 2, 1>(rows, n_rows, cands, n_c, len, stride, out);
+    lds_dots_blk<T, 2, 1, SC>(rows, n_rows, cands, n_c, len, stride, out);
 }
 
 // Stage `n` rows of `len` elements (row stride `rs` elements) into LDS fp32
@@ -1207,6 +1224,614 @@ __global__ __launch_bounds__(kApplyThreads) void block_ring_kernel(const coda_ba
   }
 }
 
+// ------------------------------------------------------------ fused block write
+// The chunk's whole bank update in one launch when its working set fits in
+// LDS: NZ workgroups per (sequence b, head h), with the routing rows, bank
+// slots and ring pieces of head h split over them.  Workgroup (h, z, b):
+//   1. stages the raw K and V rows of the chunk's candidates for head h
+//      (the plan's first max(Te, Ts) tokens: the exact candidates are the
+//      first Te, the summary candidates the first Ts), its own bank slots,
+//      the norm caches its routing rows need, and the sequence's bank
+//      metadata (used bits, LRU stamps, candidate gates, LRU victim order);
+//   2. normalises its share of the routing rows (exact candidates z, z +
+//      NZ, ... as V rows, summary candidates z, z + NZ, ... as LF-K
+//      bands) and forms their dots with head h's norm caches (the CPU
+//      matmul order) into the workspace;
+//   -- sync 1 of the Hkv * NZ workgroups of b (meanwhile: the LRU order) --
+//   3. routes the tokens it is assigned (token i of [Te | Ts] goes to
+//      workgroup i mod (Hkv * NZ)): head-mean of the dots, first-occurrence
+//      argmax, published to the workspace;
+//   -- sync 2 (meanwhile: its share of head h's ring) --
+//   4. reads every token's routing, takes the exact decisions (the same
+//      serial walk, from the same values, in every workgroup) and applies
+//      them and the summary routing to its own slots of head h (exact delta
+//      write-back, summary accumulate + EMA, norm caches).
+// Workgroup (0, 0, b) (the lead) commits what the sequence shares: LRU stamps,
+// visibility bytes, ring gates, counters and the decision trace, after
+// sync 1 (every workgroup has read them by then).
+// Sync: every workgroup of b stores (2 epoch + k) at sync k in its own
+// 64-bit flag word of the workspace and waits until all flags of b reach
+// it; the epoch is unique per launch, so no word needs clearing.  What
+// crosses a sync (dots, routing) is written and read with agent-scope
+// atomic accesses (coherent across the XCDs' L2s, no cache write-back or
+// invalidation), and a workgroup's flag is stored only after all its
+// waves' such stores have completed.  A workgroup waits on workgroups of b
+// only; they lie in one contiguous range of launch order (with whole other
+// sequences at most, at most 64 workgroups), dispatched after every earlier
+// range: one that waits never holds back one it waits for.  Waits are
+// bounded (kSyncSpinLimit sleeps, about 0.1 s); a workgroup that gives up
+// counts itself in g_block_sync_timeouts.
+static constexpr int kFusedThreads = 512;
+static constexpr int kFusedMaxGroup = 64;  // Hkv * NZ: one wave polls every flag of a sequence
+static constexpr int kSyncSpinLimit = 1 << 20;
+static __device__ unsigned int g_block_sync_timeouts;
+
+// Sync of the K workgroups of one sequence (see above).  While wave 0
+// polls, waves 1 .. hold `busy`: work that needs nothing from the other
+// workgroups (it sees thread ids from 0 and a stride of blockDim - 64).
+template <typename F>
+__device__ __forceinline__ void group_sync(unsigned long long* flags, int K, int me, unsigned long long val,
+                                           unsigned long long alt, F&& busy) {
+  // this wave's coherent stores complete, then the workgroup's
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(flags + me, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    for (int n = 0;; ++n) {
+      bool ok = true;
+      if (lane < K) {
+        const unsigned long long v = __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = v == val || v == alt;
+      }
+      if (__all(ok)) break;
+      if (n >= kSyncSpinLimit) {
+        if (lane == 0) atomicAdd(&g_block_sync_timeouts, 1u);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  } else {
+    busy((int)threadIdx.x - 64, (int)blockDim.x - 64);
+  }
+  __syncthreads();
+}
+
+struct FusedLds {
+  int raw_k, raw_v, own_ek, own_ev, own_sv, own_sk, gate, used, last, rk, lru, pc, idx_e, fl_e, bv_e, bi_e, idx_s,
+      wtok, eflag, smask, scnt, sflag, knew, ov, total;
+};
+__host__ __device__ __forceinline__ int al16(int x) { return (x + 15) & ~15; }
+__host__ __device__ __forceinline__ FusedLds fused_lds(int DH, int esz, int Me, int Ms, int Te, int Ts, int NZ) {
+  const int TT = Te > Ts ? Te : Ts, LF = DH / 2;
+  const int PE = (Me + NZ - 1) / NZ, PS = (Ms + NZ - 1) / NZ;
+  const int ne = (Te + NZ - 1) / NZ, ns = (Ts + NZ - 1) / NZ;
+  FusedLds L;
+  int o = 0;
+  L.raw_k = o; o += al16(TT * DH * esz);
+  L.raw_v = o; o += al16(TT * DH * esz);
+  L.own_ek = o; o += al16(PE * DH * esz);
+  L.own_ev = o; o += al16(PE * DH * esz);
+  L.own_sv = o; o += al16(PS * DH * esz);
+  L.own_sk = o; o += al16(PS * LF * esz);
+  L.gate = o; o += al16(4 * TT);
+  L.used = o; o += al16(4 * (Me + Ms));
+  L.last = o; o += al16(8 * Me);
+  L.rk = o; o += al16(16 * Me);
+  L.lru = o; o += al16(4 * Me);
+  L.pc = o; o += al16(4 * TT);
+  L.idx_e = o; o += al16(4 * Te);
+  L.fl_e = o; o += al16(4 * Te);
+  L.bv_e = o; o += al16(4 * Te);
+  L.bi_e = o; o += al16(4 * Te);
+  L.idx_s = o; o += al16(4 * Ts);
+  L.wtok = o; o += al16(4 * Ts);
+  L.eflag = o; o += al16(4 * Me);
+  L.smask = o; o += al16(8 * Ms);
+  L.scnt = o; o += al16(4 * Ms);
+  L.sflag = o; o += al16(4 * Ms);
+  L.knew = o; o += al16(4 * PS * LF);
+  L.ov = o;
+  // routing rows: head h's norm caches and this workgroup's normalised rows
+  L.total = o + al16(4 * ((Me + ne) * (DH + 4) + (Ms + ns) * (LF + 4)));
+  return L;
+}
+
+template <typename T, int DH>
+__global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_bank_desc s, BlockGeom g, int NZ,
+                                                                    const T* kbk, const T* vbk, const float* gb,
+                                                                    const int32_t* __restrict__ plan_c, float* ws,
+                                                                    unsigned long long* flags_all,
+                                                                    unsigned long long epoch) {
+  using E = Elt<T>;
+  constexpr int NV = (DH + 63) / 64, LF = DH / 2, NCOL = DH + LF, CH = DH / 8;
+  extern __shared__ __attribute__((aligned(16))) char fsm[];
+  __shared__ int ties, any_used_s;
+  // workgroup -> (sequence, head, z): workgroups are dealt round robin to
+  // the 8 XCDs, so the NZ workgroups of one (sequence, head) pair take
+  // consecutive turns of one XCD (they share its L2); the workgroups of a
+  // sequence still fill one contiguous range of launch order
+  const int xcd = blockIdx.x & 7, turn = blockIdx.x >> 3;
+  const int pair = (turn / NZ) * 8 + xcd, z = turn % NZ;
+  const int b = pair / s.Hkv, h = pair % s.Hkv;
+  if (b >= s.B) return;
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6, NT = blockDim.x, NW = NT >> 6;
+  const int W = s.W, Me = s.Me, Ms = s.Ms, Hkv = s.Hkv, Te = g.Te, Ts = g.Ts;
+  const int TT = max(Te, Ts), Lbuf = W + Me + Ms, K = Hkv * NZ, me = h * NZ + z;
+  const bool lead = me == 0;
+  const int Ae = s.active_exact, n_lru = min(Te, Ae);
+  const FusedLds L = fused_lds(DH, (int)sizeof(T), Me, Ms, Te, Ts, NZ);
+  T* raw_k = reinterpret_cast<T*>(fsm + L.raw_k);    // [TT][DH] candidate K rows of head h
+  T* raw_v = reinterpret_cast<T*>(fsm + L.raw_v);    // [TT][DH] candidate V rows
+  T* own_ek = reinterpret_cast<T*>(fsm + L.own_ek);  // [PE][DH] own exact slots: K
+  T* own_ev = reinterpret_cast<T*>(fsm + L.own_ev);  // V
+  T* own_sv = reinterpret_cast<T*>(fsm + L.own_sv);  // [PS][DH] own summary slots: V
+  T* own_sk = reinterpret_cast<T*>(fsm + L.own_sk);  // [PS][LF] K channels [DH/2, DH)
+  float* gate = reinterpret_cast<float*>(fsm + L.gate);
+  int32_t* used = reinterpret_cast<int32_t*>(fsm + L.used);
+  int64_t* last = reinterpret_cast<int64_t*>(fsm + L.last);
+  sel::Item<int64_t>* rk = reinterpret_cast<sel::Item<int64_t>*>(fsm + L.rk);
+  int32_t* lru = reinterpret_cast<int32_t*>(fsm + L.lru);
+  int32_t* pcl = reinterpret_cast<int32_t*>(fsm + L.pc);
+  int32_t* idx_e = reinterpret_cast<int32_t*>(fsm + L.idx_e);
+  int32_t* fl_e = reinterpret_cast<int32_t*>(fsm + L.fl_e);
+  float* bv_e = reinterpret_cast<float*>(fsm + L.bv_e);
+  int32_t* bi_e = reinterpret_cast<int32_t*>(fsm + L.bi_e);
+  int32_t* idx_s = reinterpret_cast<int32_t*>(fsm + L.idx_s);
+  float* wtok = reinterpret_cast<float*>(fsm + L.wtok);
+  int32_t* eflag = reinterpret_cast<int32_t*>(fsm + L.eflag);
+  uint64_t* smask = reinterpret_cast<uint64_t*>(fsm + L.smask);
+  float* scnt = reinterpret_cast<float*>(fsm + L.scnt);
+  int32_t* sflag = reinterpret_cast<int32_t*>(fsm + L.sflag);
+  float* knew = reinterpret_cast<float*>(fsm + L.knew);  // [PS][LF]
+  const int le = DH + 4, lsum = LF + 4;
+  // this workgroup's routing rows: exact candidates e = z, z + NZ, ... and
+  // summary candidates z, z + NZ, ... (every workgroup forms both kinds)
+  const int ne = z < Te ? (Te - z + NZ - 1) / NZ : 0, ns = z < Ts ? (Ts - z + NZ - 1) / NZ : 0;
+  float* nrm_e = reinterpret_cast<float*>(fsm + L.ov);  // [Me][le]
+  float* cnd_e = nrm_e + (ne > 0 ? Me * le : 0);          // [ne][le]
+  float* nrm_s = cnd_e + ne * le;                         // [Ms][lsum]
+  float* cnd_s = nrm_s + (ns > 0 ? Ms * lsum : 0);        // [ns][lsum]
+  // this workgroup's bank slots of head h
+  const int PE = (Me + NZ - 1) / NZ, e0 = min(Me, z * PE), e1 = min(Me, e0 + PE);
+  const int PS = (Ms + NZ - 1) / NZ, s0 = min(Ms, z * PS), s1 = min(Ms, s0 + PS);
+  T* kb = (T*)s.k_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
+  T* vb = (T*)s.v_buf + ((int64_t)b * Hkv + h) * Lbuf * DH;
+  uint8_t* al = s.allowed + (int64_t)b * Lbuf;
+  const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
+  unsigned long long* flags = flags_all + (int64_t)b * K;
+  const Dec dx = dec_of(s, g, ws, b);  // exchange: idx_s [Ts], best value / slot of the exact tokens
+  const int Lr = g.ring_filled, first = max(Lr, g.n_ev), rhead = (Lr == W) ? g.ring_head : 0;
+
+  // ---- 1. staging: plan, metadata, own slots, norm caches
+  for (int i = t; i < TT; i += NT) pcl[i] = pc[i];
+  for (int m = t; m < Me + Ms; m += NT) used[m] = al[W + m];
+  for (int m = t; m < Me; m += NT) last[m] = s.mem_last[(int64_t)b * Me + m];
+  for (int i = t; i < (e1 - e0) * CH; i += NT) {
+    const int r = i / CH, c = i % CH;
+    st8<T>(own_ek + r * DH + 8 * c, ld8<T>(kb + (int64_t)(W + e0 + r) * DH + 8 * c));
+    st8<T>(own_ev + r * DH + 8 * c, ld8<T>(vb + (int64_t)(W + e0 + r) * DH + 8 * c));
+  }
+  for (int i = t; i < (s1 - s0) * CH; i += NT) {
+    const int r = i / CH, c = i % CH;
+    st8<T>(own_sv + r * DH + 8 * c, ld8<T>(vb + (int64_t)(W + Me + s0 + r) * DH + 8 * c));
+    if (c >= CH / 2)
+      st8<T>(own_sk + r * LF + 8 * (c - CH / 2), ld8<T>(kb + (int64_t)(W + Me + s0 + r) * DH + 8 * c));
+  }
+  if (ne > 0) stage_rows<T>(nrm_e, le, (const T*)s.exact_v_norm + ((int64_t)b * Hkv + h) * Me * DH, DH, Me, DH);
+  if (ns > 0) stage_rows<T>(nrm_s, lsum, (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + h) * Ms * LF, LF, Ms, LF);
+  __syncthreads();
+  // candidate gates and raw rows, 16-byte pieces (loads first)
+  for (int i = t; i < TT; i += NT) gate[i] = cand_gate(s, g, gb, b, pcl[i]);
+  for (int base = t; base < TT * CH; base += kRingPre * NT) {
+    Piece8<T> pk[kRingPre], pv[kRingPre];
+#pragma unroll
+    for (int u = 0; u < kRingPre; ++u) {
+      const int i = min(base + u * NT, TT * CH - 1), r = i / CH, c = i % CH;
+      pk[u] = ld8<T>(cand_row<T, DH>(s, g, kbk, b, h, pcl[r], false) + 8 * c);
+      pv[u] = ld8<T>(cand_row<T, DH>(s, g, vbk, b, h, pcl[r], true) + 8 * c);
+    }
+#pragma unroll
+    for (int u = 0; u < kRingPre; ++u) {
+      const int i = base + u * NT;
+      if (i < TT * CH) {
+        st8<T>(raw_k + i * 8, pk[u]);
+        st8<T>(raw_v + i * 8, pv[u]);
+      }
+    }
+  }
+  // LRU keys over the pre-update stamps (memory_banks.py:640-660):
+  // ascending stamps of used active slots, unused ones first
+  if (Te > 0)
+    for (int m = t; m < Me; m += NT) {
+      const bool u = used[m] != 0 && m < Ae;
+      rk[m] = sel::Item<int64_t>{u ? last[m] : kNegBig, (int64_t)m};
+    }
+  if (t == 0) ties = 0;
+  __syncthreads();
+  // ---- 2. this workgroup's routing rows, normalised (exact: V, all DH
+  // channels; summary: K channels [DH/2, DH)), then their dots with head
+  // h's norm caches, one dot per thread (lanes over bank slots)
+  for (int r = wv; r < ne + ns; r += NW) {
+    const bool ex = r < ne;
+    const int k = ex ? r : r - ne, c = z + k * NZ;
+    float x[NV];
+    bool act[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int d = lane + 64 * i;
+      act[i] = ex ? d < DH : (d >= LF && d < DH);
+      x[i] = E::ld((ex ? raw_v : raw_k)[c * DH + min(d, DH - 1)]);
+    }
+    if (ex) {
+      wave_unit<T, NV>(x, act);
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) cnd_e[k * le + lane + 64 * i] = x[i];
+    } else {
+      wave_unit<T, NV, LF>(x, act);
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) cnd_s[k * lsum + lane + 64 * i - LF] = x[i];
+    }
+  }
+  __syncthreads();
+  {
+    float* dot_e = ws + ((int64_t)b * Hkv + h) * Te * Me;
+    float* dot_s = ws + CODA_WS(ws_dot_s, s, g) + ((int64_t)b * Hkv + h) * Ts * Ms;
+    const int n_e = ne * Me, n_all = n_e + ns * Ms;
+    for (int it = t; it < n_all; it += NT) {
+      const bool ex = it < n_e;
+      const int k = ex ? it / Me : (it - n_e) / Ms, m = ex ? it % Me : (it - n_e) % Ms;
+      const float* rw = ex ? nrm_e + m * le : nrm_s + m * lsum;
+      const float* cd = ex ? cnd_e + k * le : cnd_s + k * lsum;
+      const int len = ex ? DH : LF;
+      float acc = 0.f;
+#pragma unroll 4
+      for (int d = 0; d < len; d += 4) {
+        const float4 rv = *reinterpret_cast<const float4*>(rw + d);
+        const float4 cv = *reinterpret_cast<const float4*>(cd + d);
+        acc = dot_pair(acc, cv.x, rv.x, cv.y, rv.y);
+        acc = dot_pair(acc, cv.z, rv.z, cv.w, rv.w);
+      }
+      // coherent at agent scope: read by workgroups on other XCDs
+      float* o = ex ? dot_e + (int64_t)(z + k * NZ) * Me + m : dot_s + (int64_t)(z + k * NZ) * Ms + m;
+      __hip_atomic_store(o, E::rnd(acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // sync 1; meanwhile the LRU victim order (rank of each key among all)
+  group_sync(flags, K, me, 2 * epoch, 2 * epoch + 1, [&](int t1, int nt1) {
+    if (Te > 0)
+      for (int m = t1; m < Me; m += nt1) {
+        const int64_t km = rk[m].v;
+        int lt = 0, eq = 0;
+        for (int j = 0; j < Me; ++j) {
+          const int64_t kj = rk[j].v;
+          lt += kj < km;
+          eq += (kj == km) & (j != m);
+        }
+        if (lt < n_lru) {
+          if (eq) atomicOr(&ties, 1);
+          else lru[lt] = m;
+        }
+      }
+  });
+  // ---- 3. routing of this workgroup's tokens (token i of [Te | Ts] goes
+  // to workgroup i mod K): one wave per token
+  {
+    const float* dall_e = ws + (int64_t)b * Hkv * Te * Me;
+    const float* dall_s = ws + CODA_WS(ws_dot_s, s, g) + (int64_t)b * Hkv * Ts * Ms;
+    for (int i = me + K * wv; i < Te + Ts; i += K * NW) {
+      const bool ex = i < Te;
+      const int tt = ex ? i : i - Te, M = ex ? Me : Ms;
+      float bv = -INFINITY;
+      int bi = 0x7fffffff;
+      for (int m = lane; m < M; m += 64) {
+        float acc = 0.f;
+        if (ex) {
+          for (int hh = 0; hh < Hkv; ++hh)
+            acc += __hip_atomic_load(dall_e + ((int64_t)hh * Te + tt) * Me + m, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          for (int hh = 0; hh < Hkv; ++hh)
+            acc += __hip_atomic_load(dall_s + ((int64_t)hh * Ts + tt) * Ms + m, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+        }
+        float v = E::rnd(acc / (float)Hkv);
+        if (ex ? (m >= Ae || used[m] == 0) : m >= s.active_summary) v = neg_fill<T>();
+        if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
+      }
+      wave_argmax(bv, bi);
+      if (lane == 0) {
+        if (ex) {
+          __hip_atomic_store(dx.fl_e + tt, __builtin_bit_cast(int32_t, bv), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(dx.idx_e + tt, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          __hip_atomic_store(dx.idx_s + tt, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  }
+  if (Te > 0 && ties) {
+    // ties among the leading LRU keys: libstdc++'s order
+    if (t == 0) sel::topk_order<int64_t>(rk, Me, n_lru, false, true);
+    __syncthreads();
+    for (int r = t; r < n_lru; r += NT) lru[r] = (int32_t)rk[r].i;
+  }
+  // sync 2; meanwhile this workgroup's share of head h's ring (every
+  // workgroup of head h has read its candidate rows before sync 1)
+  group_sync(flags, K, me, 2 * epoch + 1, 2 * epoch + 1, [&](int t1, int nt1) {
+    const int n_all = (Lr + g.blk - first) * CH;
+    const int pz = (n_all + NZ - 1) / NZ, p0 = min(n_all, z * pz), p1 = min(n_all, p0 + pz);
+    for (int base = p0 + t1; base < p1; base += kRingPre * nt1) {
+      Piece8<T> pk[kRingPre], pv[kRingPre];
+#pragma unroll
+      for (int u = 0; u < kRingPre; ++u) {
+        const int i = min(base + u * nt1, p1 - 1);
+        const int jb = first + i / CH - Lr, c = i % CH;
+        pk[u] = ld8<T>(kbk + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl + 8 * c);
+        pv[u] = ld8<T>(vbk + b * g.b_sb + h * g.b_sh + (int64_t)jb * g.b_sl + 8 * c);
+      }
+#pragma unroll
+      for (int u = 0; u < kRingPre; ++u) {
+        const int i = base + u * nt1;
+        if (i < p1) {
+          const int slot = (rhead + first + i / CH) % W, c = i % CH;
+          st8<T>(kb + (int64_t)slot * DH + 8 * c, pk[u]);
+          st8<T>(vb + (int64_t)slot * DH + 8 * c, pv[u]);
+        }
+      }
+    }
+  });
+  // ---- 4a. every token's routing; exact decisions (memory_banks.py:640-697)
+  for (int i = t; i < Te; i += NT) {
+    bv_e[i] = __builtin_bit_cast(float, __hip_atomic_load(dx.fl_e + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    bi_e[i] = __hip_atomic_load(dx.idx_e + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  for (int i = t; i < Ts; i += NT) {
+    idx_s[i] = __hip_atomic_load(dx.idx_s + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float gt = gate[i];
+    wtok[i] = (!s.gated || gt >= s.tau_summary) ? E::rnd(gt) : 0.f;
+  }
+  if (wv == 0) {
+    int u = 0;
+    for (int m = lane; m < Me; m += 64) u |= used[m] != 0;
+    u = wave_or(u);
+    if (lane == 0) any_used_s = u;
+  }
+  __syncthreads();
+  if (Te > 0 && t == 0) {
+    const int any_used = any_used_s;
+    int rank = -1;
+    int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
+    for (int tt = 0; tt < Te; ++tt) {
+      const bool keep = s.gated ? (gate[tt] >= s.tau_exact) : true;
+      const float bv = bv_e[tt];
+      const bool novel = !any_used || bv < E::rnd(s.tau_novel);
+      const bool hit = any_used && bv >= E::rnd(s.tau_match);
+      const bool nk = novel && keep;
+      if (nk) ++rank;  // cumsum(novel & keep) - 1 at tt
+      const bool cap = nk && rank < Ae;
+      int idx = bi_e[tt];
+      if (cap) {
+        int r = rank < 0 ? 0 : rank;
+        if (r > n_lru - 1) r = n_lru - 1;
+        idx = lru[r];
+      }
+      const bool touch = keep && (!novel || cap);
+      const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
+      idx_e[tt] = idx;
+      fl_e[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
+      cnt_ow += ow;
+      cnt_cap += cap;
+      cnt_hit += (hit && keep);
+      cnt_gated += !keep;
+      cnt_fr += (nk && !cap);
+    }
+    if (lead) {
+      if (s.metrics) {
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, cnt_ow);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, cnt_fr);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, cnt_cap);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, cnt_hit);
+        if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, cnt_gated);
+      }
+      if (s.frustrated) atomic_add_i64(s.frustrated + 0, cnt_fr);
+    }
+  }
+  // summary slots, 8 per wave and pass: token masks (ballots over the
+  // tokens), then lane u sums slot u's weights in token order (fp32: the
+  // scatter_add order) and sets its active / newly used flags
+  for (int m0 = 8 * wv; m0 < Ms; m0 += 8 * NW) {
+    uint64_t mine = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const uint64_t mk = __ballot(lane < Ts && idx_s[min(lane, max(Ts, 1) - 1)] == m0 + u);
+      if (lane == u) mine = mk;
+    }
+    const int m = m0 + lane;
+    if (lane < 8 && m < Ms) {
+      float c = 0.f;
+      for (uint64_t r = mine; r; r &= r - 1) c += wtok[__builtin_ctzll(r)];
+      c = E::rnd(c);
+      smask[m] = mine;
+      scnt[m] = c;
+      const bool active = c > 0.f;
+      sflag[m] = (active ? 1 : 0) | ((active && used[Me + m] == 0) ? 2 : 0);
+    }
+  }
+  __syncthreads();
+  // exact slots, one wave per slot (lanes over the tokens): written (an
+  // overwriting token) and touched (max position of the touching tokens)
+  if (Te > 0)
+    for (int m = wv; m < Me; m += NW) {
+      const bool on = lane < Te && idx_e[min(lane, Te - 1)] == m;
+      const int f = fl_e[min(lane, Te - 1)];
+      const int ow = __any(on && (f & 1));
+      int64_t pv = (on && (f & 2)) ? g.pos0 - g.ring_filled + pcl[min(lane, Te - 1)] : kNegBig;
+      for (int o = 32; o > 0; o >>= 1) {
+        const int64_t q = __shfl_xor(pv, o, 64);
+        pv = q > pv ? q : pv;
+      }
+      if (lane == 0) {
+        eflag[m] = ow;
+        if (lead) {
+          if (pv != kNegBig) s.mem_last[(int64_t)b * Me + m] = pv;  // LRU: max pos of the touching tokens
+          if (ow) al[W + m] = 1;
+        }
+      }
+    }
+  if (lead) {
+    int32_t* tr = s.trace ? s.trace + (int64_t)b * (2 * Te + Ts) : nullptr;
+    if (tr) {
+      for (int tt = t; tt < Te; tt += NT) {
+        tr[tt] = idx_e[tt];
+        tr[Te + tt] = fl_e[tt];
+      }
+      for (int tt = t; tt < Ts; tt += NT) tr[2 * Te + tt] = idx_s[tt];
+    }
+    for (int m = t; m < Ms; m += NT)
+      if (sflag[m] & 1) al[W + Me + m] = 1;
+    if (Ts > 0 && wv == 0) {
+      int64_t upd = 0, ins = 0;
+      int all_used = 1, any_cnt = 0;
+      for (int m = lane; m < Ms; m += 64) {
+        const int f = sflag[m];
+        upd += f & 1;
+        ins += (f >> 1) & 1;
+        if (m < s.active_summary) {
+          if (!(used[Me + m] != 0 || (f & 1))) all_used = 0;
+          if (f & 1) any_cnt = 1;
+        }
+      }
+      for (int o = 32; o > 0; o >>= 1) {
+        upd += __shfl_xor(upd, o, 64);
+        ins += __shfl_xor(ins, o, 64);
+      }
+      all_used = wave_and(all_used);
+      any_cnt = wave_or(any_cnt);
+      if (lane == 0) {
+        if (s.metrics) {
+          atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, upd);
+          if (s.overwrite_on_insert) atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_INSERTS, ins);
+        }
+        if (s.frustrated) {
+          if (!all_used) atomic_add_i64(s.frustrated + 1, 1);
+          if (any_cnt) atomic_add_i64(s.frustrated + 2, 1);
+        }
+      }
+    }
+    // ring gates and visibility bytes of the chunk's surviving tokens
+    for (int r = first + t; r < Lr + g.blk; r += NT) {
+      const int slot = (rhead + r) % W;
+      s.g_recent[(int64_t)b * W + slot] = gb[(int64_t)b * g.g_sb + (r - Lr)];
+      al[slot] = 1;
+    }
+  }
+  __syncthreads();
+  // ---- 4b. exact write-back of this workgroup's slots (memory_banks.py:
+  // 707-742): one wave per written slot, deltas summed in token order
+  if (Te > 0) {
+    for (int m = e0 + wv; m < e1; m += NW) {
+      if (!eflag[m]) continue;
+      const int r = m - e0;
+      float mk[NV], mv[NV], ak[NV], av[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int d = min(lane + 64 * i, DH - 1);
+        mk[i] = E::ld(own_ek[r * DH + d]);
+        mv[i] = E::ld(own_ev[r * DH + d]);
+        ak[i] = 0.f;
+        av[i] = 0.f;
+      }
+      for (int tt = 0; tt < Te; ++tt) {
+        if (idx_e[tt] != m || !(fl_e[tt] & 1)) continue;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          const int d = min(lane + 64 * i, DH - 1);
+          ak[i] += E::rnd(E::ld(raw_k[tt * DH + d]) - mk[i]);
+          av[i] += E::rnd(E::ld(raw_v[tt * DH + d]) - mv[i]);
+        }
+      }
+      T* kr = kb + (int64_t)(W + m) * DH;
+      T* vr = vb + (int64_t)(W + m) * DH;
+      float nv[NV];
+      bool act[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int d = lane + 64 * i;
+        act[i] = d < DH;
+        nv[i] = 0.f;
+        if (act[i]) {
+          kr[d] = E::st(mk[i] + E::rnd(ak[i]));
+          nv[i] = E::rnd(mv[i] + E::rnd(av[i]));
+          vr[d] = E::st(nv[i]);
+        }
+      }
+      wave_unit<T, NV>(nv, act);
+      T* nr = (T*)s.exact_v_norm + (((int64_t)b * Hkv + h) * Me + m) * DH;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) nr[lane + 64 * i] = E::st(nv[i]);
+    }
+  }
+  // ---- 4c. summary accumulate + EMA of this workgroup's slots
+  // (memory_banks.py:880-932): thread (group q, column col) takes slots
+  // s0 + q, s0 + q + NG, ...; column col < DH is V channel col, else K
+  // channel DH/2 + col - DH
+  if (Ts > 0) {
+    const float eta_h = s.eta[h];
+    constexpr int NG = kFusedThreads / NCOL;
+    const int q = t / NCOL, col = t % NCOL;
+    if (q < NG) {
+      const bool is_v = col < DH;
+      const int d = is_v ? col : LF + (col - DH);
+      const T* tokv = (is_v ? raw_v : raw_k) + d;
+      for (int m = s0 + q; m < s1; m += NG) {
+        if (!(sflag[m] & 1)) continue;
+        uint64_t r = smask[m];
+        int tt = __builtin_ctzll(r);
+        float a = E::rnd(E::ld(tokv[tt * DH]) * wtok[tt]);
+        for (r &= r - 1; r; r &= r - 1) {
+          tt = __builtin_ctzll(r);
+          a += E::rnd(E::ld(tokv[tt * DH]) * wtok[tt]);
+        }
+        const float eta = (s.overwrite_on_insert && (sflag[m] & 2)) ? 1.f : eta_h;
+        const float avg = E::rnd(E::rnd(a) / fmaxf(scnt[m], eps_r<T>()));
+        const int rl = m - s0;
+        if (is_v) {
+          const float mem = E::ld(own_sv[rl * DH + d]);
+          vb[(int64_t)(W + Me + m) * DH + d] = E::st(mem + E::rnd(eta * E::rnd(avg - mem)));
+        } else {
+          const float mem = E::ld(own_sk[rl * LF + (col - DH)]);
+          const float dk = E::rnd(E::rnd(avg * s.energy_scale) - mem);
+          const float nkv = E::rnd(mem + E::rnd(eta * dk));
+          kb[(int64_t)(W + Me + m) * DH + d] = E::st(nkv);
+          knew[rl * LF + (col - DH)] = nkv;  // new LF key for the norm cache
+        }
+      }
+    }
+    __syncthreads();
+    for (int m = s0 + wv; m < s1; m += NW) {
+      if (!(sflag[m] & 1)) continue;
+      const int rl = m - s0;
+      float x[NV];
+      bool act[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int dd = lane + 64 * i;
+        act[i] = dd < LF;
+        x[i] = act[i] ? knew[rl * LF + dd] : 0.f;
+      }
+      wave_unit<T, NV>(x, act);
+      T* nr = (T*)s.sum_lf_k_norm + (((int64_t)b * Hkv + h) * Ms + m) * LF;
+#pragma unroll
+      for (int i = 0; i < NV; ++i)
+        if (act[i]) nr[lane + 64 * i] = E::st(x[i]);
+    }
+  }
+}
+
 // Rotate a full ring into time order: slot s <- slot (head + s) % W.
 template <typename T, int DH>
 __global__ __launch_bounds__(256) void ring_rotate_kernel(const coda_bank_desc s, int head, T* tmp, float* gtmp) {
@@ -1309,11 +1934,8 @@ template <typename T, int DH>
 static int launch_dbank(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
                         const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st) {
   const size_t lds = dbank_lds(*s);
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)decode_bank_kernel<T, DH>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return fail(CODA_EHIP, "coda_decode_step: LDS attribute: %s", hipGetErrorString(e));
-  }
+  const int rc = lds_limit<decode_bank_kernel<T, DH>>(lds, "coda_decode_step");
+  if (rc) return rc;
   hipLaunchKernelGGL((decode_bank_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(256), lds, st, *s, (const T*)k_new,
                      (const T*)v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out);
   return check_launch("decode_bank");
@@ -1346,11 +1968,8 @@ static int launch_decode(const coda_bank_desc* s, const void* k_new, const void*
                          int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled, int64_t pos,
                          hipStream_t st) {
   const size_t lds = decode_lds(s);
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)decode_write_kernel<T, DH>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return fail(CODA_EHIP, "coda_decode_write: LDS attribute: %s", hipGetErrorString(e));
-  }
+  const int rc = lds_limit<decode_write_kernel<T, DH>>(lds, "coda_decode_write");
+  if (rc) return rc;
   hipLaunchKernelGGL((decode_write_kernel<T, DH>), dim3(s->B), dim3(512), lds, st, *s, (const T*)k_new,
                      (const T*)v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos);
   return check_launch("decode_write");
@@ -1422,14 +2041,20 @@ extern "C" int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, siz
   return CODA_OK;
 }
 
-template <typename K>
-static int ensure_lds(K kern, size_t lds, const char* who) {
-  if (lds > 160 * 1024) return fail(CODA_EUNSUP, "%s: %zu bytes of LDS needed (max 160 KiB)", who, lds);
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return fail(CODA_EHIP, "%s: LDS attribute: %s", who, hipGetErrorString(e));
-  }
-  return CODA_OK;
+// Launch epochs of the fused block write: unique per launch in the process
+// (48 bits), started from a clock-derived value so that a sync word left in
+// a reused workspace never carries the epoch of a later launch.
+static unsigned long long next_epoch() {
+  static std::atomic<unsigned long long> ep{
+      (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count() * 0x9E3779B97F4A7C15ull};
+  return ep.fetch_add(1, std::memory_order_relaxed) & ((1ull << 48) - 1);
+}
+
+// The fused kernel runs when its LDS fits and CODA_BLOCK_FUSED is not "0"
+// (read at every call, so that one process can compare the two paths).
+static bool fused_enabled() {
+  const char* e = getenv("CODA_BLOCK_FUSED");
+  return !(e && e[0] == '0');
 }
 
 template <typename T, int DH>
@@ -1437,6 +2062,26 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
                         const int32_t* plan_c, float* ws, hipStream_t st) {
   const int LF = DH - s->lf;
   const int TT = g.Te > g.Ts ? g.Te : g.Ts;
+  if (g.n_ev > 0 && TT > 0 && g.Te <= 64 && g.Ts <= 64 && s->Hkv <= kFusedMaxGroup && fused_enabled()) {
+    // each head over NZ workgroups: about 256 in all (more where one
+    // workgroup's LDS would not fit), at most 8 per head and 64 per sequence
+    const int pairs = s->B * s->Hkv;
+    const int nz_max = std::max(1, std::min({kFusedMaxGroup / s->Hkv, 8, g.Te + g.Ts}));
+    int NZ = std::max(1, std::min((256 + pairs - 1) / pairs, nz_max));
+    size_t lds = fused_lds(DH, (int)sizeof(T), s->Me, s->Ms, g.Te, g.Ts, NZ).total;
+    while (lds + 1024 > kLdsMax && NZ < nz_max) lds = fused_lds(DH, (int)sizeof(T), s->Me, s->Ms, g.Te, g.Ts, ++NZ).total;
+    if (lds + 1024 <= kLdsMax) {  // the kernel's own static LDS is under 1 KiB
+      int rc = lds_limit<block_fused_kernel<T, DH>>(lds, "coda_block_write");
+      if (rc) return rc;
+      unsigned long long* flags = reinterpret_cast<unsigned long long*>(ws + CODA_WS(ws_sync, *s, g));
+      // (sequence, head) pairs in blocks of 8, one pair per XCD (a pair
+      // beyond B * Hkv exits at once)
+      const int nwg = ((pairs + 7) / 8) * 8 * NZ;
+      hipLaunchKernelGGL((block_fused_kernel<T, DH>), dim3(nwg), dim3(kFusedThreads), lds, st, *s, g, NZ,
+                         (const T*)kb, (const T*)vb, gb, plan_c, ws, flags, next_epoch());
+      return check_launch("block_fused");
+    }
+  }
   if (g.n_ev > 0 && TT > 0) {
     // candidate rows split over nz workgroups per (sequence, head): about
     // 512 workgroups in all, at least 8 rows each
@@ -1448,7 +2093,7 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
     const size_t lds1 = std::max(sizeof(float) * ((ne > 0 ? (s->Me + ne) * (DH + 4) : 0) +
                                                   (ns > 0 ? (s->Ms + ns) * (LF + 4) : 0)),
                                  sizeof(sel::Item<int64_t>) * (size_t)s->Me);
-    int rc = ensure_lds(block_route_kernel<T, DH>, lds1, "coda_block_write");
+    int rc = lds_limit<block_route_kernel<T, DH>>(lds1, "coda_block_write");
     if (rc) return rc;
     hipLaunchKernelGGL((block_route_kernel<T, DH>), dim3(s->Hkv + 1, s->B, nz), dim3(256), lds1, st, *s, g,
                        (const T*)kb, (const T*)vb, gb, plan_c, ws);
@@ -1460,7 +2105,7 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
     const size_t lds_d = std::max(sizeof(float) * ((size_t)s->Hkv * g.Te * s->Me + (size_t)g.Te * s->Me) +
                                       sizeof(int) * ((size_t)s->Me + 2 * g.Te),
                                   sizeof(float) * (size_t)s->Hkv * kDecideChunk * s->Ms);
-    int rc = ensure_lds(block_decide_kernel<T>, lds_d, "coda_block_write");
+    int rc = lds_limit<block_decide_kernel<T>>(lds_d, "coda_block_write");
     if (rc) return rc;
     hipLaunchKernelGGL((block_decide_kernel<T>), dim3(1 + nsc, s->B), dim3(256), lds_d, st, *s, g, plan_c, ws);
     rc = check_launch("block_decide");
@@ -1474,7 +2119,7 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
     nz = std::max(1, std::min(nz, std::max(s->Me, s->Ms)));
     const int PS = (s->Ms + nz - 1) / nz;
     const size_t lds_a = apply_lds_bytes(s->Ms, g.Te, g.Ts, PS, LF);
-    int rc = ensure_lds(block_apply_kernel<T, DH>, lds_a, "coda_block_write");
+    int rc = lds_limit<block_apply_kernel<T, DH>>(lds_a, "coda_block_write");
     if (rc) return rc;
     hipLaunchKernelGGL((block_apply_kernel<T, DH>), dim3(s->Hkv, s->B, nz), dim3(kApplyThreads), lds_a, st, *s, g,
                        (const T*)kb, (const T*)vb, plan_c, ws);
@@ -1559,6 +2204,14 @@ static int noalloc_scratch(void** out) {
     per_device[dev] = p;
   }
   *out = per_device[dev];
+  return CODA_OK;
+}
+
+extern "C" int coda_block_sync_timeouts(unsigned int* out) {
+  CODA_REQUIRE(out != nullptr, "coda_block_sync_timeouts: null out pointer");
+  const hipError_t e = hipMemcpyFromSymbol(out, HIP_SYMBOL(g_block_sync_timeouts), sizeof(unsigned int), 0,
+                                           hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return fail(CODA_EHIP, "coda_block_sync_timeouts: %s", hipGetErrorString(e));
   return CODA_OK;
 }
 

@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <atomic>
 #include <string>
 
 #include "../../include/coda_mi355x.h"
@@ -19,6 +21,36 @@ int check_launch(const char* what);
   do {                                                            \
     if (!(cond)) return ::coda::fail(CODA_EINVAL, __VA_ARGS__);   \
   } while (0)
+
+// Dynamic LDS above 64 KiB needs the kernel's limit raised: raised once per
+// kernel and device to all that the kernel's static LDS leaves of the CU's
+// 160 KiB (a limit, not a reservation: each launch still takes only the
+// LDS it asks for).  KERN is the kernel.
+static constexpr size_t kLdsMax = 160 * 1024;
+template <auto KERN>
+inline int lds_limit(size_t lds, const char* who) {
+  if (lds <= 64 * 1024) return CODA_OK;
+  static std::atomic<uint64_t> done{0};
+  static std::atomic<int64_t> room{-1};
+  int64_t r = room.load(std::memory_order_acquire);
+  if (r < 0) {
+    hipFuncAttributes fa;
+    const hipError_t e = hipFuncGetAttributes(&fa, (const void*)KERN);
+    if (e != hipSuccess) return fail(CODA_EHIP, "%s: kernel attributes: %s", who, hipGetErrorString(e));
+    r = (int64_t)kLdsMax - (int64_t)fa.sharedSizeBytes;
+    room.store(r, std::memory_order_release);
+  }
+  if ((int64_t)lds > r)
+    return fail(CODA_EUNSUP, "%s: %zu bytes of LDS needed (%lld available)", who, lds, (long long)r);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  const uint64_t bit = dev < 64 ? (uint64_t(1) << dev) : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return CODA_OK;
+  const hipError_t e = hipFuncSetAttribute((const void*)KERN, hipFuncAttributeMaxDynamicSharedMemorySize, (int)r);
+  if (e != hipSuccess) return fail(CODA_EHIP, "%s: LDS attribute: %s", who, hipGetErrorString(e));
+  done.fetch_or(bit, std::memory_order_acq_rel);
+  return CODA_OK;
+}
 
 // ----------------------------------------------------------------- types
 typedef uint16_t bf16_t;  // raw bfloat16 bits

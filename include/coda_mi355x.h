@@ -255,6 +255,10 @@ int coda_block_plan(const float* g_ring, int ring_head, int ring_filled, int W,
  * (b_sb, b_sh, b_sl); gb (B, blk) float with row stride g_sb; plan_c points
  * at this chunk's (B, Kmax) candidate rows of coda_block_plan.
  * The ring is kept circular: head = oldest slot, filled = occupancy.
+ * One launch per chunk when the chunk's working set fits a CU's LDS (one
+ * workgroup per (KV head, sequence); the heads of a sequence meet at a
+ * per-sequence sync word in the workspace), else four (route, decide,
+ * apply, ring).  Calls that share a workspace must not overlap.
  * Replaces: _write_block_fast (memory_banks.py:438-564) with
  *   _exact_update_block_vectorized (:570-774, PyTorch branch) and
  *   _summary_update_block_hard (:780-950, PyTorch branch). */
@@ -266,6 +270,14 @@ int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb,
 
 /* Device scratch for coda_block_write. */
 int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, size_t* bytes);
+
+/* Number of times, since the library was loaded on the current device, that
+ * a workgroup of the one-launch block write gave up waiting for the other
+ * heads of its sequence (bounded wait, about 0.1 s; the chunk's results are
+ * then wrong).  Zero in every correct run.  Synchronous; for tests.
+ * No counterpart in the reference (the reference has no cross-workgroup
+ * wait). */
+int coda_block_sync_timeouts(unsigned int* out);
 
 /* coda_block_write without a workspace argument and without any allocation:
  * the chunk's scratch (routing dots, metadata snapshot, decisions) lives in a

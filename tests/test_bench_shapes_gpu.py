@@ -132,3 +132,63 @@ def test_bench_shape_trajectory_matches_oracle(name):
         p.decision_trace = None
         assert_close(hp.permute(0, 2, 1, 3), ho, dtype, f"{name} decode step {t} heads")
         compare_states(st_p, st_o, dtype, W, Me, f"{name} decode step {t}")
+
+
+def _cpu_copy(st):
+    from types import SimpleNamespace
+    f = lambda t: None if t is None else t.detach().cpu()
+    return SimpleNamespace(
+        k_buf=f(st.k_buf), v_buf=f(st.v_buf), allowed=f(st.allowed), g_recent=f(st.g_recent),
+        recent_idx=st.recent_idx, recent_filled=st.recent_filled, mem_last_exact=f(st.mem_last_exact), pos=st.pos,
+        active_exact=st.active_exact, active_summary=st.active_summary, _exact_v_norm=f(st._exact_v_norm),
+        _sum_lf_k_norm=f(st._sum_lf_k_norm))
+
+
+@pytest.mark.parametrize("name", ["c2_g4_b4_blk256", "c2_g4_b4_f32", "c5_g8_b4_blk256", "tiny_b256"])
+@torch.no_grad()
+def test_one_launch_block_write_equals_four_launch_path(name, monkeypatch):
+    """The one-launch chunk update (heads of a sequence meeting at a sync
+    word) and the four-launch pipeline (route, decide, apply, ring) leave
+    byte-identical states and decision traces after a chunked prefill."""
+    _need_gpu()
+    from coda_oracle import OracleLayer
+    H, Hkv, Dh, W, Me, Ms, B, L, block, kind, _, dtype = SHAPES[name]
+    print(f"[one launch vs four] {name}: B{B} L{L} block {block} {dtype}", flush=True)
+    kw = dict(embed_dim=H * Dh, num_heads=H, num_kv_heads=Hkv, window=W, num_landmarks_exact=Me,
+              num_landmarks_summary=Ms, rope_base=1e4)
+    torch.manual_seed(41)
+    m = OracleLayer(**kw).to(dtype).eval()
+    p = product_like(m, {"kw": kw}, dtype, DEV)
+    st0 = m.init_state(batch_size=B, dtype=dtype)
+    g = torch.Generator().manual_seed(42)
+    q, k, v, gate, lam = _inputs(m, B, L, dtype, kind, g)
+    c, s = m.rope_tables(L, 0, dtype)
+    out = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("CODA_BLOCK_FUSED", mode)
+        st = to_product_state(st0, DEV)
+        p.decision_trace = []
+        heads = p.prefill_core(q.to(DEV), k.to(DEV), v.to(DEV), gate.to(DEV), lam.squeeze(-1).to(DEV), c.to(DEV),
+                               s.to(DEV), st, block_size=block)
+        torch.cuda.synchronize()
+        trace = [tuple(x.cpu() if torch.is_tensor(x) else x for x in ev) for ev in p.decision_trace]
+        p.decision_trace = None
+        out[mode] = (heads.cpu(), st, trace)
+    h0, s0, t0 = out["0"]
+    h1, s1, t1 = out["1"]
+    assert torch.equal(h0, h1), f"{name}: heads differ"
+    assert len(t0) == len(t1), f"{name}: {len(t0)} vs {len(t1)} trace events"
+    for i, (a, b) in enumerate(zip(t0, t1)):
+        assert a[0] == b[0] and all(torch.equal(x, y) for x, y in zip(a[1:], b[1:])), f"{name}: trace event {i} differs"
+    compare_states(s1, _cpu_copy(s0), dtype, W, Me, f"{name} one launch vs four")
+
+
+def test_block_write_sync_never_gave_up():
+    """No workgroup of the one-launch block write gave up its bounded wait
+    for the other heads of its sequence in any run of this process."""
+    _need_gpu()
+    import ctypes
+    from coda_gqa_l import _hip
+    n = ctypes.c_uint(0)
+    _hip.check(_hip.lib().coda_block_sync_timeouts(ctypes.byref(n)))
+    assert n.value == 0, f"{n.value} workgroups gave up waiting at a block-write sync word"
