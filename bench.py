@@ -13,11 +13,15 @@ update, and the differential attention over the updated cache), with the
 post-projection inputs of every step already resident in HBM.  `value` =
 batch * steps / wall time of the K timed steps.
 
-Also reported (extra keys): the chunked-prefill figure of configs[2]
-(B=4, 32768 tokens, block 256) for the hot path (attention + banks per
-chunk), the dominant kernels' rooflines from HIP events recorded around
-every launch in the timed region, and the CPU oracle timed on a bounded
-sample on this host's cores.
+Also reported (extra keys): configs[1] decode at batch 1 and 16; the
+chunked-prefill figures of configs[2] (B=4, 32768 tokens, blocks 256 and
+128) for the hot path (attention + banks per chunk); configs[3]'s
+unbounded attention; configs[4]'s decode (batch 128) and chunked prefill
+(batch 8); the whole 7B layer, projections included (decode batch 64,
+prefill batch 4); the dominant kernels' rooflines from HIP events on the
+launch stream; and the CPU oracle on this host's cores: the configs[1]
+decode sample (`cpu_baseline`) and the C1 / C3 / C4 legs
+(`cpu_baseline_legs`), each on a bounded sample stated with it.
 """
 
 from __future__ import annotations
@@ -48,7 +52,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the configs[2] prefill figure")
     ap.add_argument("--no-unbounded", action="store_true", help="skip the configs[3] unbounded attention figure")
-    ap.add_argument("--no-c5", action="store_true", help="skip the configs[4] 70B-shaped decode figure")
+    ap.add_argument("--no-c5", action="store_true", help="skip the configs[4] 70B-shaped decode / prefill figures")
+    ap.add_argument("--no-small-batch", action="store_true", help="skip the configs[1] batch 1 / 16 decode figures")
+    ap.add_argument("--no-layer", action="store_true", help="skip the whole-layer (projections included) figures")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="before timing, run 5 device-to-device copies of this many MiB (a plain copy kernel of "
@@ -215,10 +221,26 @@ def main():
 
     print(f"# decode: {tok_s:.0f} tok/s, {ms_step * 1e3:.1f} us/step, kernels {step_gpu_ms * 1e3:.1f} us "
           f"({achieved:.0f} GB/s)", file=sys.stderr, flush=True)
+    # ---------------------------------------------------------------- decode at batch 1 / 16
+    if not a.no_small_batch:
+        for bs in (1, 16):
+            t_s, ms_s, gms = run_decode(torch, coda, m, bs, a.prefill_tokens, 2048, a.steps, a.warmup, a.block)[:3]
+            ab, bb = decode_bytes(m, bs)
+            ach = (ab + bb) / (gms * 1e-3) / 1e9
+            out["decode_b%d" % bs] = {
+                "metric": "decode tok/s, configs[1] layer, batch %d" % bs, "value": round(t_s, 1), "unit": "tok/s",
+                "batch": bs, "steps": a.steps, "ms_per_step": round(ms_s, 5),
+                "roofline": {"bound": "hbm", "kernel": "decode_step_bf16<128>", "achieved": round(ach, 1),
+                             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                             "bytes_per_launch": ab + bb, "avg_launch_ms": round(gms, 5)}}
+            print(f"# decode B{bs}: {t_s:.0f} tok/s, {ms_s * 1e3:.1f} us/step ({ach:.0f} GB/s)", file=sys.stderr,
+                  flush=True)
     # ---------------------------------------------------------------- prefill
     if not a.no_prefill:
-        out["prefill"] = bench_prefill(torch, coda, m, a)
+        out["prefill"] = bench_prefill(torch, coda, m, a, a.block)
         print(f"# prefill: {out['prefill']['value']:.0f} tok/s", file=sys.stderr, flush=True)
+        out["prefill_blk128"] = bench_prefill(torch, coda, m, a, 128)
+        print(f"# prefill block 128: {out['prefill_blk128']['value']:.0f} tok/s", file=sys.stderr, flush=True)
     # ---------------------------------------------------------------- unbounded
     if not a.no_unbounded:
         out["unbounded"] = bench_unbounded(torch, coda)
@@ -229,16 +251,28 @@ def main():
         out["decode_c5"] = bench_decode_c5(torch, coda, a)
         print(f"# decode configs[4]: {out['decode_c5']['value']:.0f} tok/s, "
               f"{out['decode_c5']['roofline']['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+        out["prefill_c5"] = bench_prefill_c5(torch, coda, a)
+        print(f"# prefill configs[4]: {out['prefill_c5']['value']:.0f} tok/s", file=sys.stderr, flush=True)
+    # ---------------------------------------------------------------- whole layer, projections included
+    if not a.no_layer:
+        out["layer"] = bench_layer(torch, coda, m, a)
+        print(f"# layer: decode {out['layer']['decode']['value']:.0f} tok/s, prefill "
+              f"{out['layer']['prefill']['value']:.0f} tok/s", file=sys.stderr, flush=True)
     # ---------------------------------------------------------------- CPU baseline
     if not a.no_cpu:
         out["cpu_baseline"] = cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a)
+        out["cpu_baseline_legs"] = cpu_legs(torch)
     print(json.dumps(out), flush=True)
 
 
-def bench_prefill(torch, coda, m, a):
+def bench_prefill(torch, coda, m, a, blk):
+    """chunked prefill of an N(0,1) sequence through the layer's
+    projections (outside the timed region), then the hot path (attention +
+    bank update per chunk) timed over the whole sequence; the attention
+    kernel alone timed on a steady-state chunk (full prefix)."""
     dev = "cuda:0"
     dt = torch.bfloat16
-    B, L, blk = a.prefill_batch, a.prefill_len, a.block
+    B, L = a.prefill_batch, a.prefill_len
     g = torch.Generator(device=dev).manual_seed(7)
     st = m.init_state(batch_size=B, device=dev, dtype=dt)
     x = torch.randn(B, L, 4096, generator=g, device=dev, dtype=dt)
@@ -284,10 +318,10 @@ def bench_prefill(torch, coda, m, a):
     return {"metric": "chunked-prefill tok/s (configs[2], hot path: attention + banks per chunk)",
             "value": round(B * L / wall, 1), "unit": "tok/s", "batch": B, "seq_len": L, "block": blk,
             "ms_total": round(wall * 1e3, 3),
-            "roofline": {"bound": "mfma", "kernel": "attn_fa_bf16<128,8,2,1>", "achieved": round(tflops, 2),
+            "roofline": {"bound": "mfma", "kernel": "attn_f3_bf16<128,8,0>", "achieved": round(tflops, 2),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                          "flops_per_launch": flops, "avg_launch_ms": round(attn_ms, 5),
-                         "traffic": profile_traffic("prefill_chunk_b%d attn_fa_bf16<128,8>" % B),
+                         "traffic": profile_traffic("prefill_chunk_b%d_blk%d attn_f3_bf16<128,8,0>" % (B, blk)),
                          "valid_prefix_slots": n_prefix}}
 
 
@@ -310,6 +344,121 @@ def bench_decode_c5(torch, coda, a, B=128, steps=50, warmup=10):
             "roofline": {"bound": "hbm", "kernel": "decode_step_bf16<128>", "achieved": round(achieved, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                          "bytes_per_launch": attn_b + bank_b, "avg_launch_ms": round(gpu_ms, 5)}}
+
+
+def bench_prefill_c5(torch, coda, a, B=8, L=8192, blk=256):
+    """configs[4]'s chunked prefill on a steady-state sample: the 70B-shaped
+    layer (hidden 8192, 64 q heads, 8 KV heads, W512 / Me128 / Ms128, Lbuf
+    768) at batch 8, block 256, over 8192 N(0,1) tokens (32 chunks; the ring
+    fills after 2) through the layer's projections (outside the timed
+    region); hot path timed as in the configs[2] figure."""
+    dev = "cuda:0"
+    dt = torch.bfloat16
+    torch.manual_seed(0)
+    m = coda.CoDAGQALandmarkPerf2(embed_dim=8192, num_heads=64, num_kv_heads=8, window=512,
+                                  num_landmarks_exact=128, num_landmarks_summary=128, rope_base=1e4)
+    m = m.to(dtype=dt).to(dev).eval()
+    g = torch.Generator(device=dev).manual_seed(9)
+    with torch.no_grad():
+        x = torch.randn(B, L, 8192, generator=g, device=dev, dtype=dt)
+        q = m._project_q(x)
+        kr, v = m._project_kv_raw(x)
+        cos, sin = m.rope(seq_len=L, offset=0, device=dev, dtype=dt)
+        cos, sin = cos.contiguous(), sin.contiguous()
+        k = torch.empty((B, L, m.num_kv_heads, m.head_dim), dtype=dt, device=dev).permute(0, 2, 1, 3)
+        coda.apply_rope(kr, cos, sin, interleaved=m.rope_interleaved, out=k)
+        gate = m._write_gate(x)
+        lam = m._lambda(x)
+        del x, kr
+        heads = torch.empty((B, L, m.num_heads, m.head_dim), dtype=dt, device=dev)
+        st_w = m.init_state(batch_size=B, device=dev, dtype=dt)
+        m.prefill_core(q[:, :, :4 * blk], k[:, :, :4 * blk], v[:, :, :4 * blk], gate[:, :4 * blk],
+                       lam[:, :, :4 * blk], cos, sin, st_w, block_size=blk, out=heads)
+        del st_w
+        st = m.init_state(batch_size=B, device=dev, dtype=dt)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m.prefill_core(q, k, v, gate, lam, cos, sin, st, block_size=blk, out=heads)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        t_s = L - blk
+        ct, sn = m._theta_tables(dt)
+        w = m._rms_weight(dt)
+        e0.record(stream)
+        for _ in range(reps):
+            coda.ops.bounded_attention(
+                q=q[:, :, t_s:], rope_cos=cos[t_s:], rope_sin=sin[t_s:], rope_interleaved=m.rope_interleaved,
+                theta_cos=ct, theta_sin=sn, k_prefix=st.k_buf, v_prefix=st.v_buf, allowed=st.allowed,
+                k_block=k[:, :, t_s:], v_block=v[:, :, t_s:], lam=lam[:, :, t_s:], rms_weight=w, eps=m._eps,
+                out=heads[:, t_s:].permute(0, 2, 1, 3))
+        e1.record(stream)
+        torch.cuda.synchronize()
+        attn_ms = e0.elapsed_time(e1) / reps
+        n_prefix = int(st.allowed[0].sum().item())
+    flops = prefill_chunk_flops(m, B, blk, n_prefix)
+    tflops = flops / (attn_ms * 1e-3) / 1e12
+    return {"metric": "chunked-prefill tok/s (configs[4], 70B-shaped layer, steady-state sample)",
+            "value": round(B * L / wall, 1), "unit": "tok/s", "batch": B, "seq_len": L, "block": blk,
+            "ms_total": round(wall * 1e3, 3),
+            "sample": "8192 of configs[4]'s 131072 tokens per sequence (32 chunks, ring full after 2)",
+            "roofline": {"bound": "mfma", "kernel": "attn_f3_bf16<128,8,0>", "achieved": round(tflops, 2),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                         "flops_per_launch": flops, "avg_launch_ms": round(attn_ms, 5),
+                         "valid_prefix_slots": n_prefix}}
+
+
+def bench_layer(torch, coda, m, a, B_dec=64, steps=100, B_pre=4, L_pre=8192):
+    """The whole 7B-shaped layer, projections included (q / k / v / lambda /
+    gate, RoPE, the hot path, o_proj): `step` at batch 64 from a state
+    pre-filled with 4096 tokens, and `prefill_chunked` at batch 4 over 8192
+    tokens (block 256).  Per token: 2 x (weights) FLOPs for the projections
+    plus the attention; per decode step the weights (80 MiB at 7B) and the
+    state traffic cross HBM once."""
+    dev = "cuda:0"
+    dt = torch.bfloat16
+    E = m.num_heads * m.head_dim
+    n_w = sum(p.numel() for p in m.parameters())
+    w_bytes = n_w * 2
+    g = torch.Generator(device=dev).manual_seed(11)
+    with torch.no_grad():
+        st = m.init_state(batch_size=B_dec, device=dev, dtype=dt)
+        for t0 in range(0, a.prefill_tokens, 2048):
+            x = torch.randn(B_dec, min(2048, a.prefill_tokens - t0), E, generator=g, device=dev, dtype=dt)
+            _, st = m.prefill_chunked(x, st, block_size=a.block, return_outputs=False)
+        xs = torch.randn(steps + 10, B_dec, 1, E, generator=g, device=dev, dtype=dt)
+        for i in range(10):
+            _, st = m.step(xs[i], st)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            _, st = m.step(xs[10 + i], st)
+        torch.cuda.synchronize()
+        wall_d = time.perf_counter() - t0
+        ab, bb = decode_bytes(m, B_dec)
+        step_bytes = w_bytes + ab + bb
+        # prefill
+        x = torch.randn(B_pre, L_pre, E, generator=g, device=dev, dtype=dt)
+        st = m.init_state(batch_size=B_pre, device=dev, dtype=dt)
+        m.prefill_chunked(x[:, :4 * a.block], st, block_size=a.block)
+        st = m.init_state(batch_size=B_pre, device=dev, dtype=dt)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        m.prefill_chunked(x, st, block_size=a.block)
+        torch.cuda.synchronize()
+        wall_p = time.perf_counter() - t0
+    ms_step = wall_d * 1e3 / steps
+    return {"decode": {"metric": "whole-layer decode tok/s (configs[1] layer, projections included)",
+                       "value": round(B_dec * steps / wall_d, 1), "unit": "tok/s", "batch": B_dec,
+                       "ms_per_step": round(ms_step, 5), "bytes_per_step": step_bytes,
+                       "weight_bytes": w_bytes, "flops_per_token": 2 * n_w,
+                       "hbm_frac": round(step_bytes / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "prefill": {"metric": "whole-layer chunked-prefill tok/s (configs[2] layer, projections included)",
+                        "value": round(B_pre * L_pre / wall_p, 1), "unit": "tok/s", "batch": B_pre,
+                        "seq_len": L_pre, "block": a.block, "ms_total": round(wall_p * 1e3, 3),
+                        "flops_per_token_projections": 2 * n_w}}
 
 
 def bench_unbounded(torch, coda, B=2, L=8192, H=32, Hkv=8, Dh=128, reps=5):
@@ -382,6 +531,87 @@ def cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a):
     return {"value": round(B * n_done / wall, 2), "unit": "tok/s", "cores": torch.get_num_threads(),
             "kind": "port", "sample": f"{n_done} decode steps at batch {B} of the same state "
                                       f"(banks + attention, post-projection inputs), {wall:.1f} s"}
+
+
+def cpu_legs(torch):
+    """The CPU oracle on the other configs' bounded samples (post-projection
+    inputs where the GPU figure excludes the projections), on this host's
+    cores, in the same run:
+      C1  configs[0] in full: D512 layer, fp32, batch 1, prefill_chunked of
+          2048 tokens (block 256), then 1000 decode steps (step, projections
+          included);
+      C3  configs[2]: 16 steady-state chunks (block 256, batch 4, bf16) after
+          two chunks that fill the ring, attention + bank update;
+      C4  configs[3]: one full causal forward at L 8192, batch 2, bf16,
+          computed in blocks of 512 query rows (each against its visible
+          keys)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from coda_oracle import OracleLayer, ops
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    legs = {}
+    g = torch.Generator().manual_seed(21)
+    with torch.no_grad():
+        # C1
+        torch.manual_seed(0)
+        m = OracleLayer(embed_dim=512, num_heads=8, num_kv_heads=2, window=256, num_landmarks_exact=64,
+                        num_landmarks_summary=64).eval()
+        st = m.init_state(batch_size=1, dtype=torch.float32)
+        x = torch.randn(1, 2048, 512, generator=g)
+        xs = torch.randn(1000, 1, 1, 512, generator=g)
+        t0 = time.perf_counter()
+        m.prefill_chunked(x, st, block_size=256)
+        t1 = time.perf_counter()
+        for i in range(1000):
+            m.step(xs[i], st)
+        t2 = time.perf_counter()
+        legs["C1"] = {"value": round(2048 / (t1 - t0), 1), "unit": "tok/s (prefill)",
+                      "decode_value": round(1000 / (t2 - t1), 1), "decode_unit": "tok/s",
+                      "cores": torch.get_num_threads(), "kind": "port",
+                      "sample": f"configs[0] in full: 2048-token prefill {t1 - t0:.2f} s, 1000 decode steps "
+                                f"{t2 - t1:.2f} s"}
+        # C3
+        dt = torch.bfloat16
+        torch.manual_seed(0)
+        m = OracleLayer(embed_dim=4096, num_heads=32, num_kv_heads=8, window=256, num_landmarks_exact=64,
+                        num_landmarks_summary=64, rope_base=1e4).to(dt).eval()
+        B, blk, n_warm, n_chunks = 4, 256, 2, 16
+        L = blk * (n_warm + n_chunks)
+        q = torch.randn(B, 32, L, 128, generator=g).to(dt)
+        k = torch.randn(B, 8, L, 128, generator=g).to(dt)
+        v = torch.randn(B, 8, L, 128, generator=g).to(dt)
+        gs = torch.sigmoid(torch.randn(B, L, generator=g) - 2.0)
+        lam = torch.sigmoid(torch.randn(B, 32, L, 1, generator=g) - 1.0).to(dt)
+        st = m.init_state(batch_size=B, dtype=dt)
+        w = blk * n_warm
+        m.prefill_core(q[:, :, :w], k[:, :, :w], v[:, :, :w], gs[:, :w], lam[:, :, :w], st, block_size=blk)
+        t0 = time.perf_counter()
+        m.prefill_core(q[:, :, w:], k[:, :, w:], v[:, :, w:], gs[:, w:], lam[:, :, w:], st, block_size=blk)
+        t1 = time.perf_counter()
+        legs["C3"] = {"value": round(B * blk * n_chunks / (t1 - t0), 1), "unit": "tok/s",
+                      "cores": torch.get_num_threads(), "kind": "port",
+                      "sample": f"{n_chunks} steady-state chunks of block {blk} at batch {B} (post-projection "
+                                f"N(0,1) inputs), {t1 - t0:.2f} s"}
+        # C4
+        B, L, H, Hkv, Dh, rb = 2, 8192, 32, 8, 128, 512
+        wgt = torch.ones(Dh, dtype=dt)
+        t_tot = 0.0
+        for b in range(B):
+            qb = torch.randn(1, H, L, Dh, generator=g).to(dt)
+            qn = torch.randn(1, H, L, Dh, generator=g).to(dt)
+            kb = torch.randn(1, Hkv, L, Dh, generator=g).to(dt)
+            vb = torch.randn(1, Hkv, L, Dh, generator=g).to(dt)
+            lb = (0.1 + 0.8 * torch.rand(1, H, L, 1, generator=g)).to(dt)
+            t0 = time.perf_counter()
+            for r0 in range(0, L, rb):
+                r1 = r0 + rb
+                ops.diff_attention(qb[:, :, r0:r1], qn[:, :, r0:r1], kb[:, :, :r1], vb[:, :, :r1], lb[:, :, r0:r1],
+                                   rms_weight=wgt, is_causal=True)
+            t_tot += time.perf_counter() - t0
+        legs["C4"] = {"value": round(B * L / t_tot, 1), "unit": "tok/s", "cores": torch.get_num_threads(),
+                      "kind": "port", "sample": f"one full causal forward, L {L}, batch {B}, in blocks of {rb} "
+                                                f"query rows, {t_tot:.2f} s"}
+    return legs
 
 
 if __name__ == "__main__":
