@@ -28,7 +28,7 @@ import torch
 import torch.nn as nn
 
 from . import _hip, ops
-from .memory_banks import METRIC_KEYS, MemoryBankMixin
+from .memory_banks import METRIC_KEYS, DeviceMetrics, MemoryBankMixin
 from .primitives import HeadwiseRMSNorm, RotaryEmbedding, apply_rope
 from .state import CoDAGQALandmarkStatePerf2
 
@@ -193,7 +193,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
                                         k_buf[:, :, W + Me:, self.lf_start:].data_ptr(), self.Lbuf * Dh, Dh,
                                         B * Hkv, Ms, LF, stream))
         if self.collect_metrics:
-            st.metrics = {k: (0.0 if k.endswith("ratio") else 0) for k in METRIC_KEYS}
+            st.metrics = DeviceMetrics({k: (0.0 if k.endswith("ratio") else 0) for k in METRIC_KEYS})
             st.metrics["active_exact"] = st.active_exact
             st.metrics["active_summary"] = st.active_summary
         return st

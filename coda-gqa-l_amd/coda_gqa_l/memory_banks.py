@@ -19,7 +19,8 @@ the optional metrics dict.
 from __future__ import annotations
 
 import ctypes
-from typing import Optional
+import collections
+from typing import Dict, Optional
 
 import torch
 
@@ -36,6 +37,86 @@ _COUNTER_KEYS = {
     _hip.CNT_SUMMARY_INSERTS: "summary_inserts", _hip.CNT_TOKENS_GATED_OUT: "tokens_gated_out",
     _hip.CNT_EXACT_FRUSTRATED: "exact_frustrated",
 }
+
+
+class DeviceMetrics(dict):
+    """A state's ``metrics`` dict (the reference's keys and value types)
+    whose bank-update counters stay on the device: each bank update adds
+    into ``pending`` (int64, one slot per kernel counter plus one for
+    ``summary_frustrated``) and leaves the latest fill ratios as device
+    scalars, with no host sync; the first read of a value folds them in.
+    Pickled, it is a mapping of the folded values; save_state writes a
+    plain dict, the reference's format."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.pending: Optional[torch.Tensor] = None
+        self.fill: Dict[str, torch.Tensor] = {}
+
+    def accumulator(self, device) -> torch.Tensor:
+        if self.pending is None or self.pending.device != torch.device(device):
+            self._fold()
+            self.pending = torch.zeros(_hip.NUM_COUNTERS + 1, dtype=torch.int64, device=device)
+        return self.pending
+
+    def add_host(self, key: str, n: int) -> None:
+        """A host-known increment (no fold)."""
+        dict.__setitem__(self, key, dict.__getitem__(self, key) + n)
+
+    def _fold(self) -> None:
+        p, f = self.pending, self.fill
+        if p is None and not f:
+            return
+        if p is not None:
+            c = p.tolist()
+            p.zero_()
+            for i, key in _COUNTER_KEYS.items():
+                dict.__setitem__(self, key, dict.__getitem__(self, key) + int(c[i]))
+            dict.__setitem__(self, "summary_frustrated",
+                             dict.__getitem__(self, "summary_frustrated") + int(c[_hip.NUM_COUNTERS]))
+        for key, v in list(f.items()):
+            dict.__setitem__(self, key, float(v.item()))
+        f.clear()
+
+    def __getitem__(self, key):
+        self._fold()
+        return super().__getitem__(key)
+
+    def get(self, key, default=None):
+        self._fold()
+        return super().get(key, default)
+
+    def items(self):
+        self._fold()
+        return super().items()
+
+    def values(self):
+        self._fold()
+        return super().values()
+
+    def __iter__(self):
+        self._fold()
+        return super().__iter__()
+
+    def __eq__(self, other):
+        self._fold()
+        return super().__eq__(other)
+
+    __hash__ = None
+
+    def __repr__(self):
+        self._fold()
+        return super().__repr__()
+
+    def copy(self):
+        self._fold()
+        return dict(super().items())
+
+    def __reduce__(self):
+        # an OrderedDict of the folded values: loads anywhere, torch.load
+        # with weights_only=True included (save_state writes a plain dict)
+        self._fold()
+        return (collections.OrderedDict, (list(super().items()),))
 
 
 class MemoryBankMixin:
@@ -150,32 +231,46 @@ class MemoryBankMixin:
         if Ts > 0:
             out.append(("summary_block", tr[:, 2 * Te:2 * Te + Ts].long()))
 
+    @staticmethod
+    def _device_metrics(st) -> Optional[DeviceMetrics]:
+        mt = st.metrics
+        if mt is not None and not isinstance(mt, DeviceMetrics):
+            mt = st.metrics = DeviceMetrics(mt)
+        return mt
+
     def _aux_buffers(self, st, device):
-        metrics = torch.zeros(_hip.NUM_COUNTERS, dtype=torch.int64, device=device) if st.metrics is not None \
-            else None
+        """The kernels' counter array (the state's device accumulator, added
+        into by every bank update) and frustration flags."""
+        mt = self._device_metrics(st)
+        metrics = mt.accumulator(device)[:_hip.NUM_COUNTERS] if mt is not None else None
         need_fr = (self._expandable() and not self.training) or st.metrics is not None
         frustrated = torch.zeros(4, dtype=torch.int64, device=device) if need_fr else None
         return metrics, frustrated
 
     def _fold_metrics(self, st, counters: Optional[torch.Tensor], evictions: int, exact_ran: bool,
                       summary_ran: bool) -> None:
-        """Device counters -> the state's metrics dict (reference keys)."""
+        """Host-known metrics and the latest fill ratios (device scalars);
+        the kernel counters are already in the state's accumulator."""
         mt = st.metrics
         if mt is None or counters is None:
             return
-        c = counters.tolist()
-        for i, key in _COUNTER_KEYS.items():
-            mt[key] += int(c[i])
-        mt["total_evictions"] += int(evictions)
+        mt.add_host("total_evictions", int(evictions))
         W, Me = self.window, self.Me
         if exact_ran and Me > 0:
-            mt["exact_fill_ratio"] = float(st.allowed[:, W:W + Me].any(dim=0).float().mean().item())
+            mt.fill["exact_fill_ratio"] = st.allowed[:, W:W + Me].any(dim=0).float().mean()
         if summary_ran and self.Ms > 0:
-            mt["summary_fill_ratio"] = float(st.allowed[:, W + Me:].any(dim=0).float().mean().item())
+            mt.fill["summary_fill_ratio"] = st.allowed[:, W + Me:].any(dim=0).float().mean()
 
     def _expand_from(self, st, fr: Optional[torch.Tensor], exact_count_mode: bool, ran_e: bool, ran_s: bool):
-        """Dynamic expansion after a bank update (attention.py:358-390)."""
+        """Dynamic expansion after a bank update (attention.py:358-390).
+        Expansion changes host sizes, so it reads the flags (a host sync);
+        without it the summary frustration count stays on the device."""
         if fr is None:
+            return
+        if not (self._expandable() and not self.training):
+            if ran_s and st.metrics is not None:
+                acc = st.metrics.accumulator(fr.device)
+                acc[_hip.NUM_COUNTERS:] += ((fr[1] == 0) & (fr[2] > 0)).to(torch.int64)
             return
         f = fr.tolist()
         if ran_e:
