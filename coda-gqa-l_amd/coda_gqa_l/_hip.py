@@ -63,6 +63,18 @@ class BankDesc(ctypes.Structure):
     ]
 
 
+class ProjDesc(ctypes.Structure):
+    """coda_proj_desc (include/coda_mi355x.h)."""
+
+    _fields_ = [
+        ("dtype", _i32), ("M", _i32), ("D", _i32), ("L", _i32), ("H", _i32), ("Hkv", _i32), ("Dh", _i32),
+        ("rope_interleaved", _i32), ("gate", _i32), ("pad0", _i32),
+        ("x", _vp), ("x_sm", _i64), ("w", _vp), ("bias", _vp), ("rope_cos", _vp), ("rope_sin", _vp),
+        ("q", _vp), ("q_sm", _i64), ("k", _vp), ("k_sm", _i64), ("v", _vp), ("v_sm", _i64),
+        ("lam", _vp), ("lam_sm", _i64), ("g", _vp), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 _lock = threading.Lock()
 _lib: Optional[ctypes.CDLL] = None
 
@@ -92,6 +104,9 @@ _SIGS = {
     "coda_block_write_noalloc_max_bytes": (ctypes.c_size_t, []),
     "coda_ring_rotate": (_i32, [ctypes.POINTER(BankDesc), _i32, _vp, ctypes.c_size_t, _vp]),
     "coda_unit_rows": (_i32, [_i32, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
+    "coda_project": (_i32, [ctypes.POINTER(ProjDesc), _vp]),
+    "coda_project_workspace_bytes": (_i32, [ctypes.POINTER(ProjDesc), ctypes.POINTER(ctypes.c_size_t)]),
+    "coda_project_epilogue": (_i32, [ctypes.POINTER(ProjDesc), _vp, _i64, _vp]),
     "coda_topk_order_host": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     "coda_topk_order_host_i64": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
 }

@@ -21,6 +21,7 @@ The layer is inference-only on this path: a module in training mode raises
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional, Tuple
 
@@ -267,6 +268,130 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         w = self.head_norm.weight
         return self._derived("rms_w", w, dtype, lambda: w.detach().to(dtype).contiguous())
 
+    # ------------------------------------------------------------ projection front end
+    def _rope_rows(self, p0: int, L: int, device, dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor]:
+        """RoPE tables (L, Dh/2) of positions p0 .. p0 + L - 1: rows of one
+        cached table, grown by doubling; every element is the same fp32
+        product and cos / sin as in a table made for these positions alone."""
+        cache = self.__dict__.setdefault("_rope_cache", {})
+        key = (torch.device(device), dtype)
+        tab = cache.get(key)
+        need = int(p0) + int(L)
+        if tab is None or tab[0].shape[0] < need:
+            n = 1 << max(12, (need - 1).bit_length())
+            c, s_ = self.rope(seq_len=n, offset=0, device=device, dtype=dtype)
+            tab = cache[key] = (c.contiguous(), s_.contiguous())
+        return tab[0][p0:need], tab[1][p0:need]
+
+    def _proj_pack(self, dtype: torch.dtype, kind: str):
+        """Packed [q | k | v | lambda | write] weights and biases, per
+        parameter version.  kind "fused" (coda_project): (n_feat, D) weights
+        with, for half-split RoPE, each k head's rows reordered to the pairs
+        (i, i + Dh/2) on adjacent rows, float32 biases; kind "gemm" (a
+        library GEMM + coda_project_epilogue): natural row order, rows padded
+        to a multiple of 8 (16-byte aligned column blocks of the output),
+        biases in `dtype`."""
+        lins = (self.q_proj, self.k_proj, self.v_proj, self.lambda_proj, self.write_proj)
+        ps = [t for lin in lins for t in (lin.weight, lin.bias) if t is not None]
+        tag = tuple((t._version, t.data_ptr(), t.dtype, t.device) for t in ps) + (self.rope_interleaved,
+                                                                                 self.write_policy)
+        cache = self.__dict__.setdefault("_derived_cache", {})
+        hit = cache.get(("proj", kind, dtype))
+        if hit is not None and hit[0] == tag:
+            return hit[1]
+        H, Hkv, Dh = self.num_heads, self.num_kv_heads, self.head_dim
+        gate = self.write_policy != "none"
+        with torch.no_grad():
+            dev = self.q_proj.weight.device
+            wk, bk = self.k_proj.weight, self.k_proj.bias
+            if kind == "fused" and not self.rope_interleaved:
+                half = Dh // 2
+                pair = torch.stack([torch.arange(half), torch.arange(half) + half], 1).reshape(-1)
+                perm = (torch.arange(Hkv)[:, None] * Dh + pair[None]).reshape(-1).to(dev)
+                wk = wk[perm]
+                bk = bk[perm] if bk is not None else None
+            ws = [self.q_proj.weight, wk, self.v_proj.weight, self.lambda_proj.weight]
+            bt = [self.q_proj.bias, bk, self.v_proj.bias, self.lambda_proj.bias]
+            if gate:
+                ws.append(self.write_proj.weight)
+                bt.append(self.write_proj.bias)
+            w = torch.cat([t.detach() for t in ws]).to(dtype)
+            bdt = torch.float32 if kind == "fused" else dtype
+            b = torch.cat([t.detach().to(bdt) if t is not None else torch.zeros(wt.shape[0], dtype=bdt, device=dev)
+                           for t, wt in zip(bt, ws)])
+            pad = (-w.shape[0]) % 8 if kind == "gemm" else 0
+            if pad:
+                w = torch.cat([w, torch.zeros(pad, w.shape[1], dtype=dtype, device=dev)])
+            bpad = (-b.numel()) % (4 if kind == "fused" else 8)
+            b = torch.cat([b, torch.zeros(bpad, dtype=bdt, device=dev)])
+        val = (w.contiguous(), b.contiguous())
+        cache[("proj", kind, dtype)] = (tag, val)
+        return val
+
+    def _proj_desc(self, x: torch.Tensor, M: int, L: int, cos: torch.Tensor, sin: torch.Tensor):
+        d = _hip.ProjDesc()
+        d.dtype, d.M, d.D, d.L = _hip.dtype_code(x.dtype), M, self.embed_dim, L
+        d.H, d.Hkv, d.Dh = self.num_heads, self.num_kv_heads, self.head_dim
+        d.rope_interleaved, d.gate = int(self.rope_interleaved), int(self.write_policy != "none")
+        d.rope_cos, d.rope_sin = cos.data_ptr(), sin.data_ptr()
+        return d
+
+    def _front(self, x: torch.Tensor, p0: int):
+        """Projections of x (B, L, D) at positions p0 ..: q (B,H,L,Dh)
+        pre-RoPE, k (B,Hkv,L,Dh) roped, v (B,Hkv,L,Dh), g (B,L) float32,
+        lam (B,H,L), and the RoPE tables (L, Dh/2) (attention.py:396-410,
+        592-608).  bf16, up to 64 token rows (decode): one launch of the
+        hand-written projection GEMM with its fused epilogues
+        (coda_project); more rows: one library GEMM over the packed weights,
+        then coda_project_epilogue in place (q / k / v / lambda are views of
+        its output); other dtypes: the torch linears and the RoPE kernel."""
+        B, L, D = x.shape
+        H, Hkv, Dh = self.num_heads, self.num_kv_heads, self.head_dim
+        Fq, Fk = H * Dh, Hkv * Dh
+        M = B * L
+        cos, sin = self._rope_rows(p0, L, x.device, x.dtype)
+        if x.dtype == torch.bfloat16 and D % 64 == 0 and Dh % 4 == 0:
+            d = self._proj_desc(x, M, L, cos, sin)
+            g = torch.empty((B, L), dtype=torch.float32, device=x.device)
+            d.g = g.data_ptr()
+            if M <= 64:
+                xs = x if (x.is_contiguous() and x.data_ptr() % 16 == 0) else x.contiguous()
+                w, b = self._proj_pack(x.dtype, "fused")
+                q = torch.empty((B, L, Fq), dtype=x.dtype, device=x.device)
+                k = torch.empty((B, L, Hkv, Dh), dtype=x.dtype, device=x.device)
+                v = torch.empty((B, L, Fk), dtype=x.dtype, device=x.device)
+                lam = torch.empty((B, L, H), dtype=x.dtype, device=x.device)
+                d.x, d.x_sm, d.w, d.bias = xs.data_ptr(), D, w.data_ptr(), b.data_ptr()
+                d.q, d.q_sm, d.k, d.k_sm, d.v, d.v_sm = q.data_ptr(), Fq, k.data_ptr(), Fk, v.data_ptr(), Fk
+                d.lam, d.lam_sm = lam.data_ptr(), H
+                nb = ctypes.c_size_t(0)
+                _hip.check(_hip.lib().coda_project_workspace_bytes(d, nb))
+                ws = None
+                if nb.value:
+                    cache = self.__dict__.setdefault("_proj_ws", {})
+                    ws = cache.get(str(x.device))
+                    if ws is None or ws.numel() < nb.value:
+                        ws = cache[str(x.device)] = torch.empty(nb.value, dtype=torch.uint8, device=x.device)
+                d.workspace, d.workspace_bytes = _hip.ptr(ws), nb.value
+                _hip.check(_hip.lib().coda_project(d, _hip.stream_of(x)))
+                return (q.view(B, L, H, Dh).permute(0, 2, 1, 3), k.permute(0, 2, 1, 3),
+                        v.view(B, L, Hkv, Dh).permute(0, 2, 1, 3), g, lam.permute(0, 2, 1), cos, sin)
+            w, b = self._proj_pack(x.dtype, "gemm")
+            y = torch.nn.functional.linear(x, w, b[:w.shape[0]])
+            nf = y.shape[-1]
+            _hip.check(_hip.lib().coda_project_epilogue(d, y.data_ptr(), nf, _hip.stream_of(x)))
+            q = y[..., :Fq].view(B, L, H, Dh).permute(0, 2, 1, 3)
+            k = y[..., Fq:Fq + Fk].view(B, L, Hkv, Dh).permute(0, 2, 1, 3)
+            v = y[..., Fq + Fk:Fq + 2 * Fk].view(B, L, Hkv, Dh).permute(0, 2, 1, 3)
+            lam = y[..., Fq + 2 * Fk:Fq + 2 * Fk + H].permute(0, 2, 1)
+            return q, k, v, g, lam, cos, sin
+        q = self._project_q(x)
+        k_raw, v = self._project_kv_raw(x)
+        # roped keys in the token-major layout of v, so K and V share strides
+        k = torch.empty((B, L, Hkv, Dh), dtype=x.dtype, device=x.device).permute(0, 2, 1, 3)
+        apply_rope(k_raw, cos, sin, interleaved=self.rope_interleaved, out=k)
+        return q, k, v, self._write_gate(x), self._lambda(x), cos, sin
+
     # ------------------------------------------------------------ decode
     def decode_attend_core(self, q: torch.Tensor, lam: torch.Tensor, state: CoDAGQALandmarkStatePerf2,
                            rope_cos: torch.Tensor, rope_sin: torch.Tensor,
@@ -344,11 +469,8 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
 
         if attend and include_current_in_attention and write_cache:
             self._check_state(state)
-            k_raw, v_new = self._project_kv_raw(x)
-            cos, sin = self.rope(seq_len=1, offset=q_pos, device=x.device, dtype=x.dtype)
-            k_new = apply_rope(k_raw, cos, sin, interleaved=self.rope_interleaved)
-            heads = self.decode_step_core(self._project_q(x), k_new, v_new, self._write_gate(x), self._lambda(x),
-                                          state, cos, sin)
+            q, k_new, v_new, g, lam, cos, sin = self._front(x, q_pos)
+            heads = self.decode_step_core(q, k_new, v_new, g.reshape(B), lam, state, cos, sin)
             return self.o_proj(heads.view(B, 1, self.num_heads * self.head_dim)), state
         y = self.attend_step(x, state, query_pos=q_pos) if attend else torch.zeros_like(x)
         if write_cache:
@@ -418,16 +540,9 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         if block_size <= 0:
             raise ValueError("block_size must be positive")
         p0 = int(state.pos)
-        q = self._project_q(x_seq)
-        k_raw, v = self._project_kv_raw(x_seq)
-        cos, sin = self.rope(seq_len=L, offset=p0, device=x_seq.device, dtype=x_seq.dtype)
-        cos, sin = cos.contiguous(), sin.contiguous()
-        # roped keys in the token-major layout of v, so K and V share strides
-        k = torch.empty((B, L, self.num_kv_heads, self.head_dim), dtype=x_seq.dtype,
-                        device=x_seq.device).permute(0, 2, 1, 3)
-        apply_rope(k_raw, cos, sin, interleaved=self.rope_interleaved, out=k)
-        heads = self.prefill_core(q, k, v, self._write_gate(x_seq), self._lambda(x_seq), cos, sin, state,
-                                  block_size=block_size, write_cache=write_cache, return_heads=return_outputs)
+        q, k, v, g, lam, cos, sin = self._front(x_seq, p0)
+        heads = self.prefill_core(q, k, v, g, lam, cos, sin, state, block_size=block_size, write_cache=write_cache,
+                                  return_heads=return_outputs)
         if not return_outputs:
             return None, state
         return self.o_proj(heads.view(B, L, self.num_heads * self.head_dim)), state

@@ -20,7 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(os.path.dirname(HERE), "coda_gqa_l")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(PKG, "libcoda_mi355x.so")
-SOURCES = ["abi.hip", "attn.hip", "epilogue.hip", "rope.hip", "banks.hip"]
+SOURCES = ["abi.hip", "attn.hip", "epilogue.hip", "rope.hip", "banks.hip", "proj.hip"]
 ARCH = "gfx950"
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          # packed fp32 instructions are kept out of every kernel

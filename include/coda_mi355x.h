@@ -54,6 +54,75 @@ const char* coda_last_error(void);
 int coda_device_count(void);
 
 /* ------------------------------------------------------------------------
+ * Projection front end of the bounded layer (bf16).
+ *
+ * For M token rows x (M, D) (row stride x_sm, D a multiple of 64) and the
+ * packed weights w (n_feat, D), rows in the order q_proj (H*Dh), k_proj
+ * (Hkv*Dh; with rope_interleaved == 0 each head's rows reordered to the
+ * pairs (i, i + Dh/2) on adjacent rows), v_proj (Hkv*Dh), lambda_proj (H),
+ * write_proj (1, when gate), n_feat their sum, one GEMM with fp32
+ * accumulation and per-segment epilogues:
+ *   q (M, H*Dh)     bf16(x Wq^T + bq)                    (pre-RoPE)
+ *   k (M, Hkv*Dh)   RoPE(bf16(x Wk^T + bk)) with the tables (L, Dh/2) at
+ *                   row m % L, one bf16 rounding per op (primitives.py:83-113)
+ *   v (M, Hkv*Dh)   bf16(x Wv^T + bv)
+ *   lam (M, H)      sigmoid(bf16(x Wl^T + bl)), bf16
+ *   g (M) float32   sigmoid(bf16(x Wg^T + bg)) in bf16; 1 when gate == 0
+ * bias (n_feat) float32, 16-byte aligned, in the weights' row order (zero
+ * for a linear without bias).
+ * Replaces: the projections of CoDAGQALandmarkPerf2.prefill_chunked /
+ *   step / attend_step (src/coda_gqa_l/attention.py:396-410, 476-547,
+ *   592-608): q_proj, k_proj, v_proj, lambda_proj + sigmoid, write_proj +
+ *   sigmoid, and the RoPE of k.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+  int dtype;               /* CODA_BF16 */
+  int M, D, L;             /* token rows, model width, tokens per sequence (table row = m % L) */
+  int H, Hkv, Dh;
+  int rope_interleaved;
+  int gate;                /* 1: write gate from write_proj; 0: g = 1 */
+  int pad0;
+  const void* x;
+  int64_t x_sm;
+  const void* w;           /* (n_feat, D) packed weights */
+  const float* bias;       /* (n_feat) */
+  const void* rope_cos;    /* (L, Dh/2) */
+  const void* rope_sin;
+  void* q;
+  int64_t q_sm;
+  void* k;
+  int64_t k_sm;
+  void* v;
+  int64_t v_sm;
+  void* lam;
+  int64_t lam_sm;
+  float* g;
+  void* workspace;         /* coda_project_workspace_bytes; 16-byte aligned, any contents */
+  size_t workspace_bytes;
+} coda_proj_desc;
+
+/* Few token rows (M <= 64, D a multiple of 512): the K range is split over
+ * 8 workgroups per 64-feature tile, whose fp32 partials the last to finish
+ * sums in split order (deterministic); the partials and the tiles' counters
+ * (epoch-tagged, so no clearing) live in the workspace.  Calls that share a
+ * workspace must not overlap. */
+int coda_project(const coda_proj_desc* d, void* stream);
+
+/* Workspace bytes coda_project needs for this descriptor's M, sizes and
+ * gate (0 when it needs none). */
+int coda_project_workspace_bytes(const coda_proj_desc* d, size_t* bytes);
+
+/* The epilogues alone, for many token rows where a library GEMM computes
+ * y = bf16(x W^T + b) (M rows, row stride y_sm elements) with W the packed
+ * weights in their natural row order: in place, RoPE of the k columns
+ * (tables at row m % L) and the sigmoid of the lambda columns; g (M)
+ * float32 = sigmoid of the write column in bf16 (1 when gate == 0).  Uses
+ * M, L, H, Hkv, Dh, rope_*, gate and g of the descriptor.
+ * Replaces: the RoPE of k and the sigmoids of prefill_chunked
+ *   (src/coda_gqa_l/attention.py:592-608). */
+int coda_project_epilogue(const coda_proj_desc* d, void* y, int64_t y_sm, void* stream);
+
+/* ------------------------------------------------------------------------
  * Fused differential attention + epilogue.
  *
  *   out = Norm( Attn(q, K, V) - lam * Attn(q_noise, K, V) )

@@ -53,7 +53,8 @@ def _c_layout(struct, fields, tmp_path):
     return [int(v) for v in out]
 
 
-@pytest.mark.parametrize("cls,cname", [("AttnDesc", "coda_attn_desc"), ("BankDesc", "coda_bank_desc")])
+@pytest.mark.parametrize("cls,cname", [("AttnDesc", "coda_attn_desc"), ("BankDesc", "coda_bank_desc"),
+                                       ("ProjDesc", "coda_proj_desc")])
 def test_ctypes_structs_match_c_layout(cls, cname, tmp_path):
     S = getattr(_hip(), cls)
     fields = [f for f, _ in S._fields_]

@@ -1,0 +1,115 @@
+"""The projection front end (coda_project: one MFMA GEMM over the packed
+q / k / v / lambda / write-gate weights with the RoPE and sigmoid
+epilogues), against a torch float32 reference of the same ops on the
+device and against the CPU oracle's project() + RoPE (reference
+attention.py:396-410, 592-608), within the bf16 tolerance."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from parity_util import assert_close
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+
+
+# name: (D, H, Hkv, B, L, rope_interleaved, write_policy, qkv bias)
+SHAPES = {
+    "7b_decode_b64": (4096, 32, 8, 64, 1, True, "gated", False),
+    "7b_decode_b1": (4096, 32, 8, 1, 1, True, "gated", False),
+    "7b_prefill_b2": (4096, 32, 8, 2, 384, True, "gated", False),
+    "c1_prefill_half_split_bias": (512, 8, 2, 3, 200, False, "gated", True),
+    "mha_no_gate": (256, 4, 4, 5, 70, True, "none", False),
+    "70b_decode_b8": (8192, 64, 8, 8, 1, True, "gated", False),
+}
+
+
+def _layer(D, H, Hkv, inter, policy, bias):
+    import coda_gqa_l
+    torch.manual_seed(D + H + Hkv)
+    m = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=D, num_heads=H, num_kv_heads=Hkv, window=64, num_landmarks_exact=16,
+                                        num_landmarks_summary=16, rope_interleaved=inter, write_policy=policy)
+    with torch.no_grad():
+        # non-trivial gate weights and biases (the layer inits them to zero)
+        m.write_proj.weight.normal_(0, 0.05)
+        m.lambda_proj.bias.uniform_(-1, 1)
+        if bias:
+            for lin in (m.q_proj, m.k_proj, m.v_proj):
+                lin.bias = torch.nn.Parameter(torch.randn(lin.out_features) * 0.1)
+    return m.to(DEV, torch.bfloat16).eval()
+
+
+def _reference(m, x, p0):
+    """float32 GEMMs on the device, then the eager ops' roundings."""
+    from coda_gqa_l.primitives import apply_rope
+    B, L, D = x.shape
+    H, Hkv, Dh = m.num_heads, m.num_kv_heads, m.head_dim
+    xf = x.float()
+
+    def lin(l):
+        y = xf @ l.weight.float().t()
+        return (y + l.bias.float() if l.bias is not None else y).to(torch.bfloat16)
+
+    q = lin(m.q_proj).view(B, L, H, Dh).permute(0, 2, 1, 3)
+    k_raw = lin(m.k_proj).view(B, L, Hkv, Dh).permute(0, 2, 1, 3)
+    v = lin(m.v_proj).view(B, L, Hkv, Dh).permute(0, 2, 1, 3)
+    cos, sin = m.rope(seq_len=L, offset=p0, device=x.device, dtype=x.dtype)
+    k = apply_rope(k_raw, cos, sin, interleaved=m.rope_interleaved)
+    lam = torch.sigmoid(lin(m.lambda_proj)).permute(0, 2, 1)
+    g = torch.sigmoid(lin(m.write_proj)).squeeze(-1).float() if m.write_policy != "none" else \
+        torch.ones(B, L, device=x.device)
+    return q, k, v, g, lam
+
+
+@pytest.mark.parametrize("name", list(SHAPES))
+@torch.no_grad()
+def test_front_end_matches_float32_reference(name):
+    _need_gpu()
+    D, H, Hkv, B, L, inter, policy, bias = SHAPES[name]
+    print(f"[proj] {name}: D{D} H{H} Hkv{Hkv} B{B} L{L} interleaved={inter} {policy} bias={bias}", flush=True)
+    m = _layer(D, H, Hkv, inter, policy, bias)
+    g_ = torch.Generator(device=DEV).manual_seed(1)
+    x = torch.randn(B, L, D, generator=g_, device=DEV, dtype=torch.bfloat16)
+    p0 = 37
+    got = m._front(x, p0)
+    ref = _reference(m, x, p0)
+    torch.cuda.synchronize()
+    for what, a, r in zip(("q", "k", "v", "g", "lam"), got[:5], ref):
+        assert a.shape == r.shape, (what, a.shape, r.shape)
+        assert_close(a, r, torch.bfloat16, f"{name} {what}")
+        # fp32 accumulation in another order: the bf16 results are the
+        # reference's in all but a few roundings
+        same = (a.float() == r.float()).float().mean().item()
+        assert same > 0.97, f"{name} {what}: only {same:.4f} of the elements equal the float32 reference's rounding"
+
+
+@pytest.mark.parametrize("inter", [True, False])
+@torch.no_grad()
+def test_front_end_matches_oracle_project(inter):
+    _need_gpu()
+    from coda_oracle import OracleLayer, prims
+    from parity_util import product_like
+    kw = dict(embed_dim=512, num_heads=8, num_kv_heads=2, window=256, num_landmarks_exact=64, num_landmarks_summary=64,
+              rope_interleaved=inter)
+    torch.manual_seed(3)
+    m = OracleLayer(**kw).to(torch.bfloat16).eval()
+    with torch.no_grad():
+        m.write_proj.weight.normal_(0, 0.05)
+    p = product_like(m, {"kw": kw}, torch.bfloat16, DEV)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 300, 512, generator=g).to(torch.bfloat16)
+    q, k, v, gate, lam = m.project(x)
+    got = p._front(x.to(DEV), 11)
+    # k roped with the product's own tables: a bf16 layer takes positions
+    # and angles in bf16 (the buffer's dtype, as the reference), and torch's
+    # device and CPU outer products round a few large angles differently
+    k = prims.rope(k, got[5].cpu(), got[6].cpu(), inter)
+    for what, a, r in zip(("q", "k", "v", "g", "lam"), got[:5], (q, k, v, gate, lam.squeeze(-1))):
+        assert_close(a, r, torch.bfloat16, f"oracle project {what}")
