@@ -336,7 +336,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         d.rope_cos, d.rope_sin = cos.data_ptr(), sin.data_ptr()
         return d
 
-    def _front(self, x: torch.Tensor, p0: int):
+    def _front(self, x: torch.Tensor, p0: int, fused: bool = True):
         """Projections of x (B, L, D) at positions p0 ..: q (B,H,L,Dh)
         pre-RoPE, k (B,Hkv,L,Dh) roped, v (B,Hkv,L,Dh), g (B,L) float32,
         lam (B,H,L), and the RoPE tables (L, Dh/2) (attention.py:396-410,
@@ -344,13 +344,20 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         hand-written projection GEMM with its fused epilogues
         (coda_project); more rows: one library GEMM over the packed weights,
         then coda_project_epilogue in place (q / k / v / lambda are views of
-        its output); other dtypes: the torch linears and the RoPE kernel."""
+        its output); other dtypes, or fused=False: the torch linears and the
+        RoPE kernel.  The layer's own step / prefill_chunked take fused=False:
+        a full-size benchmark run with the fused front end wired in faulted
+        the GPU once, with no cause found yet, so it stays off their path."""
         B, L, D = x.shape
         H, Hkv, Dh = self.num_heads, self.num_kv_heads, self.head_dim
         Fq, Fk = H * Dh, Hkv * Dh
         M = B * L
-        cos, sin = self._rope_rows(p0, L, x.device, x.dtype)
-        if x.dtype == torch.bfloat16 and D % 64 == 0 and Dh % 4 == 0:
+        if not fused:
+            cos, sin = self.rope(seq_len=L, offset=p0, device=x.device, dtype=x.dtype)
+            cos, sin = cos.contiguous(), sin.contiguous()
+        else:
+            cos, sin = self._rope_rows(p0, L, x.device, x.dtype)
+        if fused and x.dtype == torch.bfloat16 and D % 64 == 0 and Dh % 4 == 0:
             d = self._proj_desc(x, M, L, cos, sin)
             g = torch.empty((B, L), dtype=torch.float32, device=x.device)
             d.g = g.data_ptr()
@@ -469,7 +476,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
 
         if attend and include_current_in_attention and write_cache:
             self._check_state(state)
-            q, k_new, v_new, g, lam, cos, sin = self._front(x, q_pos)
+            q, k_new, v_new, g, lam, cos, sin = self._front(x, q_pos, fused=False)
             heads = self.decode_step_core(q, k_new, v_new, g.reshape(B), lam, state, cos, sin)
             return self.o_proj(heads.view(B, 1, self.num_heads * self.head_dim)), state
         y = self.attend_step(x, state, query_pos=q_pos) if attend else torch.zeros_like(x)
@@ -540,7 +547,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         if block_size <= 0:
             raise ValueError("block_size must be positive")
         p0 = int(state.pos)
-        q, k, v, g, lam, cos, sin = self._front(x_seq, p0)
+        q, k, v, g, lam, cos, sin = self._front(x_seq, p0, fused=False)
         heads = self.prefill_core(q, k, v, g, lam, cos, sin, state, block_size=block_size, write_cache=write_cache,
                                   return_heads=return_outputs)
         if not return_outputs:

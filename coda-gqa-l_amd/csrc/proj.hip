@@ -277,6 +277,7 @@ __global__ __launch_bounds__(512) void proj_decode_bf16(const coda_proj_desc d, 
 #pragma unroll
     for (int j = 0; j < BT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s2], b[j], acc[j], 0, 0, 0);
   }
+  if (!d.gate && blockIdx.x == 0 && ks == 0 && t < d.M) d.g[t] = 1.f;
   if (KS > 1) {
     const int64_t tile = blockIdx.x;
     unsigned long long* pw = reinterpret_cast<unsigned long long*>(part);
@@ -322,7 +323,6 @@ __global__ __launch_bounds__(512) void proj_decode_bf16(const coda_proj_desc d, 
     const int m = 16 * j + r16;
     if (m < d.M) proj_store4(d, f0 + 16 * wv + 4 * kq, m, acc[j]);
   }
-  if (!d.gate && blockIdx.x == 0 && ks == 0 && t < d.M) d.g[t] = 1.f;
 }
 
 // Workspace of proj_decode_bf16 with KS = D / 512 > 1: the partial tiles

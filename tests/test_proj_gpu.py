@@ -11,7 +11,9 @@ import torch
 
 from parity_util import assert_close
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.skip(
+    reason="fused projection front end off: a full-size bench run with it on the layer path faulted the GPU; "
+           "cause not found yet, so its kernels stay off the GPU")]
 DEV = "cuda:0"
 
 
