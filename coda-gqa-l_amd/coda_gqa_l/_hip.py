@@ -14,8 +14,11 @@ from typing import Optional
 
 import torch
 
+from ._srchash import source_hash
+
 LIB_NAME = "libcoda_mi355x.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+_DEFAULT_LIB_PATH = LIB_PATH
 
 CODA_F32, CODA_BF16, CODA_F16 = 0, 1, 2
 DTYPE_CODE = {torch.float32: CODA_F32, torch.bfloat16: CODA_BF16, torch.float16: CODA_F16}
@@ -81,6 +84,7 @@ _lib: Optional[ctypes.CDLL] = None
 _SIGS = {
     "coda_abi_version": (_i32, []),
     "coda_last_error": (ctypes.c_char_p, []),
+    "coda_source_hash": (ctypes.c_char_p, []),
     "coda_device_count": (_i32, []),
     "coda_attn_workspace_bytes": (_i32, [ctypes.POINTER(AttnDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "coda_diff_attn_fwd": (_i32, [ctypes.POINTER(AttnDesc), _vp]),
@@ -112,6 +116,20 @@ _SIGS = {
 }
 
 
+def _check_fresh(L: ctypes.CDLL) -> None:
+    """The in-tree library must be built from the sources beside it (a
+    library loaded from another path, LIB_PATH changed, is not checked)."""
+    if os.path.abspath(LIB_PATH) != _DEFAULT_LIB_PATH:
+        return
+    want = source_hash()
+    if want is None:
+        return
+    have = L.coda_source_hash().decode(errors="replace")
+    if have != want:
+        raise RuntimeError(f"{LIB_NAME} was built from other sources (hash {have}) than the ones beside it "
+                           f"(hash {want}); rebuild it: `python coda-gqa-l_amd/csrc/build.py`")
+
+
 def lib() -> ctypes.CDLL:
     """Load the library once; raise if it has not been built."""
     global _lib
@@ -127,6 +145,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(L, name)
                 fn.restype = res
                 fn.argtypes = args
+            _check_fresh(L)
             _lib = L
     return _lib
 

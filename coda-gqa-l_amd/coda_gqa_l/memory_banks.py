@@ -507,7 +507,7 @@ class MemoryBankMixin:
             tr = torch.full((B, 2 * Te + Ts), -1, dtype=torch.int32, device=k_blk.device)
         d = self._bank_desc(st, eta, metrics, fr, tr)
         ws_ptr, ws_bytes = (workspace.data_ptr(), workspace.numel()) if workspace is not None else (None, 0)
-        if k_blk.stride() != v_blk.stride():
+        if k_blk.stride() != v_blk.stride() or k_blk.stride(-1) != 1:
             v_blk = v_blk.contiguous()
             k_blk = k_blk.contiguous()
         _hip.check(_hip.lib().coda_block_write(

@@ -114,7 +114,11 @@ def attention_desc(*, q: torch.Tensor, rope_cos: Optional[torch.Tensor], rope_si
     (torch SDPA is_causal), 0 none; lam (B,H,Lq) view.
     """
     B, H, Lq, Dh = q.shape
-    keep = []
+    if out.stride(-1) != 1:
+        raise RuntimeError("bounded attention: out must have unit stride over head_dim (the kernels write "
+                           "whole 16-byte channel runs)")
+    q = _last_dim_contig(q)
+    keep = [q]
     d = _hip.AttnDesc()
     d.dtype = _hip.dtype_code(q.dtype)
     d.B, d.H, d.Lq, d.Dh = B, H, Lq, Dh
@@ -124,7 +128,7 @@ def attention_desc(*, q: torch.Tensor, rope_cos: Optional[torch.Tensor], rope_si
         d.rope_cos, d.rope_sin = rope_cos.data_ptr(), rope_sin.data_ptr()
     d.rope_interleaved = int(bool(rope_interleaved))
     Hkv = None
-    if k_prefix is not None and k_prefix.stride() != v_prefix.stride():
+    if k_prefix is not None and (k_prefix.stride() != v_prefix.stride() or k_prefix.stride(-1) != 1):
         k_prefix, v_prefix = k_prefix.contiguous(), v_prefix.contiguous()
         keep += [k_prefix, v_prefix]
     if k_block is not None and (k_block.stride() != v_block.stride() or k_block.stride(-1) != 1):

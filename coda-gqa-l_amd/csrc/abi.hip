@@ -39,6 +39,12 @@ extern "C" int coda_abi_version(void) { return CODA_ABI_VERSION; }
 
 extern "C" const char* coda_last_error(void) { return coda::g_last_error.c_str(); }
 
+// build.py defines it as the hash of the sources it compiled
+#ifndef CODA_SOURCE_HASH
+#define CODA_SOURCE_HASH "unknown"
+#endif
+extern "C" const char* coda_source_hash(void) { return CODA_SOURCE_HASH; }
+
 extern "C" int coda_device_count(void) {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess) {

@@ -18,6 +18,9 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.join(os.path.dirname(HERE), "coda_gqa_l")
+sys.path.insert(0, PKG)
+from _srchash import source_hash  # noqa: E402  (no torch import)
+sys.path.pop(0)
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(PKG, "libcoda_mi355x.so")
 SOURCES = ["abi.hip", "attn.hip", "epilogue.hip", "rope.hip", "banks.hip", "proj.hip"]
@@ -42,9 +45,9 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build the MI355X kernels)")
 
 
-def _compile(src: str) -> str:
+def _compile(src: str, tag: str) -> str:
     obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [hipcc(), *FLAGS, f'-DCODA_SOURCE_HASH="{tag}"', "-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
@@ -56,8 +59,10 @@ def _compile(src: str) -> str:
 def build(jobs: int = 0) -> str:
     os.makedirs(OBJ, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 8)
+    # the loader compares this with the sources it finds (coda_source_hash)
+    tag = source_hash() or "unknown"
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda src: _compile(src, tag), SOURCES))
     tmp = LIB + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -50,6 +50,12 @@ int coda_abi_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* coda_last_error(void);
 
+/* Hash of the sources the library was built from (16 hex digits, or
+ * "unknown"); the Python loader refuses a library whose hash differs from
+ * the sources beside it.  No counterpart in the reference, whose epilogue
+ * extension setuptools builds (kernels/coda_diff_epilogue/setup.py). */
+const char* coda_source_hash(void);
+
 /* Number of HIP devices visible (0 on a host without a GPU; never fails). */
 int coda_device_count(void);
 

@@ -39,6 +39,25 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert set(names) <= set(_hip()._SIGS), "ctypes signatures missing for: %s" % (set(names) - set(_hip()._SIGS))
 
 
+def test_library_is_built_from_the_sources_beside_it():
+    from coda_gqa_l import _srchash
+    H = _hip()
+    want = _srchash.source_hash()
+    assert want is not None and len(want) == 16
+    assert H.lib().coda_source_hash().decode() == want
+
+
+def test_loader_refuses_a_library_built_from_other_sources(monkeypatch):
+    H = _hip()
+    H.lib()
+    monkeypatch.setattr(H, "_lib", None)
+    monkeypatch.setattr(H, "source_hash", lambda: "0123456789abcdef")
+    with pytest.raises(RuntimeError, match="built from other sources"):
+        H.lib()
+    monkeypatch.undo()
+    assert H.lib() is not None
+
+
 def _c_layout(struct, fields, tmp_path):
     prog = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){",
             f'printf("%zu\\n", sizeof({struct}));']
