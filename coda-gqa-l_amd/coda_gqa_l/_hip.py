@@ -102,6 +102,7 @@ _SIGS = {
     "coda_block_write": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,
                                 _i32, _i64, _vp, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp]),
     "coda_block_workspace_bytes": (_i32, [ctypes.POINTER(BankDesc), _i32, ctypes.POINTER(ctypes.c_size_t)]),
+    "coda_block_write_check": (_i32, [ctypes.POINTER(BankDesc), _i32, _i32]),
     "coda_block_sync_timeouts": (_i32, [ctypes.POINTER(ctypes.c_uint)]),
     "coda_block_write_noalloc": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,
                                         _i32, _i64, _vp, _i32, _i32, _i32, _vp]),
@@ -128,6 +129,11 @@ def _check_fresh(L: ctypes.CDLL) -> None:
     if have != want:
         raise RuntimeError(f"{LIB_NAME} was built from other sources (hash {have}) than the ones beside it "
                            f"(hash {want}); rebuild it: `python coda-gqa-l_amd/csrc/build.py`")
+
+
+def available() -> bool:
+    """Whether the library is built in place (no load, no HIP call)."""
+    return os.path.exists(LIB_PATH)
 
 
 def lib() -> ctypes.CDLL:

@@ -145,6 +145,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             raise ValueError(f"head_norm_mode must be 'full' or 'identity', got {head_norm_mode!r}")
         self.o_proj = nn.Linear(H * Dh, D, bias=False)
         self._eps = float(eps)
+        self._check_bank_sizes()
 
     # ------------------------------------------------------------ state
     def init_state(self, *, batch_size: int, device: torch.device, dtype: torch.dtype,
@@ -508,6 +509,12 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         head = int(state.recent_idx) if state.recent_filled >= self.window else 0
         filled = int(state.recent_filled)
         if write_cache:
+            te = min(self.exact_candidates_per_block, block_size) if self.Me > 0 else 0
+            ts = min(self.summary_candidates_per_block, block_size) if self.Ms > 0 else 0
+            ck = (B, state.k_buf.dtype, te, ts, self.Me_max, self.Ms_max)
+            if self.__dict__.get("_block_checked") != ck:
+                self._block_check(B, state.k_buf.dtype, te, ts)
+                self.__dict__["_block_checked"] = ck
             plan, kmax, do_e, do_s = self._plan_candidates(state, g, L, block_size)
             ws = self._block_workspace(state, kmax)
             eta = self._eta_f32(q.device, state.k_buf.dtype) if self.Ms > 0 else None

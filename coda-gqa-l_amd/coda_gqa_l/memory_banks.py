@@ -173,6 +173,30 @@ class MemoryBankMixin:
 
         return self._derived("eta", p, (device, dtype), make)
 
+    def _block_check(self, B: int, dtype: torch.dtype, Te: int, Ts: int) -> None:
+        """coda_block_write_check: a clear error, before anything runs, for
+        bank sizes and candidate counts whose chunk update does not fit the
+        kernels' LDS (B = 0: any batch)."""
+        d = _hip.BankDesc()
+        d.dtype, d.B = _hip.dtype_code(dtype), int(B)
+        d.Hkv, d.Dh, d.W, d.Me, d.Ms, d.lf = self.num_kv_heads, self.head_dim, self.window, self.Me_max, \
+            self.Ms_max, self.lf_start
+        d.active_exact, d.active_summary = self.Me_max, self.Ms_max
+        _hip.check(_hip.lib().coda_block_write_check(d, int(Te), int(Ts)))
+
+    def _check_bank_sizes(self) -> None:
+        """At construction: the bank sizes alone (one candidate of each kind)
+        must fit; skipped when the library is not built (every call raises
+        then)."""
+        if not _hip.available():
+            return
+        te = 1 if self.Me_max > 0 and self.exact_candidates_per_block > 0 else 0
+        ts = 1 if self.Ms_max > 0 and self.summary_candidates_per_block > 0 else 0
+        try:
+            self._block_check(0, torch.bfloat16, te, ts)
+        except RuntimeError as e:
+            raise ValueError(f"bank sizes beyond this build's prefill kernels: {e}") from None
+
     def _bank_desc(self, st: CoDAGQALandmarkStatePerf2, eta: Optional[torch.Tensor],
                    metrics: Optional[torch.Tensor], frustrated: Optional[torch.Tensor],
                    trace: Optional[torch.Tensor] = None) -> _hip.BankDesc:

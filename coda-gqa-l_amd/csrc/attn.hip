@@ -3346,9 +3346,16 @@ static int validate_step(const coda_bank_desc* s, const coda_attn_desc* a) {
 
 // the fused decode step kernel: bf16, a full ring, every row of a head's
 // plane in the LDS visibility copy, all query rows in one MFMA tile
+// CODA_DECODE_FUSED=0 sends every decode step through the bank kernel +
+// split attention launches (read at every call, so that one process can
+// compare the two paths)
+static bool fused_step_enabled() {
+  const char* e = getenv("CODA_DECODE_FUSED");
+  return !(e && e[0] == '0');
+}
 static bool fused_step_ok(const coda_bank_desc* s, const coda_attn_desc* a) {
   const int G = a->H / a->Hkv;
-  return s->dtype == CODA_BF16 && (s->Dh == 64 || s->Dh == 128) && 2 * G <= 16 && s->W >= 16 &&
+  return fused_step_enabled() && s->dtype == CODA_BF16 && (s->Dh == 64 || s->Dh == 128) && 2 * G <= 16 && s->W >= 16 &&
          s->Me + s->Ms <= kFusedMaxBank && s->W + s->Me + s->Ms <= kMaxRowsPrefix && 2 * s->lf == s->Dh &&
          a->causal == 0 && a->allowed != nullptr;
 }

@@ -692,25 +692,6 @@ __device__ __forceinline__ Dec dec_of(const coda_bank_desc& s, const BlockGeom& 
 // Summary candidates per decide workgroup.
 static constexpr int kDecideChunk = 8;
 
-// fp32 copy global -> LDS by the workgroup, 16 independent loads per thread
-// in flight before their stores.
-__device__ __forceinline__ void wg_copy_f32(float* dst, const float* src, int n) {
-  const int nt = blockDim.x;
-  for (int base = threadIdx.x; base < n; base += 16 * nt) {
-    float x[16];
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int i = base + u * nt;
-      x[u] = i < n ? src[i] : 0.f;
-    }
-#pragma unroll
-    for (int u = 0; u < 16; ++u) {
-      const int i = base + u * nt;
-      if (i < n) dst[i] = x[u];
-    }
-  }
-}
-
 // Decisions of one chunk (memory_banks.py:640-697 exact, :866-878 summary).
 // Workgroup x == 0: exact decisions of sequence b from the per-head dots
 // and the metadata snapshot (LRU stamps are committed here, the only
@@ -728,22 +709,13 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
   const Dec dc = dec_of(s, g, ws, b);
   if (x == 0) {
     if (Te == 0) return;
-    float* dl = dsm2;                           // [Hkv][Te][Me]
-    float* sc = dl + Hkv * Te * Me;             // [Te][Me]
-    int* used = reinterpret_cast<int*>(sc + Te * Me);  // [Me]
-    int* idx_l = used + Me;                      // [Te]
-    int* fl_l = idx_l + Te;                      // [Te]
-    wg_copy_f32(dl, ws + (int64_t)b * Hkv * Te * Me, Hkv * Te * Me);
+    // the per-head dots stay in global memory (read once each, coalesced
+    // over slots), so LDS does not grow with the number of heads
+    const float* dg = ws + (int64_t)b * Hkv * Te * Me;  // [Hkv][Te][Me]
+    int* used = reinterpret_cast<int*>(dsm2);           // [Me]
+    int* idx_l = used + Me;                             // [Te]
+    int* fl_l = idx_l + Te;                             // [Te]
     for (int m = t; m < Me; m += blockDim.x) used[m] = sn.used[m];
-    __syncthreads();
-    for (int i = t; i < Te * Me; i += blockDim.x) {
-      float acc = 0.f;
-      for (int hh = 0; hh < Hkv; ++hh) acc += dl[hh * Te * Me + i];
-      float v = E::rnd(acc / (float)Hkv);
-      const int m = i % Me;
-      if (m >= s.active_exact || used[m] == 0) v = neg_fill<T>();
-      sc[i] = v;
-    }
     __syncthreads();
     __shared__ int any_used_s;
     if (wv == 0) {
@@ -766,7 +738,11 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
         float bv = -INFINITY;
         int bi = 0x7fffffff;
         for (int m = lane; m < Me; m += 64) {
-          const float v = sc[tt * Me + m];
+          // head mean in head order (the reference's mean over heads)
+          float acc = 0.f;
+          for (int hh = 0; hh < Hkv; ++hh) acc += dg[((int64_t)hh * Te + tt) * Me + m];
+          float v = E::rnd(acc / (float)Hkv);
+          if (m >= s.active_exact || used[m] == 0) v = neg_fill<T>();
           if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
         }
         wave_argmax(bv, bi);
@@ -846,31 +822,14 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
   const int t0 = (x - 1) * kDecideChunk;
   const int nt = min(kDecideChunk, Ts - t0);
   if (nt <= 0) return;
-  float* dl = dsm2;  // [Hkv][nt][Ms]
-  const float* dsd = ws + CODA_WS(ws_dot_s, s, g) + (int64_t)b * Hkv * Ts * Ms;
-  {
-    const int per = nt * Ms, total = Hkv * per, ntr = blockDim.x;
-    for (int base = t; base < total; base += 16 * ntr) {
-      float xv[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int i = base + u * ntr;
-        xv[u] = i < total ? dsd[((int64_t)(i / per) * Ts + t0) * Ms + (i % per)] : 0.f;
-      }
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int i = base + u * ntr;
-        if (i < total) dl[i] = xv[u];
-      }
-    }
-  }
-  __syncthreads();
+  // per-head dots read from global memory (coalesced over slots)
+  const float* dsd = ws + CODA_WS(ws_dot_s, s, g) + (int64_t)b * Hkv * Ts * Ms;  // [Hkv][Ts][Ms]
   for (int tt = wv; tt < nt; tt += blockDim.x >> 6) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     for (int m = lane; m < Ms; m += 64) {
       float acc = 0.f;
-      for (int hh = 0; hh < Hkv; ++hh) acc += dl[(hh * nt + tt) * Ms + m];
+      for (int hh = 0; hh < Hkv; ++hh) acc += dsd[((int64_t)hh * Ts + t0 + tt) * Ms + m];
       float v = E::rnd(acc / (float)Hkv);
       if (m >= s.active_summary) v = neg_fill<T>();
       if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
@@ -2057,20 +2016,70 @@ static bool fused_enabled() {
   return !(e && e[0] == '0');
 }
 
+// Launch shapes and dynamic LDS of a chunk's bank update with Te / Ts
+// candidates over `pairs` (sequence, head) pairs, shared by the launcher and
+// coda_block_write_check.  The one-launch kernel: each head over NZ
+// workgroups, about 256 in all (more where one workgroup's LDS would not
+// fit), at most 8 per head and 64 per sequence; nz = 0 when it cannot run.
+struct FusedShape {
+  int nz;
+  size_t lds;
+};
+static FusedShape fused_shape(const coda_bank_desc* s, int esz, int Te, int Ts, int pairs) {
+  FusedShape f{0, 0};
+  if (!(Te <= 64 && Ts <= 64 && Te + Ts > 0 && s->Hkv <= kFusedMaxGroup)) return f;
+  const int nz_max = std::max(1, std::min({kFusedMaxGroup / s->Hkv, 8, Te + Ts}));
+  int NZ = std::max(1, std::min((256 + pairs - 1) / pairs, nz_max));
+  size_t lds = fused_lds(s->Dh, esz, s->Me, s->Ms, Te, Ts, NZ).total;
+  while (lds + 1024 > kLdsMax && NZ < nz_max) lds = fused_lds(s->Dh, esz, s->Me, s->Ms, Te, Ts, ++NZ).total;
+  if (lds + 1024 <= kLdsMax) f = FusedShape{NZ, lds};  // the kernel's own static LDS is under 1 KiB
+  return f;
+}
+// The four-kernel path: candidate rows split over nz_r route workgroups per
+// (sequence, head) (about 512 in all, at least 8 rows each); bank slots over
+// nz_a apply workgroups (about 512 in all), PS summary slots each.
+struct SplitShape {
+  int nz_r, nz_a, PS;
+  size_t lds_route, lds_decide, lds_apply;
+};
+static SplitShape split_shape(const coda_bank_desc* s, int Te, int Ts, int pairs) {
+  const int DH = s->Dh, LF = DH - s->lf, n = Te + Ts;
+  const size_t room = kLdsMax - 1024;  // each kernel's static LDS is under 1 KiB
+  SplitShape p;
+  auto route_lds = [&](int nz) {
+    const int per = (n + nz - 1) / nz;
+    const size_t ne = (size_t)std::min(per, Te), ns = (size_t)std::min(per, Ts);
+    return std::max(sizeof(float) * ((ne > 0 ? (s->Me + ne) * (DH + 4) : 0) + (ns > 0 ? (s->Ms + ns) * (LF + 4) : 0)),
+                    sizeof(sel::Item<int64_t>) * (size_t)s->Me);
+  };
+  // more route workgroups where one's candidate rows would not fit
+  p.nz_r = std::max(1, std::min((512 + pairs - 1) / pairs, (n + 7) / 8));
+  p.lds_route = route_lds(p.nz_r);
+  while (p.lds_route > room && p.nz_r < n) p.lds_route = route_lds(++p.nz_r);
+  p.lds_decide = sizeof(int) * ((size_t)s->Me + 2 * Te);
+  // more apply workgroups where one's summary token lists would not fit
+  const int nz_a_max = std::max(1, std::max(s->Me, s->Ms));
+  p.nz_a = std::max(1, std::min((512 + pairs - 1) / pairs, nz_a_max));
+  p.PS = (s->Ms + p.nz_a - 1) / p.nz_a;
+  p.lds_apply = apply_lds_bytes(s->Ms, Te, Ts, p.PS, LF);
+  while (p.lds_apply > room && p.nz_a < nz_a_max) {
+    ++p.nz_a;
+    p.PS = (s->Ms + p.nz_a - 1) / p.nz_a;
+    p.lds_apply = apply_lds_bytes(s->Ms, Te, Ts, p.PS, LF);
+  }
+  return p;
+}
+
 template <typename T, int DH>
 static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb, const float* gb, BlockGeom g,
                         const int32_t* plan_c, float* ws, hipStream_t st) {
-  const int LF = DH - s->lf;
   const int TT = g.Te > g.Ts ? g.Te : g.Ts;
-  if (g.n_ev > 0 && TT > 0 && g.Te <= 64 && g.Ts <= 64 && s->Hkv <= kFusedMaxGroup && fused_enabled()) {
-    // each head over NZ workgroups: about 256 in all (more where one
-    // workgroup's LDS would not fit), at most 8 per head and 64 per sequence
-    const int pairs = s->B * s->Hkv;
-    const int nz_max = std::max(1, std::min({kFusedMaxGroup / s->Hkv, 8, g.Te + g.Ts}));
-    int NZ = std::max(1, std::min((256 + pairs - 1) / pairs, nz_max));
-    size_t lds = fused_lds(DH, (int)sizeof(T), s->Me, s->Ms, g.Te, g.Ts, NZ).total;
-    while (lds + 1024 > kLdsMax && NZ < nz_max) lds = fused_lds(DH, (int)sizeof(T), s->Me, s->Ms, g.Te, g.Ts, ++NZ).total;
-    if (lds + 1024 <= kLdsMax) {  // the kernel's own static LDS is under 1 KiB
+  const int pairs = s->B * s->Hkv;
+  if (g.n_ev > 0 && TT > 0 && fused_enabled()) {
+    const FusedShape fs = fused_shape(s, (int)sizeof(T), g.Te, g.Ts, pairs);
+    const int NZ = fs.nz;
+    const size_t lds = fs.lds;
+    if (NZ > 0) {
       int rc = lds_limit<block_fused_kernel<T, DH>>(lds, "coda_block_write");
       if (rc) return rc;
       unsigned long long* flags = reinterpret_cast<unsigned long long*>(ws + CODA_WS(ws_sync, *s, g));
@@ -2082,29 +2091,18 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
       return check_launch("block_fused");
     }
   }
+  const SplitShape sp = split_shape(s, g.Te, g.Ts, pairs);
   if (g.n_ev > 0 && TT > 0) {
-    // candidate rows split over nz workgroups per (sequence, head): about
-    // 512 workgroups in all, at least 8 rows each
-    const int n = g.Te + g.Ts, pairs = s->B * s->Hkv;
-    int nz = (512 + pairs - 1) / pairs;
-    nz = std::max(1, std::min(nz, (n + 7) / 8));
-    const int per = (n + nz - 1) / nz;
-    const size_t ne = (size_t)std::min(per, g.Te), ns = (size_t)std::min(per, g.Ts);
-    const size_t lds1 = std::max(sizeof(float) * ((ne > 0 ? (s->Me + ne) * (DH + 4) : 0) +
-                                                  (ns > 0 ? (s->Ms + ns) * (LF + 4) : 0)),
-                                 sizeof(sel::Item<int64_t>) * (size_t)s->Me);
-    int rc = lds_limit<block_route_kernel<T, DH>>(lds1, "coda_block_write");
+    int rc = lds_limit<block_route_kernel<T, DH>>(sp.lds_route, "coda_block_write");
     if (rc) return rc;
-    hipLaunchKernelGGL((block_route_kernel<T, DH>), dim3(s->Hkv + 1, s->B, nz), dim3(256), lds1, st, *s, g,
-                       (const T*)kb, (const T*)vb, gb, plan_c, ws);
+    hipLaunchKernelGGL((block_route_kernel<T, DH>), dim3(s->Hkv + 1, s->B, sp.nz_r), dim3(256), sp.lds_route, st,
+                       *s, g, (const T*)kb, (const T*)vb, gb, plan_c, ws);
     rc = check_launch("block_route");
     if (rc) return rc;
   }
   const int nsc = (g.Ts + kDecideChunk - 1) / kDecideChunk;
   if (g.n_ev > 0 && TT > 0) {
-    const size_t lds_d = std::max(sizeof(float) * ((size_t)s->Hkv * g.Te * s->Me + (size_t)g.Te * s->Me) +
-                                      sizeof(int) * ((size_t)s->Me + 2 * g.Te),
-                                  sizeof(float) * (size_t)s->Hkv * kDecideChunk * s->Ms);
+    const size_t lds_d = sp.lds_decide;
     int rc = lds_limit<block_decide_kernel<T>>(lds_d, "coda_block_write");
     if (rc) return rc;
     hipLaunchKernelGGL((block_decide_kernel<T>), dim3(1 + nsc, s->B), dim3(256), lds_d, st, *s, g, plan_c, ws);
@@ -2112,17 +2110,10 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
     if (rc) return rc;
   }
   if (g.n_ev > 0 && TT > 0) {
-    // bank slots split over nz workgroups per (sequence, head): about 512
-    // workgroups in all
-    const int pairs = s->B * s->Hkv;
-    int nz = (512 + pairs - 1) / pairs;
-    nz = std::max(1, std::min(nz, std::max(s->Me, s->Ms)));
-    const int PS = (s->Ms + nz - 1) / nz;
-    const size_t lds_a = apply_lds_bytes(s->Ms, g.Te, g.Ts, PS, LF);
-    int rc = lds_limit<block_apply_kernel<T, DH>>(lds_a, "coda_block_write");
+    int rc = lds_limit<block_apply_kernel<T, DH>>(sp.lds_apply, "coda_block_write");
     if (rc) return rc;
-    hipLaunchKernelGGL((block_apply_kernel<T, DH>), dim3(s->Hkv, s->B, nz), dim3(kApplyThreads), lds_a, st, *s, g,
-                       (const T*)kb, (const T*)vb, plan_c, ws);
+    hipLaunchKernelGGL((block_apply_kernel<T, DH>), dim3(s->Hkv, s->B, sp.nz_a), dim3(kApplyThreads), sp.lds_apply,
+                       st, *s, g, (const T*)kb, (const T*)vb, plan_c, ws);
     rc = check_launch("block_apply");
     if (rc) return rc;
   }
@@ -2135,6 +2126,27 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
                        (const T*)kb, (const T*)vb, gb);
   }
   return check_launch("block_ring");
+}
+
+extern "C" int coda_block_write_check(const coda_bank_desc* s, int Te, int Ts) {
+  int rc = validate_sizes(s, "coda_block_write_check");
+  if (rc) return rc;
+  CODA_REQUIRE(Te >= 0 && Ts >= 0, "coda_block_write_check: negative candidate counts");
+  if (Te + Ts == 0) return CODA_OK;
+  const int esz = s->dtype == CODA_BF16 ? 2 : 4;
+  // every batch size: one pair stands for a large batch (one workgroup per
+  // (sequence, head) in the four-kernel path), B * Hkv for a given B
+  const int pairs = s->B > 0 ? s->B * s->Hkv : (1 << 20);
+  if (fused_shape(s, esz, Te, Ts, pairs).nz > 0) return CODA_OK;
+  const SplitShape p = split_shape(s, Te, Ts, pairs);
+  const size_t room = kLdsMax - 1024;
+  CODA_REQUIRE(p.lds_route <= room && p.lds_decide <= room && p.lds_apply <= room,
+               "coda_block_write_check: a chunk with %d exact and %d summary candidates at head_dim %d, Me=%d, "
+               "Ms=%d needs %zu / %zu / %zu bytes of LDS (routing / decisions / bank writes), above the %zu a "
+               "workgroup has on gfx950: the norm caches of one head (Me*(Dh+4) + Ms*(Dh/2+4) floats) and the "
+               "summary token lists (Ms*Ts words) must fit",
+               Te, Ts, s->Dh, s->Me, s->Ms, p.lds_route, p.lds_decide, p.lds_apply, room);
+  return CODA_OK;
 }
 
 extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb, int64_t b_sh,

@@ -346,6 +346,16 @@ int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb,
 /* Device scratch for coda_block_write. */
 int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, size_t* bytes);
 
+/* Whether coda_block_write can run chunks with Te exact and Ts summary
+ * candidates for these bank sizes (s->B > 0: at that batch; s->B == 0: at
+ * every batch; no buffers needed): CODA_OK, or CODA_EUNSUP with a message
+ * naming the LDS that the sizes need.  The kernels stage one head's norm
+ * caches in LDS, so Me*(Dh+4) + Ms*(Dh/2+4) floats (plus the candidates)
+ * must fit in a workgroup's 160 KiB.  The reference has no such limit; the
+ * layer calls this at construction so that a configuration beyond it fails
+ * there (memory_banks.py:438-564 is the path it guards). */
+int coda_block_write_check(const coda_bank_desc* s, int Te, int Ts);
+
 /* Number of times, since the library was loaded on the current device, that
  * a workgroup of the one-launch block write gave up waiting for the other
  * heads of its sequence (bounded wait, about 0.1 s; the chunk's results are

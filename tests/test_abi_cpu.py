@@ -196,3 +196,37 @@ def test_product_weights_equal_reference_init():
         m = coda_gqa_l.CoDAGQALandmarkPerf2(**case["kw"]).to(dtype=dtype)
         ck = np.array([checksum(p) for _, p in sorted(m.state_dict().items())])
         np.testing.assert_array_equal(ck, load(name)["weights_ck"])
+
+
+def _sizes_desc(Me, Ms, Dh=128, Hkv=8, B=0, dt=None):
+    H = _hip()
+    d = H.BankDesc()
+    d.dtype = H.CODA_BF16 if dt is None else dt
+    d.B, d.Hkv, d.Dh, d.W, d.Me, d.Ms, d.lf = B, Hkv, Dh, 256, Me, Ms, Dh // 2
+    d.active_exact, d.active_summary = Me, Ms
+    return d
+
+
+@pytest.mark.parametrize("Me,Ms,Te,Ts,ok", [
+    (64, 64, 8, 64, True),        # configs[1] / [2] (medium cache)
+    (128, 128, 8, 64, True),      # configs[4] (large cache)
+    (128, 128, 64, 64, True),
+    (128, 128, 256, 256, True),   # every token of a 256-block a candidate (four-kernel path)
+    (160, 160, 8, 64, True),
+    (256, 256, 1, 1, False),      # one head's norm caches alone exceed a workgroup's LDS
+    (1024, 0, 8, 0, False),
+])
+def test_block_write_check_bounds_the_bank_sizes(Me, Ms, Te, Ts, ok):
+    H = _hip()
+    rc = H.lib().coda_block_write_check(_sizes_desc(Me, Ms), Te, Ts)
+    assert (rc == 0) == ok, H.lib().coda_last_error()
+    if not ok:
+        assert b"LDS" in H.lib().coda_last_error()
+
+
+def test_layer_rejects_bank_sizes_beyond_the_kernels_at_construction():
+    import coda_gqa_l
+    kw = dict(embed_dim=1024, num_heads=8, num_kv_heads=2, window=64, num_landmarks_summary=8)
+    coda_gqa_l.CoDAGQALandmarkPerf2(num_landmarks_exact=128, **kw)
+    with pytest.raises(ValueError, match="LDS"):
+        coda_gqa_l.CoDAGQALandmarkPerf2(num_landmarks_exact=512, **kw)

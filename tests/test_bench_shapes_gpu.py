@@ -192,3 +192,49 @@ def test_block_write_sync_never_gave_up():
     n = ctypes.c_uint(0)
     _hip.check(_hip.lib().coda_block_sync_timeouts(ctypes.byref(n)))
     assert n.value == 0, f"{n.value} workgroups gave up waiting at a block-write sync word"
+
+
+@torch.no_grad()
+def test_many_candidates_split_path_matches_oracle_and_is_batch_independent():
+    """Every evicted token of a 256-block a candidate of both banks (Te = Ts
+    = 256, past the one-launch kernel's 64) at the large cache (Me = Ms =
+    128): the four-launch path, whose route and apply kernels take more
+    workgroups per (sequence, head) where one's LDS would not fit.  B = 4
+    against the oracle; at B = 64 (B * Hkv = 512, one route workgroup would
+    need ~300 KB) the first four sequences equal the B = 4 run bit for bit."""
+    _need_gpu()
+    from coda_oracle import OracleLayer
+    H, Hkv, Dh, W, Me, Ms, L, block, dtype = 16, 8, 128, 256, 128, 128, 768, 256, torch.bfloat16
+    print(f"[many candidates] H{H} Hkv{Hkv} Me{Me} Ms{Ms} Te=Ts=256 L{L}", flush=True)
+    kw = dict(embed_dim=H * Dh, num_heads=H, num_kv_heads=Hkv, window=W, num_landmarks_exact=Me,
+              num_landmarks_summary=Ms, rope_base=1e4, exact_candidates_per_block=256,
+              summary_candidates_per_block=256)
+    torch.manual_seed(51)
+    m = OracleLayer(**kw).to(dtype).eval()
+    p = product_like(m, {"kw": kw}, dtype, DEV)
+    torch.manual_seed(52)
+    st_big = m.init_state(batch_size=64, dtype=dtype)
+    g = torch.Generator().manual_seed(53)
+    q, k, v, gate, lam = _inputs(m, 64, L, dtype, "random", g)
+    # B = 4 against the oracle
+    import dataclasses
+    first4 = lambda st: dataclasses.replace(st, **{f.name: getattr(st, f.name)[:4].clone() for f in
+                                                   dataclasses.fields(st) if torch.is_tensor(getattr(st, f.name))})
+    st_o = first4(st_big)
+    st_p4 = to_product_state(st_o, DEV)
+    _prefill_both(m, p, st_o, st_p4, q[:4], k[:4], v[:4], gate[:4], lam[:4], block, dtype, "many candidates B4")
+    # B = 64 and B = 4 on the device from the same initial state
+    c, s = m.rope_tables(L, 0, dtype)
+    st_p64 = to_product_state(st_big, DEV)
+    h64 = p.prefill_core(q.to(DEV), k.to(DEV), v.to(DEV), gate.to(DEV), lam.squeeze(-1).to(DEV), c.to(DEV),
+                         s.to(DEV), st_p64, block_size=block)
+    st_p4b = to_product_state(first4(st_big), DEV)
+    h4 = p.prefill_core(q[:4].to(DEV), k[:4].to(DEV), v[:4].to(DEV), gate[:4].to(DEV),
+                        lam[:4].squeeze(-1).to(DEV), c.to(DEV), s.to(DEV), st_p4b, block_size=block)
+    torch.cuda.synchronize()
+    assert torch.equal(h64[:4].cpu(), h4.cpu()), "heads of sequences 0-3 depend on the batch"
+    for f in ("k_buf", "v_buf", "allowed", "g_recent", "mem_last_exact", "_exact_v_norm", "_sum_lf_k_norm"):
+        a, b = getattr(st_p64, f), getattr(st_p4b, f)
+        if a is None:
+            continue
+        assert torch.equal(a[:4].cpu(), b.cpu()), f"state field {f} of sequences 0-3 depends on the batch"
