@@ -106,8 +106,9 @@ def prefill_chunk_flops(m, B, blk, n_prefix):
 def run_decode(torch, coda, m, B, prefill_tokens, prefill_call, steps, warmup, block, copy_calib_mib=0):
     """Decode throughput of ``m`` at batch ``B``: the state pre-filled with
     ``prefill_tokens`` N(0,1) tokens, post-projection inputs of every step
-    resident in HBM, then ``warmup`` + ``steps`` calls of the decode step
-    (one launch of the fused step kernel each).  Returns tok/s, wall ms per
+    resident in HBM (k as projected, before RoPE: the step kernel ropes it),
+    then ``warmup`` + ``steps`` calls of the decode step (one launch of the
+    fused step kernel each).  Returns tok/s, wall ms per
     step, kernel ms per step (one pair of HIP events on the launch stream
     around the timed steps), the state and the step inputs."""
     dev = "cuda:0"
@@ -131,7 +132,7 @@ def run_decode(torch, coda, m, B, prefill_tokens, prefill_call, steps, warmup, b
             x = torch.randn(B, 1, E, generator=g, device=dev, dtype=dt)
             q_all.append(m._project_q(x))
             kr, v = m._project_kv_raw(x)
-            k_all.append(coda.apply_rope(kr, cos[i:i + 1], sin[i:i + 1], interleaved=m.rope_interleaved))
+            k_all.append(kr)
             v_all.append(v)
             g_all.append(m._write_gate(x).reshape(B).contiguous())
             lam_all.append(m._lambda(x))
@@ -151,7 +152,7 @@ def run_decode(torch, coda, m, B, prefill_tokens, prefill_call, steps, warmup, b
         # one library call: one launch of the fused decode step kernel (the
         # routing record is carried from the previous step)
         m.decode_step_core(q_all[i], k_all[i], v_all[i], g_all[i], lam_all[i], st, cs_all[i][0], cs_all[i][1],
-                           out=heads)
+                           out=heads, k_roped=False)
 
     with torch.no_grad():
         for i in range(warmup):
@@ -503,7 +504,7 @@ def cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a):
     """The CPU oracle (a restatement of the reference's CPU eager path) on a
     bounded sample of the same decode workload, on this host's cores."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from coda_oracle import OracleLayer, OracleState, banks
+    from coda_oracle import OracleLayer, OracleState, banks, prims
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     dt = torch.bfloat16
@@ -522,7 +523,10 @@ def cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a):
         while True:
             i = n_done % len(q_all)
             qp = so.pos
-            banks.write_one(o, so, k_all[i].cpu(), v_all[i].cpu(), g_all[i].cpu().view(B, 1))
+            # the step's k RoPE (k_all holds the raw projections)
+            c, s_ = o.rope_tables(1, qp, dt)
+            k_new = prims.rope(k_all[i].cpu(), c, s_, o.rope_interleaved)
+            banks.write_one(o, so, k_new, v_all[i].cpu(), g_all[i].cpu().view(B, 1))
             o.attend_core(q_all[i].cpu(), lam_all[i].cpu().unsqueeze(-1), so, qp)
             n_done += 1
             if time.perf_counter() - t0 > a.cpu_seconds or n_done >= 2000:
@@ -530,7 +534,7 @@ def cpu_baseline(torch, m, st, q_all, k_all, v_all, g_all, lam_all, a):
     wall = time.perf_counter() - t0
     return {"value": round(B * n_done / wall, 2), "unit": "tok/s", "cores": torch.get_num_threads(),
             "kind": "port", "sample": f"{n_done} decode steps at batch {B} of the same state "
-                                      f"(banks + attention, post-projection inputs), {wall:.1f} s"}
+                                      f"(k RoPE + banks + attention, post-projection inputs), {wall:.1f} s"}
 
 
 def cpu_legs(torch):

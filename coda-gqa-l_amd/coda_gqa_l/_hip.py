@@ -97,6 +97,8 @@ _SIGS = {
                                                  ctypes.POINTER(ctypes.c_size_t)]),
     "coda_decode_step": (_i32, [ctypes.POINTER(BankDesc), ctypes.POINTER(AttnDesc), _vp, _vp, _i64, _i64, _vp, _i32,
                                 _i32, _i64, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), _vp]),
+    "coda_decode_step_raw_k": (_i32, [ctypes.POINTER(BankDesc), ctypes.POINTER(AttnDesc), _vp, _vp, _i64, _i64, _vp, _i32,
+                                _i32, _i64, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), _vp]),
     "coda_block_plan": (_i32, [_vp, _i32, _i32, _i32, _vp, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp,
                                _i32, _vp]),
     "coda_block_write": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,

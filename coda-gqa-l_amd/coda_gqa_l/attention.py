@@ -422,18 +422,20 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
 
     def decode_step_core(self, q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor, g_new: torch.Tensor,
                          lam: torch.Tensor, state: CoDAGQALandmarkStatePerf2, rope_cos: torch.Tensor,
-                         rope_sin: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                         rope_sin: torch.Tensor, out: Optional[torch.Tensor] = None,
+                         k_roped: bool = True) -> torch.Tensor:
         """Write one token into the bounded cache, then attend with its query
         (attention.py:526-536 after the projections), as one library call.
 
-        q (B,H,1,Dh) pre-RoPE, k_new (B,Hkv,1,Dh) roped, v_new, g_new (B,)
-        float32, lam (B,H,1), tables (1, Dh/2) at the token's position.
-        Returns head outputs (B, 1, H, Dh)."""
+        q (B,H,1,Dh) pre-RoPE, k_new (B,Hkv,1,Dh) roped (k_roped False: the
+        raw k projection, roped inside the step with the same tables), v_new,
+        g_new (B,) float32, lam (B,H,1), tables (1, Dh/2) at the token's
+        position.  Returns head outputs (B, 1, H, Dh)."""
         B = q.shape[0]
         H, Dh = self.num_heads, self.head_dim
         if out is None:
             out = torch.empty((B, 1, H, Dh), dtype=q.dtype, device=q.device)
-        if self._decode_step_planned(state, q, k_new, v_new, g_new, lam, rope_cos, rope_sin, out):
+        if self._decode_step_planned(state, q, k_new, v_new, g_new, lam, rope_cos, rope_sin, out, k_roped):
             return out
         self._check_state(state)
         ct, sn = self._theta_tables(q.dtype)
@@ -443,7 +445,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             v_prefix=state.v_buf, allowed=state.allowed if self.mask_unused_memory else None, k_block=None,
             v_block=None, lam=lam, rms_weight=self._rms_weight(q.dtype), eps=self._eps,
             out=out.permute(0, 2, 1, 3))
-        self._decode_step(state, k_new=k_new, v_new=v_new, g_new=g_new, attn_desc=desc)
+        self._decode_step(state, k_new=k_new, v_new=v_new, g_new=g_new, attn_desc=desc, k_roped=k_roped)
         return out
 
     def attend_step(self, x: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *,
@@ -476,9 +478,12 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             self._write_one(state, k_new=k_new, v_new=v_new, g_new=self._write_gate(x))
 
         if attend and include_current_in_attention and write_cache:
+            # the raw k projection: the step ropes it with the query's tables
             self._check_state(state)
-            q, k_new, v_new, g, lam, cos, sin = self._front(x, q_pos, fused=False)
-            heads = self.decode_step_core(q, k_new, v_new, g.reshape(B), lam, state, cos, sin)
+            cos, sin = self.rope(seq_len=1, offset=q_pos, device=x.device, dtype=x.dtype)
+            k_raw, v_new = self._project_kv_raw(x)
+            heads = self.decode_step_core(self._project_q(x), k_raw, v_new, self._write_gate(x).reshape(B),
+                                          self._lambda(x), state, cos.contiguous(), sin.contiguous(), k_roped=False)
             return self.o_proj(heads.view(B, 1, self.num_heads * self.head_dim)), state
         y = self.attend_step(x, state, query_pos=q_pos) if attend else torch.zeros_like(x)
         if write_cache:

@@ -340,9 +340,11 @@ class MemoryBankMixin:
         st.pos += 1
 
     def _decode_step(self, st: CoDAGQALandmarkStatePerf2, *, k_new: torch.Tensor, v_new: torch.Tensor,
-                     g_new: torch.Tensor, attn_desc) -> None:
+                     g_new: torch.Tensor, attn_desc, k_roped: bool = True) -> None:
         """Write one token then attend (coda_decode_step): the bank update of
         _write_one and the attention described by attn_desc, in one call.
+        k_roped False: k_new is the raw projection, roped by the kernels with
+        the query's tables (coda_decode_step_raw_k).
 
         The library leaves the routing record of the next token in the
         workspace; it is handed back (one launch per token) only while this
@@ -374,7 +376,8 @@ class MemoryBankMixin:
         ws = self._route_workspace(dev, need)
         routed = ctypes.c_int(1 if self.__dict__.get("_route_tag") == self._route_key(st, ws) else 0)
         self.__dict__["_route_tag"] = None
-        _hip.check(L.coda_decode_step(
+        fn = L.coda_decode_step if k_roped else L.coda_decode_step_raw_k
+        _hip.check(fn(
             d, attn_desc, kn.data_ptr(), vn.data_ptr(), kn.stride(0), kn.stride(1), g.data_ptr(),
             int(st.recent_idx), int(st.recent_filled), int(st.pos), _hip.ptr(ws), need, ctypes.byref(routed),
             _hip.stream_of(kn)))
@@ -400,7 +403,7 @@ class MemoryBankMixin:
                 None if w is None else w._version, self.summary_eta_logit._version)
 
     def _decode_step_planned(self, st: CoDAGQALandmarkStatePerf2, q, k_new, v_new, g_new, lam, rope_cos, rope_sin,
-                             out) -> bool:
+                             out, k_roped: bool = True) -> bool:
         """Steady-state decode step through descriptors cached per state:
         full ring, no metrics dict, fixed bank sizes.  Per call only the
         token's pointers change, so the host side is a few field updates and
@@ -429,7 +432,7 @@ class MemoryBankMixin:
             ws = self._route_workspace(q.device, nb.value)
             plan = {"key": key, "attn": a, "bank": d, "keep": (keep, ct, sn, eta, self._rms_weight(dt)),
                     "ws": ws, "ws_ptr": _hip.ptr(ws), "ws_bytes": nb.value, "routed": ctypes.c_int(0),
-                    "fn": _hip.lib().coda_decode_step}
+                    "fn": _hip.lib().coda_decode_step, "fn_raw_k": _hip.lib().coda_decode_step_raw_k}
             self.__dict__["_dplan"] = plan
         a = plan["attn"]
         a.q = q.data_ptr()
@@ -449,7 +452,8 @@ class MemoryBankMixin:
         tag = self._route_key(st, plan["ws"])
         routed.value = 1 if self.__dict__.get("_route_tag") == tag else 0
         self.__dict__["_route_tag"] = None
-        _hip.check(plan["fn"](plan["bank"], a, k_new.data_ptr(), v_new.data_ptr(), kst[0], kst[1], g_new.data_ptr(),
+        fn = plan["fn"] if k_roped else plan["fn_raw_k"]
+        _hip.check(fn(plan["bank"], a, k_new.data_ptr(), v_new.data_ptr(), kst[0], kst[1], g_new.data_ptr(),
                               int(st.recent_idx), int(st.recent_filled), int(st.pos), plan["ws_ptr"],
                               plan["ws_bytes"], ctypes.byref(routed), _hip.stream_of(q)))
         j = int(st.recent_idx)

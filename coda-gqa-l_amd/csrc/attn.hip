@@ -939,7 +939,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
                                                         const bf16_t* __restrict__ v_new, int64_t nb_sb,
                                                         int64_t nb_sh, const float* __restrict__ g_new, int j,
                                                         int64_t pos, const float* __restrict__ rec_in,
-                                                        float* __restrict__ rec_out) {
+                                                        float* __restrict__ rec_out, RopeK rpk) {
   using T = bf16_t;
   constexpr int NC = DH / 32, NM = DH / 16, NW = 4, NVb = (DH + 63) / 64;
   __shared__ __attribute__((aligned(16))) char vt_smem[NW][VtLayout<DH>::kTileBytes];
@@ -982,8 +982,21 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   const __amdgpu_buffer_rsrc_t rv = rsrc((const T*)a.vp + poff, Lbuf * DH * 2);
   const __amdgpu_buffer_rsrc_t rkn = rsrc(kn_row, DH * 2);
   const __amdgpu_buffer_rsrc_t rvn = rsrc(vn_row, DH * 2);
+  // a raw new K (rpk.mode != 0): the table entries of this lane's chunks load
+  // with the new token's tile (interleaved: the 4 pairs of chunk c in
+  // kcs[c]; half-split: the 8 entries chunks q and q + NC/2 share in
+  // kcs[2q], kcs[2q + 1])
+  uint2 kcs[NC], ksn[NC];
   // tile at key kt of the plane, or (nt) the new token in every row
   auto issue = [&](int kt, bool nt, bf16x8_t (&kf)[NC], uint4 (&vv)[4]) {
+    if (nt && rpk.mode) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int e0 = rpk.mode == 1 ? 16 * c + 4 * g4 : 32 * (c >> 1) + 8 * g4 + 4 * (c & 1);
+        kcs[c] = *reinterpret_cast<const uint2*>((const T*)rpk.cs + e0);
+        ksn[c] = *reinterpret_cast<const uint2*>((const T*)rpk.sn + e0);
+      }
+    }
     const int koff = nt ? 16 * g4 : (kt + n) * (DH * 2) + 16 * g4;
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -993,6 +1006,48 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     for (int jj = 0; jj < 4; ++jj)
       vv[jj] = __builtin_bit_cast(
           uint4, __builtin_amdgcn_raw_buffer_load_b128(nt ? rvn : rv, voff + (nt ? 0 : jj * DH * 2), 0, 0));
+  };
+  // RoPE of the new token's K fragments (lane: channels 32 c + 8 g4 .. + 8
+  // of chunk c), each value as the bank wave writes it into the ring
+  auto rope_nt = [&](bf16x8_t (&kf)[NC]) {
+    auto half16 = [](uint32_t w, int hi) { return bf2f((bf16_t)(hi ? (w >> 16) : (w & 0xffffu))); };
+    auto word = [](const uint2& u, int i) { return i ? u.y : u.x; };
+    if (rpk.mode == 1) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 u = __builtin_bit_cast(uint4, kf[c]);
+        uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          float r0, r1;
+          rope_pair_t<T>(half16(w[pp], 0), half16(w[pp], 1), half16(word(kcs[c], pp >> 1), pp & 1),
+                         half16(word(ksn[c], pp >> 1), pp & 1), true, r0, r1);
+          w[pp] = pk_bf16(r0, r1);
+        }
+        kf[c] = __builtin_bit_cast(bf16x8_t, uint4{w[0], w[1], w[2], w[3]});
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < NC / 2; ++q) {
+        const uint4 ul = __builtin_bit_cast(uint4, kf[q]), uh = __builtin_bit_cast(uint4, kf[q + NC / 2]);
+        uint32_t wl[4] = {ul.x, ul.y, ul.z, ul.w}, wh[4] = {uh.x, uh.y, uh.z, uh.w};
+        float rl[8], rh[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint2& cw = kcs[2 * q + (e >> 2)];
+          const uint2& sw = ksn[2 * q + (e >> 2)];
+          rope_pair_t<T>(half16(wl[e >> 1], e & 1), half16(wh[e >> 1], e & 1), half16(word(cw, (e >> 1) & 1), e & 1),
+                         half16(word(sw, (e >> 1) & 1), e & 1), false, rl[e], rh[e]);
+        }
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+          wl[pp] = pk_bf16(rl[2 * pp], rl[2 * pp + 1]);
+          wh[pp] = pk_bf16(rh[2 * pp], rh[2 * pp + 1]);
+        }
+        kf[q] = __builtin_bit_cast(bf16x8_t, uint4{wl[0], wl[1], wl[2], wl[3]});
+        kf[q + NC / 2] = __builtin_bit_cast(bf16x8_t, uint4{wh[0], wh[1], wh[2], wh[3]});
+      }
+    }
   };
   // visibility of this lane's keys kt + 4 g4 + jj of a bank tile: inside
   // [W, Lbuf) and allowed (LDS copy with this step's update applied)
@@ -1264,6 +1319,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     for (int i = 0; i < n1_w; i += 2) {
       const int u0 = wv + 3 * i;
       vm0 = ring_mask(p1_kt(u0), u0 == nR, al0);
+      if (rpk.mode && u0 == nR) rope_nt(kf0);
       __builtin_amdgcn_sched_barrier(0);
       consume(kf0, vv0, vm0);
       issue(p1_kt(u0 + 6), u0 + 6 == nR, kf0, vv0);
@@ -1271,6 +1327,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       if (i + 1 >= n1_w) break;
       const int u1 = u0 + 3;
       vm1 = ring_mask(p1_kt(u1), u1 == nR, al1);
+      if (rpk.mode && u1 == nR) rope_nt(kf1);
       __builtin_amdgcn_sched_barrier(0);
       consume(kf1, vv1, vm1);
       issue(p1_kt(u1 + 6), u1 + 6 == nR, kf1, vv1);
@@ -1360,7 +1417,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the decision (lane 0) is in LDS
     __builtin_amdgcn_wave_barrier();
     const DecodeDecision dd = dec;
-    apply_head<T, DH>(s, b, hk, dd, ke, ve, kn_row, vn_row, j, g_e, lane, nnorm_e, nnorm_s, &newrows[0][0]);
+    apply_head<T, DH>(s, b, hk, dd, ke, ve, kn_row, vn_row, j, g_e, lane, nnorm_e, nnorm_s, &newrows[0][0], rpk);
     if (hk == 0) {
       // metadata of the sequence, and the next record's snapshot of it
       const DStepWs wn = dstep_ws(rec_out, b, Hkv, Me, Ms);
@@ -3363,7 +3420,7 @@ static bool fused_step_ok(const coda_bank_desc* s, const coda_attn_desc* a) {
 template <int DH>
 static int launch_fused_step(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new, const void* v_new,
                              int64_t nb_sb, int64_t nb_sh, const float* g_new, int j, int64_t pos,
-                             const float* rec_in, float* rec_out, hipStream_t st) {
+                             const float* rec_in, float* rec_out, hipStream_t st, RopeK rk) {
   const int R = 2 * (a->H / a->Hkv);
   // record, two rewritten norm rows, ke / ve / vnrm / knrm; then the merge
   size_t lds = sizeof(float) * (size_t)dstep_words(s->Hkv, s->Me, s->Ms) + 2 * 2 * (size_t)DH + 4 * sizeof(float) * DH;
@@ -3373,7 +3430,7 @@ static int launch_fused_step(const coda_bank_desc* s, const coda_attn_desc* a, c
   const int rc = lds_limit<decode_step_bf16<DH>>(lds, "coda_decode_step");
   if (rc) return rc;
   hipLaunchKernelGGL((decode_step_bf16<DH>), dim3(s->Hkv, s->B), dim3(256), lds, st, *a, *s, (const bf16_t*)k_new,
-                     (const bf16_t*)v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out);
+                     (const bf16_t*)v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out, rk);
   return check_launch("decode_step_bf16");
 }
 
@@ -3388,11 +3445,24 @@ extern "C" int coda_decode_step_workspace_bytes(const coda_bank_desc* s, const c
   return CODA_OK;
 }
 
-extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new, const void* v_new,
-                                int64_t nb_sb, int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled,
-                                int64_t pos, void* workspace, size_t workspace_bytes, int* routed, void* stream) {
+// The decode step; raw_k: k_new comes before RoPE and the kernels rope it
+// with the query's tables (the token's own position in a write-then-attend
+// step) wherever they write or read it.
+static int decode_step_impl(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new, const void* v_new,
+                            int64_t nb_sb, int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled,
+                            int64_t pos, void* workspace, size_t workspace_bytes, int* routed, void* stream,
+                            bool raw_k, const char* who) {
   int rc = validate_step(s, a);
   if (rc) return rc;
+  RopeK rk{nullptr, nullptr, 0};
+  if (raw_k) {
+    CODA_REQUIRE(a->rope_cos && a->rope_sin,
+                 "%s: a raw new K is roped with the query's tables: rope_cos / rope_sin of the attention descriptor "
+                 "missing", who);
+    CODA_REQUIRE((uintptr_t)a->rope_cos % 16 == 0 && (uintptr_t)a->rope_sin % 16 == 0,
+                 "%s: RoPE tables must be 16-byte aligned", who);
+    rk = RopeK{a->rope_cos, a->rope_sin, a->rope_interleaved ? 1 : 2};
+  }
   const int have_route = routed != nullptr && *routed != 0;
   if (routed) *routed = 0;
   hipStream_t st = (hipStream_t)stream;
@@ -3400,7 +3470,7 @@ extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a
   coda_attn_desc d = *a;
   if (!step_routed(s, ring_filled)) {
     // ring still filling (or no banks): bank kernel, then the attention kernel
-    rc = coda_decode_write(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, stream);
+    rc = decode_write_impl(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st, rk, who);
     if (rc) return rc;
     d.workspace = workspace;
     d.workspace_bytes = workspace_bytes;
@@ -3425,16 +3495,32 @@ extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a
     if (rc) return rc;
   }
   if (fused_step_ok(s, a)) {
-    rc = s->Dh == 128 ? launch_fused_step<128>(s, a, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st)
-                      : launch_fused_step<64>(s, a, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st);
+    rc = s->Dh == 128
+             ? launch_fused_step<128>(s, a, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st, rk)
+             : launch_fused_step<64>(s, a, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st, rk);
     if (rc == CODA_OK && routed) *routed = 1;
     return rc;
   }
-  rc = launch_decode_bank(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st);
+  rc = launch_decode_bank(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, pos, rec_in, rec_out, st, rk);
   if (rc) return rc;
   d.workspace = (char*)workspace + 2 * rec;
   d.workspace_bytes = workspace_bytes - 2 * rec;
   rc = coda_diff_attn_fwd(&d, stream);
   if (rc == CODA_OK && routed) *routed = 1;
   return rc;
+}
+
+extern "C" int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new, const void* v_new,
+                                int64_t nb_sb, int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled,
+                                int64_t pos, void* workspace, size_t workspace_bytes, int* routed, void* stream) {
+  return decode_step_impl(s, a, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, workspace,
+                          workspace_bytes, routed, stream, false, "coda_decode_step");
+}
+
+extern "C" int coda_decode_step_raw_k(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new,
+                                      const void* v_new, int64_t nb_sb, int64_t nb_sh, const float* g_new,
+                                      int ring_idx, int ring_filled, int64_t pos, void* workspace,
+                                      size_t workspace_bytes, int* routed, void* stream) {
+  return decode_step_impl(s, a, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, workspace,
+                          workspace_bytes, routed, stream, true, "coda_decode_step_raw_k");
 }

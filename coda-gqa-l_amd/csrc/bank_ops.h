@@ -349,14 +349,15 @@ __device__ __forceinline__ float raw_f<float>(uint32_t u) { return __builtin_bit
 //            LF-K-norm cache row refreshed
 //   ring   : slot j <- new token
 // (memory_banks.py:296-331, :381-416, :214-222).  ke / ve: the evicted
-// row of head h as floats; kn_src / vn_src: the new token of head h.
+// row of head h as floats; kn_src / vn_src: the new token of head h (its K
+// roped here first when rk.mode != 0).
 // With patch_e / patch_s (may be null) the refreshed V-norm row and LF-K-norm
 // row are also written to those copies (rows of DH and LF elements).
 template <typename T, int DH>
 __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h, const DecodeDecision& dec,
                                            const float* ke, const float* ve, const T* kn_src, const T* vn_src,
                                            int j, float g_e, int lane, T* patch_e = nullptr,
-                                           T* patch_s = nullptr, T* rows_out = nullptr) {
+                                           T* patch_s = nullptr, T* rows_out = nullptr, RopeK rk = RopeK{nullptr, nullptr, 0}) {
   using E = Elt<T>;
   constexpr int NV = (DH + 63) / 64;
   const int Hkv = s.Hkv, W = s.W, Me = s.Me, Ms = s.Ms, lf = s.lf, LF = DH - lf;
@@ -379,7 +380,12 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
   const T* lve = do_e ? vre : vn_src;
   const T* lks = do_s ? krs : kn_src;
   const T* lvs = do_s ? vrs : vn_src;
-  uint32_t r_ke[NV], r_ve[NV], r_ks[NV], r_vs[NV], r_kn[NV], r_vn[NV];
+  uint32_t r_ke[NV], r_ve[NV], r_ks[NV], r_vs[NV], r_kn[NV], r_vn[NV], r_kp[NV], r_c[NV], r_s[NV];
+  // a raw new K: its partner elements and table entries load with the rest
+  // (from valid addresses: the row itself when there is no RoPE)
+  const bool rope = rk.mode != 0;
+  const T* rcs = rope ? (const T*)rk.cs : kn_src;
+  const T* rsn = rope ? (const T*)rk.sn : kn_src;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int d = min(lane + 64 * i, DH - 1);
@@ -389,6 +395,9 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
     r_vs[i] = raw_ld(lvs + d);
     r_kn[i] = raw_ld(kn_src + d);
     r_vn[i] = raw_ld(vn_src + d);
+    r_kp[i] = raw_ld(kn_src + (rope ? rope_k_partner(d, DH, rk.mode) : d));
+    r_c[i] = raw_ld(rcs + (rope ? rope_k_table(d, DH, rk.mode) : 0));
+    r_s[i] = raw_ld(rsn + (rope ? rope_k_table(d, DH, rk.mode) : 0));
   }
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -397,6 +406,9 @@ __device__ __forceinline__ void apply_head(const coda_bank_desc& s, int b, int h
     mks[i] = do_s ? raw_f<T>(r_ks[i]) : 0.f;
     mvs[i] = do_s ? raw_f<T>(r_vs[i]) : 0.f;
     kn[i] = raw_f<T>(r_kn[i]);
+    if (rope)
+      kn[i] = rope_k_elem<T>(kn[i], raw_f<T>(r_kp[i]), raw_f<T>(r_c[i]), raw_f<T>(r_s[i]),
+                             min(lane + 64 * i, DH - 1), DH, rk.mode);
     vn[i] = raw_f<T>(r_vn[i]);
   }
   if (do_e) {
@@ -599,10 +611,15 @@ __device__ __forceinline__ void route_head_dots(const coda_bank_desc& s, int b, 
   }
 }
 
-// Host launchers of decode_route_kernel and decode_bank_kernel (defined
-// with the bank kernels).
+// Host launchers of decode_route_kernel, decode_bank_kernel and
+// decode_write_kernel (defined with the bank kernels); rk: the new K's RoPE
+// when it is handed over raw.
 int launch_decode_route(const coda_bank_desc* s, int j, float* ws, hipStream_t st);
 int launch_decode_bank(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
-                       const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st);
+                       const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st,
+                       RopeK rk);
+int decode_write_impl(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
+                      const float* g_new, int ring_idx, int ring_filled, int64_t pos, hipStream_t st, RopeK rk,
+                      const char* who);
 
 }  // namespace coda

@@ -35,7 +35,7 @@ template <typename T, int DH>
 __global__ __launch_bounds__(512) void decode_write_kernel(const coda_bank_desc s, const T* __restrict__ k_new,
                                                            const T* __restrict__ v_new, int64_t nb_sb,
                                                            int64_t nb_sh, const float* __restrict__ g_new,
-                                                           int j, int filled, int64_t pos) {
+                                                           int j, int filled, int64_t pos, RopeK rk) {
   using E = Elt<T>;
   constexpr int NWV = 8, NT = 512, NV = (DH + 63) / 64;
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -52,7 +52,14 @@ __global__ __launch_bounds__(512) void decode_write_kernel(const coda_bank_desc 
   if (filled < W) {
     for (int i = t; i < Hkv * DH; i += NT) {
       const int h = i / DH, d = i % DH;
-      kb[((int64_t)h * Lbuf + filled) * DH + d] = kn_src[h * nb_sh + d];
+      const T* kr = kn_src + h * nb_sh;
+      T kv = kr[d];
+      if (rk.mode) {
+        const int pi = rope_k_partner(d, DH, rk.mode), ti = rope_k_table(d, DH, rk.mode);
+        kv = E::st(rope_k_elem<T>(E::ld(kv), E::ld(kr[pi]), E::ld(((const T*)rk.cs)[ti]),
+                                  E::ld(((const T*)rk.sn)[ti]), d, DH, rk.mode));
+      }
+      kb[((int64_t)h * Lbuf + filled) * DH + d] = kv;
       vb[((int64_t)h * Lbuf + filled) * DH + d] = vn_src[h * nb_sh + d];
     }
     if (t == 0) {
@@ -123,7 +130,7 @@ __global__ __launch_bounds__(512) void decode_write_kernel(const coda_bank_desc 
   __syncthreads();
   for (int h = wv; h < Hkv; h += NWV)
     apply_head<T, DH>(s, b, h, dec, ke + h * DH, ve + h * DH, kn_src + h * nb_sh, vn_src + h * nb_sh, j, g_e,
-                      lane);
+                      lane, nullptr, nullptr, nullptr, rk);
   if (t == 0) commit_decode_meta(s, b, dec, j, pos_e, g_new[b]);
 }
 
@@ -181,7 +188,7 @@ __global__ __launch_bounds__(256) void decode_bank_kernel(const coda_bank_desc s
                                                           const T* __restrict__ v_new, int64_t nb_sb, int64_t nb_sh,
                                                           const float* __restrict__ g_new, int j, int64_t pos,
                                                           const float* __restrict__ rec_in,
-                                                          float* __restrict__ rec_out) {
+                                                          float* __restrict__ rec_out, RopeK rk) {
   using E = Elt<T>;
   constexpr int NV = (DH + 63) / 64;
   extern __shared__ __attribute__((aligned(16))) float dsm[];
@@ -226,6 +233,12 @@ __global__ __launch_bounds__(256) void decode_bank_kernel(const coda_bank_desc s
     an[i] = wv == 2 ? d < DH : d < LF;
     const int dc = an[i] ? d : 0;
     xn[i] = (wv >= 2 && an[i]) ? E::ld(wv == 2 ? vx[dc] : kx[lf + dc]) : 0.f;
+    if (wv == 3 && an[i] && jn == j && rk.mode) {
+      // a one-slot ring: the token evicted next is this raw new K, roped
+      const int dd = lf + dc, pi = rope_k_partner(dd, DH, rk.mode), ti = rope_k_table(dd, DH, rk.mode);
+      xn[i] = rope_k_elem<T>(xn[i], E::ld(kx[pi]), E::ld(((const T*)rk.cs)[ti]), E::ld(((const T*)rk.sn)[ti]), dd,
+                             DH, rk.mode);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the direct LDS loads have landed
   __syncthreads();
@@ -244,7 +257,7 @@ __global__ __launch_bounds__(256) void decode_bank_kernel(const coda_bank_desc s
   // ---- 3. row writes of head hk, metadata
   if (wv == 0)
     apply_head<T, DH>(s, b, hk, dec, ke, ve, kn_row, vn_row, j, g_e, lane, Me > 0 ? stage + dec.idx_e * DH : nullptr,
-                      Ms > 0 ? stage + Me * DH + dec.idx_s * LF : nullptr);
+                      Ms > 0 ? stage + Me * DH + dec.idx_s * LF : nullptr, nullptr, rk);
   if (wv == 1 && hk == 0) {
     // metadata of the sequence, and the next record's snapshot of it
     const DStepWs wn = dstep_ws(rec_out, b, Hkv, Me, Ms);
@@ -1891,23 +1904,25 @@ int launch_decode_route(const coda_bank_desc* s, int j, float* ws, hipStream_t s
 
 template <typename T, int DH>
 static int launch_dbank(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
-                        const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st) {
+                        const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st,
+                        RopeK rk) {
   const size_t lds = dbank_lds(*s);
   const int rc = lds_limit<decode_bank_kernel<T, DH>>(lds, "coda_decode_step");
   if (rc) return rc;
   hipLaunchKernelGGL((decode_bank_kernel<T, DH>), dim3(s->Hkv, s->B), dim3(256), lds, st, *s, (const T*)k_new,
-                     (const T*)v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out);
+                     (const T*)v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out, rk);
   return check_launch("decode_bank");
 }
 
 int launch_decode_bank(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
-                       const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st) {
+                       const float* g_new, int j, int64_t pos, const float* rec_in, float* rec_out, hipStream_t st,
+                       RopeK rk) {
   if (dbank_lds(*s) > 160 * 1024)
     return fail(CODA_EUNSUP, "coda_decode_step: bank of %d + %d rows does not fit one workgroup", s->Me, s->Ms);
   const bool bf = s->dtype == CODA_BF16;
-#define CODA_DBANK(D)                                                                                     \
-  return bf ? launch_dbank<bf16_t, D>(s, k_new, v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out, st) \
-            : launch_dbank<float, D>(s, k_new, v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out, st)
+#define CODA_DBANK(D)                                                                                         \
+  return bf ? launch_dbank<bf16_t, D>(s, k_new, v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out, st, rk) \
+            : launch_dbank<float, D>(s, k_new, v_new, nb_sb, nb_sh, g_new, j, pos, rec_in, rec_out, st, rk)
   switch (s->Dh) {
     case 32: CODA_DBANK(32);
     case 64: CODA_DBANK(64);
@@ -1925,13 +1940,36 @@ static size_t decode_lds(const coda_bank_desc* s) {
 template <typename T, int DH>
 static int launch_decode(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb,
                          int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled, int64_t pos,
-                         hipStream_t st) {
+                         hipStream_t st, RopeK rk) {
   const size_t lds = decode_lds(s);
   const int rc = lds_limit<decode_write_kernel<T, DH>>(lds, "coda_decode_write");
   if (rc) return rc;
   hipLaunchKernelGGL((decode_write_kernel<T, DH>), dim3(s->B), dim3(512), lds, st, *s, (const T*)k_new,
-                     (const T*)v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos);
+                     (const T*)v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, rk);
   return check_launch("decode_write");
+}
+
+int decode_write_impl(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb, int64_t nb_sh,
+                      const float* g_new, int ring_idx, int ring_filled, int64_t pos, hipStream_t st, RopeK rk,
+                      const char* who) {
+  int rc = validate_bank(s, who);
+  if (rc) return rc;
+  CODA_REQUIRE(k_new && v_new && g_new, "%s: new token pointers missing", who);
+  CODA_REQUIRE(ring_filled >= 0 && ring_filled <= s->W, "%s: ring_filled %d outside [0, %d]", who, ring_filled, s->W);
+  CODA_REQUIRE(ring_filled < s->W || (ring_idx >= 0 && ring_idx < s->W), "%s: ring_idx %d outside [0, %d)", who,
+               ring_idx, s->W);
+  CODA_REQUIRE(decode_lds(s) <= 160 * 1024, "%s: Hkv=%d too large for one workgroup", who, s->Hkv);
+  if (s->B == 0) return CODA_OK;
+  const bool bf = s->dtype == CODA_BF16;
+#define CODA_DWRITE(D)                                                                                             \
+  return bf ? launch_decode<bf16_t, D>(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st, rk) \
+            : launch_decode<float, D>(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st, rk)
+  switch (s->Dh) {
+    case 32: CODA_DWRITE(32);
+    case 64: CODA_DWRITE(64);
+    default: CODA_DWRITE(128);
+  }
+#undef CODA_DWRITE
 }
 
 }  // namespace coda
@@ -1941,28 +1979,8 @@ using namespace coda;
 extern "C" int coda_decode_write(const coda_bank_desc* s, const void* k_new, const void* v_new, int64_t nb_sb,
                                  int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled, int64_t pos,
                                  void* stream) {
-  int rc = validate_bank(s, "coda_decode_write");
-  if (rc) return rc;
-  CODA_REQUIRE(k_new && v_new && g_new, "coda_decode_write: new token pointers missing");
-  CODA_REQUIRE(ring_filled >= 0 && ring_filled <= s->W, "coda_decode_write: ring_filled %d outside [0, %d]",
-               ring_filled, s->W);
-  CODA_REQUIRE(ring_filled < s->W || (ring_idx >= 0 && ring_idx < s->W),
-               "coda_decode_write: ring_idx %d outside [0, %d)", ring_idx, s->W);
-  CODA_REQUIRE(decode_lds(s) <= 160 * 1024, "coda_decode_write: Hkv=%d too large for one workgroup", s->Hkv);
-  if (s->B == 0) return CODA_OK;
-  hipStream_t st = (hipStream_t)stream;
-  const bool bf = s->dtype == CODA_BF16;
-  switch (s->Dh) {
-    case 32:
-      return bf ? launch_decode<bf16_t, 32>(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st)
-                : launch_decode<float, 32>(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st);
-    case 64:
-      return bf ? launch_decode<bf16_t, 64>(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st)
-                : launch_decode<float, 64>(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st);
-    default:
-      return bf ? launch_decode<bf16_t, 128>(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st)
-                : launch_decode<float, 128>(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, st);
-  }
+  return decode_write_impl(s, k_new, v_new, nb_sb, nb_sh, g_new, ring_idx, ring_filled, pos, (hipStream_t)stream,
+                           RopeK{nullptr, nullptr, 0}, "coda_decode_write");
 }
 
 extern "C" int coda_block_plan(const float* g_ring, int ring_head, int ring_filled, int W, const float* g_seq,

@@ -88,6 +88,51 @@ template <> struct Elt<bf16_t> {
   static __host__ __device__ __forceinline__ float rnd(float x) { return bf2f(f2bf(x)); }
 };
 
+// RoPE of one pair with (c, s), one rounding to T per multiply and add, as
+// the reference's element-wise torch ops (primitives.py:83-113):
+//   interleaved (e, o) = (x[2i], x[2i+1]):      (e c - o s, e s + o c)
+//   half-split  (e, o) = (x[i], x[i + Dh/2]):   (e c + (-o) s, o c + e s)
+template <typename T>
+__device__ __forceinline__ void rope_pair_t(float e, float o, float c, float s, bool inter, float& r0, float& r1) {
+  using E = Elt<T>;
+  if (inter) {
+    r0 = E::rnd(E::rnd(e * c) - E::rnd(o * s));
+    r1 = E::rnd(E::rnd(e * s) + E::rnd(o * c));
+  } else {
+    r0 = E::rnd(E::rnd(e * c) + E::rnd(-o * s));
+    r1 = E::rnd(E::rnd(o * c) + E::rnd(e * s));
+  }
+}
+
+// The new token's K handed to a decode-step kernel before RoPE: the kernel
+// ropes it with the token's own tables (cs / sn: Dh/2 entries of the
+// element type) as it writes and reads it.  mode 0: K already roped,
+// 1: interleaved pairs, 2: half-split pairs.
+struct RopeK {
+  const void* cs;
+  const void* sn;
+  int mode;
+};
+// Element d of the roped row from the raw row: partner element and table
+// entry, then the pair's formula (one value of the pair)
+template <typename T>
+__device__ __forceinline__ float rope_k_elem(float x, float partner, float c, float s, int d, int DH, int mode) {
+  float r0, r1;
+  if (mode == 1) {
+    const bool ev = (d & 1) == 0;
+    rope_pair_t<T>(ev ? x : partner, ev ? partner : x, c, s, true, r0, r1);
+    return ev ? r0 : r1;
+  }
+  const bool lo = d < DH / 2;
+  rope_pair_t<T>(lo ? x : partner, lo ? partner : x, c, s, false, r0, r1);
+  return lo ? r0 : r1;
+}
+// (partner index, table index) of element d
+__device__ __forceinline__ int rope_k_partner(int d, int DH, int mode) {
+  return mode == 1 ? (d ^ 1) : (d < DH / 2 ? d + DH / 2 : d - DH / 2);
+}
+__device__ __forceinline__ int rope_k_table(int d, int DH, int mode) { return mode == 1 ? (d >> 1) : (d % (DH / 2)); }
+
 // ----------------------------------------------------------------- wave64
 // Cross-lane moves without LDS traffic: DPP within 16-lane rows, the gfx950
 // permlane swaps across rows (each hands both lanes of a pair the same two

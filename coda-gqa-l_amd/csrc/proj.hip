@@ -27,19 +27,6 @@ static constexpr int kProjPitch = 72;     // LDS row pitch (bf16): 144 bytes, co
 
 __device__ __forceinline__ float proj_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
 
-// RoPE of one pair (e, o) with (c, s), one bf16 rounding per op
-//   interleaved: (e c - o s, e s + o c); half-split: (a c + (-b) s, b c + a s)
-__device__ __forceinline__ void rope_pair(float e, float o, float c, float s, bool inter, float& r0, float& r1) {
-  using E = Elt<bf16_t>;
-  if (inter) {
-    r0 = E::rnd(E::rnd(e * c) - E::rnd(o * s));
-    r1 = E::rnd(E::rnd(e * s) + E::rnd(o * c));
-  } else {
-    r0 = E::rnd(E::rnd(e * c) + E::rnd(-o * s));
-    r1 = E::rnd(E::rnd(o * c) + E::rnd(e * s));
-  }
-}
-
 // Epilogue of features f .. f + 3 (f a multiple of 4) of token row m:
 // the fp32 accumulators plus bias, rounded and routed to q / k (RoPE) / v /
 // lambda / gate
@@ -70,7 +57,7 @@ __device__ __forceinline__ void proj_store4(const coda_proj_desc& d, int f, int 
     for (int pp = 0; pp < 2; ++pp) {
       const int p = c / 2 + pp;  // pair index
       const float cc = E::ld(cs[(int64_t)prow * half + p]), ss = E::ld(sn[(int64_t)prow * half + p]);
-      rope_pair(E::rnd(v[2 * pp]), E::rnd(v[2 * pp + 1]), cc, ss, inter, r[2 * pp], r[2 * pp + 1]);
+      rope_pair_t<bf16_t>(E::rnd(v[2 * pp]), E::rnd(v[2 * pp + 1]), cc, ss, inter, r[2 * pp], r[2 * pp + 1]);
     }
     if (inter) {
       uint2 w;
@@ -207,7 +194,7 @@ __global__ __launch_bounds__(256) void proj_epilogue_bf16(const coda_proj_desc d
     const float cc = E::ld(((const bf16_t*)d.rope_cos)[(int64_t)prow * half + p]);
     const float ss = E::ld(((const bf16_t*)d.rope_sin)[(int64_t)prow * half + p]);
     float r0, r1;
-    rope_pair(E::ld(kh[c0]), E::ld(kh[c1]), cc, ss, inter, r0, r1);
+    rope_pair_t<bf16_t>(E::ld(kh[c0]), E::ld(kh[c1]), cc, ss, inter, r0, r1);
     kh[c0] = E::st(r0);
     kh[c1] = E::st(r1);
   } else if (u < n_pairs + d.H) {

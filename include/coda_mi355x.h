@@ -310,6 +310,19 @@ int coda_decode_step(const coda_bank_desc* s, const coda_attn_desc* a, const voi
                      int64_t nb_sb, int64_t nb_sh, const float* g_new, int ring_idx, int ring_filled,
                      int64_t pos, void* workspace, size_t workspace_bytes, int* routed, void* stream);
 
+/* coda_decode_step with the new token's K before RoPE (the layer's k_proj
+ * output): every kernel that writes or reads it ropes it with the query's
+ * tables a->rope_cos / a->rope_sin (row 0, the token's own position in a
+ * write-then-attend step; a->rope_interleaved picks the pairing), in the
+ * reference's per-op rounding, so the ring holds the same bytes as after
+ * coda_rope_fwd + coda_decode_step.  Needs the tables (16-byte aligned).
+ * Replaces: the k RoPE of CoDAGQALandmarkPerf2.step together with the step
+ *   (src/coda_gqa_l/attention.py:526-533). */
+int coda_decode_step_raw_k(const coda_bank_desc* s, const coda_attn_desc* a, const void* k_new,
+                           const void* v_new, int64_t nb_sb, int64_t nb_sh, const float* g_new,
+                           int ring_idx, int ring_filled, int64_t pos, void* workspace,
+                           size_t workspace_bytes, int* routed, void* stream);
+
 /* Candidate plan of a chunked prefill: for every chunk c (block_size
  * tokens, last one ragged) and sequence b, the evicted-token indices picked
  * by the reference's CPU topk(g_e, k, sorted=False) (libstdc++ nth_element /

@@ -110,7 +110,10 @@ def test_bench_shape_trajectory_matches_oracle(name):
     del q, k, v, gate, lam
     # ---- decode, free-running: the HIP side keeps its state (and routing
     # record) from step to step; even steps record their decisions (the
-    # uncached launch path), odd steps run through the cached descriptors
+    # uncached launch path), odd steps run through the cached descriptors;
+    # steps 1, 2 (mod 4) hand the kernel the raw k projection (it ropes k
+    # itself), the others k roped as the oracle gets it
+    from coda_oracle import prims
     for t in range(steps):
         traced = t % 2 == 0
         tr_o = [] if traced else None
@@ -121,11 +124,12 @@ def test_bench_shape_trajectory_matches_oracle(name):
         vn = torch.randn(B, Hkv, 1, Dh, generator=g).to(dtype)
         gn = _gates(kind, B, 1, g)
         lamt = torch.sigmoid(torch.randn(B, H, 1, 1, generator=g) - 1.0).to(dtype)
-        banks.write_one(m, st_o, kn, vn, gn, tr_o)
-        ho = m.attend_core(qt, lamt, st_o, qp)
         ct, sn = m.rope_tables(1, qp, dtype)
+        raw = t % 4 in (1, 2)
+        banks.write_one(m, st_o, prims.rope(kn, ct, sn, m.rope_interleaved) if raw else kn, vn, gn, tr_o)
+        ho = m.attend_core(qt, lamt, st_o, qp)
         hp = p.decode_step_core(qt.to(DEV), kn.to(DEV), vn.to(DEV), gn.reshape(B).to(DEV), lamt.squeeze(-1).to(DEV),
-                                st_p, ct.to(DEV), sn.to(DEV))
+                                st_p, ct.to(DEV), sn.to(DEV), k_roped=not raw)
         torch.cuda.synchronize()
         if traced:
             compare_traces(p.decision_trace, tr_o, m, f"{name} decode step {t} decisions")
@@ -238,3 +242,50 @@ def test_many_candidates_split_path_matches_oracle_and_is_batch_independent():
         if a is None:
             continue
         assert torch.equal(a[:4].cpu(), b.cpu()), f"state field {f} of sequences 0-3 depends on the batch"
+
+
+@pytest.mark.parametrize("Dh,inter", [(128, True), (128, False), (64, True), (64, False)])
+@torch.no_grad()
+def test_raw_k_decode_equals_roped_k(Dh, inter, monkeypatch):
+    """The decode step handed the raw k projection (coda_decode_step_raw_k:
+    the kernels rope it) leaves the same state bytes and head outputs as the
+    step handed k roped by the RoPE kernel, from an empty ring through its
+    filling (decode write kernel) into eviction, on the one-launch path and
+    on the two-launch path (CODA_DECODE_FUSED=0), for both RoPE pairings."""
+    _need_gpu()
+    import coda_gqa_l
+    H, Hkv, W, Me, Ms, B, n = 8, 2, 16, 8, 8, 3, 40
+    print(f"[raw k] Dh{Dh} interleaved {inter}", flush=True)
+    torch.manual_seed(61)
+    p = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=H * Dh, num_heads=H, num_kv_heads=Hkv, window=W,
+                                        num_landmarks_exact=Me, num_landmarks_summary=Ms, rope_base=1e4,
+                                        rope_interleaved=inter).to(DEV, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(62)
+    seq = [(torch.randn(B, H, 1, Dh, generator=g), torch.randn(B, Hkv, 1, Dh, generator=g),
+            torch.randn(B, Hkv, 1, Dh, generator=g), torch.sigmoid(torch.randn(B, generator=g) * 2),
+            torch.sigmoid(torch.randn(B, H, 1, generator=g))) for _ in range(n)]
+    runs = {}
+    for fused in ("1", "0"):
+        monkeypatch.setenv("CODA_DECODE_FUSED", fused)
+        for raw in (False, True):
+            torch.manual_seed(63)
+            st = p.init_state(batch_size=B, device=DEV, dtype=torch.bfloat16)
+            heads = []
+            for q, k, v, gt, lam in seq:
+                pos = int(st.pos)
+                c, s_ = p.rope(seq_len=1, offset=pos, device=DEV, dtype=torch.bfloat16)
+                c, s_ = c.contiguous(), s_.contiguous()
+                kd = k.to(DEV, torch.bfloat16)
+                if not raw:
+                    kd = coda_gqa_l.apply_rope(kd, c, s_, interleaved=inter)
+                h = p.decode_step_core(q.to(DEV, torch.bfloat16), kd, v.to(DEV, torch.bfloat16), gt.to(DEV),
+                                       lam.to(DEV, torch.bfloat16), st, c, s_, k_roped=not raw)
+                heads.append(h.cpu())
+            torch.cuda.synchronize()
+            runs[(fused, raw)] = (torch.stack(heads), _cpu_copy(st))
+    for fused in ("1", "0"):
+        h0, s0 = runs[(fused, False)]
+        h1, s1 = runs[(fused, True)]
+        assert torch.equal(h0, h1), f"fused={fused}: heads differ between raw and roped k"
+        for f in ("k_buf", "v_buf", "allowed", "g_recent", "mem_last_exact", "_exact_v_norm", "_sum_lf_k_norm"):
+            assert torch.equal(getattr(s0, f), getattr(s1, f)), f"fused={fused}: state field {f} differs"
