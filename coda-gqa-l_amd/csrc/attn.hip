@@ -2845,30 +2845,49 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
       const bf16_t wl = (a.rms_w ? (const bf16_t*)a.rms_w : (const bf16_t*)a.q)[a.rms_w ? (tid & (DH - 1)) : 0];
       w_raw = a.rms_w ? wl : (bf16_t)0x3f80;
       const bool slow = a.allowed != nullptr && !have;
+      if (slow) {
+        // visibility bytes that are not 16-byte aligned: one load a byte
+        // (their own branch, so the usual path has no load in it)
+#pragma unroll
+        for (int c = 0; c < ALC; ++c) {
+          const int i0 = 16 * (lane + 64 * c);
+          uint32_t wd[4] = {0, 0, 0, 0};
+          for (int i = 0; i < 16; ++i)
+            if (i0 + i < a.Lp) wd[i >> 2] |= (uint32_t)a.allowed[(int64_t)b * a.al_sb + i0 + i] << (8 * (i & 3));
+          al_c[c] = uint4{wd[0], wd[1], wd[2], wd[3]};
+        }
+      }
 #pragma unroll
       for (int c = 0; c < ALC; ++c) {
         const int i0 = 16 * (lane + 64 * c);
         uint32_t wd[4] = {al_c[c].x, al_c[c].y, al_c[c].z, al_c[c].w};
+        // each byte to 0 / 1: set and inside the prefix (every prefix byte
+        // without visibility bytes), branch-free
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
+          uint32_t r = 0;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int i = i0 + 4 * q4 + e;
-            uint32_t byte = (wd[q4] >> (8 * e)) & 0xffu;
-            if (a.allowed == nullptr) byte = 1;
-            else if (slow) byte = i < a.Lp ? a.allowed[(int64_t)b * a.al_sb + i] : 0;
-            if (i >= a.Lp) byte = 0;
-            wd[q4] = (wd[q4] & ~(0xffu << (8 * e))) | ((byte ? 1u : 0u) << (8 * e));
+            const bool set = a.allowed == nullptr || ((wd[q4] >> (8 * e)) & 0xffu) != 0;
+            r |= (uint32_t)(set && i < a.Lp) << (8 * e);
           }
+          wd[q4] = r;
         }
         al_c[c] = uint4{wd[0], wd[1], wd[2], wd[3]};
         const bool all16 = ((wd[0] & wd[1] & wd[2] & wd[3]) == 0x01010101u);
-        const uint64_t m = __ballot(all16);
         // 16-byte chunk k of this group is lane k: block e of the group is
-        // chunks 2e, 2e + 1
-#pragma unroll
-        for (int e = 0; e < 32; ++e)
-          allvis |= (uint64_t)(((m >> (2 * e)) & 3ull) == 3ull) << (32 * c + e);
+        // chunks 2e, 2e + 1, so bit e of the group's 32 is (bit 2e & bit
+        // 2e + 1) of the ballot, gathered from the even bits
+        uint64_t x = __ballot(all16);
+        x &= x >> 1;
+        x &= 0x5555555555555555ull;
+        x = (x | (x >> 1)) & 0x3333333333333333ull;
+        x = (x | (x >> 2)) & 0x0f0f0f0f0f0f0f0full;
+        x = (x | (x >> 4)) & 0x00ff00ff00ff00ffull;
+        x = (x | (x >> 8)) & 0x0000ffff0000ffffull;
+        x = (x | (x >> 16)) & 0x00000000ffffffffull;
+        allvis |= x << (32 * c);
       }
       if (wv == 0) {
 #pragma unroll
