@@ -896,6 +896,23 @@ __device__ __forceinline__ void st8(T* p, const Piece8<T> x) {
 #pragma unroll
   for (int i = 0; i < Piece8<T>::PW; ++i) reinterpret_cast<uint4*>(p)[i] = x.w[i];
 }
+// The eight values of a piece as floats.
+template <typename T>
+__device__ __forceinline__ void piece8_f(const Piece8<T>& x, float f[8]) {
+#pragma unroll
+  for (int q = 0; q < Piece8<T>::PW; ++q) {
+    const uint32_t w[4] = {x.w[q].x, x.w[q].y, x.w[q].z, x.w[q].w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (sizeof(T) == 2) {
+        f[2 * i] = bf2f((bf16_t)(w[i] & 0xffffu));
+        f[2 * i + 1] = bf2f((bf16_t)(w[i] >> 16));
+      } else {
+        f[4 * q + i] = __builtin_bit_cast(float, w[i]);
+      }
+    }
+  }
+}
 
 template <typename T, int DH>
 __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_bank_desc s, BlockGeom g, const T* kbk,
@@ -1375,43 +1392,97 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   const Dec dx = dec_of(s, g, ws, b);  // exchange: idx_s [Ts], best value / slot of the exact tokens
   const int Lr = g.ring_filled, first = max(Lr, g.n_ev), rhead = (Lr == W) ? g.ring_head : 0;
 
-  // ---- 1. staging: plan, metadata, own slots, norm caches
-  for (int i = t; i < TT; i += NT) pcl[i] = pc[i];
-  for (int m = t; m < Me + Ms; m += NT) used[m] = al[W + m];
-  for (int m = t; m < Me; m += NT) last[m] = s.mem_last[(int64_t)b * Me + m];
-  for (int i = t; i < (e1 - e0) * CH; i += NT) {
-    const int r = i / CH, c = i % CH;
-    st8<T>(own_ek + r * DH + 8 * c, ld8<T>(kb + (int64_t)(W + e0 + r) * DH + 8 * c));
-    st8<T>(own_ev + r * DH + 8 * c, ld8<T>(vb + (int64_t)(W + e0 + r) * DH + 8 * c));
-  }
-  for (int i = t; i < (s1 - s0) * CH; i += NT) {
-    const int r = i / CH, c = i % CH;
-    st8<T>(own_sv + r * DH + 8 * c, ld8<T>(vb + (int64_t)(W + Me + s0 + r) * DH + 8 * c));
-    if (c >= CH / 2)
-      st8<T>(own_sk + r * LF + 8 * (c - CH / 2), ld8<T>(kb + (int64_t)(W + Me + s0 + r) * DH + 8 * c));
-  }
-  if (ne > 0) stage_rows<T>(nrm_e, le, (const T*)s.exact_v_norm + ((int64_t)b * Hkv + h) * Me * DH, DH, Me, DH);
-  if (ns > 0) stage_rows<T>(nrm_s, lsum, (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + h) * Ms * LF, LF, Ms, LF);
-  __syncthreads();
-  // candidate gates and raw rows, 16-byte pieces (loads first)
-  for (int i = t; i < TT; i += NT) gate[i] = cand_gate(s, g, gb, b, pcl[i]);
-  for (int base = t; base < TT * CH; base += kRingPre * NT) {
-    Piece8<T> pk[kRingPre], pv[kRingPre];
+  // ---- 1. staging in one batch of loads: the plan entries behind this
+  // thread's candidate pieces first, then plan, metadata, own bank slots
+  // and norm caches, then the candidate rows and gates through those plan
+  // entries (their wait covers only the entries), then every LDS store
+  {
+    constexpr int UR = 2;  // pieces of each kind per thread and round
+    constexpr int CHL = LF / 8;
+    const int n_raw = TT * CH, n_us = Me + Ms, n_ee = (e1 - e0) * CH, n_ss = (s1 - s0) * CH;
+    const int n_ne = ne > 0 ? Me * CH : 0, n_ns = ns > 0 ? Ms * CHL : 0;
+    const int n_rnd = max(max(max(n_raw, TT), max(n_us, n_ee)), max(max(n_ss, n_ne), n_ns));
+    const T* nre = (const T*)s.exact_v_norm + ((int64_t)b * Hkv + h) * Me * DH;
+    const T* nrs = (const T*)s.sum_lf_k_norm + ((int64_t)b * Hkv + h) * Ms * LF;
+    for (int base = t; base < n_rnd; base += UR * NT) {
+      int32_t rr[UR], vpc[UR];
+      uint32_t vus[UR];
+      int64_t vla[UR];
+      Piece8<T> vek[UR], vev[UR], vsv[UR], vsk[UR], vne[UR], vns[UR], vrk[UR], vrv[UR];
+      float vg[UR];
 #pragma unroll
-    for (int u = 0; u < kRingPre; ++u) {
-      const int i = min(base + u * NT, TT * CH - 1), r = i / CH, c = i % CH;
-      pk[u] = ld8<T>(cand_row<T, DH>(s, g, kbk, b, h, pcl[r], false) + 8 * c);
-      pv[u] = ld8<T>(cand_row<T, DH>(s, g, vbk, b, h, pcl[r], true) + 8 * c);
-    }
+      for (int u = 0; u < UR; ++u) {
+        const int i = base + u * NT;
+        rr[u] = i < n_raw ? pc[i / CH] : 0;
+      }
 #pragma unroll
-    for (int u = 0; u < kRingPre; ++u) {
-      const int i = base + u * NT;
-      if (i < TT * CH) {
-        st8<T>(raw_k + i * 8, pk[u]);
-        st8<T>(raw_v + i * 8, pv[u]);
+      for (int u = 0; u < UR; ++u) {
+        const int i = base + u * NT;
+        vpc[u] = i < TT ? pc[i] : 0;
+        vus[u] = i < n_us ? al[W + i] : 0;
+        vla[u] = i < Me ? s.mem_last[(int64_t)b * Me + i] : 0;
+        if (i < n_ee) {
+          const int r = i / CH, c = i % CH;
+          vek[u] = ld8<T>(kb + (int64_t)(W + e0 + r) * DH + 8 * c);
+          vev[u] = ld8<T>(vb + (int64_t)(W + e0 + r) * DH + 8 * c);
+        }
+        if (i < n_ss) {
+          const int r = i / CH, c = i % CH;
+          vsv[u] = ld8<T>(vb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
+          if (c >= CH / 2) vsk[u] = ld8<T>(kb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
+        }
+        if (i < n_ne) vne[u] = ld8<T>(nre + 8 * (int64_t)i);
+        if (i < n_ns) vns[u] = ld8<T>(nrs + 8 * (int64_t)i);
+      }
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        const int i = base + u * NT;
+        if (i < n_raw) {
+          const int c = i % CH;
+          vrk[u] = ld8<T>(cand_row<T, DH>(s, g, kbk, b, h, rr[u], false) + 8 * c);
+          vrv[u] = ld8<T>(cand_row<T, DH>(s, g, vbk, b, h, rr[u], true) + 8 * c);
+          vg[u] = c == 0 ? cand_gate(s, g, gb, b, rr[u]) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        const int i = base + u * NT;
+        if (i < TT) pcl[i] = vpc[u];
+        if (i < n_us) used[i] = (int32_t)(vus[u] & 0xffu);
+        if (i < Me) last[i] = vla[u];
+        if (i < n_ee) {
+          const int r = i / CH, c = i % CH;
+          st8<T>(own_ek + r * DH + 8 * c, vek[u]);
+          st8<T>(own_ev + r * DH + 8 * c, vev[u]);
+        }
+        if (i < n_ss) {
+          const int r = i / CH, c = i % CH;
+          st8<T>(own_sv + r * DH + 8 * c, vsv[u]);
+          if (c >= CH / 2) st8<T>(own_sk + r * LF + 8 * (c - CH / 2), vsk[u]);
+        }
+        if (i < n_ne) {
+          float x[8];
+          piece8_f<T>(vne[u], x);
+          float4* d = reinterpret_cast<float4*>(nrm_e + (i / CH) * le + 8 * (i % CH));
+          d[0] = make_float4(x[0], x[1], x[2], x[3]);
+          d[1] = make_float4(x[4], x[5], x[6], x[7]);
+        }
+        if (i < n_ns) {
+          float x[8];
+          piece8_f<T>(vns[u], x);
+          float4* d = reinterpret_cast<float4*>(nrm_s + (i / CHL) * lsum + 8 * (i % CHL));
+          d[0] = make_float4(x[0], x[1], x[2], x[3]);
+          d[1] = make_float4(x[4], x[5], x[6], x[7]);
+        }
+        if (i < n_raw) {
+          st8<T>(raw_k + 8 * i, vrk[u]);
+          st8<T>(raw_v + 8 * i, vrv[u]);
+          if (i % CH == 0) gate[i / CH] = vg[u];
+        }
       }
     }
   }
+  __syncthreads();
   // LRU keys over the pre-update stamps (memory_banks.py:640-660):
   // ascending stamps of used active slots, unused ones first
   if (Te > 0)
