@@ -1682,6 +1682,12 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       if (s.frustrated) atomic_add_i64(s.frustrated + 0, cnt_fr);
     }
   }
+  // (exact flags and touch stamps start cleared; the staged stamps are no
+  // longer read)
+  for (int m = t; m < Me; m += NT) {
+    eflag[m] = 0;
+    last[m] = kNegBig;
+  }
   // summary slots, 8 per wave and pass: token masks (ballots over the
   // tokens), then lane u sums slot u's weights in token order (fp32: the
   // scatter_add order) and sets its active / newly used flags
@@ -1704,26 +1710,21 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
     }
   }
   __syncthreads();
-  // exact slots, one wave per slot (lanes over the tokens): written (an
+  // exact slots, one thread per token through LDS atomics: written (an
   // overwriting token) and touched (max position of the touching tokens)
-  if (Te > 0)
-    for (int m = wv; m < Me; m += NW) {
-      const bool on = lane < Te && idx_e[min(lane, Te - 1)] == m;
-      const int f = fl_e[min(lane, Te - 1)];
-      const int ow = __any(on && (f & 1));
-      int64_t pv = (on && (f & 2)) ? g.pos0 - g.ring_filled + pcl[min(lane, Te - 1)] : kNegBig;
-      for (int o = 32; o > 0; o >>= 1) {
-        const int64_t q = __shfl_xor(pv, o, 64);
-        pv = q > pv ? q : pv;
-      }
-      if (lane == 0) {
-        eflag[m] = ow;
-        if (lead) {
-          if (pv != kNegBig) s.mem_last[(int64_t)b * Me + m] = pv;  // LRU: max pos of the touching tokens
-          if (ow) al[W + m] = 1;
-        }
-      }
+  if (Te > 0) {
+    for (int tt = t; tt < Te; tt += NT) {
+      const int m = idx_e[tt], f = fl_e[tt];
+      if (f & 1) atomicOr(&eflag[m], 1);
+      if (f & 2) atomicMax(reinterpret_cast<long long*>(&last[m]), (long long)(g.pos0 - g.ring_filled + pcl[tt]));
     }
+    __syncthreads();
+    if (lead)
+      for (int m = t; m < Me; m += NT) {
+        if (last[m] != kNegBig) s.mem_last[(int64_t)b * Me + m] = last[m];  // LRU: max pos of the touching tokens
+        if (eflag[m]) al[W + m] = 1;
+      }
+  }
   if (lead) {
     int32_t* tr = s.trace ? s.trace + (int64_t)b * (2 * Te + Ts) : nullptr;
     if (tr) {
