@@ -2669,11 +2669,14 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 // barrier per tile suffices and a tile's loads have two iterations to land.
 // Whole tiles inside the prefix or the block load from a wave-uniform base
 // plus per-lane offsets.
-template <int DH, int NW, int QM>
+static constexpr int kTabRows = 64;  // query rows whose RoPE tables attn_f3_bf16 stages in LDS
+template <int DH, int NW, int QM, bool TB>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_f3_bf16(
     const coda_attn_desc a, int NQ, int nqb, int npairs) {
   using Lay = F2Layout<DH>;
   constexpr int NS = 4;
+  static_assert(!TB || QM == 0 || QM == 1, "tables staged for the RoPE + rotation query cases");
+  constexpr int kTabPitch = DH / 2 + 8;  // table row pitch in LDS (bf16)
   constexpr int KT = Lay::KT, NKS = Lay::NKS, NDB = Lay::NDB, KCH = Lay::KCH, VCH = Lay::VCH;
   constexpr int KCW = (KCH + NW - 1) / NW, VCW = (VCH + NW - 1) / NW;
   static_assert(KCH % NW == 0 && VCH % NW == 0, "tile pieces split evenly over the waves");
@@ -2681,6 +2684,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   extern __shared__ __attribute__((aligned(16))) char f3_smem[];
   __shared__ __attribute__((aligned(16))) uint8_t al_lds[kMaxRowsPrefix];
   __shared__ __attribute__((aligned(16))) float w_lds[DH];
+  // TB: cos / sin rows of the workgroup's queries, cos / sin of its heads'
+  // noise angles
+  __shared__ __attribute__((aligned(16))) bf16_t tab_rope[TB ? 2 : 1][TB ? kTabRows * kTabPitch : 8];
+  __shared__ __attribute__((aligned(16))) bf16_t tab_th[TB ? 2 : 1][TB ? 8 * (DH / 2) : 8];
 
   const int id = blockIdx.x;
   int qb, pair;
@@ -2810,23 +2817,49 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const bf16_t* ths = !given ? (const bf16_t*)a.theta_sin + (int64_t)h * half : nullptr;
     uint4 uq[NKS], up[NKS], rc[NKS], rs[NKS];
     uint2 rc2[NKS], rs2[NKS], tcs[NKS], tsn[NKS];
+    // TB: the workgroup's RoPE rows (its 16 NQ queries) and noise angles
+    // (its G heads) load once per workgroup, 16-byte pieces spread over the
+    // threads, and reach the lanes through LDS: per-lane table loads were
+    // most of the prologue's load instructions, and a CU's prologue is
+    // bound by how many it can have in flight
+    constexpr int TCH = half / 8;  // 16-byte pieces of a table row
+    constexpr int TPT = (2 * kTabRows * TCH + 2 * 8 * TCH + NW * 64 - 1) / (NW * 64);
+    uint4 tv[TPT];
+    const int nrow = 16 * NQ, nrope = 2 * nrow * TCH, ntab = nrope + 2 * G * TCH;
+    if constexpr (TB) {
+#pragma unroll
+      for (int u = 0; u < TPT; ++u) {
+        // (threads past the last piece reload it)
+        const int c = min(tid + NW * 64 * u, ntab - 1);
+        const bool th = c >= nrope;
+        const int cc = th ? c - nrope : c;
+        const int nr = th ? G : nrow;
+        const int which = cc / (nr * TCH), rr = (cc / TCH) % nr, ch = cc % TCH;
+        const bf16_t* src = th ? (const bf16_t*)(which ? a.theta_sin : a.theta_cos) + (int64_t)(hk * G + rr) * half + 8 * ch
+                               : (const bf16_t*)(which ? a.rope_sin : a.rope_cos) +
+                                     (int64_t)min(qb * 16 * NQ + rr, a.Lq - 1) * half + 8 * ch;
+        tv[u] = NW * 64 * u < ntab ? *reinterpret_cast<const uint4*>(src) : uint4{0, 0, 0, 0};
+      }
+    }
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) {
       const int d0 = 16 * ks + 8 * hl;
       uq[ks] = *reinterpret_cast<const uint4*>(qr + d0);
-      if (rope && inter) {
-        rc2[ks] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
-        rs2[ks] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
-      }
-      if (rope && !inter) {
-        const int f0 = d0 < half ? d0 : d0 - half;
-        up[ks] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
-        rc[ks] = *reinterpret_cast<const uint4*>(csr + f0);
-        rs[ks] = *reinterpret_cast<const uint4*>(snr + f0);
-      }
-      if (!given) {
-        tcs[ks] = *reinterpret_cast<const uint2*>(thc + d0 / 2);
-        tsn[ks] = *reinterpret_cast<const uint2*>(ths + d0 / 2);
+      if (rope && !inter) up[ks] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
+      if constexpr (!TB) {
+        if (rope && inter) {
+          rc2[ks] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
+          rs2[ks] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
+        }
+        if (rope && !inter) {
+          const int f0 = d0 < half ? d0 : d0 - half;
+          rc[ks] = *reinterpret_cast<const uint4*>(csr + f0);
+          rs[ks] = *reinterpret_cast<const uint4*>(snr + f0);
+        }
+        if (!given) {
+          tcs[ks] = *reinterpret_cast<const uint2*>(thc + d0 / 2);
+          tsn[ks] = *reinterpret_cast<const uint2*>(ths + d0 / 2);
+        }
       }
     }
     lam_raw = ((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl];
@@ -2897,6 +2930,39 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         }
       }
       if (tid < DH) w_lds[tid] = bf2f(w_raw);
+    }
+    if constexpr (TB) {
+      // tables to LDS (rows padded by 16 bytes, so the 16 query rows of a
+      // wave's reads spread over the banks), then each lane reads its
+      // entries, before any direct global->LDS load is in flight
+#pragma unroll
+      for (int u = 0; u < TPT; ++u) {
+        const int c = tid + NW * 64 * u;
+        if (c < ntab) {
+          const bool th = c >= nrope;
+          const int cc = th ? c - nrope : c;
+          const int nr = th ? G : nrow;
+          const int which = cc / (nr * TCH), rr = (cc / TCH) % nr, ch = cc % TCH;
+          bf16_t* dst = th ? &tab_th[which][rr * half + 8 * ch] : &tab_rope[which][rr * kTabPitch + 8 * ch];
+          *reinterpret_cast<uint4*>(dst) = tv[u];
+        }
+      }
+      __syncthreads();
+      const int rl = 16 * qsub + qn;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        const int d0 = 16 * ks + 8 * hl;
+        if (inter) {
+          rc2[ks] = *reinterpret_cast<const uint2*>(&tab_rope[0][rl * kTabPitch + d0 / 2]);
+          rs2[ks] = *reinterpret_cast<const uint2*>(&tab_rope[1][rl * kTabPitch + d0 / 2]);
+        } else {
+          const int f0 = d0 < half ? d0 : d0 - half;
+          rc[ks] = *reinterpret_cast<const uint4*>(&tab_rope[0][rl * kTabPitch + f0]);
+          rs[ks] = *reinterpret_cast<const uint4*>(&tab_rope[1][rl * kTabPitch + f0]);
+        }
+        tcs[ks] = *reinterpret_cast<const uint2*>(&tab_th[0][g * half + d0 / 2]);
+        tsn[ks] = *reinterpret_cast<const uint2*>(&tab_th[1][g * half + d0 / 2]);
+      }
     }
     // tiles 0 .. NS-2 behind everything else
 #pragma unroll
@@ -3290,25 +3356,30 @@ static int launch_f2_nw(const coda_attn_desc* d, hipStream_t st, int G) {
 }
 // pipelined 32-row flash tiles: 8 waves, G heads x 8 / G groups of 16
 // queries; QM the query case (see attn_f3_bf16)
-template <int DH, int QM>
+template <int DH, int QM, bool TB>
 static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G) {
   constexpr int NW = 8;
   const int npairs = d->B * d->Hkv;
   const int NQ = NW / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
   const size_t lds = 4 * (size_t)(F2Layout<DH>::KBYTES + F2Layout<DH>::VBYTES);
-  int rc = lds_limit<attn_f3_bf16<DH, NW, QM>>(lds, "coda_diff_attn_fwd");
+  int rc = lds_limit<attn_f3_bf16<DH, NW, QM, TB>>(lds, "coda_diff_attn_fwd");
   if (rc) return rc;
-  hipLaunchKernelGGL((attn_f3_bf16<DH, NW, QM>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk,
+  hipLaunchKernelGGL((attn_f3_bf16<DH, NW, QM, TB>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk,
                      npairs);
   return check_launch("attn_f3_bf16");
 }
 template <int DH>
 static int launch_f3(const coda_attn_desc* d, hipStream_t st, int G) {
-  if (!d->q_noise && d->rope_cos) return d->rope_interleaved ? launch_f3_qm<DH, 0>(d, st, G)
-                                                             : launch_f3_qm<DH, 1>(d, st, G);
-  if (d->q_noise && !d->rope_cos) return launch_f3_qm<DH, 2>(d, st, G);
-  return launch_f3_qm<DH, 3>(d, st, G);
+  // the RoPE + rotation cases stage their tables in LDS while the
+  // workgroup's 16 * 8 / G query rows fit (G >= 2)
+  const bool tb = 16 * (8 / G) <= kTabRows && G <= 8;
+  if (!d->q_noise && d->rope_cos) {
+    if (d->rope_interleaved) return tb ? launch_f3_qm<DH, 0, true>(d, st, G) : launch_f3_qm<DH, 0, false>(d, st, G);
+    return tb ? launch_f3_qm<DH, 1, true>(d, st, G) : launch_f3_qm<DH, 1, false>(d, st, G);
+  }
+  if (d->q_noise && !d->rope_cos) return launch_f3_qm<DH, 2, false>(d, st, G);
+  return launch_f3_qm<DH, 3, false>(d, st, G);
 }
 // CODA_PREFILL_KERNEL selects the prefill attention kernel for launch-shape
 // tuning: fa16 (16-row flash tiles), f2 / f2q2 (32-row tiles, one / two
