@@ -1570,15 +1570,20 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       float bv = -INFINITY;
       int bi = 0x7fffffff;
       for (int m = lane; m < M; m += 64) {
+        // the heads' dots 8 at a time, all in flight before the sum (kept
+        // in head order: the reference's mean over heads)
+        const float* src = ex ? dall_e + (int64_t)tt * Me + m : dall_s + (int64_t)tt * Ms + m;
+        const int64_t hstride = ex ? (int64_t)Te * Me : (int64_t)Ts * Ms;
         float acc = 0.f;
-        if (ex) {
-          for (int hh = 0; hh < Hkv; ++hh)
-            acc += __hip_atomic_load(dall_e + ((int64_t)hh * Te + tt) * Me + m, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          for (int hh = 0; hh < Hkv; ++hh)
-            acc += __hip_atomic_load(dall_s + ((int64_t)hh * Ts + tt) * Ms + m, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
+        for (int h0 = 0; h0 < Hkv; h0 += 8) {
+          float hv[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            hv[u] = h0 + u < Hkv ? __hip_atomic_load(src + (h0 + u) * hstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0.f;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (h0 + u < Hkv) acc += hv[u];
         }
         float v = E::rnd(acc / (float)Hkv);
         if (ex ? (m >= Ae || used[m] == 0) : m >= s.active_summary) v = neg_fill<T>();
@@ -1626,15 +1631,22 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       }
     }
   });
-  // ---- 4a. every token's routing; exact decisions (memory_banks.py:640-697)
-  for (int i = t; i < Te; i += NT) {
-    bv_e[i] = __builtin_bit_cast(float, __hip_atomic_load(dx.fl_e + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    bi_e[i] = __hip_atomic_load(dx.idx_e + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  for (int i = t; i < Ts; i += NT) {
-    idx_s[i] = __hip_atomic_load(dx.idx_s + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const float gt = gate[i];
-    wtok[i] = (!s.gated || gt >= s.tau_summary) ? E::rnd(gt) : 0.f;
+  // ---- 4a. every token's routing (all three loads in flight together);
+  // exact decisions (memory_banks.py:640-697)
+  for (int i = t; i < TT; i += NT) {
+    const int ie = min(i, max(Te, 1) - 1), is = min(i, max(Ts, 1) - 1);
+    const int32_t fe = Te > 0 ? __hip_atomic_load(dx.fl_e + ie, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    const int32_t xe = Te > 0 ? __hip_atomic_load(dx.idx_e + ie, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    const int32_t xs = Ts > 0 ? __hip_atomic_load(dx.idx_s + is, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    if (i < Te) {
+      bv_e[i] = __builtin_bit_cast(float, fe);
+      bi_e[i] = xe;
+    }
+    if (i < Ts) {
+      idx_s[i] = xs;
+      const float gt = gate[i];
+      wtok[i] = (!s.gated || gt >= s.tau_summary) ? E::rnd(gt) : 0.f;
+    }
   }
   if (wv == 0) {
     int u = 0;
