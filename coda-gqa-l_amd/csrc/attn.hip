@@ -2248,6 +2248,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
 // when a tile's max exceeds it by more than 2^8); P rounded to bf16 by the
 // hardware conversion.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x16 mfma_32x32x16(const bf16x8_t& a, const bf16x8_t& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -2815,8 +2816,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
     const bf16_t* thc = !given ? (const bf16_t*)a.theta_cos + (int64_t)h * half : nullptr;
     const bf16_t* ths = !given ? (const bf16_t*)a.theta_sin + (int64_t)h * half : nullptr;
-    uint4 uq[NKS], up[NKS], rc[NKS], rs[NKS];
-    uint2 rc2[NKS], rs2[NKS], tcs[NKS], tsn[NKS];
+    // QM 0 / 1 (RoPE and the noise rotation): the signal and noise lanes of
+    // a query split its channel steps, NOWN each (the signal lane the first
+    // half, the noise lane the second), rope and rotate their own, and trade
+    // with one permlane16 swap: the signal lane sends the rotated values the
+    // noise lane needs and gets the roped values it needs
+    constexpr bool SPLIT = QM == 0 || QM == 1;
+    constexpr int NOWN = SPLIT ? NKS / 2 : NKS;
+    const int ks_base = SPLIT ? NOWN * strm : 0;
+    uint4 uq[NOWN], up[NOWN], rc[NOWN], rs[NOWN];
+    uint2 rc2[NOWN], rs2[NOWN], tcs[NOWN], tsn[NOWN];
     // TB: the workgroup's RoPE rows (its 16 NQ queries) and noise angles
     // (its G heads) load once per workgroup, 16-byte pieces spread over the
     // threads, and reach the lanes through LDS: per-lane table loads were
@@ -2842,23 +2851,23 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
       }
     }
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      const int d0 = 16 * ks + 8 * hl;
-      uq[ks] = *reinterpret_cast<const uint4*>(qr + d0);
-      if (rope && !inter) up[ks] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
+    for (int u = 0; u < NOWN; ++u) {
+      const int d0 = 16 * (ks_base + u) + 8 * hl;
+      uq[u] = *reinterpret_cast<const uint4*>(qr + d0);
+      if (rope && !inter) up[u] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
       if constexpr (!TB) {
         if (rope && inter) {
-          rc2[ks] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
-          rs2[ks] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
+          rc2[u] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
+          rs2[u] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
         }
         if (rope && !inter) {
           const int f0 = d0 < half ? d0 : d0 - half;
-          rc[ks] = *reinterpret_cast<const uint4*>(csr + f0);
-          rs[ks] = *reinterpret_cast<const uint4*>(snr + f0);
+          rc[u] = *reinterpret_cast<const uint4*>(csr + f0);
+          rs[u] = *reinterpret_cast<const uint4*>(snr + f0);
         }
         if (!given) {
-          tcs[ks] = *reinterpret_cast<const uint2*>(thc + d0 / 2);
-          tsn[ks] = *reinterpret_cast<const uint2*>(ths + d0 / 2);
+          tcs[u] = *reinterpret_cast<const uint2*>(thc + d0 / 2);
+          tsn[u] = *reinterpret_cast<const uint2*>(ths + d0 / 2);
         }
       }
     }
@@ -2950,18 +2959,18 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
       __syncthreads();
       const int rl = 16 * qsub + qn;
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) {
-        const int d0 = 16 * ks + 8 * hl;
+      for (int u = 0; u < NOWN; ++u) {
+        const int d0 = 16 * (ks_base + u) + 8 * hl;
         if (inter) {
-          rc2[ks] = *reinterpret_cast<const uint2*>(&tab_rope[0][rl * kTabPitch + d0 / 2]);
-          rs2[ks] = *reinterpret_cast<const uint2*>(&tab_rope[1][rl * kTabPitch + d0 / 2]);
+          rc2[u] = *reinterpret_cast<const uint2*>(&tab_rope[0][rl * kTabPitch + d0 / 2]);
+          rs2[u] = *reinterpret_cast<const uint2*>(&tab_rope[1][rl * kTabPitch + d0 / 2]);
         } else {
           const int f0 = d0 < half ? d0 : d0 - half;
-          rc[ks] = *reinterpret_cast<const uint4*>(&tab_rope[0][rl * kTabPitch + f0]);
-          rs[ks] = *reinterpret_cast<const uint4*>(&tab_rope[1][rl * kTabPitch + f0]);
+          rc[u] = *reinterpret_cast<const uint4*>(&tab_rope[0][rl * kTabPitch + f0]);
+          rs[u] = *reinterpret_cast<const uint4*>(&tab_rope[1][rl * kTabPitch + f0]);
         }
-        tcs[ks] = *reinterpret_cast<const uint2*>(&tab_th[0][g * half + d0 / 2]);
-        tsn[ks] = *reinterpret_cast<const uint2*>(&tab_th[1][g * half + d0 / 2]);
+        tcs[u] = *reinterpret_cast<const uint2*>(&tab_th[0][g * half + d0 / 2]);
+        tsn[u] = *reinterpret_cast<const uint2*>(&tab_th[1][g * half + d0 / 2]);
       }
     }
     // tiles 0 .. NS-2 behind everything else
@@ -2969,25 +2978,25 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int t = 0; t < NS - 1; ++t)
       if (t < ntile) tile_load(t * KT, t);
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      const int d0 = 16 * ks + 8 * hl;
-      uint32_t w[4] = {uq[ks].x, uq[ks].y, uq[ks].z, uq[ks].w};
+    for (int u = 0; u < NOWN; ++u) {
+      const int d0 = 16 * (ks_base + u) + 8 * hl;
+      uint32_t w[4] = {uq[u].x, uq[u].y, uq[u].z, uq[u].w};
       if (rope && inter) {
         // pairs (2p, 2p+1) rotated by angle d0/2 + p: one bf16 dot2 per
         // output (fp32 products and sum, one rounding)
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-          const uint32_t r = rot_pair(w[pp], pp >> 1 ? rc2[ks].y : rc2[ks].x, pp >> 1 ? rs2[ks].y : rs2[ks].x, pp & 1);
+          const uint32_t r = rot_pair(w[pp], pp >> 1 ? rc2[u].y : rc2[u].x, pp >> 1 ? rs2[u].y : rs2[u].x, pp & 1);
           w[pp] = rope_lane ? r : w[pp];
         }
       }
       if (rope && !inter) {
         // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin
         float x[8], cc[8], ss[8], y[8];
-        unpack8(uq[ks], x);
-        unpack8(rc[ks], cc);
-        unpack8(rs[ks], ss);
-        unpack8(up[ks], y);
+        unpack8(uq[u], x);
+        unpack8(rc[u], cc);
+        unpack8(rs[u], ss);
+        unpack8(up[u], y);
         const bool lo = d0 < half;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -2997,14 +3006,33 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) w[pp] = rope_lane ? pk_bf16(x[2 * pp], x[2 * pp + 1]) : w[pp];
       }
-      if (!given) {
+      if constexpr (SPLIT) {
+        // this lane's roped values (r) and their rotation (t); the swap
+        // leaves the signal lane r of step u and r of step u + NOWN (its
+        // partner's), the noise lane t of step u (its partner's) and t of
+        // step u + NOWN
+        uint32_t lo4[4], hi4[4];
 #pragma unroll
         for (int pp = 0; pp < 4; ++pp) {
-          const uint32_t r = rot_pair(w[pp], pp >> 1 ? tcs[ks].y : tcs[ks].x, pp >> 1 ? tsn[ks].y : tsn[ks].x, pp & 1);
-          w[pp] = noise ? r : w[pp];
+          const uint32_t t = rot_pair(w[pp], pp >> 1 ? tcs[u].y : tcs[u].x, pp >> 1 ? tsn[u].y : tsn[u].x, pp & 1);
+          const auto sw = __builtin_amdgcn_permlane16_swap(w[pp], t, false, false);
+          lo4[pp] = (uint32_t)sw[0];
+          hi4[pp] = (uint32_t)sw[1];
         }
+        // (a row past Lq read row 0: finite values, and its output is not
+        // stored)
+        qf[u] = __builtin_bit_cast(bf16x8_t, uint4{lo4[0], lo4[1], lo4[2], lo4[3]});
+        qf[u + NOWN] = __builtin_bit_cast(bf16x8_t, uint4{hi4[0], hi4[1], hi4[2], hi4[3]});
+      } else {
+        if (!given) {
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) {
+            const uint32_t r = rot_pair(w[pp], pp >> 1 ? tcs[u].y : tcs[u].x, pp >> 1 ? tsn[u].y : tsn[u].x, pp & 1);
+            w[pp] = noise ? r : w[pp];
+          }
+        }
+        qf[u] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
       }
-      qf[ks] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
     }
   }
 
@@ -3025,6 +3053,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
   for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
 
+  f32x16 st[2][2];  // S of two tiles: [parity][key block]
   // per-entry masking a tile needs: 1 = the end / causal threshold only,
   // 2 = also hidden prefix slots (visibility bytes), 0 = none
   auto tile_mask_mode = [&](int kt0) {
@@ -3037,12 +3066,33 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
     return al_m ? 2 : thr_m ? 1 : 0;
   };
-  auto mask_entry = [&](float v, int kt0, int kb, int j, int mode) {
+  // (branch-free: every lane reads a byte of the LDS copy, a valid one
+  // past the prefix, and selects)
+  auto mask_entry = [&](float v, int kt0, int kb, int j, auto mode_c) {
     const int kidx = kt0 + 32 * kb + 4 * hl + kk(j);
-    if (mode == 1) return kidx <= thr ? v : -INFINITY;
-    const bool pre = kidx < a.Lp;
-    const bool vis = pre ? al_lds[pre ? kidx : 0] != 0 : kidx <= thr;
-    return vis ? v : -INFINITY;
+    const int thr_ok = kidx <= thr;
+    if constexpr (decltype(mode_c)::value == 1) {
+      return thr_ok ? v : -INFINITY;
+    } else {
+      const int byte = al_lds[min(kidx, kMaxRowsPrefix - 1)];
+      const int pre = kidx < a.Lp;
+      return ((pre & (byte != 0)) | ((pre ^ 1) & thr_ok)) ? v : -INFINITY;
+    }
+  };
+  // a tile's mask in place, one straight-line loop per mode
+  auto mask_tile = [&](auto par_c, int kt0, int mode) {
+    constexpr int P = decltype(par_c)::value;
+    if (mode == 1) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) st[P][kb][j] = mask_entry(st[P][kb][j], kt0, kb, j, std::integral_constant<int, 1>{});
+    } else if (mode == 2) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) st[P][kb][j] = mask_entry(st[P][kb][j], kt0, kb, j, std::integral_constant<int, 2>{});
+    }
   };
   // running-max update from a tile's masked scores (lanes l and l ^ 32
   // share a row), with the lazy rescale of O and the row sum
@@ -3058,7 +3108,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
   };
 
-  f32x16 st[2][2];  // S of two tiles: [parity][key block]
   // ---- S(0), masked, max folded
   if (ntile > 0) {
     vm_wait(LPT * (min(ntile, NS - 1) - 1));
@@ -3080,13 +3129,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
       st[0][kb] = mfma_32x32x16(__builtin_bit_cast(bf16x8_t, kr[f % 4]), qf[ks], ks == 0 ? f32x16{} : st[0][kb]);
       __builtin_amdgcn_sched_barrier(0);
     });
-    const int mode0 = tile_mask_mode(0);
-    if (mode0) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) st[0][kb][j] = mask_entry(st[0][kb][j], 0, kb, j, mode0);
-    }
+    mask_tile(std::integral_constant<int, 0>{}, 0, tile_mask_mode(0));
     float mx = st[0][0][0];
 #pragma unroll
     for (int j = 1; j < 16; ++j) mx = fmaxf(mx, st[0][0][j]);
@@ -3115,8 +3158,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
       const int kb = e >> 4, j = e & 15;
       const float p0 = fast_exp2(fmaf(st[PAR][kb][j], scale, -mu));
       const float p1 = fast_exp2(fmaf(st[PAR][kb][j + 1], scale, -mu));
-      ls += p0 + p1;
       pw[e >> 1] = pk_bf16(p0, p1);
+      // the row sum adds the bf16 values the PV product uses: one dot2
+      // with (1, 1) a pair
+      ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, pw[e >> 1]),
+                                           bf16x2v_t{(__bf16)1.f, (__bf16)1.f}, ls, false);
     };
     // ---- phase A: S(it + 1) products, each with one pair of P(it)
     if (has_next) {
@@ -3145,15 +3191,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     l_s += ls;
     // ---- S(it + 1)'s mask, where the tile needs one (rare: the tile on the
     // causal diagonal, the end, hidden prefix slots)
-    if (has_next) {
-      const int mode = tile_mask_mode(kt1);
-      if (mode) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) st[NXT][kb][j] = mask_entry(st[NXT][kb][j], kt1, kb, j, mode);
-      }
-    }
+    if (has_next) mask_tile(std::integral_constant<int, NXT>{}, kt1, tile_mask_mode(kt1));
     // ---- phase C: O += V(it)^T P(it), each product with the running max
     // of two entries of S(it + 1) (four at head_dim 64; a stale S when
     // there is no next tile, whose max is then dropped)
