@@ -2835,6 +2835,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     constexpr int TPT = (2 * kTabRows * TCH + 2 * 8 * TCH + NW * 64 - 1) / (NW * 64);
     uint4 tv[TPT];
     const int nrow = 16 * NQ, nrope = 2 * nrow * TCH, ntab = nrope + 2 * G * TCH;
+    // piece c of a table: (which, row, 16-byte piece) by shifts (G and the
+    // row count are powers of two here, TCH a power of two)
+    static_assert((TCH & (TCH - 1)) == 0, "table pieces per row");
+    constexpr int lg_tch = __builtin_ctz(TCH);
+    const int lg_g = __builtin_ctz(G), lg_row = __builtin_ctz(nrow);
     if constexpr (TB) {
 #pragma unroll
       for (int u = 0; u < TPT; ++u) {
@@ -2842,8 +2847,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         const int c = min(tid + NW * 64 * u, ntab - 1);
         const bool th = c >= nrope;
         const int cc = th ? c - nrope : c;
-        const int nr = th ? G : nrow;
-        const int which = cc / (nr * TCH), rr = (cc / TCH) % nr, ch = cc % TCH;
+        const int lgn = th ? lg_g : lg_row;
+        const int which = cc >> (lgn + lg_tch), rr = (cc >> lg_tch) & ((1 << lgn) - 1), ch = cc & (TCH - 1);
         const bf16_t* src = th ? (const bf16_t*)(which ? a.theta_sin : a.theta_cos) + (int64_t)(hk * G + rr) * half + 8 * ch
                                : (const bf16_t*)(which ? a.rope_sin : a.rope_cos) +
                                      (int64_t)min(qb * 16 * NQ + rr, a.Lq - 1) * half + 8 * ch;
@@ -2902,22 +2907,16 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
       for (int c = 0; c < ALC; ++c) {
         const int i0 = 16 * (lane + 64 * c);
-        uint32_t wd[4] = {al_c[c].x, al_c[c].y, al_c[c].z, al_c[c].w};
-        // each byte to 0 / 1: set and inside the prefix (every prefix byte
-        // without visibility bytes), branch-free
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          uint32_t r = 0;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = i0 + 4 * q4 + e;
-            const bool set = a.allowed == nullptr || ((wd[q4] >> (8 * e)) & 0xffu) != 0;
-            r |= (uint32_t)(set && i < a.Lp) << (8 * e);
-          }
-          wd[q4] = r;
-        }
-        al_c[c] = uint4{wd[0], wd[1], wd[2], wd[3]};
-        const bool all16 = ((wd[0] & wd[1] & wd[2] & wd[3]) == 0x01010101u);
+        // a prefix key is visible when its byte is nonzero (every prefix key
+        // without visibility bytes; the per-entry mask reads bytes of keys
+        // inside the prefix only); the chunk's 16 keys are all visible when
+        // the chunk lies inside the prefix and has no zero byte (a word has
+        // one exactly when (w - 0x01010101) & ~w & 0x80808080 is nonzero)
+        const uint4 v = a.allowed == nullptr ? uint4{0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u} : al_c[c];
+        al_c[c] = v;
+        const uint32_t z = ((v.x - 0x01010101u) & ~v.x) | ((v.y - 0x01010101u) & ~v.y) |
+                           ((v.z - 0x01010101u) & ~v.z) | ((v.w - 0x01010101u) & ~v.w);
+        const bool all16 = i0 + 16 <= a.Lp && (z & 0x80808080u) == 0u;
         // 16-byte chunk k of this group is lane k: block e of the group is
         // chunks 2e, 2e + 1, so bit e of the group's 32 is (bit 2e & bit
         // 2e + 1) of the ballot, gathered from the even bits
@@ -2950,8 +2949,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         if (c < ntab) {
           const bool th = c >= nrope;
           const int cc = th ? c - nrope : c;
-          const int nr = th ? G : nrow;
-          const int which = cc / (nr * TCH), rr = (cc / TCH) % nr, ch = cc % TCH;
+          const int lgn = th ? lg_g : lg_row;
+          const int which = cc >> (lgn + lg_tch), rr = (cc >> lg_tch) & ((1 << lgn) - 1), ch = cc & (TCH - 1);
           bf16_t* dst = th ? &tab_th[which][rr * half + 8 * ch] : &tab_rope[which][rr * kTabPitch + 8 * ch];
           *reinterpret_cast<uint4*>(dst) = tv[u];
         }
