@@ -1336,6 +1336,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   constexpr int NV = (DH + 63) / 64, LF = DH / 2, NCOL = DH + LF, CH = DH / 8;
   extern __shared__ __attribute__((aligned(16))) char fsm[];
   __shared__ int ties, any_used_s;
+  __shared__ int dec_wave[kFusedThreads / 64], dec_cnt[5];
   // workgroup -> (sequence, head, z): workgroups are dealt round robin to
   // the 8 XCDs, so the NZ workgroups of one (sequence, head) pair take
   // consecutive turns of one XCD (they share its L2); the workgroups of a
@@ -1491,6 +1492,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       rk[m] = sel::Item<int64_t>{u ? last[m] : kNegBig, (int64_t)m};
     }
   if (t == 0) ties = 0;
+  if (t < 5) dec_cnt[t] = 0;
   __syncthreads();
   // ---- 2. this workgroup's routing rows, normalised (exact: V, all DH
   // channels; summary: K channels [DH/2, DH)), then their dots with head
@@ -1655,43 +1657,65 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
     if (lane == 0) any_used_s = u;
   }
   __syncthreads();
-  if (Te > 0 && t == 0) {
+  if (Te > 0) {
+    // exact decisions, one thread per token; the rank of a novel kept token
+    // (the reference's cumsum(novel & keep) - 1) from the ballots of the
+    // waves before it and the lanes before it
     const int any_used = any_used_s;
-    int rank = -1;
-    int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
-    for (int tt = 0; tt < Te; ++tt) {
-      const bool keep = s.gated ? (gate[tt] >= s.tau_exact) : true;
-      const float bv = bv_e[tt];
+    const uint64_t lt_mask = lane ? (~0ull >> (64 - lane)) : 0ull;
+    int carry = 0;  // novel kept tokens of the earlier passes
+    for (int base = 0; base < Te; base += NT) {
+      const int tt = base + t;
+      const bool in = tt < Te;
+      const int ti = in ? tt : Te - 1;
+      const bool keep = s.gated ? (gate[ti] >= s.tau_exact) : true;
+      const float bv = bv_e[ti];
       const bool novel = !any_used || bv < E::rnd(s.tau_novel);
       const bool hit = any_used && bv >= E::rnd(s.tau_match);
-      const bool nk = novel && keep;
-      if (nk) ++rank;  // cumsum(novel & keep) - 1 at tt
-      const bool cap = nk && rank < Ae;
-      int idx = bi_e[tt];
-      if (cap) {
-        int r = rank < 0 ? 0 : rank;
-        if (r > n_lru - 1) r = n_lru - 1;
-        idx = lru[r];
+      const bool nk = in && novel && keep;
+      const uint64_t bal = __ballot(nk);
+      if (lane == 0) dec_wave[wv] = __popcll(bal);
+      __syncthreads();
+      int before = carry, total = carry;
+      for (int w = 0; w < NW; ++w) {
+        const int c = dec_wave[w];
+        before += w < wv ? c : 0;
+        total += c;
       }
+      const int rank = before + __popcll(bal & lt_mask) + (nk ? 1 : 0) - 1;
+      const bool cap = nk && rank < Ae;
+      int idx = bi_e[ti];
+      if (cap) idx = lru[min(max(rank, 0), n_lru - 1)];
       const bool touch = keep && (!novel || cap);
       const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
-      idx_e[tt] = idx;
-      fl_e[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
-      cnt_ow += ow;
-      cnt_cap += cap;
-      cnt_hit += (hit && keep);
-      cnt_gated += !keep;
-      cnt_fr += (nk && !cap);
-    }
-    if (lead) {
-      if (s.metrics) {
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, cnt_ow);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, cnt_fr);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, cnt_cap);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, cnt_hit);
-        if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, cnt_gated);
+      if (in) {
+        idx_e[tt] = idx;
+        fl_e[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
       }
-      if (s.frustrated) atomic_add_i64(s.frustrated + 0, cnt_fr);
+      if (lead && (s.metrics || s.frustrated)) {
+        const int c_ow = __popcll(__ballot(in && ow)), c_cap = __popcll(__ballot(in && cap));
+        const int c_hit = __popcll(__ballot(in && hit && keep)), c_gated = __popcll(__ballot(in && !keep));
+        const int c_fr = __popcll(__ballot(nk && !cap));
+        if (lane == 0) {
+          atomicAdd(&dec_cnt[0], c_ow);
+          atomicAdd(&dec_cnt[1], c_cap);
+          atomicAdd(&dec_cnt[2], c_hit);
+          atomicAdd(&dec_cnt[3], c_gated);
+          atomicAdd(&dec_cnt[4], c_fr);
+        }
+      }
+      carry = total;
+      __syncthreads();
+    }
+    if (lead && t == 0) {
+      if (s.metrics) {
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, dec_cnt[0]);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, dec_cnt[4]);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, dec_cnt[1]);
+        atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, dec_cnt[2]);
+        if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, dec_cnt[3]);
+      }
+      if (s.frustrated) atomic_add_i64(s.frustrated + 0, dec_cnt[4]);
     }
   }
   // (exact flags and touch stamps start cleared; the staged stamps are no
