@@ -1632,6 +1632,17 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
         }
       }
     }
+    // ring gates and visibility bytes of the chunk's surviving tokens
+    // (per sequence: head 0's workgroups share them)
+    if (h == 0) {
+      const int n_tok = Lr + g.blk - first;
+      const int pt = (n_tok + NZ - 1) / NZ, q0 = min(n_tok, z * pt), q1 = min(n_tok, q0 + pt);
+      for (int i = q0 + t1; i < q1; i += nt1) {
+        const int r = first + i, slot = (rhead + r) % W;
+        s.g_recent[(int64_t)b * W + slot] = gb[(int64_t)b * g.g_sb + (r - Lr)];
+        al[slot] = 1;
+      }
+    }
   });
   // ---- 4a. every token's routing (all three loads in flight together);
   // exact decisions (memory_banks.py:640-697)
@@ -1773,23 +1784,18 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
     for (int m = t; m < Ms; m += NT)
       if (sflag[m] & 1) al[W + Me + m] = 1;
     if (Ts > 0 && wv == 0) {
+      // counts and flags by ballots (no shuffle chain on the lead's path)
       int64_t upd = 0, ins = 0;
-      int all_used = 1, any_cnt = 0;
-      for (int m = lane; m < Ms; m += 64) {
-        const int f = sflag[m];
-        upd += f & 1;
-        ins += (f >> 1) & 1;
-        if (m < s.active_summary) {
-          if (!(used[Me + m] != 0 || (f & 1))) all_used = 0;
-          if (f & 1) any_cnt = 1;
-        }
+      bool all_used = true, any_cnt = false;
+      for (int m0 = 0; m0 < Ms; m0 += 64) {
+        const int m = m0 + lane;
+        const int f = m < Ms ? sflag[m] : 0;
+        const bool act = m < Ms && m < s.active_summary;
+        upd += __popcll(__ballot(f & 1));
+        ins += __popcll(__ballot((f >> 1) & 1));
+        all_used = all_used && __ballot(act && !(used[Me + min(m, Ms - 1)] != 0 || (f & 1))) == 0;
+        any_cnt = any_cnt || __ballot(act && (f & 1)) != 0;
       }
-      for (int o = 32; o > 0; o >>= 1) {
-        upd += __shfl_xor(upd, o, 64);
-        ins += __shfl_xor(ins, o, 64);
-      }
-      all_used = wave_and(all_used);
-      any_cnt = wave_or(any_cnt);
       if (lane == 0) {
         if (s.metrics) {
           atomic_add_i64(s.metrics + CODA_CNT_SUMMARY_UPDATES, upd);
@@ -1800,12 +1806,6 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
           if (any_cnt) atomic_add_i64(s.frustrated + 2, 1);
         }
       }
-    }
-    // ring gates and visibility bytes of the chunk's surviving tokens
-    for (int r = first + t; r < Lr + g.blk; r += NT) {
-      const int slot = (rhead + r) % W;
-      s.g_recent[(int64_t)b * W + slot] = gb[(int64_t)b * g.g_sb + (r - Lr)];
-      al[slot] = 1;
     }
   }
   __syncthreads();
