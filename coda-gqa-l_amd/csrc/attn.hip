@@ -2248,7 +2248,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) vo
 // when a tile's max exceeds it by more than 2^8); P rounded to bf16 by the
 // hardware conversion.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f32x16 mfma_32x32x16(const bf16x8_t& a, const bf16x8_t& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -3158,10 +3157,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
       const float p0 = fast_exp2(fmaf(st[PAR][kb][j], scale, -mu));
       const float p1 = fast_exp2(fmaf(st[PAR][kb][j + 1], scale, -mu));
       pw[e >> 1] = pk_bf16(p0, p1);
-      // the row sum adds the bf16 values the PV product uses: one dot2
-      // with (1, 1) a pair
-      ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, pw[e >> 1]),
-                                           bf16x2v_t{(__bf16)1.f, (__bf16)1.f}, ls, false);
+      // (plain adds: a dot2 does not issue beside a running product)
+      ls += p0 + p1;
     };
     // ---- phase A: S(it + 1) products, each with one pair of P(it)
     if (has_next) {
