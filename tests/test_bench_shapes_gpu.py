@@ -289,3 +289,52 @@ def test_raw_k_decode_equals_roped_k(Dh, inter, monkeypatch):
         assert torch.equal(h0, h1), f"fused={fused}: heads differ between raw and roped k"
         for f in ("k_buf", "v_buf", "allowed", "g_recent", "mem_last_exact", "_exact_v_norm", "_sum_lf_k_norm"):
             assert torch.equal(getattr(s0, f), getattr(s1, f)), f"fused={fused}: state field {f} differs"
+
+
+@pytest.mark.parametrize("G,Dh", [(2, 128), (4, 128), (8, 128), (4, 64)])
+@torch.no_grad()
+def test_decode_heads_do_not_depend_on_batch(G, Dh):
+    """A batch of 32 (Hkv x B = 256 workgroups, one per CU) gives its first
+    sequences exactly the head outputs and state bytes they get in a batch of
+    4 from the same initial state, steps into eviction included: nothing in
+    the step couples the sequences of a batch."""
+    _need_gpu()
+    import dataclasses
+    from coda_oracle import OracleLayer
+    Hkv, W, Me, Ms, n = 8, 16, 8, 8, 28
+    H, Bbig, Bs = G * Hkv, 32, 4
+    print(f"[batch independence] G{G} Dh{Dh}", flush=True)
+    kw = dict(embed_dim=H * Dh, num_heads=H, num_kv_heads=Hkv, window=W, num_landmarks_exact=Me,
+              num_landmarks_summary=Ms, rope_base=1e4, rope_interleaved=True)
+    torch.manual_seed(71)
+    m = OracleLayer(**kw).to(torch.bfloat16).eval()
+    p = product_like(m, {"kw": kw}, torch.bfloat16, DEV)
+    torch.manual_seed(72)
+    st_big = m.init_state(batch_size=Bbig, dtype=torch.bfloat16)
+    first = lambda st: dataclasses.replace(st, **{f.name: getattr(st, f.name)[:Bs].clone() for f in
+                                                  dataclasses.fields(st) if torch.is_tensor(getattr(st, f.name))})
+    g = torch.Generator().manual_seed(73)
+    seq = [(torch.randn(Bbig, H, 1, Dh, generator=g), torch.randn(Bbig, Hkv, 1, Dh, generator=g),
+            torch.randn(Bbig, Hkv, 1, Dh, generator=g), torch.sigmoid(torch.randn(Bbig, generator=g) * 2),
+            torch.sigmoid(torch.randn(Bbig, H, 1, generator=g))) for _ in range(n)]
+    runs = {}
+    for B, st0 in ((Bbig, st_big), (Bs, first(st_big))):
+        st = to_product_state(st0, DEV)
+        heads = []
+        for q, k, v, gt, lam in seq:
+            pos = int(st.pos)
+            c, s_ = p.rope(seq_len=1, offset=pos, device=DEV, dtype=torch.bfloat16)
+            h = p.decode_step_core(q[:B].to(DEV, torch.bfloat16), k[:B].to(DEV, torch.bfloat16),
+                                   v[:B].to(DEV, torch.bfloat16), gt[:B].to(DEV), lam[:B].to(DEV, torch.bfloat16),
+                                   st, c.contiguous(), s_.contiguous(), k_roped=False)
+            heads.append(h[:Bs].cpu())
+        torch.cuda.synchronize()
+        runs[B] = (torch.stack(heads), _cpu_copy(st))
+    hb, sb = runs[Bbig]
+    hs, ss = runs[Bs]
+    assert torch.equal(hb, hs), f"G{G} Dh{Dh}: heads of sequences 0-3 depend on the batch"
+    for f in ("k_buf", "v_buf", "allowed", "g_recent", "mem_last_exact", "_exact_v_norm", "_sum_lf_k_norm"):
+        a, b = getattr(sb, f), getattr(ss, f)
+        if a is None:
+            continue
+        assert torch.equal(a[:Bs], b), f"G{G} Dh{Dh}: state field {f} of sequences 0-3 depends on the batch"
