@@ -2684,6 +2684,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   extern __shared__ __attribute__((aligned(16))) char f3_smem[];
   __shared__ __attribute__((aligned(16))) uint8_t al_lds[kMaxRowsPrefix];
   __shared__ __attribute__((aligned(16))) float w_lds[DH];
+  // each wave's 16 lambda values (through LDS: a register across the tile
+  // loop would spill)
+  __shared__ float lam_lds[NW * 16];
   // TB: cos / sin rows of the workgroup's queries, cos / sin of its heads'
   // noise angles
   __shared__ __attribute__((aligned(16))) bf16_t tab_rope[TB ? 2 : 1][TB ? kTabRows * kTabPitch : 8];
@@ -2937,6 +2940,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         }
       }
       if (tid < DH) w_lds[tid] = bf2f(w_raw);
+      if (lane < 16) lam_lds[wv * 16 + lane] = bf2f(lam_raw);
     }
     if constexpr (TB) {
       // tables to LDS (rows padded by 16 bytes, so the 16 query rows of a
@@ -3235,7 +3239,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   // ---- epilogue (see attn_f2_bf16)
   const float l_tot = xsum32(l_s);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  const float lam = bf2f(lam_raw);
+  const float lam = lam_lds[wv * 16 + qn];
   float y[NDB][16];
   float sq = 0.f;
 #pragma unroll
