@@ -1378,8 +1378,10 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       __builtin_amdgcn_wave_barrier();
       for (int r = 64 * wv + lane; r < Me + Ms; r += 192) {
         const bool ex = r < Me;
-        const float acc = ex ? lane_dot_cpu_order<T>(en + (int64_t)r * DH, un, DH)
-                             : lane_dot_cpu_order<T>(sn + (int64_t)(r - Me) * LF, un + DH, LF);
+        // (every 16-byte piece of the row in flight at once: one memory
+        // round trip before the chain instead of one per few pieces)
+        const float acc = ex ? lane_dot_cpu_order<T, DH / 16>(en + (int64_t)r * DH, un, DH)
+                             : lane_dot_cpu_order<T, DH / 16>(sn + (int64_t)(r - Me) * LF, un + DH, LF);
         dots_lds[r] = Elt<T>::rnd(acc);
       }
     }
@@ -1442,11 +1444,13 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
     __builtin_amdgcn_wave_barrier();
     // the record dots of the norm rows this update rewrote: exact row on
     // lane 0, summary row on lane 1
+    // (one call on operands chosen per lane, so the two chains run side by
+    // side rather than one after the other)
     if (lane < 2) {
       const bool ex = lane == 0;
       if (ex ? (Me > 0 && dd.ow_e) : (Ms > 0 && dd.keep_s))
-        fix_lds[lane] = Elt<T>::rnd(ex ? lane_dot_cpu_order<T>(nnorm_e, vnrm, DH)
-                                       : lane_dot_cpu_order<T>(nnorm_s, knrm, LF));
+        fix_lds[lane] = Elt<T>::rnd(lane_dot_cpu_order<T, DH / 8>(ex ? nnorm_e : nnorm_s, ex ? vnrm : knrm,
+                                                                   ex ? DH : LF));
     }
   }
   if (wv == 3) {

@@ -130,13 +130,18 @@ __device__ __forceinline__ float wave_sumsq_cpu_order(const float (&x)[NV], cons
   const int nv = len - len % VW;
   const int j = threadIdx.x & 7;
   // accumulator j on lanes j, j + 8, ... (lane j's copy is read); row
-  // channel r0 + j lives in register (LO + r0) / 64, lane (LO + r0) % 64 + j
+  // channel r0 + j lives in register (LO + r0) / 64, lane (LO + r0) % 64 + j.
+  // Every cross-lane fetch is issued before the chain starts: fetched one
+  // at a time, each waits out the full LDS-crossbar latency
+  constexpr int NR = (64 * NV - LO) / 8;
+  float vals[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) vals[k] = __shfl(x[(LO + 8 * k) >> 6], ((LO + 8 * k) & 63) + j, 64);
+  __builtin_amdgcn_sched_barrier(0);
   float acc = 0.f;
 #pragma unroll
-  for (int r0 = 0; r0 < 64 * NV - LO; r0 += 8) {
-    const float v = __shfl(x[(LO + r0) >> 6], ((LO + r0) & 63) + j, 64);
-    if (r0 + j < nv) acc = fmaf(v, v, acc);
-  }
+  for (int k = 0; k < NR; ++k)
+    if (8 * k + j < nv) acc = fmaf(vals[k], vals[k], acc);
   float ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc), 0));
 #pragma unroll
   for (int q = 1; q < 8; ++q)
