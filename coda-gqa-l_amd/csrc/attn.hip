@@ -1290,7 +1290,9 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
       p[jj] = bf2f(f2bf(fast_exp2(sv[jj] - muse)));
       ps += p[jj];
     }
-    ps = xsum32(xsum16(ps));
+    // (l_i is this lane's share of the row sum, rescaled with the row's
+    // alpha, which every lane group of the row shares; the four shares add
+    // up once, before the merge)
     l_i = l_i * alpha + ps;
     m_i = mnew;
     const short4_t pf = pack4(p[0], p[1], p[2], p[3]);
@@ -1499,6 +1501,7 @@ __global__ __launch_bounds__(256) void decode_step_bf16(const coda_attn_desc a, 
   }
   // ---- merge the 4 waves (rows r < R), epilogue (the bank stage is free)
   float* red_o = reinterpret_cast<float*>(ds_u);  // [NW][R][DH + 4]
+  l_i = xsum32(xsum16(l_i));
   if (g4 == 0) {
     red_m[wv][n] = m_i;
     red_l[wv][n] = l_i;
