@@ -62,7 +62,7 @@ class BankDesc(ctypes.Structure):
         ("exact_v_norm", _vp), ("sum_lf_k_norm", _vp), ("eta", _vp),
         ("gated", _i32), ("tau_exact", _f32), ("tau_summary", _f32), ("tau_match", _f32), ("tau_novel", _f32),
         ("refresh_on_hit", _i32), ("overwrite_on_insert", _i32), ("energy_scale", _f32),
-        ("metrics", _vp), ("frustrated", _vp), ("trace", _vp),
+        ("metrics", _vp), ("frustrated", _vp), ("trace", _vp), ("active", _vp),
     ]
 
 
@@ -106,6 +106,8 @@ _SIGS = {
     "coda_block_workspace_bytes": (_i32, [ctypes.POINTER(BankDesc), _i32, ctypes.POINTER(ctypes.c_size_t)]),
     "coda_block_write_check": (_i32, [ctypes.POINTER(BankDesc), _i32, _i32]),
     "coda_block_sync_timeouts": (_i32, [ctypes.POINTER(ctypes.c_uint)]),
+    "coda_bank_expand": (_i32, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
+    "coda_block_sync_spin_limit": (_i32, [_i32]),
     "coda_block_write_noalloc": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,
                                         _i32, _i64, _vp, _i32, _i32, _i32, _vp]),
     "coda_block_write_noalloc_max_bytes": (ctypes.c_size_t, []),
@@ -115,6 +117,10 @@ _SIGS = {
     "coda_project_workspace_bytes": (_i32, [ctypes.POINTER(ProjDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "coda_project_epilogue": (_i32, [ctypes.POINTER(ProjDesc), _vp, _i64, _vp]),
     "coda_topk_order_host": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
+    # the reference's typed epilogue symbols (void, errors in coda_last_error)
+    **{"diff_epilogue_forward_" + t: (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp])
+       for t in ("bf16", "fp16", "fp32")},
+    **{"diff_sub_only_forward_" + t: (None, [_vp, _vp, _vp, _vp, _i32, _i32, _vp]) for t in ("bf16", "fp16", "fp32")},
     "coda_topk_order_host_i64": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
 }
 

@@ -234,6 +234,10 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         if self.training:
             raise NotImplementedError("CoDAGQALandmarkPerf2 on MI355X is inference-only (no backward kernels); "
                                       "call .eval()")
+        # a give-up of an earlier prefill call's bank update, once its status
+        # copy has landed (no host sync)
+        if self.__dict__.get("_status_pending"):
+            self.check_bank_status(wait=False)
 
     def _project_q(self, x: torch.Tensor) -> torch.Tensor:
         """(B, L, D) -> (B, H, L, Dh) view of the projection."""
@@ -337,62 +341,65 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         d.rope_cos, d.rope_sin = cos.data_ptr(), sin.data_ptr()
         return d
 
-    def _front(self, x: torch.Tensor, p0: int, fused: bool = True):
+    def _fused_front_ok(self, x: torch.Tensor) -> bool:
+        """Whether coda_project serves x: bf16, at most 64 token rows, D a
+        multiple of 64, head_dim a multiple of 4."""
+        B, L, D = x.shape
+        return x.dtype == torch.bfloat16 and B * L <= 64 and D % 64 == 0 and self.head_dim % 4 == 0
+
+    def _front(self, x: torch.Tensor, p0: int, fused: bool = False):
         """Projections of x (B, L, D) at positions p0 ..: q (B,H,L,Dh)
         pre-RoPE, k (B,Hkv,L,Dh) roped, v (B,Hkv,L,Dh), g (B,L) float32,
         lam (B,H,L), and the RoPE tables (L, Dh/2) (attention.py:396-410,
-        592-608).  bf16, up to 64 token rows (decode): one launch of the
-        hand-written projection GEMM with its fused epilogues
-        (coda_project); more rows: one library GEMM over the packed weights,
-        then coda_project_epilogue in place (q / k / v / lambda are views of
-        its output); other dtypes, or fused=False: the torch linears and the
-        RoPE kernel.  The layer's own step / prefill_chunked take fused=False:
-        a full-size benchmark run with the fused front end wired in faulted
-        the GPU once, with no cause found yet, so it stays off their path."""
+        592-608).  fused (decode-shaped input, _fused_front_ok): one launch of
+        the hand-written projection kernel with its RoPE and sigmoid
+        epilogues (coda_project), outputs in the torch path's layouts.
+        Otherwise the torch linears and the RoPE kernel.  The fused path for
+        many token rows (a library GEMM over the packed weights, the epilogue
+        kernel in place, q / k / v / lambda as strided views of its output)
+        is switched off: a full-size prefill with it faulted the GPU once and
+        no cause has been shown yet."""
         B, L, D = x.shape
         H, Hkv, Dh = self.num_heads, self.num_kv_heads, self.head_dim
         Fq, Fk = H * Dh, Hkv * Dh
         M = B * L
-        if not fused:
-            cos, sin = self.rope(seq_len=L, offset=p0, device=x.device, dtype=x.dtype)
-            cos, sin = cos.contiguous(), sin.contiguous()
-        else:
+        if fused:
+            if not self._fused_front_ok(x):
+                raise NotImplementedError(
+                    "the fused projection front end serves bf16 inputs of at most 64 token rows; its many-row form "
+                    "(coda_project_epilogue over a library GEMM) is switched off: a full-size run with it on the "
+                    "layer's path faulted the GPU and no cause has been shown yet")
             cos, sin = self._rope_rows(p0, L, x.device, x.dtype)
-        if fused and x.dtype == torch.bfloat16 and D % 64 == 0 and Dh % 4 == 0:
             d = self._proj_desc(x, M, L, cos, sin)
             g = torch.empty((B, L), dtype=torch.float32, device=x.device)
             d.g = g.data_ptr()
-            if M <= 64:
-                xs = x if (x.is_contiguous() and x.data_ptr() % 16 == 0) else x.contiguous()
-                w, b = self._proj_pack(x.dtype, "fused")
-                q = torch.empty((B, L, Fq), dtype=x.dtype, device=x.device)
-                k = torch.empty((B, L, Hkv, Dh), dtype=x.dtype, device=x.device)
-                v = torch.empty((B, L, Fk), dtype=x.dtype, device=x.device)
-                lam = torch.empty((B, L, H), dtype=x.dtype, device=x.device)
-                d.x, d.x_sm, d.w, d.bias = xs.data_ptr(), D, w.data_ptr(), b.data_ptr()
-                d.q, d.q_sm, d.k, d.k_sm, d.v, d.v_sm = q.data_ptr(), Fq, k.data_ptr(), Fk, v.data_ptr(), Fk
-                d.lam, d.lam_sm = lam.data_ptr(), H
-                nb = ctypes.c_size_t(0)
-                _hip.check(_hip.lib().coda_project_workspace_bytes(d, nb))
-                ws = None
-                if nb.value:
-                    cache = self.__dict__.setdefault("_proj_ws", {})
-                    ws = cache.get(str(x.device))
-                    if ws is None or ws.numel() < nb.value:
-                        ws = cache[str(x.device)] = torch.empty(nb.value, dtype=torch.uint8, device=x.device)
-                d.workspace, d.workspace_bytes = _hip.ptr(ws), nb.value
-                _hip.check(_hip.lib().coda_project(d, _hip.stream_of(x)))
-                return (q.view(B, L, H, Dh).permute(0, 2, 1, 3), k.permute(0, 2, 1, 3),
-                        v.view(B, L, Hkv, Dh).permute(0, 2, 1, 3), g, lam.permute(0, 2, 1), cos, sin)
-            w, b = self._proj_pack(x.dtype, "gemm")
-            y = torch.nn.functional.linear(x, w, b[:w.shape[0]])
-            nf = y.shape[-1]
-            _hip.check(_hip.lib().coda_project_epilogue(d, y.data_ptr(), nf, _hip.stream_of(x)))
-            q = y[..., :Fq].view(B, L, H, Dh).permute(0, 2, 1, 3)
-            k = y[..., Fq:Fq + Fk].view(B, L, Hkv, Dh).permute(0, 2, 1, 3)
-            v = y[..., Fq + Fk:Fq + 2 * Fk].view(B, L, Hkv, Dh).permute(0, 2, 1, 3)
-            lam = y[..., Fq + 2 * Fk:Fq + 2 * Fk + H].permute(0, 2, 1)
-            return q, k, v, g, lam, cos, sin
+            xs = x if (x.is_contiguous() and x.data_ptr() % 16 == 0) else x.contiguous()
+            w, b = self._proj_pack(x.dtype, "fused")
+            q = torch.empty((B, L, Fq), dtype=x.dtype, device=x.device)
+            k = torch.empty((B, L, Hkv, Dh), dtype=x.dtype, device=x.device)
+            v = torch.empty((B, L, Fk), dtype=x.dtype, device=x.device)
+            lam = torch.empty((B, L, H), dtype=x.dtype, device=x.device)
+            d.x, d.x_sm, d.w, d.bias = xs.data_ptr(), D, w.data_ptr(), b.data_ptr()
+            d.q, d.q_sm, d.k, d.k_sm, d.v, d.v_sm = q.data_ptr(), Fq, k.data_ptr(), Fk, v.data_ptr(), Fk
+            d.lam, d.lam_sm = lam.data_ptr(), H
+            nb = self.__dict__.setdefault("_proj_ws_bytes", {})
+            key = (M, D, H, Hkv, Dh, d.gate)
+            if key not in nb:
+                n = ctypes.c_size_t(0)
+                _hip.check(_hip.lib().coda_project_workspace_bytes(d, n))
+                nb[key] = n.value
+            ws = None
+            if nb[key]:
+                cache = self.__dict__.setdefault("_proj_ws", {})
+                ws = cache.get(str(x.device))
+                if ws is None or ws.numel() < nb[key]:
+                    ws = cache[str(x.device)] = torch.empty(nb[key], dtype=torch.uint8, device=x.device)
+            d.workspace, d.workspace_bytes = _hip.ptr(ws), nb[key]
+            _hip.check(_hip.lib().coda_project(d, _hip.stream_of(x)))
+            return (q.view(B, L, H, Dh).permute(0, 2, 1, 3), k.permute(0, 2, 1, 3),
+                    v.view(B, L, Hkv, Dh).permute(0, 2, 1, 3), g, lam.permute(0, 2, 1), cos, sin)
+        cos, sin = self.rope(seq_len=L, offset=p0, device=x.device, dtype=x.dtype)
+        cos, sin = cos.contiguous(), sin.contiguous()
         q = self._project_q(x)
         k_raw, v = self._project_kv_raw(x)
         # roped keys in the token-major layout of v, so K and V share strides
@@ -545,6 +552,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             c += 1
         if write_cache:
             self._ring_to_time_order(state, head, filled)
+            self._queue_status_check(ws)
         return out
 
     def prefill_chunked(self, x_seq: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *, block_size: int = 256,

@@ -31,6 +31,9 @@ METRIC_KEYS = ("exact_hits", "exact_inserts", "exact_overwrites", "exact_fill_ra
                "summary_inserts", "summary_fill_ratio", "tokens_gated_out", "total_evictions", "exact_frustrated",
                "summary_frustrated", "active_exact", "active_summary", "expansions_exact", "expansions_summary")
 
+# device counters after the kernels' own (coda_bank_expand)
+_EXPAND_KEYS = ("summary_frustrated", "expansions_exact", "expansions_summary")
+
 _COUNTER_KEYS = {
     _hip.CNT_EXACT_HITS: "exact_hits", _hip.CNT_EXACT_INSERTS: "exact_inserts",
     _hip.CNT_EXACT_OVERWRITES: "exact_overwrites", _hip.CNT_SUMMARY_UPDATES: "summary_updates",
@@ -54,9 +57,12 @@ class DeviceMetrics(dict):
         self.fill: Dict[str, torch.Tensor] = {}
 
     def accumulator(self, device) -> torch.Tensor:
+        """int64 device counters: the kernels' NUM_COUNTERS, then
+        summary_frustrated, expansions_exact, expansions_summary
+        (coda_bank_expand)."""
         if self.pending is None or self.pending.device != torch.device(device):
             self._fold()
-            self.pending = torch.zeros(_hip.NUM_COUNTERS + 1, dtype=torch.int64, device=device)
+            self.pending = torch.zeros(_hip.NUM_COUNTERS + len(_EXPAND_KEYS), dtype=torch.int64, device=device)
         return self.pending
 
     def add_host(self, key: str, n: int) -> None:
@@ -70,17 +76,51 @@ class DeviceMetrics(dict):
         if p is not None:
             c = p.tolist()
             p.zero_()
-            for i, key in _COUNTER_KEYS.items():
-                dict.__setitem__(self, key, dict.__getitem__(self, key) + int(c[i]))
-            dict.__setitem__(self, "summary_frustrated",
-                             dict.__getitem__(self, "summary_frustrated") + int(c[_hip.NUM_COUNTERS]))
+            # (a key the caller removed comes back only with a new count)
+            keys = list(_COUNTER_KEYS.items()) + [(_hip.NUM_COUNTERS + i, k) for i, k in enumerate(_EXPAND_KEYS)]
+            for i, key in keys:
+                if int(c[i]) or dict.__contains__(self, key):
+                    dict.__setitem__(self, key, dict.get(self, key, 0) + int(c[i]))
         for key, v in list(f.items()):
-            dict.__setitem__(self, key, float(v.item()))
+            old = dict.get(self, key)
+            val = v.item()
+            dict.__setitem__(self, key, int(val) if isinstance(old, int) and not isinstance(old, bool) else float(val))
         f.clear()
 
     def __getitem__(self, key):
         self._fold()
         return super().__getitem__(key)
+
+    # writes fold first, so a value set directly (a reset to 0, as on the
+    # reference's plain dict) is not later raised by counts that were still
+    # pending on the device when it was set
+    def __setitem__(self, key, value):
+        self._fold()
+        super().__setitem__(key, value)
+
+    def __delitem__(self, key):
+        self._fold()
+        super().__delitem__(key)
+
+    def update(self, *args, **kwargs):
+        self._fold()
+        super().update(*args, **kwargs)
+
+    def pop(self, key, *default):
+        self._fold()
+        return super().pop(key, *default)
+
+    def popitem(self):
+        self._fold()
+        return super().popitem()
+
+    def setdefault(self, key, default=None):
+        self._fold()
+        return super().setdefault(key, default)
+
+    def clear(self):
+        self._fold()
+        super().clear()
 
     def get(self, key, default=None):
         self._fold()
@@ -205,7 +245,13 @@ class MemoryBankMixin:
         d.B = st.k_buf.shape[0]
         d.Hkv, d.Dh, d.W, d.Me, d.Ms, d.lf = self.num_kv_heads, self.head_dim, self.window, self.Me, self.Ms, \
             self.lf_start
-        d.active_exact, d.active_summary = int(st.active_exact), int(st.active_summary)
+        # the host ints as they stand (no fold: with dynamic expansion the
+        # kernels read the device words instead)
+        sd = st.__dict__
+        d.active_exact = min(max(int(sd["active_exact"]), 0), self.Me)
+        d.active_summary = min(max(int(sd["active_summary"]), 0), self.Ms)
+        if self._expandable():
+            d.active = self._active_words(st).data_ptr()
         d.k_buf, d.v_buf = st.k_buf.data_ptr(), st.v_buf.data_ptr()
         d.allowed, d.g_recent, d.mem_last = st.allowed.data_ptr(), st.g_recent.data_ptr(), \
             st.mem_last_exact.data_ptr()
@@ -285,28 +331,43 @@ class MemoryBankMixin:
         if summary_ran and self.Ms > 0:
             mt.fill["summary_fill_ratio"] = st.allowed[:, W + Me:].any(dim=0).float().mean()
 
+    def _active_words(self, st) -> torch.Tensor:
+        """The state's active bank sizes as device words (int32 [exact,
+        summary]), made from its host ints when missing or on another device
+        (two fill launches, no host sync)."""
+        d = st.__dict__
+        dev = st.k_buf.device
+        w = d.get("_active_dev")
+        if w is None or w.device != dev:
+            a, b = int(st.active_exact), int(st.active_summary)  # (folds a stale copy from another device)
+            w = torch.empty(2, dtype=torch.int32, device=dev)
+            w[0:1].fill_(a)
+            w[1:2].fill_(b)
+            d["_active_dev"] = w
+            d["_active_stale"] = False
+        return w
+
     def _expand_from(self, st, fr: Optional[torch.Tensor], exact_count_mode: bool, ran_e: bool, ran_s: bool):
-        """Dynamic expansion after a bank update (attention.py:358-390).
-        Expansion changes host sizes, so it reads the flags (a host sync);
-        without it the summary frustration count stays on the device."""
+        """Dynamic expansion after a bank update (attention.py:358-390) and
+        its metrics, on the device (coda_bank_expand): the active sizes grow
+        in the state's device words, which the next update's kernels read;
+        the host ints fold in on their next read."""
         if fr is None:
             return
-        if not (self._expandable() and not self.training):
-            if ran_s and st.metrics is not None:
-                acc = st.metrics.accumulator(fr.device)
-                acc[_hip.NUM_COUNTERS:] += ((fr[1] == 0) & (fr[2] > 0)).to(torch.int64)
+        expand = self._expandable() and not self.training
+        mt = st.metrics if isinstance(st.metrics, DeviceMetrics) else None
+        counters = mt.accumulator(fr.device)[_hip.NUM_COUNTERS:] if mt is not None else None
+        if not expand and counters is None:
             return
-        f = fr.tolist()
-        if ran_e:
-            fr_e = int(f[0]) if exact_count_mode else int(f[0] > 0)
-            if fr_e > 0 and not self.training:
-                self._try_expand(st, fr_e, 0)
-        if ran_s:
-            fr_s = int(f[1] == 0 and f[2] > 0)
-            if st.metrics is not None:
-                st.metrics["summary_frustrated"] += fr_s
-            if fr_s > 0 and not self.training:
-                self._try_expand(st, 0, fr_s)
+        act = self._active_words(st) if expand else None
+        ce, cs = self._log_ceiling(int(st.pos))
+        _hip.check(_hip.lib().coda_bank_expand(_hip.ptr(act), fr.data_ptr(), int(ce), int(cs), int(exact_count_mode),
+                                               int(ran_e), int(ran_s), _hip.ptr(counters), _hip.stream_of(fr)))
+        if expand:
+            st.__dict__["_active_stale"] = True
+            if mt is not None:
+                mt.fill["active_exact"] = act[0]
+                mt.fill["active_summary"] = act[1]
 
     # ------------------------------------------------------------ decode
     def _write_one(self, st: CoDAGQALandmarkStatePerf2, *, k_new: torch.Tensor, v_new: torch.Tensor,
@@ -552,12 +613,61 @@ class MemoryBankMixin:
         return head, keep_len
 
     def _block_workspace(self, st, kmax: int) -> Optional[torch.Tensor]:
+        """Scratch of the chunk updates, kept per device and batch and zeroed
+        once when made: its tail holds the per-sequence generation words and
+        the status word (coda_block_write), which carry over between calls."""
         need = ctypes.c_size_t(0)
         d = self._bank_desc(st, None, None, None)
         _hip.check(_hip.lib().coda_block_workspace_bytes(d, kmax, need))
         if need.value == 0:
             return None
-        return torch.empty(need.value, dtype=torch.uint8, device=st.k_buf.device)
+        self.check_bank_status(wait=False)
+        cache = self.__dict__.setdefault("_block_ws", {})
+        key = (str(st.k_buf.device), st.k_buf.shape[0])
+        buf = cache.get(key)
+        if buf is None or buf.numel() < need.value:
+            # tail words at the end of the buffer: a new size starts them over
+            buf = cache[key] = torch.zeros(need.value, dtype=torch.uint8, device=st.k_buf.device)
+        return buf
+
+    @staticmethod
+    def _status_word(ws: torch.Tensor) -> torch.Tensor:
+        n = (ws.numel() // 8) * 8
+        return ws[n - 8:n].view(torch.int64)
+
+    def _queue_status_check(self, ws: Optional[torch.Tensor]) -> None:
+        """After a prefill call: copy the workspace's status word to pinned
+        host memory behind the call's kernels (no host sync); the next entry
+        into the layer, or check_bank_status(), reads it."""
+        if ws is None:
+            return
+        host = torch.empty(1, dtype=torch.int64, pin_memory=True)
+        host.copy_(self._status_word(ws), non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record(torch.cuda.current_stream(ws.device))
+        self.__dict__.setdefault("_status_pending", []).append((ev, host, ws))
+
+    def check_bank_status(self, wait: bool = True) -> None:
+        """Raise if a chunk update of an earlier prefill call gave up waiting
+        for the other heads of its sequence (its bank state is then
+        incomplete).  wait=False reads only the status copies that have
+        already landed, without a host sync."""
+        pend = self.__dict__.get("_status_pending")
+        while pend:
+            ev, host, ws = pend[0]
+            if not ev.query():
+                if not wait:
+                    return
+                ev.synchronize()
+            pend.pop(0)
+            n = int(host[0])
+            if n:
+                pend.clear()
+                self._status_word(ws).zero_()
+                raise RuntimeError(
+                    f"coda_block_write: {n} workgroup(s) of a prefill chunk's bank update gave up waiting for the "
+                    "other heads of their sequence; that call's bank state is incomplete and must be discarded "
+                    "(re-run the prefill from a saved state)")
 
     def _ring_to_time_order(self, st, head: int, filled: int) -> None:
         """Circular ring -> time order at slots 0..filled-1 (memory_banks.py:152-177)."""

@@ -12,7 +12,7 @@ high-frequency band.
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, fields
 from typing import Any, Dict, Optional
 
 import torch
@@ -39,3 +39,48 @@ class CoDAGQALandmarkStatePerf2:
     _sum_lf_k_norm: Optional[torch.Tensor] = field(default=None, repr=False)   # (B, Hkv, Ms, Dh - lf)
 
     metrics: Optional[Dict[str, Any]] = field(default=None, repr=False)
+
+    def __getstate__(self):
+        # the dataclass fields only, active sizes folded in from the device
+        # (the reference's pickled layout; the device words stay behind)
+        _fold_active(self)
+        d = self.__dict__
+        return {k: d[k] for k in _FIELD_NAMES if k in d}
+
+
+_FIELD_NAMES = tuple(f.name for f in fields(CoDAGQALandmarkStatePerf2))
+
+
+# Dynamic bank expansion runs on the device: after a bank update the layer
+# leaves the grown active sizes in the state's device words
+# (__dict__["_active_dev"], int32 [exact, summary]) and marks the host ints
+# stale.  Reading active_exact / active_summary folds them in (one host
+# sync, the first read after an update only); assigning either one makes the
+# host ints authoritative again (the layer re-makes the device words from
+# them at its next bank update).
+def _fold_active(st) -> None:
+    d = st.__dict__
+    if d.get("_active_stale"):
+        a, b = d["_active_dev"].tolist()
+        d["active_exact"], d["active_summary"] = int(a), int(b)
+        d["_active_stale"] = False
+
+
+def _active_property(name: str) -> property:
+    def get(self):
+        if self.__dict__.get("_active_stale"):
+            _fold_active(self)
+        return self.__dict__[name]
+
+    def set(self, value):
+        d = self.__dict__
+        if d.get("_active_stale"):
+            _fold_active(self)  # the other size stays current
+        d[name] = value
+        d.pop("_active_dev", None)
+
+    return property(get, set, doc=f"{name} (folded in from the device after a dynamic expansion)")
+
+
+CoDAGQALandmarkStatePerf2.active_exact = _active_property("active_exact")
+CoDAGQALandmarkStatePerf2.active_summary = _active_property("active_summary")

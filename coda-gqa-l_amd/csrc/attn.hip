@@ -1725,37 +1725,6 @@ __global__ __launch_bounds__(NW * 64) void attn_tile_bf16(const coda_attn_desc a
   }
 }
 
-// ------------------------------------------------------------ prefill flash tiles
-// attn_fa_bf16: the MFMA path for prefill chunks and unbounded causal
-// attention.  Workgroup = (query block, KV head, sequence); wave w owns head
-// g = w / NQ and 16 queries (both streams), so one K/V tile in LDS serves
-// the G heads that share the KV head.  Per 64-key tile, double-buffered,
-// both operands go straight from global memory to LDS (global_load_lds, 16
-// bytes a lane, no register transit):
-//   K in MFMA fragment order: the 1 KiB chunk (sub-tile st of 16 keys,
-//     channel block c of 32) holds, at lane l = n + 16 g4, K[16 st + n][32 c
-//     + 8 g4 .. + 8), so the A fragment of S^T = K Q^T is one contiguous
-//     16-byte read per lane;
-//   V row-major (one key a row) with the 16-byte chunks of row k permuted
-//     by XOR with vswz(k); the A fragment of the k=32 PV MFMA (V^T, keys
-//     4 g4 .. +3 of each of the pair's two 16-key sub-tiles, matching the
-//     S^T accumulator that becomes the B fragment) is two ds_read_b64_tr_b16
-//     transposed reads, whose 16 rows land on distinct bank pairs.
-// Online softmax per stream with a lazy rescale: the running max moves
-// (and O is rescaled) only when a row's new max exceeds it by more than
-// 2^8, so most tiles skip the rescale; P is rounded to bf16 by the
-// hardware conversion for the PV MFMA.
-template <int DH, int NS = 2>
-struct FaLayout {
-  static constexpr int KT = 64, NST = 4, NC = DH / 32, NM = DH / 16;
-  static constexpr int KBYTES = NST * NC * 1024;  // K tile
-  static constexpr int ROWB = DH * 2;             // V row (one key)
-  static constexpr int VBYTES = KT * ROWB;        // V tile
-  static constexpr int CPR = DH / 8;              // 16-byte chunks per V row
-  static constexpr int RPI = 1024 / ROWB;         // V rows per 1 KiB direct load
-  static constexpr int LDS = NS * (KBYTES + VBYTES);  // NS tiles in flight
-};
-
 // s_waitcnt vmcnt(n) for a run-time n in [0, 15] (the count is an immediate)
 __device__ __forceinline__ void vm_wait(int n) {
   switch (n) {
@@ -1768,471 +1737,10 @@ __device__ __forceinline__ void vm_wait(int n) {
   }
 }
 
-template <int DH, int NW, int NS, int QG>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4))) void attn_fa_bf16(const coda_attn_desc a, int NQ, int nqb, int npairs) {
-  using Lay = FaLayout<DH, NS>;
-  constexpr int KT = Lay::KT, NC = Lay::NC, NM = Lay::NM;
-  constexpr int KCH = Lay::NST * NC;          // 1 KiB K chunks per tile
-  constexpr int KCW = (KCH + NW - 1) / NW;    // per wave
-  constexpr int VCH = Lay::VBYTES / 1024;     // 1 KiB V pieces per tile
-  constexpr int VCW = (VCH + NW - 1) / NW;    // per wave
-  extern __shared__ __attribute__((aligned(16))) char fa_smem[];
-  __shared__ uint8_t al_lds[kMaxRowsPrefix];
-  __shared__ uint8_t al32[kMaxRowsPrefix / 32];
-  __shared__ float w_lds[DH];
-  char* kbuf = fa_smem;
-  char* vbuf = fa_smem + NS * Lay::KBYTES;
-
-  // block -> (query block, KV head, sequence); with a multiple of 8 pairs
-  // the query blocks of one (sequence, KV head) share an XCD (dispatch is
-  // round robin over the 8 XCDs), so its K/V stay in that XCD's L2
-  const int id = blockIdx.x;
-  int qb, pair;
-  if (npairs % 8 == 0) {
-    const int local = id >> 3;
-    pair = (id & 7) + 8 * (local / nqb);
-    qb = local % nqb;
-  } else {
-    pair = id / nqb;
-    qb = id % nqb;
-  }
-  const int hk = pair % a.Hkv, b = pair / a.Hkv;
-  const int G = a.H / a.Hkv;
-  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 15, g4 = lane >> 4;
-  // wave = (stream, head, QG groups of 16 queries): waves 2r and 2r + 1
-  // hold the signal and the noise stream of the same queries; each K / V
-  // fragment read from LDS feeds the QG groups' MFMAs
-  constexpr int QW = 16 * QG;  // queries per wave
-  const int strm = wv & 1, r = wv >> 1;
-  const int g = r / NQ, qsub = r % NQ, h = hk * G + g;
-  const int q0 = qb * QW * NQ + QW * qsub;
-  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
-  const int Lk = a.Lp + a.Lb;
-  const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
-  const int q_hi = min(a.Lq - 1, qb * QW * NQ + QW * NQ - 1);
-  const int klim = a.causal ? min(Lk, a.Lp + q_hi + coff + 1) : Lk;
-  const int ntile = (klim + KT - 1) / KT;
-
-  const bf16_t* kpb = a.Lp > 0 ? (const bf16_t*)a.kp + b * a.p_sb + hk * a.p_sh : nullptr;
-  const bf16_t* vpb = a.Lp > 0 ? (const bf16_t*)a.vp + b * a.p_sb + hk * a.p_sh : nullptr;
-  const bf16_t* kbb = a.Lb > 0 ? (const bf16_t*)a.kb + b * a.b_sb + hk * a.b_sh : nullptr;
-  const bf16_t* vbb = a.Lb > 0 ? (const bf16_t*)a.vb + b * a.b_sb + hk * a.b_sh : nullptr;
-
-  // this lane's byte offsets in the direct loads of a tile, relative to
-  // the tile's first row in the prefix (P) or in the block (B): K chunk
-  // ci = wv + NW j is sub-tile ci / NC, channel block ci % NC; V piece
-  // vi = wv + NW j is rows RPI vi ..; piece j adds a wave-uniform step
-  // (the launcher checks the offsets fit 31 bits)
-  static_assert(KCH % NW == 0 || NW % KCH == 0, "K chunks split evenly over the waves");
-  static_assert(VCH % NW == 0 || NW % VCH == 0, "V pieces split evenly over the waves");
-  const int psl = (int)a.p_sl, bsl = (int)a.b_sl;
-  const bool kw = KCH >= NW || wv < KCH, vw = VCH >= NW || wv < VCH;  // waves with a K chunk / V piece
-  const int k_key0 = 16 * ((wv % KCH) / NC) + n, k_ch = 32 * (wv % NC) + 8 * g4;
-  const int v_key0 = Lay::RPI * (wv % VCH) + lane / Lay::CPR;
-  const int v_ch = 8 * ((lane % Lay::CPR) ^ fa_vswz<DH>(v_key0));
-  constexpr int KSTEP = 16 * (NW / NC), VSTEP = Lay::RPI * NW;  // rows per piece step
-  const uint32_t kofP = 2u * (uint32_t)(k_key0 * psl + k_ch), kofB = 2u * (uint32_t)(k_key0 * bsl + k_ch);
-  const uint32_t vofP = 2u * (uint32_t)(v_key0 * psl + v_ch), vofB = 2u * (uint32_t)(v_key0 * bsl + v_ch);
-  // rows wholly in the prefix or wholly in the block take a wave-uniform
-  // base; a tile across the boundary or the end picks per row (rows past
-  // Lk read row 0, a valid row, and are masked)
-  auto tile_load = [&](int kt0, int bi) {
-    char* kd = kbuf + bi * Lay::KBYTES + wv * 1024;
-    char* vd = vbuf + bi * Lay::VBYTES + wv * 1024;
-    if (kt0 + KT <= a.Lp) {
-      const char* kb0 = (const char*)(kpb + (int64_t)kt0 * a.p_sl) + kofP;
-      const char* vb0 = (const char*)(vpb + (int64_t)kt0 * a.p_sl) + vofP;
-      if (kw) {
-#pragma unroll
-        for (int j = 0; j < KCW; ++j) lds_load16(kb0 + (int64_t)j * KSTEP * 2 * psl, kd + NW * j * 1024);
-      }
-      if (vw) {
-#pragma unroll
-        for (int j = 0; j < VCW; ++j) lds_load16(vb0 + (int64_t)j * VSTEP * 2 * psl, vd + NW * j * 1024);
-      }
-    } else if (kt0 >= a.Lp && kt0 + KT <= Lk) {
-      const char* kb0 = (const char*)(kbb + (int64_t)(kt0 - a.Lp) * a.b_sl) + kofB;
-      const char* vb0 = (const char*)(vbb + (int64_t)(kt0 - a.Lp) * a.b_sl) + vofB;
-      if (kw) {
-#pragma unroll
-        for (int j = 0; j < KCW; ++j) lds_load16(kb0 + (int64_t)j * KSTEP * 2 * bsl, kd + NW * j * 1024);
-      }
-      if (vw) {
-#pragma unroll
-        for (int j = 0; j < VCW; ++j) lds_load16(vb0 + (int64_t)j * VSTEP * 2 * bsl, vd + NW * j * 1024);
-      }
-    } else {
-      if (kw) {
-#pragma unroll
-        for (int j = 0; j < KCW; ++j) {
-          int kidx = kt0 + k_key0 + KSTEP * j;
-          kidx = kidx < Lk ? kidx : 0;
-          const bool pre = kidx < a.Lp;
-          const bf16_t* base = pre ? kpb : kbb;
-          const int off = pre ? kidx * psl : (kidx - a.Lp) * bsl;
-          lds_load16(base + off + k_ch, kd + NW * j * 1024);
-        }
-      }
-      if (vw) {
-#pragma unroll
-        for (int j = 0; j < VCW; ++j) {
-          int kidx = kt0 + v_key0 + VSTEP * j;
-          kidx = kidx < Lk ? kidx : 0;
-          const bool pre = kidx < a.Lp;
-          const bf16_t* base = pre ? vpb : vbb;
-          const int off = pre ? kidx * psl : (kidx - a.Lp) * bsl;
-          lds_load16(base + off + v_ch, vd + NW * j * 1024);
-        }
-      }
-    }
-  };
-
-  // every global load of the prologue is issued before the first use of
-  // any (the compiler waits for all outstanding loads once direct LDS
-  // loads are in flight): tile 0's K/V, the visibility bytes of the prefix
-  // and the norm weight (into registers, stored to LDS after the query
-  // math), the queries and their tables
-  if (ntile > 0) tile_load(0, 0);
-  constexpr int ALR = kMaxRowsPrefix / (NW * 64);
-  uint8_t al_r[ALR];
-#pragma unroll
-  for (int k = 0; k < ALR; ++k) {
-    const int i = tid + NW * 64 * k;
-    al_r[k] = i < a.Lp ? (a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1) : (uint8_t)0;
-  }
-  const bf16_t w_raw = tid < DH && a.rms_w ? ((const bf16_t*)a.rms_w)[tid] : (bf16_t)0x3f80;
-
-  // ---- queries of this lane (row q0 + 16 qg + n, channels 32 c + 8 g4 ..
-  // + 8) for this wave's stream: RoPE with the eager-op rounding, then for
-  // the noise stream the per-head rotation (primitives.py:58-113), unless
-  // the noise queries are given.  All loads go out before any math.
-  bf16x8_t qf[QG][NC];
-  bf16_t lam_raw[QG];
-  {
-    using E = Elt<bf16_t>;
-    constexpr int half = DH / 2;
-    const bool given = strm == 1 && a.q_noise != nullptr;
-    const bool rot = strm == 1 && a.q_noise == nullptr;
-    const bool rope = a.rope_cos != nullptr && !given, inter = a.rope_interleaved != 0;
-    uint4 uq[QG][NC], up[QG][NC], rc[QG][NC], rs[QG][NC];
-    uint2 rc2[QG][NC], rs2[QG][NC], tcs[NC], tsn[NC];
-#pragma unroll
-    for (int qg = 0; qg < QG; ++qg) {
-      const int qrow = q0 + 16 * qg + n;
-      const int qi = qrow < a.Lq ? qrow : 0;
-      const bf16_t* qr = given ? (const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh + (int64_t)qi * a.qn_sl
-                               : (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
-      const bf16_t* csr = rope ? (const bf16_t*)a.rope_cos + (int64_t)qi * half : nullptr;
-      const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int d0 = 32 * c + 8 * g4;
-        uq[qg][c] = *reinterpret_cast<const uint4*>(qr + d0);
-        if (rope && inter) {
-          rc2[qg][c] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
-          rs2[qg][c] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
-        }
-        if (rope && !inter) {
-          const int f0 = d0 < half ? d0 : d0 - half;
-          up[qg][c] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
-          rc[qg][c] = *reinterpret_cast<const uint4*>(csr + f0);
-          rs[qg][c] = *reinterpret_cast<const uint4*>(snr + f0);
-        }
-        if (rot && qg == 0) {
-          tcs[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_cos + (int64_t)h * half + d0 / 2);
-          tsn[c] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_sin + (int64_t)h * half + d0 / 2);
-        }
-      }
-      lam_raw[qg] = ((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl];
-    }
-#pragma unroll
-    for (int qg = 0; qg < QG; ++qg) {
-      const bool qlive = q0 + 16 * qg + n < a.Lq;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int d0 = 32 * c + 8 * g4;
-        if (given) {
-          qf[qg][c] = __builtin_bit_cast(bf16x8_t, qlive ? uq[qg][c] : uint4{0, 0, 0, 0});
-          continue;
-        }
-        uint32_t w[4] = {uq[qg][c].x, uq[qg][c].y, uq[qg][c].z, uq[qg][c].w};
-        if (rope && inter) {
-          // pairs (2p, 2p+1) rotated by angle d0/2 + p: one bf16 dot2 per
-          // output (fp32 products and sum, one rounding)
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) w[pp] = rot_pair(w[pp], pp >> 1 ? rc2[qg][c].y : rc2[qg][c].x,
-                                                          pp >> 1 ? rs2[qg][c].y : rs2[qg][c].x, pp & 1);
-        }
-        if (rope && !inter) {
-          // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin, with
-          // the eager-op rounding of each product and sum
-          float x[8], cc[8], ss[8], y[8];
-          unpack8(uq[qg][c], x);
-          unpack8(rc[qg][c], cc);
-          unpack8(rs[qg][c], ss);
-          unpack8(up[qg][c], y);
-          const bool lo = d0 < half;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float rt = lo ? -y[j] : y[j];
-            x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rt * ss[j]));
-          }
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) w[pp] = pk_bf16(x[2 * pp], x[2 * pp + 1]);
-        }
-        if (rot) {
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) w[pp] = rot_pair(w[pp], pp >> 1 ? tcs[c].y : tcs[c].x,
-                                                          pp >> 1 ? tsn[c].y : tsn[c].x, pp & 1);
-        }
-        qf[qg][c] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
-      }
-    }
-  }
-  // visibility bytes of the prefix, per-32-key "all visible" flags (one
-  // ballot per 64 keys), norm weight
-#pragma unroll
-  for (int k = 0; k < ALR; ++k) {
-    const int i = tid + NW * 64 * k;
-    if (i < a.Lp) al_lds[i] = al_r[k];
-  }
-  if (tid < DH) w_lds[tid] = bf2f(w_raw);
-  // tiles 1 .. NS-2 go out now, behind tile 0 (the query math above waited
-  // for every load in flight)
-#pragma unroll
-  for (int t = 1; t < NS - 1; ++t)
-    if (t < ntile) tile_load(t * KT, t);
-  // a bare barrier: the LDS stores above are done (lgkmcnt), the tile loads
-  // stay in flight
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_s_barrier();
-  for (int base = 64 * wv; base < a.Lp; base += 64 * NW) {
-    const int i = base + lane;
-    const uint64_t m = __ballot(i < a.Lp && al_lds[i] != 0);
-    const int e = (base >> 5) + lane;
-    if (lane < 2 && 32 * e < a.Lp) al32[e] = (uint8_t)(((m >> (32 * lane)) & 0xffffffffull) == 0xffffffffull);
-  }
-  // V transposed-read addresses: rows 4 g4 + (n >> 2) (+ 16) of a key
-  // pair, channels 16 mt + 4 (n & 3); the row's chunk permutation folds
-  // into a per-lane offset for each mt
-  const int vrow = 4 * g4 + (n >> 2);
-  int v_off[NM];
-#pragma unroll
-  for (int mt = 0; mt < NM; ++mt)
-    v_off[mt] = vrow * Lay::ROWB + 16 * ((2 * mt + ((n & 3) >> 1)) ^ fa_vswz<DH>(vrow)) + 8 * (n & 1);
-
-  float m_s[QG], l_s[QG];
-  f32x4 o[QG][NM];
-#pragma unroll
-  for (int qg = 0; qg < QG; ++qg) {
-    m_s[qg] = -INFINITY;
-    l_s[qg] = 0.f;
-#pragma unroll
-    for (int i = 0; i < NM; ++i) o[qg][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
-  // direct loads this wave issues per tile
-  const int lpt = (kw ? KCW : 0) + (vw ? VCW : 0);
-  for (int it = 0; it < ntile; ++it) {
-    const int bi = it % NS, kt0 = it * KT;
-    // tile it's direct loads have landed (the tiles after it may stay in
-    // flight), this wave's reads of tile it - 1 are done; after the bare
-    // barrier the same holds for every wave, so tile it + NS - 1 can go into
-    // the buffer of tile it - 1
-    vm_wait(lpt * (min(ntile - 1, it + NS - 2) - it));
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_s_barrier();
-    if (it + NS - 1 < ntile) tile_load(kt0 + (NS - 1) * KT, (it + NS - 1) % NS);
-    const char* kb_t = kbuf + bi * Lay::KBYTES;
-    // S^T: st[qg][sub][j] = score of key kt0 + 16 sub + 4 g4 + j against
-    // query q0 + 16 qg + n.  Channel block c at a time over the 4 sub-tiles
-    // (4 independent accumulation chains), block c + 1's fragments read
-    // before block c's products
-    f32x4 st[QG][4];
-#pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const bf16x8_t kf =
-            __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(kb_t + (sub * NC + c) * 1024 + 16 * lane));
-#pragma unroll
-        for (int qg = 0; qg < QG; ++qg)
-          st[qg][sub] = mfma_k32(kf, qf[qg][c], c == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[qg][sub]);
-      }
-    }
-    uint4 pb[QG][2];
-#pragma unroll
-    for (int qg = 0; qg < QG; ++qg) {
-      const int qg0 = q0 + 16 * qg, qrow = qg0 + n;
-      // hide the keys these queries may not see (only where some may be)
-      bool need = false;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int pk0 = kt0 + 32 * hh;
-        need |= (pk0 + 32 > Lk) || (pk0 < a.Lp && !al32[pk0 >> 5]) ||
-                (pk0 + 32 > a.Lp && a.causal && (pk0 + 31 - a.Lp) > qg0 + coff);
-      }
-      if (need) {
-#pragma unroll
-        for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            // branch-free: the visibility byte is read at a clamped index
-            const int kidx = kt0 + 16 * sub + 4 * g4 + j;
-            const int jb = kidx - a.Lp;
-            const bool pre = kidx < a.Lp;
-            const bool al_ok = al_lds[pre ? kidx : 0] != 0;
-            const bool blk_ok = (jb < a.Lb) & ((a.causal == 0) | (jb <= qrow + coff));
-            const bool vis = pre ? al_ok : blk_ok;
-            st[qg][sub][j] = vis ? st[qg][sub][j] : -INFINITY;
-          }
-      }
-      float t0 = fmaxf(fmaxf(st[qg][0][0], st[qg][0][1]), fmaxf(st[qg][0][2], st[qg][0][3]));
-      float t1 = fmaxf(fmaxf(st[qg][1][0], st[qg][1][1]), fmaxf(st[qg][1][2], st[qg][1][3]));
-      float t2 = fmaxf(fmaxf(st[qg][2][0], st[qg][2][1]), fmaxf(st[qg][2][2], st[qg][2][3]));
-      float t3 = fmaxf(fmaxf(st[qg][3][0], st[qg][3][1]), fmaxf(st[qg][3][2], st[qg][3][3]));
-      const float tsc = xmax32(xmax16(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)))) * scale;
-      if (__ballot(tsc > m_s[qg] + 8.f)) {
-        const float mnew = fmaxf(m_s[qg], tsc);
-        const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s[qg] - mnew);
-#pragma unroll
-        for (int i = 0; i < NM; ++i) o[qg][i] *= alpha;
-        l_s[qg] *= alpha;
-        m_s[qg] = mnew;
-      }
-      const float mu = m_s[qg] == -INFINITY ? 0.f : m_s[qg];
-      float pr[4][4];
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pr[sub][j] = fast_exp2(fmaf(st[qg][sub][j], scale, -mu));
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        pb[qg][hh].x = pk_bf16(pr[2 * hh][0], pr[2 * hh][1]);
-        pb[qg][hh].y = pk_bf16(pr[2 * hh][2], pr[2 * hh][3]);
-        pb[qg][hh].z = pk_bf16(pr[2 * hh + 1][0], pr[2 * hh + 1][1]);
-        pb[qg][hh].w = pk_bf16(pr[2 * hh + 1][2], pr[2 * hh + 1][3]);
-      }
-      float q4[4];
-#pragma unroll
-      for (int sub = 0; sub < 4; ++sub) q4[sub] = (pr[sub][0] + pr[sub][1]) + (pr[sub][2] + pr[sub][3]);
-      l_s[qg] += (q4[0] + q4[1]) + (q4[2] + q4[3]);
-    }
-    // PV: the tile's NM pairs of (hh, mt, mt + 1) products, each fed by
-    // four transposed reads; two pairs' reads in flight (three rotating
-    // register sets), each pair waits only for its own reads
-    const uint32_t vt_a = lds_addr(vbuf + bi * Lay::VBYTES);
-    constexpr int NP = NM;  // 2 halves x NM / 2 pairs
-    uint2 rd[3][4];
-    auto pv_issue = [&](auto p_c) {
-      constexpr int p = decltype(p_c)::value;
-      if constexpr (p < NP) {
-        constexpr int hh = p / (NM / 2), mt = 2 * (p % (NM / 2));
-        constexpr int HOFF = 32 * hh * Lay::ROWB, ROW16 = 16 * Lay::ROWB;
-        const uint32_t a0 = vt_a + v_off[mt], a1 = vt_a + v_off[mt + 1];
-        rd[p % 3][0] = lds_read_tr16_at<HOFF>(a0);
-        rd[p % 3][1] = lds_read_tr16_at<HOFF + ROW16>(a0);
-        rd[p % 3][2] = lds_read_tr16_at<HOFF>(a1);
-        rd[p % 3][3] = lds_read_tr16_at<HOFF + ROW16>(a1);
-      }
-    };
-    pv_issue(std::integral_constant<int, 0>{});
-    pv_issue(std::integral_constant<int, 1>{});
-    static_for<NP>([&](auto p_c) {
-      constexpr int p = decltype(p_c)::value;
-      constexpr int hh = p / (NM / 2), mt = 2 * (p % (NM / 2)), b3 = p % 3;
-      lds_wait4_n<(p + 1 < NP) ? 4 : 0>(rd[b3][0], rd[b3][1], rd[b3][2], rd[b3][3]);
-      const bf16x8_t va0 = __builtin_bit_cast(bf16x8_t, uint4{rd[b3][0].x, rd[b3][0].y, rd[b3][1].x, rd[b3][1].y});
-      const bf16x8_t va1 = __builtin_bit_cast(bf16x8_t, uint4{rd[b3][2].x, rd[b3][2].y, rd[b3][3].x, rd[b3][3].y});
-#pragma unroll
-      for (int qg = 0; qg < QG; ++qg) {
-        const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, pb[qg][hh]);
-        o[qg][mt] = mfma_k32(va0, pf, o[qg][mt]);
-        o[qg][mt + 1] = mfma_k32(va1, pf, o[qg][mt + 1]);
-      }
-      // pair p + 2's reads go out after pair p's products (into the set
-      // pair p - 1 used), then nothing crosses into the next pair
-      __builtin_amdgcn_sched_barrier(0);
-      pv_issue(std::integral_constant<int, p + 2>{});
-      __builtin_amdgcn_sched_barrier(0);
-    });
-  }
-  // ---- epilogue: lane holds channels 16 mt + 4 g4 + j of row q0 + 16 qg
-  // + n.  The noise wave hands rnd(O_noise) (bf16) to its signal wave
-  // through LDS (the K/V buffers, free once every wave has left the loop)
-  constexpr int NV = NM * 4;
-  float inv[QG];
-#pragma unroll
-  for (int qg = 0; qg < QG; ++qg) {
-    const float l = xsum32(xsum16(l_s[qg]));
-    inv[qg] = l > 0.f ? 1.f / l : 0.f;
-  }
-  uint4* xch = reinterpret_cast<uint4*>(fa_smem) + r * QG * (NV / 8) * 64;
-  __syncthreads();
-  if (strm == 1) {
-#pragma unroll
-    for (int qg = 0; qg < QG; ++qg)
-#pragma unroll
-      for (int i = 0; i < NV / 8; ++i) {
-        uint4 u;
-        u.x = pk_bf16(o[qg][2 * i][0] * inv[qg], o[qg][2 * i][1] * inv[qg]);
-        u.y = pk_bf16(o[qg][2 * i][2] * inv[qg], o[qg][2 * i][3] * inv[qg]);
-        u.z = pk_bf16(o[qg][2 * i + 1][0] * inv[qg], o[qg][2 * i + 1][1] * inv[qg]);
-        u.w = pk_bf16(o[qg][2 * i + 1][2] * inv[qg], o[qg][2 * i + 1][3] * inv[qg]);
-        xch[(qg * (NV / 8) + i) * 64 + lane] = u;
-      }
-  }
-  __syncthreads();
-  if (strm == 1) return;
-#pragma unroll
-  for (int qg = 0; qg < QG; ++qg) {
-    const int qrow = q0 + 16 * qg + n;
-    const float lam = bf2f(lam_raw[qg]);
-    // y = O_signal - lam rnd(O_noise), then the HeadwiseRMSNorm and weight,
-    // in fp32 with one rounding at the store
-    float y[NV];
-    {
-      float on[NV];
-#pragma unroll
-      for (int i = 0; i < NV / 8; ++i) unpack8(xch[(qg * (NV / 8) + i) * 64 + lane], on + 8 * i);
-      float sq = 0.f;
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = mt * 4 + j;
-          y[i] = fmaf(-lam, on[i], o[qg][mt][j] * inv[qg]);
-          sq = fmaf(y[i], y[i], sq);
-        }
-      if (a.rms_w) {
-        sq = xsum32(xsum16(sq));
-        const float rr = 1.0f / sqrtf(sq / (float)DH + a.eps);
-#pragma unroll
-        for (int mt = 0; mt < NM; ++mt)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int i = mt * 4 + j;
-            y[i] = y[i] * (rr * w_lds[16 * mt + 4 * g4 + j]);
-          }
-      }
-    }
-    if (qrow < a.Lq) {
-      bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
-#pragma unroll
-      for (int mt = 0; mt < NM; ++mt) {
-        uint2 u;
-        u.x = pk_bf16(y[mt * 4 + 0], y[mt * 4 + 1]);
-        u.y = pk_bf16(y[mt * 4 + 2], y[mt * 4 + 3]);
-        *reinterpret_cast<uint2*>(orow_p + 16 * mt + 4 * g4) = u;
-      }
-    }
-  }
-}
-
 // ------------------------------------------------------------ prefill flash tiles, 32-row MFMA
-// attn_f2_bf16: the MFMA path for prefill chunks and unbounded attention
-// (head_dim 64 / 128).  Workgroup = (query block, KV head, sequence); wave
+// The tiles of the MFMA path for prefill chunks and unbounded attention
+// (head_dim 64 / 128, attn_f3_bf16).  Workgroup = (query block, KV head,
+// sequence); wave
 // w owns head g = w / NQ and 16 queries, BOTH streams: the wave's 32 MFMA
 // rows are the 16 signal queries (rows 0-15) and the same 16 queries
 // rotated into the noise stream (rows 16-31).  Every K / V fragment a wave
@@ -2300,368 +1808,8 @@ struct F2Layout {
   }
 };
 
-template <int DH, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_f2_bf16(
-    const coda_attn_desc a, int NQ, int nqb, int npairs) {
-  using Lay = F2Layout<DH>;
-  constexpr int KT = Lay::KT, NKS = Lay::NKS, NDB = Lay::NDB, KCH = Lay::KCH, VCH = Lay::VCH;
-  constexpr int KCW = (KCH + NW - 1) / NW, VCW = (VCH + NW - 1) / NW;
-  extern __shared__ __attribute__((aligned(16))) char f2_smem[];
-  __shared__ uint8_t al_lds[kMaxRowsPrefix];
-  __shared__ uint8_t al32[kMaxRowsPrefix / 32];
-  __shared__ float w_lds[DH];
-  char* kbuf = f2_smem;
-  char* vbuf = f2_smem + 2 * Lay::KBYTES;
-
-  // block -> (query block, KV head, sequence); with a multiple of 8 pairs
-  // the query blocks of one (sequence, KV head) share an XCD (dispatch is
-  // round robin over the 8 XCDs), so its K / V stay in that XCD's L2
-  const int id = blockIdx.x;
-  int qb, pair;
-  if (npairs % 8 == 0) {
-    const int local = id >> 3;
-    pair = (id & 7) + 8 * (local / nqb);
-    qb = local % nqb;
-  } else {
-    pair = id / nqb;
-    qb = id % nqb;
-  }
-  const int hk = pair % a.Hkv, b = pair / a.Hkv;
-  const int G = a.H / a.Hkv;
-  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 31, hl = lane >> 5;  // MFMA row, channel half of a 16-channel step
-  const int strm = n >> 4, qn = n & 15;     // 0 signal / 1 noise, query of the wave
-  const int g = wv / NQ, qsub = wv % NQ, h = hk * G + g;
-  const int q0 = qb * 16 * NQ + 16 * qsub;
-  const int qrow = q0 + qn;
-  const float scale = (a.sm_scale > 0.f ? a.sm_scale : rsqrtf((float)DH)) * kLog2e;
-  const int Lk = a.Lp + a.Lb;
-  const int coff = a.causal == 2 ? 0 : a.Lb - a.Lq;
-  const int q_hi = min(a.Lq - 1, qb * 16 * NQ + 16 * NQ - 1);
-  const int klim = a.causal ? min(Lk, a.Lp + q_hi + coff + 1) : Lk;
-  const int ntile = (klim + KT - 1) / KT;
-
-  const bf16_t* kpb = a.Lp > 0 ? (const bf16_t*)a.kp + b * a.p_sb + hk * a.p_sh : nullptr;
-  const bf16_t* vpb = a.Lp > 0 ? (const bf16_t*)a.vp + b * a.p_sb + hk * a.p_sh : nullptr;
-  const bf16_t* kbb = a.Lb > 0 ? (const bf16_t*)a.kb + b * a.b_sb + hk * a.b_sh : nullptr;
-  const bf16_t* vbb = a.Lb > 0 ? (const bf16_t*)a.vb + b * a.b_sb + hk * a.b_sh : nullptr;
-  const int psl = (int)a.p_sl, bsl = (int)a.b_sl;
-
-  // this lane's piece of the direct loads: K fragment ci = (kb, ks) takes
-  // key 32 kb + k_r at channels 16 ks + k_c; V piece vi takes row
-  // RPI vi + v_r at the channels of its stored chunk
-  const int k_r = lane & 31, k_c = 8 * (lane >> 5);
-  const int v_r = lane / Lay::CPR, v_c = 8 * Lay::vchunk(v_r, lane % Lay::CPR);
-  auto row_of = [&](const bf16_t* pb, const bf16_t* bb, int kidx) {
-    kidx = kidx < Lk ? kidx : 0;  // past the end: a valid row, masked later
-    return kidx < a.Lp ? pb + (int64_t)kidx * psl : bb + (int64_t)(kidx - a.Lp) * bsl;
-  };
-  auto tile_load = [&](int kt0, int bi) {
-    char* kd = kbuf + bi * Lay::KBYTES;
-    char* vd = vbuf + bi * Lay::VBYTES;
-#pragma unroll
-    for (int j = 0; j < KCW; ++j) {
-      const int ci = wv + NW * j;
-      if (KCH % NW == 0 || ci < KCH) {
-        const int kb = ci / NKS, ks = ci % NKS;
-        lds_load16(row_of(kpb, kbb, kt0 + 32 * kb + k_r) + 16 * ks + k_c, kd + ci * 1024);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < VCW; ++j) {
-      const int vi = wv + NW * j;
-      if (VCH % NW == 0 || vi < VCH) lds_load16(row_of(vpb, vbb, kt0 + Lay::RPI * vi + v_r) + v_c, vd + vi * 1024);
-    }
-  };
-
-  // ---- prologue: every global load before the first use of any (tile 0,
-  // visibility bytes, norm weight, queries, tables, lambda)
-  if (ntile > 0) tile_load(0, 0);
-  constexpr int ALR = kMaxRowsPrefix / (NW * 64);
-  uint8_t al_r[ALR];
-#pragma unroll
-  for (int k = 0; k < ALR; ++k) {
-    const int i = tid + NW * 64 * k;
-    al_r[k] = i < a.Lp ? (a.allowed ? a.allowed[(int64_t)b * a.al_sb + i] : (uint8_t)1) : (uint8_t)0;
-  }
-  const bf16_t w_raw = tid < DH && a.rms_w ? ((const bf16_t*)a.rms_w)[tid] : (bf16_t)0x3f80;
-
-  // queries of this lane: row n (stream strm of query qrow), channels
-  // 16 ks + 8 hl .. + 8.  RoPE with the eager-op rounding, then for the
-  // noise stream the per-head rotation (primitives.py:58-113), unless the
-  // noise queries are given.
-  bf16x8_t qf[NKS];
-  bf16_t lam_raw;
-  {
-    using E = Elt<bf16_t>;
-    constexpr int half = DH / 2;
-    const bool given = strm == 1 && a.q_noise != nullptr;
-    const bool rot = strm == 1 && a.q_noise == nullptr;
-    const bool rope = a.rope_cos != nullptr && !given, inter = a.rope_interleaved != 0;
-    const bool qlive = qrow < a.Lq;
-    const int qi = qlive ? qrow : 0;
-    const bf16_t* qr = given ? (const bf16_t*)a.q_noise + b * a.qn_sb + h * a.qn_sh + (int64_t)qi * a.qn_sl
-                             : (const bf16_t*)a.q + b * a.q_sb + h * a.q_sh + (int64_t)qi * a.q_sl;
-    const bf16_t* csr = rope ? (const bf16_t*)a.rope_cos + (int64_t)qi * half : nullptr;
-    const bf16_t* snr = rope ? (const bf16_t*)a.rope_sin + (int64_t)qi * half : nullptr;
-    uint4 uq[NKS], up[NKS], rc[NKS], rs[NKS];
-    uint2 rc2[NKS], rs2[NKS], tcs[NKS], tsn[NKS];
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      const int d0 = 16 * ks + 8 * hl;
-      uq[ks] = *reinterpret_cast<const uint4*>(qr + d0);
-      if (rope && inter) {
-        rc2[ks] = *reinterpret_cast<const uint2*>(csr + d0 / 2);
-        rs2[ks] = *reinterpret_cast<const uint2*>(snr + d0 / 2);
-      }
-      if (rope && !inter) {
-        const int f0 = d0 < half ? d0 : d0 - half;
-        up[ks] = *reinterpret_cast<const uint4*>(qr + (d0 < half ? d0 + half : d0 - half));
-        rc[ks] = *reinterpret_cast<const uint4*>(csr + f0);
-        rs[ks] = *reinterpret_cast<const uint4*>(snr + f0);
-      }
-      if (rot) {
-        tcs[ks] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_cos + (int64_t)h * half + d0 / 2);
-        tsn[ks] = *reinterpret_cast<const uint2*>((const bf16_t*)a.theta_sin + (int64_t)h * half + d0 / 2);
-      }
-    }
-    lam_raw = ((const bf16_t*)a.lam)[b * a.lam_sb + h * a.lam_sh + (int64_t)qi * a.lam_sl];
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) {
-      const int d0 = 16 * ks + 8 * hl;
-      if (given) {
-        qf[ks] = __builtin_bit_cast(bf16x8_t, qlive ? uq[ks] : uint4{0, 0, 0, 0});
-        continue;
-      }
-      uint32_t w[4] = {uq[ks].x, uq[ks].y, uq[ks].z, uq[ks].w};
-      if (rope && inter) {
-        // pairs (2p, 2p+1) rotated by angle d0/2 + p: one bf16 dot2 per
-        // output (fp32 products and sum, one rounding)
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp)
-          w[pp] = rot_pair(w[pp], pp >> 1 ? rc2[ks].y : rc2[ks].x, pp >> 1 ? rs2[ks].y : rs2[ks].x, pp & 1);
-      }
-      if (rope && !inter) {
-        // half-split pairs (d, d +- Dh/2): x cos + rotate_half(x) sin, with
-        // the eager-op rounding of each product and sum
-        float x[8], cc[8], ss[8], y[8];
-        unpack8(uq[ks], x);
-        unpack8(rc[ks], cc);
-        unpack8(rs[ks], ss);
-        unpack8(up[ks], y);
-        const bool lo = d0 < half;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float rt = lo ? -y[j] : y[j];
-          x[j] = E::rnd(E::rnd(x[j] * cc[j]) + E::rnd(rt * ss[j]));
-        }
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp) w[pp] = pk_bf16(x[2 * pp], x[2 * pp + 1]);
-      }
-      if (rot) {
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp)
-          w[pp] = rot_pair(w[pp], pp >> 1 ? tcs[ks].y : tcs[ks].x, pp >> 1 ? tsn[ks].y : tsn[ks].x, pp & 1);
-      }
-      qf[ks] = __builtin_bit_cast(bf16x8_t, qlive ? uint4{w[0], w[1], w[2], w[3]} : uint4{0, 0, 0, 0});
-    }
-  }
-  // visibility bytes of the prefix, per-32-key "all visible" flags, norm weight
-#pragma unroll
-  for (int k = 0; k < ALR; ++k) {
-    const int i = tid + NW * 64 * k;
-    if (i < a.Lp) al_lds[i] = al_r[k];
-  }
-  if (tid < DH) w_lds[tid] = bf2f(w_raw);
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_s_barrier();
-  for (int base = 64 * wv; base < a.Lp; base += 64 * NW) {
-    const int i = base + lane;
-    const uint64_t m = __ballot(i < a.Lp && al_lds[i] != 0);
-    const int e = (base >> 5) + lane;
-    if (lane < 2 && 32 * e < a.Lp) al32[e] = (uint8_t)(((m >> (32 * lane)) & 0xffffffffull) == 0xffffffffull);
-  }
-
-  // LDS byte addresses: this lane's K fragment word, its V transposed-read
-  // cell for each channel block db (rows 4 hl + (p16 >> 2) of a 16-key step,
-  // channels 32 db + 16 (grp & 1) + 4 (p16 & 3), stored chunk swizzled)
-  const int grp = lane >> 4, p16 = lane & 15;
-  const int vrow = 4 * (grp >> 1) + (p16 >> 2);
-  int v_off[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-    v_off[db] = vrow * Lay::ROWB + 16 * Lay::vchunk(vrow, 4 * db + 2 * (grp & 1) + ((p16 & 3) >> 1)) + 8 * (p16 & 1);
-
-  float m_s = -INFINITY, l_s = 0.f;
-  f32x16 o[NDB];
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) o[db] = f32x16{};
-
-  for (int it = 0; it < ntile; ++it) {
-    const int bi = it & 1, kt0 = it * KT;
-    // tile it has landed and every wave is done with tile it - 1, whose
-    // buffer now takes tile it + 1
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    if (it + 1 < ntile) tile_load(kt0 + KT, bi ^ 1);
-    // ---- S^T: NKS steps x 2 key blocks, fragment reads four ahead
-    const uint32_t ka = lds_addr(kbuf + bi * Lay::KBYTES) + 16 * lane;
-    f32x16 st[2];
-    {
-      constexpr int NF = 2 * NKS;
-      u32x4v_t kr[4];
-      auto k_issue = [&](auto f_c) {
-        constexpr int f = decltype(f_c)::value;
-        if constexpr (f < NF) {
-          constexpr int ks = f / 2, kb = f % 2;
-          kr[f % 4] = lds_read_b128_at<(kb * NKS + ks) * 1024>(ka);
-        }
-      };
-      k_issue(std::integral_constant<int, 0>{});
-      k_issue(std::integral_constant<int, 1>{});
-      k_issue(std::integral_constant<int, 2>{});
-      static_for<NF>([&](auto f_c) {
-        constexpr int f = decltype(f_c)::value;
-        constexpr int ks = f / 2, kb = f % 2;
-        k_issue(std::integral_constant<int, f + 3>{});
-        lds_wait_b128<(f + 3 < NF) ? 3 : (NF - 1 - f)>(kr[f % 4]);
-        st[kb] = mfma_32x32x16(__builtin_bit_cast(bf16x8_t, kr[f % 4]), qf[ks], ks == 0 ? f32x16{} : st[kb]);
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    }
-    // ---- mask, online softmax, P
-    {
-      bool need = false;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int pk0 = kt0 + 32 * kb;
-        need |= (pk0 + 32 > Lk) || (pk0 < a.Lp && !al32[pk0 >> 5]) ||
-                (pk0 + 32 > a.Lp && a.causal && (pk0 + 31 - a.Lp) > q0 + coff);
-      }
-      if (need) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int kidx = kt0 + 32 * kb + 8 * (j >> 2) + 4 * hl + (j & 3);
-            const int jb = kidx - a.Lp;
-            const bool pre = kidx < a.Lp;
-            const bool al_ok = al_lds[pre ? kidx : 0] != 0;
-            const bool blk_ok = (jb < a.Lb) & ((a.causal == 0) | (jb <= qrow + coff));
-            st[kb][j] = (pre ? al_ok : blk_ok) ? st[kb][j] : -INFINITY;
-          }
-      }
-      float mx = st[0][0];
-#pragma unroll
-      for (int j = 1; j < 16; ++j) mx = fmaxf(mx, st[0][j]);
-#pragma unroll
-      for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[1][j]);
-      const float tsc = xmax32(mx) * scale;
-      if (__ballot(tsc > m_s + 8.f)) {
-        const float mnew = fmaxf(m_s, tsc);
-        const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(m_s - mnew);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-        l_s *= alpha;
-        m_s = mnew;
-      }
-      const float mu = m_s == -INFINITY ? 0.f : m_s;
-      float ls = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          st[kb][j] = fast_exp2(fmaf(st[kb][j], scale, -mu));
-          ls += st[kb][j];
-        }
-      l_s += ls;
-    }
-    // ---- O^T += V^T P^T: 4 key steps x NDB channel blocks, each fed by two
-    // transposed reads; two (step, block) read pairs in flight
-    {
-      const uint32_t va = lds_addr(vbuf + bi * Lay::VBYTES);
-      constexpr int NPV = 4 * NDB;
-      uint2 rd[3][2];
-      uint4 pf4[4];
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int kb = p >> 1, ph = p & 1;
-        pf4[p].x = pk_bf16(st[kb][8 * ph + 0], st[kb][8 * ph + 1]);
-        pf4[p].y = pk_bf16(st[kb][8 * ph + 2], st[kb][8 * ph + 3]);
-        pf4[p].z = pk_bf16(st[kb][8 * ph + 4], st[kb][8 * ph + 5]);
-        pf4[p].w = pk_bf16(st[kb][8 * ph + 6], st[kb][8 * ph + 7]);
-      }
-      auto v_issue = [&](auto q_c) {
-        constexpr int q = decltype(q_c)::value;
-        if constexpr (q < NPV) {
-          constexpr int p = q / NDB, db = q % NDB;
-          constexpr int ROW0 = 16 * p * Lay::ROWB, ROW8 = ROW0 + 8 * Lay::ROWB;
-          rd[q % 3][0] = lds_read_tr16_at<ROW0>(va + v_off[db]);
-          rd[q % 3][1] = lds_read_tr16_at<ROW8>(va + v_off[db]);
-        }
-      };
-      v_issue(std::integral_constant<int, 0>{});
-      v_issue(std::integral_constant<int, 1>{});
-      static_for<NPV>([&](auto q_c) {
-        constexpr int q = decltype(q_c)::value;
-        constexpr int p = q / NDB, db = q % NDB, b3 = q % 3;
-        lds_wait2_n<(q + 1 < NPV) ? 2 : 0>(rd[b3][0], rd[b3][1]);
-        const bf16x8_t va8 = __builtin_bit_cast(bf16x8_t, uint4{rd[b3][0].x, rd[b3][0].y, rd[b3][1].x, rd[b3][1].y});
-        o[db] = mfma_32x32x16(va8, __builtin_bit_cast(bf16x8_t, pf4[p]), o[db]);
-        __builtin_amdgcn_sched_barrier(0);
-        v_issue(std::integral_constant<int, q + 2>{});
-        __builtin_amdgcn_sched_barrier(0);
-      });
-    }
-  }
-
-  // ---- epilogue: lane holds row n's channels 32 db + 8 (j / 4) + 4 hl +
-  // j % 4.  Noise lanes (n >= 16) round O_noise to bf16; one permlane swap
-  // hands it to the signal lane l ^ 16; y = O_signal - lam rnd(O_noise),
-  // then the HeadwiseRMSNorm and weight in fp32, one rounding at the store.
-  const float l_tot = xsum32(l_s);
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-  const float lam = bf2f(lam_raw);
-  float y[NDB][16];
-  float sq = 0.f;
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      const uint32_t mine = pk_bf16(o[db][j] * inv, o[db][j + 1] * inv);
-      const auto r = __builtin_amdgcn_permlane16_swap(mine, mine, false, false);
-      const uint32_t nz = (uint32_t)r[1];  // the odd 16-lane row's value: the noise lane's
-      const float on0 = bf2f((bf16_t)(nz & 0xffffu)), on1 = bf2f((bf16_t)(nz >> 16));
-      y[db][j] = fmaf(-lam, on0, o[db][j] * inv);
-      y[db][j + 1] = fmaf(-lam, on1, o[db][j + 1] * inv);
-      sq = fmaf(y[db][j], y[db][j], sq);
-      sq = fmaf(y[db][j + 1], y[db][j + 1], sq);
-    }
-  if (a.rms_w) {
-    sq = xsum32(sq);
-    const float rr = 1.0f / sqrtf(sq / (float)DH + a.eps);
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) y[db][j] *= rr * w_lds[32 * db + 8 * (j >> 2) + 4 * hl + (j & 3)];
-  }
-  if (strm == 0 && qrow < a.Lq) {
-    bf16_t* orow_p = (bf16_t*)a.out + b * a.o_sb + h * a.o_sh + (int64_t)qrow * a.o_sl;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db)
-#pragma unroll
-      for (int jq = 0; jq < 4; ++jq) {
-        uint2 u;
-        u.x = pk_bf16(y[db][4 * jq + 0], y[db][4 * jq + 1]);
-        u.y = pk_bf16(y[db][4 * jq + 2], y[db][4 * jq + 3]);
-        *reinterpret_cast<uint2*>(orow_p + 32 * db + 8 * jq + 4 * hl) = u;
-      }
-  }
-}
-
 // ------------------------------------------------------------ prefill flash tiles, pipelined
-// attn_f3_bf16: attn_f2_bf16's tiles (32 MFMA rows per wave: 16 queries x
+// attn_f3_bf16: the 32-row tiles above (32 MFMA rows per wave: 16 queries x
 // both streams; S^T = K Q^T and O^T += V^T P^T as 32 x 32 x 16 products),
 // software-pipelined so the matrix and vector pipes work at the same time
 // within each wave.  Iteration it, with S(it) already masked and its row
@@ -3045,7 +2193,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
   }
 
-  // V transposed-read cells (see attn_f2_bf16)
+  // V transposed-read cells: for each channel block db, rows 4 hl +
+  // (p16 >> 2) of a 16-key step, channels 32 db + 16 (grp & 1) + 4 (p16 &
+  // 3), stored chunk swizzled (F2Layout::vchunk)
   const int grp = lane >> 4, p16 = lane & 15;
   const int vrow = 4 * (grp >> 1) + (p16 >> 2);
   int v_off[NDB];
@@ -3243,7 +2393,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     if (it + 1 < ntile) iteration(std::integral_constant<int, 1>{}, it + 1);
   }
 
-  // ---- epilogue (see attn_f2_bf16)
+  // ---- epilogue: lane holds row n's channels 32 db + 8 (j / 4) + 4 hl +
+  // j % 4.  Noise lanes (n >= 16) round O_noise to bf16; one permlane swap
+  // hands it to the signal lane l ^ 16; y = O_signal - lam rnd(O_noise),
+  // then the HeadwiseRMSNorm and weight in fp32, one rounding at the store.
   const float l_tot = xsum32(l_s);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   const float lam = lam_lds[wv * 16 + qn];
@@ -3293,12 +2446,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 // ------------------------------------------------------------ host side
 static int rows_nsplit(const coda_attn_desc* d) {
   const int Lk = d->Lp + d->Lb;
-  // CODA_ATTN_SPLIT=n forces the decode key split (launch-shape tuning)
-  static const int forced = [] {
-    const char* e = getenv("CODA_ATTN_SPLIT");
-    return e ? atoi(e) : 0;
-  }();
-  if (forced > 0) return forced;
   const int pairs = d->B * d->Hkv;
   if (pairs >= 512) return 1;
   int ns = (512 + pairs - 1) / pairs;
@@ -3354,51 +2501,14 @@ extern "C" int coda_attn_workspace_bytes(const coda_attn_desc* d, size_t* bytes)
   return CODA_OK;
 }
 
-// flash tiles (MFMA k=32 for both products, K straight to LDS)
 // the flash kernel's per-lane load offsets are 31-bit byte counts from a
 // tile's first row (or from the prefix / block start on a boundary tile)
-static bool fa_offsets_fit(const coda_attn_desc* d) {
+static bool flash_offsets_fit(const coda_attn_desc* d) {
   const int64_t lim = (int64_t)1 << 30;  // elements
   return (d->Lp == 0 || (d->p_sl >= 0 && ((int64_t)d->Lp + 64) * d->p_sl < lim)) &&
          (d->Lb == 0 || (d->b_sl >= 0 && ((int64_t)d->Lb + 64) * d->b_sl < lim));
 }
 
-template <int DH, int NW, int NS, int QG>
-static int launch_fa_nw(const coda_attn_desc* d, hipStream_t st, int G) {
-  const int npairs = d->B * d->Hkv;
-  const int NQ = NW / (2 * G);  // waves = 2 streams x G heads x NQ
-  const int nblk = (d->Lq + 16 * QG * NQ - 1) / (16 * QG * NQ);
-  const size_t lds = FaLayout<DH, NS>::LDS;
-  const int rc = lds_limit<attn_fa_bf16<DH, NW, NS, QG>>(lds, "coda_diff_attn_fwd");
-  if (rc) return rc;
-  hipLaunchKernelGGL((attn_fa_bf16<DH, NW, NS, QG>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk,
-                     npairs);
-  return check_launch("attn_fa_bf16");
-}
-template <int DH>
-static int launch_fa(const coda_attn_desc* d, hipStream_t st, int G) {
-  if constexpr (DH >= 64) {
-    // one wave per (stream, head, 16 queries): 16 waves for G = 8, else 8
-    if (G == 8) return launch_fa_nw<DH, 16, 2, 1>(d, st, G);
-    return launch_fa_nw<DH, 8, 2, 1>(d, st, G);
-  } else {
-    return fail(CODA_EUNSUP, "coda_diff_attn_fwd: flash tiles need head_dim >= 64");
-  }
-}
-
-// 32-row flash tiles: waves = G heads x NQ groups of 16 queries (both
-// streams in each wave)
-template <int DH, int NW>
-static int launch_f2_nw(const coda_attn_desc* d, hipStream_t st, int G) {
-  const int npairs = d->B * d->Hkv;
-  const int NQ = NW / G;
-  const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
-  const size_t lds = F2Layout<DH>::LDS;
-  int rc = lds_limit<attn_f2_bf16<DH, NW>>(lds, "coda_diff_attn_fwd");
-  if (rc) return rc;
-  hipLaunchKernelGGL((attn_f2_bf16<DH, NW>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk, npairs);
-  return check_launch("attn_f2_bf16");
-}
 // pipelined 32-row flash tiles: 8 waves, G heads x 8 / G groups of 16
 // queries; QM the query case (see attn_f3_bf16)
 template <int DH, int QM, bool TB>
@@ -3426,31 +2536,6 @@ static int launch_f3(const coda_attn_desc* d, hipStream_t st, int G) {
   if (d->q_noise && !d->rope_cos) return launch_f3_qm<DH, 2, false>(d, st, G);
   return launch_f3_qm<DH, 3, false>(d, st, G);
 }
-// CODA_PREFILL_KERNEL selects the prefill attention kernel for launch-shape
-// tuning: fa16 (16-row flash tiles), f2 / f2q2 (32-row tiles, one / two
-// query groups per head); the default is the pipelined 32-row kernel
-static int prefill_kernel_choice() {
-  static const int choice = [] {
-    const char* e = getenv("CODA_PREFILL_KERNEL");
-    if (e && !strcmp(e, "fa16")) return 1;
-    if (e && !strcmp(e, "f2q2")) return 2;
-    if (e && !strcmp(e, "f2")) return 3;
-    return 0;
-  }();
-  return choice;
-}
-template <int DH>
-static int launch_f2(const coda_attn_desc* d, hipStream_t st, int G) {
-  if (prefill_kernel_choice() == 0) return launch_f3<DH>(d, st, G);
-  const bool q2 = prefill_kernel_choice() == 2;
-  switch (G) {
-    case 8: return launch_f2_nw<DH, 8>(d, st, G);
-    case 4: return q2 ? launch_f2_nw<DH, 8>(d, st, G) : launch_f2_nw<DH, 4>(d, st, G);
-    case 2: return q2 ? launch_f2_nw<DH, 8>(d, st, G) : launch_f2_nw<DH, 4>(d, st, G);
-    default: return launch_f2_nw<DH, 4>(d, st, G);
-  }
-}
-
 template <int DH>
 static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
   const int G = d->H / d->Hkv;
@@ -3477,11 +2562,8 @@ static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
                        (const float*)d->workspace);
     return check_launch("attn_rows_merge");
   }
-  if (DH >= 64 && (G == 8 || G == 4 || G == 2 || G == 1) && fa_offsets_fit(d)) {
-    if constexpr (DH >= 64) {
-      if (prefill_kernel_choice() != 1) return launch_f2<DH>(d, st, G);
-    }
-    return launch_fa<DH>(d, st, G);
+  if constexpr (DH >= 64) {
+    if ((G == 8 || G == 4 || G == 2 || G == 1) && flash_offsets_fit(d)) return launch_f3<DH>(d, st, G);
   }
   const int NQ = G >= 4 ? 1 : 4 / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);

@@ -14,6 +14,13 @@
 
 namespace coda {
 
+// Active bank sizes: the caller's device words when it keeps them on the
+// device (dynamic expansion without host syncs), else the descriptor's ints
+__device__ __forceinline__ int act_exact(const coda_bank_desc& s) { return s.active ? s.active[0] : s.active_exact; }
+__device__ __forceinline__ int act_summary(const coda_bank_desc& s) {
+  return s.active ? s.active[1] : s.active_summary;
+}
+
 static constexpr int64_t kNegBig = -(int64_t(1) << 62);
 static constexpr int64_t kPosBig = int64_t(1) << 62;
 
@@ -250,7 +257,7 @@ __device__ __forceinline__ void decide_exact(const coda_bank_desc& s, const floa
                                              const int64_t* last, float g_e, DecodeDecision& dec, bool count,
                                              int lane) {
   using E = Elt<T>;
-  const int Me = s.Me, Ae = s.active_exact, Hkv = s.Hkv;
+  const int Me = s.Me, Ae = act_exact(s), Hkv = s.Hkv;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   int any_used = 0, free_i = 0x7fffffff;
@@ -301,7 +308,7 @@ template <typename T>
 __device__ __forceinline__ void decide_summary(const coda_bank_desc& s, const float* ds, const int* used, float g_e,
                                                DecodeDecision& dec, bool count, int lane) {
   using E = Elt<T>;
-  const int Ms = s.Ms, As = s.active_summary, Hkv = s.Hkv;
+  const int Ms = s.Ms, As = act_summary(s), Hkv = s.Hkv;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
   for (int m = lane; m < Ms; m += 64) {

@@ -614,7 +614,7 @@ __global__ __launch_bounds__(256) void block_route_kernel(const coda_bank_desc s
     for (int i = t; i < TT; i += blockDim.x) sn.gate[i] = cand_gate(s, g, gb, b, pc[i]);
     if (g.Te > 0) {
       sel::Item<int64_t>* rk = reinterpret_cast<sel::Item<int64_t>*>(rsm);
-      const int Ae = s.active_exact;
+      const int Ae = act_exact(s);
       for (int m = t; m < Me; m += blockDim.x) {
         const bool u = al[W + m] != 0 && m < Ae;
         rk[m] = sel::Item<int64_t>{u ? s.mem_last[(int64_t)b * Me + m] : kNegBig, (int64_t)m};
@@ -740,7 +740,7 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
     // candidates 64 at a time: the best slot of each (one wave per
     // candidate), then thread 0 walks them in token order, its rank and
     // counters carried from chunk to chunk
-    const int Ae = s.active_exact;
+    const int Ae = act_exact(s);
     const int n_lru = min(Te, Ae);
     int rank = -1;
     int64_t cnt_ow = 0, cnt_cap = 0, cnt_hit = 0, cnt_gated = 0, cnt_fr = 0;
@@ -755,7 +755,7 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
           float acc = 0.f;
           for (int hh = 0; hh < Hkv; ++hh) acc += dg[((int64_t)hh * Te + tt) * Me + m];
           float v = E::rnd(acc / (float)Hkv);
-          if (m >= s.active_exact || used[m] == 0) v = neg_fill<T>();
+          if (m >= Ae || used[m] == 0) v = neg_fill<T>();
           if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
         }
         wave_argmax(bv, bi);
@@ -840,11 +840,12 @@ __global__ __launch_bounds__(256) void block_decide_kernel(const coda_bank_desc 
   for (int tt = wv; tt < nt; tt += blockDim.x >> 6) {
     float bv = -INFINITY;
     int bi = 0x7fffffff;
+    const int As = act_summary(s);
     for (int m = lane; m < Ms; m += 64) {
       float acc = 0.f;
       for (int hh = 0; hh < Hkv; ++hh) acc += dsd[((int64_t)hh * Ts + t0 + tt) * Ms + m];
       float v = E::rnd(acc / (float)Hkv);
-      if (m >= s.active_summary) v = neg_fill<T>();
+      if (m >= As) v = neg_fill<T>();
       if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
     }
     wave_argmax(bv, bi);
@@ -1134,11 +1135,12 @@ __global__ __launch_bounds__(kApplyThreads) void block_apply_kernel(const coda_b
       if (wv == 0) {
         int64_t upd = 0, ins = 0;
         int all_used = 1, any_cnt = 0;
+        const int As = act_summary(s);
         for (int m = lane; m < Ms; m += 64) {
           const int f = fl_all[m];
           upd += f & 1;
           ins += (f >> 1) & 1;
-          if (m < s.active_summary) {
+          if (m < As) {
             if (!(sn.used[Me + m] != 0 || (f & 1))) all_used = 0;
             if (f & 1) any_cnt = 1;
           }
@@ -1240,7 +1242,12 @@ __global__ __launch_bounds__(kApplyThreads) void block_ring_kernel(const coda_ba
 // sync 1 (every workgroup has read them by then).
 // Sync: every workgroup of b stores (2 epoch + k) at sync k in its own
 // 64-bit flag word of the workspace and waits until all flags of b reach
-// it; the epoch is unique per launch, so no word needs clearing.  What
+// it; the epoch is unique per launch, so no word needs clearing.  The epoch
+// of sequence b mixes the host's per-call value with a generation word of
+// b kept in the workspace's tail, which the lead workgroup advances once
+// every workgroup of b has passed sync 2 (so all of them read the same
+// value first): a launch replayed from a captured graph, whose host value
+// is fixed, still meets its own sync words and never a stale one.  What
 // crosses a sync (dots, routing) is written and read with agent-scope
 // atomic accesses (coherent across the XCDs' L2s, no cache write-back or
 // invalidation), and a workgroup's flag is stored only after all its
@@ -1248,8 +1255,11 @@ __global__ __launch_bounds__(kApplyThreads) void block_ring_kernel(const coda_ba
 // only; they lie in one contiguous range of launch order (with whole other
 // sequences at most, at most 64 workgroups), dispatched after every earlier
 // range: one that waits never holds back one it waits for.  Waits are
-// bounded (kSyncSpinLimit sleeps, about 0.1 s); a workgroup that gives up
-// counts itself in g_block_sync_timeouts.
+// bounded (spin_limit sleeps, about 0.1 s by default); a workgroup that
+// gives up counts itself in g_block_sync_timeouts and in the workspace's
+// status word, and exits without writing any more state (the chunk's
+// update is then incomplete: the caller reads the status word and must
+// treat the state as lost).
 static constexpr int kFusedThreads = 512;
 static constexpr int kFusedMaxGroup = 64;  // Hkv * NZ: one wave polls every flag of a sequence
 static constexpr int kSyncSpinLimit = 1 << 20;
@@ -1258,9 +1268,12 @@ static __device__ unsigned int g_block_sync_timeouts;
 // Sync of the K workgroups of one sequence (see above).  While wave 0
 // polls, waves 1 .. hold `busy`: work that needs nothing from the other
 // workgroups (it sees thread ids from 0 and a stride of blockDim - 64).
+// Returns true, in every thread, when the wait gave up (spin_limit < 0:
+// at once, without polling: the host's way to take the failure path).
 template <typename F>
-__device__ __forceinline__ void group_sync(unsigned long long* flags, int K, int me, unsigned long long val,
-                                           unsigned long long alt, F&& busy) {
+__device__ __forceinline__ bool group_sync(unsigned long long* flags, int K, int me, unsigned long long val,
+                                           unsigned long long alt, int spin_limit, unsigned long long* status,
+                                           int* gave_up, F&& busy) {
   // this wave's coherent stores complete, then the workgroup's
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -1268,22 +1281,27 @@ __device__ __forceinline__ void group_sync(unsigned long long* flags, int K, int
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     for (int n = 0;; ++n) {
+      if (n > spin_limit) {
+        if (lane == 0) {
+          atomicAdd(&g_block_sync_timeouts, 1u);
+          __hip_atomic_fetch_add(status, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          *gave_up = 1;
+        }
+        break;
+      }
       bool ok = true;
       if (lane < K) {
         const unsigned long long v = __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ok = v == val || v == alt;
       }
       if (__all(ok)) break;
-      if (n >= kSyncSpinLimit) {
-        if (lane == 0) atomicAdd(&g_block_sync_timeouts, 1u);
-        break;
-      }
       __builtin_amdgcn_s_sleep(2);
     }
   } else {
     busy((int)threadIdx.x - 64, (int)blockDim.x - 64);
   }
   __syncthreads();
+  return *gave_up != 0;
 }
 
 struct FusedLds {
@@ -1331,11 +1349,12 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
                                                                     const T* kbk, const T* vbk, const float* gb,
                                                                     const int32_t* __restrict__ plan_c, float* ws,
                                                                     unsigned long long* flags_all,
-                                                                    unsigned long long epoch) {
+                                                                    unsigned long long host_epoch,
+                                                                    unsigned long long* tail, int spin_limit) {
   using E = Elt<T>;
   constexpr int NV = (DH + 63) / 64, LF = DH / 2, NCOL = DH + LF, CH = DH / 8;
   extern __shared__ __attribute__((aligned(16))) char fsm[];
-  __shared__ int ties, any_used_s;
+  __shared__ int ties, any_used_s, sync_gave_up;
   __shared__ int dec_wave[kFusedThreads / 64], dec_cnt[5];
   // workgroup -> (sequence, head, z): workgroups are dealt round robin to
   // the 8 XCDs, so the NZ workgroups of one (sequence, head) pair take
@@ -1349,7 +1368,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   const int W = s.W, Me = s.Me, Ms = s.Ms, Hkv = s.Hkv, Te = g.Te, Ts = g.Ts;
   const int TT = max(Te, Ts), Lbuf = W + Me + Ms, K = Hkv * NZ, me = h * NZ + z;
   const bool lead = me == 0;
-  const int Ae = s.active_exact, n_lru = min(Te, Ae);
+  const int Ae = act_exact(s), As = act_summary(s), n_lru = min(Te, Ae);
   const FusedLds L = fused_lds(DH, (int)sizeof(T), Me, Ms, Te, Ts, NZ);
   T* raw_k = reinterpret_cast<T*>(fsm + L.raw_k);    // [TT][DH] candidate K rows of head h
   T* raw_v = reinterpret_cast<T*>(fsm + L.raw_v);    // [TT][DH] candidate V rows
@@ -1390,6 +1409,12 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   uint8_t* al = s.allowed + (int64_t)b * Lbuf;
   const int32_t* pc = plan_c + (int64_t)b * g.Kmax;
   unsigned long long* flags = flags_all + (int64_t)b * K;
+  // epoch of this launch for sequence b: the host value mixed with b's
+  // generation word (tail[b]); tail[B] is the status word
+  unsigned long long* status = tail + s.B;
+  const unsigned long long gen_b = __hip_atomic_load(tail + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long epoch = (host_epoch + gen_b * 0x9E3779B97F4A7C15ull) & ((1ull << 62) - 1);
+  if (t == 0) sync_gave_up = 0;
   const Dec dx = dec_of(s, g, ws, b);  // exchange: idx_s [Ts], best value / slot of the exact tokens
   const int Lr = g.ring_filled, first = max(Lr, g.n_ev), rhead = (Lr == W) ? g.ring_head : 0;
 
@@ -1545,7 +1570,8 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
     }
   }
   // sync 1; meanwhile the LRU victim order (rank of each key among all)
-  group_sync(flags, K, me, 2 * epoch, 2 * epoch + 1, [&](int t1, int nt1) {
+  const bool gave_up1 = group_sync(flags, K, me, 2 * epoch, 2 * epoch + 1, spin_limit, status, &sync_gave_up,
+                                   [&](int t1, int nt1) {
     if (Te > 0)
       for (int m = t1; m < Me; m += nt1) {
         const int64_t km = rk[m].v;
@@ -1561,6 +1587,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
         }
       }
   });
+  if (gave_up1) return;
   // ---- 3. routing of this workgroup's tokens (token i of [Te | Ts] goes
   // to workgroup i mod K): one wave per token
   {
@@ -1588,7 +1615,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
             if (h0 + u < Hkv) acc += hv[u];
         }
         float v = E::rnd(acc / (float)Hkv);
-        if (ex ? (m >= Ae || used[m] == 0) : m >= s.active_summary) v = neg_fill<T>();
+        if (ex ? (m >= Ae || used[m] == 0) : m >= As) v = neg_fill<T>();
         if (v > bv || (v == bv && m < bi)) { bv = v; bi = m; }
       }
       wave_argmax(bv, bi);
@@ -1610,7 +1637,8 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   }
   // sync 2; meanwhile this workgroup's share of head h's ring (every
   // workgroup of head h has read its candidate rows before sync 1)
-  group_sync(flags, K, me, 2 * epoch + 1, 2 * epoch + 1, [&](int t1, int nt1) {
+  const bool gave_up2 = group_sync(flags, K, me, 2 * epoch + 1, 2 * epoch + 1, spin_limit, status, &sync_gave_up,
+                                   [&](int t1, int nt1) {
     const int n_all = (Lr + g.blk - first) * CH;
     const int pz = (n_all + NZ - 1) / NZ, p0 = min(n_all, z * pz), p1 = min(n_all, p0 + pz);
     for (int base = p0 + t1; base < p1; base += kRingPre * nt1) {
@@ -1644,6 +1672,10 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       }
     }
   });
+  if (gave_up2) return;
+  // every workgroup of b has read gen_b (before its sync-1 flag): the next
+  // launch on this workspace takes the next generation
+  if (lead && t == 0) __hip_atomic_store(tail + b, gen_b + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // ---- 4a. every token's routing (all three loads in flight together);
   // exact decisions (memory_banks.py:640-697)
   for (int i = t; i < TT; i += NT) {
@@ -1790,7 +1822,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       for (int m0 = 0; m0 < Ms; m0 += 64) {
         const int m = m0 + lane;
         const int f = m < Ms ? sflag[m] : 0;
-        const bool act = m < Ms && m < s.active_summary;
+        const bool act = m < Ms && m < As;
         upd += __popcll(__ballot(f & 1));
         ins += __popcll(__ballot((f >> 1) & 1));
         all_used = all_used && __ballot(act && !(used[Me + min(m, Ms - 1)] != 0 || (f & 1))) == 0;
@@ -2114,8 +2146,17 @@ extern "C" int coda_block_plan(const float* g_ring, int ring_head, int ring_fill
   return check_launch("block_plan");
 }
 
+// The workspace's tail: the last B + 1 8-byte words of the caller's buffer
+// (at a place that depends only on its size and B, so every chunk of a call
+// finds them): a generation word per sequence, then the status word (give-
+// ups of the one-launch update's waits, added by the kernel, never cleared
+// by it).
+static size_t block_tail_bytes(const coda_bank_desc* s) { return 8 * ((size_t)s->B + 1) + 8; }
+static unsigned long long* block_tail(const coda_bank_desc* s, void* workspace, size_t workspace_bytes) {
+  return reinterpret_cast<unsigned long long*>((char*)workspace + (workspace_bytes / 8) * 8) - (s->B + 1);
+}
 static size_t block_ws_bytes(const coda_bank_desc* s, int Te, int Ts) {
-  return sizeof(float) * ws_total(s->B, s->Hkv, s->Me, s->Ms, Te, Ts);
+  return sizeof(float) * ws_total(s->B, s->Hkv, s->Me, s->Ms, Te, Ts) + block_tail_bytes(s);
 }
 
 extern "C" int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, size_t* bytes) {
@@ -2126,9 +2167,10 @@ extern "C" int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, siz
   return CODA_OK;
 }
 
-// Launch epochs of the fused block write: unique per launch in the process
-// (48 bits), started from a clock-derived value so that a sync word left in
-// a reused workspace never carries the epoch of a later launch.
+// Host part of the fused block write's launch epochs: unique per launch in
+// the process (48 bits), started from a clock-derived value so that a sync
+// word left in a reused workspace never carries the epoch of a later
+// launch (the kernel mixes in the sequence's generation word).
 static unsigned long long next_epoch() {
   static std::atomic<unsigned long long> ep{
       (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count() * 0x9E3779B97F4A7C15ull};
@@ -2196,9 +2238,12 @@ static SplitShape split_shape(const coda_bank_desc* s, int Te, int Ts, int pairs
   return p;
 }
 
+// Spin limit of the fused kernel's bounded waits (coda_block_sync_spin_limit)
+static std::atomic<int> g_spin_limit{kSyncSpinLimit};
+
 template <typename T, int DH>
 static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb, const float* gb, BlockGeom g,
-                        const int32_t* plan_c, float* ws, hipStream_t st) {
+                        const int32_t* plan_c, float* ws, unsigned long long* tail, hipStream_t st) {
   const int TT = g.Te > g.Ts ? g.Te : g.Ts;
   const int pairs = s->B * s->Hkv;
   if (g.n_ev > 0 && TT > 0 && fused_enabled()) {
@@ -2213,7 +2258,8 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
       // beyond B * Hkv exits at once)
       const int nwg = ((pairs + 7) / 8) * 8 * NZ;
       hipLaunchKernelGGL((block_fused_kernel<T, DH>), dim3(nwg), dim3(kFusedThreads), lds, st, *s, g, NZ,
-                         (const T*)kb, (const T*)vb, gb, plan_c, ws, flags, next_epoch());
+                         (const T*)kb, (const T*)vb, gb, plan_c, ws, flags, next_epoch(), tail,
+                         g_spin_limit.load(std::memory_order_relaxed));
       return check_launch("block_fused");
     }
   }
@@ -2302,16 +2348,17 @@ extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const v
   hipStream_t st = (hipStream_t)stream;
   const bool bf = s->dtype == CODA_BF16;
   float* ws = (float*)workspace;
+  unsigned long long* tail = workspace ? block_tail(s, workspace, workspace_bytes) : nullptr;
   switch (s->Dh) {
     case 32:
-      return bf ? launch_block<bf16_t, 32>(s, kb, vb, gb, g, plan_c, ws, st)
-                : launch_block<float, 32>(s, kb, vb, gb, g, plan_c, ws, st);
+      return bf ? launch_block<bf16_t, 32>(s, kb, vb, gb, g, plan_c, ws, tail, st)
+                : launch_block<float, 32>(s, kb, vb, gb, g, plan_c, ws, tail, st);
     case 64:
-      return bf ? launch_block<bf16_t, 64>(s, kb, vb, gb, g, plan_c, ws, st)
-                : launch_block<float, 64>(s, kb, vb, gb, g, plan_c, ws, st);
+      return bf ? launch_block<bf16_t, 64>(s, kb, vb, gb, g, plan_c, ws, tail, st)
+                : launch_block<float, 64>(s, kb, vb, gb, g, plan_c, ws, tail, st);
     default:
-      return bf ? launch_block<bf16_t, 128>(s, kb, vb, gb, g, plan_c, ws, st)
-                : launch_block<float, 128>(s, kb, vb, gb, g, plan_c, ws, st);
+      return bf ? launch_block<bf16_t, 128>(s, kb, vb, gb, g, plan_c, ws, tail, st)
+                : launch_block<float, 128>(s, kb, vb, gb, g, plan_c, ws, tail, st);
   }
 }
 
@@ -2353,6 +2400,42 @@ extern "C" int coda_block_sync_timeouts(unsigned int* out) {
   return CODA_OK;
 }
 
+// Dynamic expansion after a bank update (attention.py:358-390): one thread.
+__global__ __launch_bounds__(64) void bank_expand_kernel(int32_t* active, const int64_t* fr, int ce, int cs,
+                                                         int count_mode, int ran_e, int ran_s, int64_t* counters) {
+  if (threadIdx.x != 0) return;
+  const int64_t fe = ran_e ? (count_mode ? fr[0] : (int64_t)(fr[0] > 0)) : 0;
+  const int64_t fs = ran_s ? (int64_t)(fr[1] == 0 && fr[2] > 0) : 0;
+  int64_t de = 0, ds = 0;
+  if (active) {
+    const int ae = active[0], as = active[1];
+    if (fe > 0 && ae < ce) de = fe < (int64_t)(ce - ae) ? fe : (int64_t)(ce - ae);
+    if (fs > 0 && as < cs) ds = fs < (int64_t)(cs - as) ? fs : (int64_t)(cs - as);
+    active[0] = ae + (int)de;
+    active[1] = as + (int)ds;
+  }
+  if (counters) {
+    counters[0] += fs;
+    counters[1] += de;
+    counters[2] += ds;
+  }
+}
+
+extern "C" int coda_bank_expand(int32_t* active, const int64_t* frustrated, int ceil_exact, int ceil_summary,
+                                int exact_count_mode, int ran_exact, int ran_summary, int64_t* counters,
+                                void* stream) {
+  CODA_REQUIRE(frustrated != nullptr, "coda_bank_expand: frustration flags missing");
+  CODA_REQUIRE(ceil_exact >= 0 && ceil_summary >= 0, "coda_bank_expand: negative ceiling");
+  if (!active && !counters) return CODA_OK;
+  hipLaunchKernelGGL(bank_expand_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, active, frustrated, ceil_exact,
+                     ceil_summary, exact_count_mode, ran_exact, ran_summary, counters);
+  return check_launch("bank_expand");
+}
+
+extern "C" int coda_block_sync_spin_limit(int limit) {
+  return g_spin_limit.exchange(limit < -1 ? -1 : limit, std::memory_order_relaxed);
+}
+
 extern "C" size_t coda_block_write_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
 
 extern "C" int coda_block_write_noalloc(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb,
@@ -2369,7 +2452,9 @@ extern "C" int coda_block_write_noalloc(const coda_bank_desc* s, const void* kb,
                "with a workspace instead",
                need, kNoAllocScratchBytes);
   // nothing in the scratch needs to start at zero: every word a chunk reads
-  // is written earlier in the same call (dots, metadata snapshot, decisions)
+  // is written earlier in the same call (dots, metadata snapshot,
+  // decisions), except the tail's generation and status words, which the
+  // array's zero initialisation starts and every call carries on
   void* ws = nullptr;
   rc = noalloc_scratch(&ws);
   if (rc) return rc;

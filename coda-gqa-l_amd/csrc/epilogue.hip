@@ -101,3 +101,26 @@ extern "C" int coda_diff_sub_only_fwd(int dtype, void* out, const void* sig, con
   if (num_rows == 0) return CODA_OK;
   return launch<false>(dtype, out, sig, noise, lam, nullptr, num_rows, head_dim, 0.f, (hipStream_t)stream);
 }
+
+// Typed entry points with the argument lists of the reference's extern "C"
+// functions (kernels/coda_diff_epilogue/kernel_src/diff_epilogue.cu:465-568),
+// so its torch binding (torch-ext/torch_binding.cpp:203-213) links against
+// this library unchanged.  They return void like the reference's; an
+// argument error or a failed launch leaves its message in coda_last_error().
+#define CODA_TYPED_EPILOGUE(SUFFIX, CODE, TYPE)                                                                \
+  extern "C" void diff_epilogue_forward_##SUFFIX(TYPE* output, const TYPE* out_sig, const TYPE* out_noise,     \
+                                                 const TYPE* lam, const TYPE* weight, int num_rows,            \
+                                                 int head_dim, float eps, void* stream) {                      \
+    (void)coda_diff_epilogue_fwd(CODE, output, out_sig, out_noise, lam, weight, num_rows, head_dim, eps,       \
+                                 stream);                                                               \
+  }                                                                                                            \
+  extern "C" void diff_sub_only_forward_##SUFFIX(TYPE* output, const TYPE* out_sig, const TYPE* out_noise,     \
+                                                 const TYPE* lam, int num_rows, int head_dim,                  \
+                                                 void* stream) {                                               \
+    (void)coda_diff_sub_only_fwd(CODE, output, out_sig, out_noise, lam, num_rows, head_dim, stream);            \
+  }
+
+CODA_TYPED_EPILOGUE(bf16, CODA_BF16, uint16_t)
+CODA_TYPED_EPILOGUE(fp16, CODA_F16, uint16_t)
+CODA_TYPED_EPILOGUE(fp32, CODA_F32, float)
+#undef CODA_TYPED_EPILOGUE

@@ -211,6 +211,31 @@ int coda_diff_epilogue_fwd(int dtype, void* out, const void* sig, const void* no
 int coda_diff_sub_only_fwd(int dtype, void* out, const void* sig, const void* noise,
                            const void* lam, int num_rows, int head_dim, void* stream);
 
+/* The same two epilogues under the reference's own typed symbols and
+ * argument lists, so its binding (torch_binding.cpp:203-213) links against
+ * this library unchanged.  bf16 and fp16 elements are passed as their
+ * 16-bit storage; stream is a hipStream_t.  Like the reference's they
+ * return nothing: an argument error or a failed launch leaves its message
+ * in coda_last_error().
+ * Replaces: diff_epilogue_forward_bf16 / _fp16 / _fp32
+ *   (kernels/coda_diff_epilogue/kernel_src/diff_epilogue.cu:465-516) and
+ *   diff_sub_only_forward_bf16 / _fp16 / _fp32 (diff_epilogue.cu:520-566). */
+void diff_epilogue_forward_bf16(uint16_t* output, const uint16_t* out_sig, const uint16_t* out_noise,
+                                const uint16_t* lam, const uint16_t* weight, int num_rows, int head_dim,
+                                float eps, void* stream);
+void diff_epilogue_forward_fp16(uint16_t* output, const uint16_t* out_sig, const uint16_t* out_noise,
+                                const uint16_t* lam, const uint16_t* weight, int num_rows, int head_dim,
+                                float eps, void* stream);
+void diff_epilogue_forward_fp32(float* output, const float* out_sig, const float* out_noise,
+                                const float* lam, const float* weight, int num_rows, int head_dim,
+                                float eps, void* stream);
+void diff_sub_only_forward_bf16(uint16_t* output, const uint16_t* out_sig, const uint16_t* out_noise,
+                                const uint16_t* lam, int num_rows, int head_dim, void* stream);
+void diff_sub_only_forward_fp16(uint16_t* output, const uint16_t* out_sig, const uint16_t* out_noise,
+                                const uint16_t* lam, int num_rows, int head_dim, void* stream);
+void diff_sub_only_forward_fp32(float* output, const float* out_sig, const float* out_noise,
+                                const float* lam, int num_rows, int head_dim, void* stream);
+
 /* ------------------------------------------------------------------------
  * RoPE of a (B, Hx, L, Dh) tensor into out (same shape, own strides), with
  * (L, Dh/2) cos/sin tables, rounding after every multiply / add in the
@@ -268,8 +293,11 @@ typedef struct {
   int refresh_on_hit, overwrite_on_insert;
   float energy_scale;                 /* sqrt(Dh / (Dh - lf)) */
   int64_t* metrics;
-  int64_t* frustrated;                /* (2,) device int64 or NULL: exact, summary */
+  int64_t* frustrated;                /* (3,) device int64 or NULL: exact, summary (not all used, kept) */
   int32_t* trace;                     /* decision record or NULL (above) */
+  const int32_t* active;              /* (2,) device int32 or NULL: the active sizes [exact, summary]
+                                         read by the kernels in place of active_exact / active_summary
+                                         (dynamic expansion kept on the device, coda_bank_expand) */
 } coda_bank_desc;
 
 /* One decode token per sequence: ring FIFO write; when the ring is full the
@@ -323,6 +351,23 @@ int coda_decode_step_raw_k(const coda_bank_desc* s, const coda_attn_desc* a, con
                            int ring_idx, int ring_filled, int64_t pos, void* workspace,
                            size_t workspace_bytes, int* routed, void* stream);
 
+/* Dynamic bank expansion after a bank update, on the device (no host
+ * sync): from the frustration flags `frustrated` the update left (see
+ * coda_bank_desc), with exact_count_mode 1 (a prefill chunk: the count of
+ * frustrated exact tokens) or 0 (a decode step: whether any), and the
+ * capacity ceilings ceil_exact / ceil_summary of the position the update
+ * ran at (a host computation from the token count), grows active[0] /
+ * active[1] like the reference and adds, when counters is not NULL, the
+ * summary frustration (0 / 1) to counters[0] and the two growths to
+ * counters[1] / counters[2].  ran_exact / ran_summary: whether the update
+ * touched that bank.  active may be NULL (no expansion configured: only
+ * the counters).  One workgroup of one thread.
+ * Replaces: CoDAGQALandmarkPerf2._try_expand with its callers' frustration
+ *   counts and metrics updates (src/coda_gqa_l/attention.py:358-390,
+ *   memory_banks.py:333-337, 418-426, 744-766, 934-946). */
+int coda_bank_expand(int32_t* active, const int64_t* frustrated, int ceil_exact, int ceil_summary,
+                     int exact_count_mode, int ran_exact, int ran_summary, int64_t* counters, void* stream);
+
 /* Candidate plan of a chunked prefill: for every chunk c (block_size
  * tokens, last one ragged) and sequence b, the evicted-token indices picked
  * by the reference's CPU topk(g_e, k, sorted=False) (libstdc++ nth_element /
@@ -347,6 +392,20 @@ int coda_block_plan(const float* g_ring, int ring_head, int ring_filled, int W,
  * workgroup per (KV head, sequence); the heads of a sequence meet at a
  * per-sequence sync word in the workspace), else four (route, decide,
  * apply, ring).  Calls that share a workspace must not overlap.
+ * The last B + 1 8-byte words of the workspace (at (workspace_bytes / 8) * 8
+ * bytes from its start, counting back) are its tail: a generation word per
+ * sequence, then a status word.  The one-launch update adds 1 to the status
+ * word for every workgroup whose bounded wait for the other heads of its
+ * sequence gave up; that workgroup then stops, the chunk's update is
+ * incomplete and the state must be treated as lost.  The caller zeroes the
+ * workspace (or at least the status word) before the first call and reads
+ * the status word after its calls; the library never clears it.  The
+ * generation words need no clearing: they keep the sync words of
+ * successive launches apart, replays of a captured graph included.
+ * The waits need every workgroup of a sequence resident at once; they are
+ * launched in one contiguous range, which in-order dispatch on one stream
+ * guarantees, so other kernels running beside them on other streams can
+ * delay them into a give-up. 
  * Replaces: _write_block_fast (memory_banks.py:438-564) with
  *   _exact_update_block_vectorized (:570-774, PyTorch branch) and
  *   _summary_update_block_hard (:780-950, PyTorch branch). */
@@ -376,6 +435,14 @@ int coda_block_write_check(const coda_bank_desc* s, int Te, int Ts);
  * No counterpart in the reference (the reference has no cross-workgroup
  * wait). */
 int coda_block_sync_timeouts(unsigned int* out);
+
+/* Sets the spin limit of the bounded waits of later coda_block_write /
+ * coda_block_write_noalloc launches (default 2^20 sleeps, about 0.1 s) and
+ * returns the previous one; a negative limit makes every wait give up at
+ * once, without polling, so a test can take the failure path with every
+ * kernel exiting normally.  Process-wide.
+ * No counterpart in the reference: a test hook of the cross-workgroup wait. */
+int coda_block_sync_spin_limit(int limit);
 
 /* coda_block_write without a workspace argument and without any allocation:
  * the chunk's scratch (routing dots, metadata snapshot, decisions) lives in a

@@ -26,13 +26,16 @@ def _hip():
 def _declared_functions():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(coda_\w+)\s*\(", src, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(coda_\w+|diff_\w+_forward_\w+)\s*\(", src,
+                                 flags=re.M)))
 
 
 def test_library_loads_and_exports_every_declared_symbol():
     L = _hip().lib()
     names = _declared_functions()
     assert len(names) >= 15, names
+    typed = ["diff_%s_forward_%s" % (k, t) for k in ("epilogue", "sub_only") for t in ("bf16", "fp16", "fp32")]
+    assert set(typed) <= set(names), "the reference's typed epilogue symbols must be declared"
     missing = [n for n in names if not hasattr(L, n)]
     assert not missing, missing
     assert L.coda_abi_version() == 1

@@ -189,13 +189,17 @@ def test_one_launch_block_write_equals_four_launch_path(name, monkeypatch):
 
 def test_block_write_sync_never_gave_up():
     """No workgroup of the one-launch block write gave up its bounded wait
-    for the other heads of its sequence in any run of this process."""
+    for the other heads of its sequence in any run of this process (other
+    than the give-ups test_block_sync_gpu forces on purpose)."""
     _need_gpu()
     import ctypes
+    import sys
     from coda_gqa_l import _hip
     n = ctypes.c_uint(0)
     _hip.check(_hip.lib().coda_block_sync_timeouts(ctypes.byref(n)))
-    assert n.value == 0, f"{n.value} workgroups gave up waiting at a block-write sync word"
+    mod = sys.modules.get("test_block_sync_gpu")
+    forced = mod.FORCED["n"] if mod is not None else 0
+    assert n.value == forced, f"{n.value - forced} workgroups gave up waiting at a block-write sync word"
 
 
 @torch.no_grad()

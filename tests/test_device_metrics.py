@@ -60,3 +60,25 @@ def test_pickles_as_a_plain_mapping_and_saves_as_a_dict():
         save_state({"states": {0: st}}, path)
         got = load_state(path)["states"][0].metrics
     assert type(got) is dict and got["exact_inserts"] == 4
+
+
+def test_direct_writes_fold_pending_counts_first():
+    """A key reset directly (reset_metrics, or metrics[k] = 0 on the
+    reference's plain dict) stays reset: counts pending on the device at the
+    time of the write are folded in before it, not added on the next read."""
+    mt, _hip = _metrics()
+    acc = mt.accumulator("cpu")
+    acc[_hip.CNT_EXACT_HITS] += 3
+    acc[_hip.CNT_EXACT_INSERTS] += 2
+    mt["exact_hits"] = 0
+    assert mt["exact_hits"] == 0 and mt["exact_inserts"] == 2
+    acc[_hip.CNT_EXACT_INSERTS] += 5
+    mt.update(exact_inserts=1)
+    assert mt["exact_inserts"] == 1
+    acc[_hip.CNT_SUMMARY_UPDATES] += 4
+    assert mt.setdefault("summary_updates", 99) == 4
+    acc[_hip.CNT_SUMMARY_INSERTS] += 6
+    assert mt.pop("summary_inserts") == 6
+    acc[_hip.CNT_TOKENS_GATED_OUT] += 1
+    mt.clear()
+    assert len(mt) == 0 and int(acc.sum()) == 0

@@ -82,6 +82,37 @@ def test_epilogue_matches_oracle(dtype):
     assert torch.equal(out.cpu(), diff_sub_only(s, n, lam)), "diff_sub_only not bit-exact"
 
 
+@pytest.mark.parametrize("dtype,suffix", [(torch.float32, "fp32"), (torch.bfloat16, "bf16"),
+                                          (torch.float16, "fp16")])
+def test_typed_epilogue_symbols_match_oracle(dtype, suffix):
+    """The reference's typed symbols (diff_epilogue.cu:465-566), called
+    through the C ABI with its argument lists, against the oracle's eager
+    epilogue (norm) and bit for bit (sub only)."""
+    _need_gpu()
+    from coda_gqa_l import _hip
+    from coda_oracle import diff_epilogue, diff_sub_only
+    g = torch.Generator().manual_seed(15)
+    rows, dh = 37, 64
+    s = torch.randn(rows, dh, generator=g).to(dtype)
+    n = torch.randn(rows, dh, generator=g).to(dtype)
+    lam = torch.rand(rows, generator=g).to(dtype)
+    w = torch.randn(dh, generator=g).to(dtype)
+    sd, nd, ld, wd = (t.to(DEV) for t in (s, n, lam, w))
+    out = torch.full_like(sd, float("nan"))
+    L = _hip.lib()
+    st = _hip.stream_of(sd)
+    getattr(L, "diff_epilogue_forward_" + suffix)(out.data_ptr(), sd.data_ptr(), nd.data_ptr(), ld.data_ptr(),
+                                                  wd.data_ptr(), rows, dh, 1e-6, st)
+    sub = torch.full_like(sd, float("nan"))
+    getattr(L, "diff_sub_only_forward_" + suffix)(sub.data_ptr(), sd.data_ptr(), nd.data_ptr(), ld.data_ptr(),
+                                                  rows, dh, st)
+    torch.cuda.synchronize()
+    ref = diff_epilogue(s, n, lam.reshape(rows, 1), w, 1e-6)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    assert_close(out, ref, torch.float32, "diff_epilogue_forward_" + suffix, tol)
+    assert torch.equal(sub.cpu(), diff_sub_only(s, n, lam.reshape(rows, 1))), "diff_sub_only_forward not bit-exact"
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("interleaved", [True, False])
 def test_rope_bit_exact(dtype, interleaved):
@@ -230,6 +261,43 @@ def test_unbounded_matches_oracle():
         y, (kt, vt) = p(x.to(DEV))
         yo, _ = o(x)
         assert_close(y, yo, dtype, f"unbounded y {dtype}", TOL[dtype] * 3)
+
+
+@torch.no_grad()
+def test_unbounded_c4_full_length_matches_oracle():
+    """configs[3] at its own size: causal differential attention, B 2, H32 /
+    Hkv8, Dh 128, L 8192, bf16, q_noise = q R with a random orthogonal R per
+    head, lambda ~ U(0.1, 0.9) (reference baseline.py:95-147 through the
+    diff_flash_attn seam), against the oracle computed in blocks of 512
+    query rows, each against its visible keys (lower-right causal = the
+    square causal mask row by row)."""
+    _need_gpu()
+    import coda_gqa_l
+    from coda_oracle import ops
+    B, H, Hkv, L, Dh, rb = 2, 32, 8, 8192, 128, 512
+    dt = torch.bfloat16
+    print(f"[c4 full length] B{B} H{H}/{Hkv} L{L} Dh{Dh} causal", flush=True)
+    g = torch.Generator().manual_seed(44)
+    q32 = torch.randn(B, H, L, Dh, generator=g)
+    rot = torch.linalg.qr(torch.randn(H, Dh, Dh, generator=g))[0]
+    qn = torch.matmul(q32, rot.unsqueeze(0)).to(dt)
+    q = q32.to(dt)
+    del q32
+    k = torch.randn(B, Hkv, L, Dh, generator=g).to(dt)
+    v = torch.randn(B, Hkv, L, Dh, generator=g).to(dt)
+    lam = (0.1 + 0.8 * torch.rand(B, H, L, 1, generator=g)).to(dt)
+    w = (1.0 + 0.1 * torch.randn(Dh, generator=g)).to(dt)
+    out = coda_gqa_l.diff_flash_attn(q.to(DEV), qn.to(DEV), k.to(DEV), v.to(DEV), lam.to(DEV), rms_weight=w.to(DEV),
+                                     is_causal=True).cpu()
+    torch.set_num_threads(max(1, min(16, len(__import__("os").sched_getaffinity(0)))))
+    worst = 0.0
+    for r0 in range(0, L, rb):
+        r1 = r0 + rb
+        ref = ops.diff_attention(q[:, :, r0:r1], qn[:, :, r0:r1], k[:, :, :r1], v[:, :, :r1], lam[:, :, r0:r1],
+                                 rms_weight=w, is_causal=True)
+        err = (out[:, :, r0:r1].float() - ref.float()).abs().max().item() / ref.float().abs().max().item()
+        worst = max(worst, err)
+    assert worst <= TOL[dt], f"C4 full length: max rel err {worst:.3e} > {TOL[dt]:.1e}"
 
 
 @torch.no_grad()

@@ -149,6 +149,71 @@ def test_two_bounded_llama_adapters_under_eviction_match_the_oracle():
 
 
 @torch.no_grad()
+def test_two_bounded_eve_adapters_under_eviction_match_the_oracle():
+    """A 2-layer residual stack of bounded EveCoDAAdapter layers (Eve-2's
+    layout: multi-head, head_dim 64, fused QKV and output projection with
+    biases, interleaved RoPE, full head norm; reference eve_adapter.py:30-465,
+    343-369) against two OracleLayers with the same weights and biases, fp32:
+    prefill of 3 windows (eviction in every chunk), then 24 decode steps."""
+    _need_gpu()
+    import torch.nn as nn
+    from coda_oracle import OracleLayer
+    from coda_gqa_l.adapters import EveCoDAAdapter
+
+    class EveAttention(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.n_embd, self.n_head, self.head_dim = 256, 4, 64
+            self.c_attn = nn.Linear(256, 768, bias=True)
+            self.c_proj = nn.Linear(256, 256, bias=True)
+
+    kw = dict(window=64, num_landmarks_exact=16, num_landmarks_summary=16)
+    torch.manual_seed(15)
+    ads = []
+    for _ in range(2):
+        eve = EveAttention()
+        with torch.no_grad():
+            for lin in (eve.c_attn, eve.c_proj):
+                lin.bias.normal_(0.0, 0.05)
+        ads.append(EveCoDAAdapter.from_eve_attention(eve, bounded=True, block_size=64, **kw).to(DEV).eval())
+    ors = []
+    for ad in ads:
+        assert ad.coda.num_kv_heads == ad.coda.num_heads == 4 and ad.coda.rope_interleaved
+        assert ad.coda.head_norm_mode == "full" and ad.coda.q_proj.bias is not None
+        o = OracleLayer(embed_dim=256, num_heads=4, num_kv_heads=4, **kw).eval()
+        for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
+            lin = getattr(o, name)
+            setattr(o, name, nn.Linear(lin.in_features, lin.out_features, bias=True))
+        o.load_state_dict({k: v.detach().cpu() for k, v in ad.coda.state_dict().items()})
+        ors.append(o)
+    B = 2
+    torch.manual_seed(16)
+    st_o = [o.init_state(batch_size=B, dtype=torch.float32) for o in ors]
+    for ad, s in zip(ads, st_o):
+        ad.set_state(to_product_state(s, DEV))
+    g = torch.Generator().manual_seed(17)
+    print("[adapters] 2 bounded Eve layers, fp32, B2: prefill 192 tokens (block 64, W64), 24 decode steps",
+          flush=True)
+    x = torch.randn(B, 192, 256, generator=g)
+    hp, ho = x.to(DEV), x.clone()
+    for li, (ad, o) in enumerate(zip(ads, ors)):
+        yp = ad(hp)
+        yo, st_o[li] = o.prefill_chunked(ho, st_o[li], block_size=64)
+        assert_close(yp, yo, torch.float32, f"Eve layer {li} prefill output")
+        _compare_close_states(ad.get_state(), st_o[li], f"Eve layer {li} after prefill")
+        hp, ho = hp + yp, ho + yo
+    for t in range(24):
+        x = torch.randn(B, 1, 256, generator=g)
+        hp, ho = x.to(DEV), x.clone()
+        for li, (ad, o) in enumerate(zip(ads, ors)):
+            yp = ad(hp)
+            yo, st_o[li] = o.step(ho, st_o[li])
+            assert_close(yp, yo, torch.float32, f"Eve layer {li} step {t} output")
+            _compare_close_states(ad.get_state(), st_o[li], f"Eve layer {li} step {t}")
+            hp, ho = hp + yp, ho + yo
+
+
+@torch.no_grad()
 def test_metrics_stay_on_the_device_until_read():
     _need_gpu()
     from coda_oracle import OracleLayer, banks, prims
@@ -194,3 +259,52 @@ def test_metrics_stay_on_the_device_until_read():
     assert st_p.metrics == pytest.approx(st_o.metrics)
     assert st_o.metrics["total_evictions"] > 0 and st_o.metrics["summary_updates"] > 0
     compare_states(st_p, st_o, dtype, m.window, m.Me, "metrics run")
+
+
+@torch.no_grad()
+def test_dynamic_expansion_runs_without_host_syncs_and_matches_the_golden():
+    """The golden case with dynamic bank expansion (min < max capacities,
+    collect_metrics) through the whole module (device projections, fp32):
+    prefill_chunked and every decode step run with each torch synchronising
+    operation made an error, so the active sizes grow on the device
+    (coda_bank_expand) with no host round trip; afterwards outputs,
+    decisions, the grown active sizes and every metric equal the reference's
+    recorded values (attention.py:344-390, memory_banks.py:333-337,
+    418-426, 744-766, 934-946)."""
+    _need_gpu()
+    import json
+    from golden_util import from_np, load
+    from test_parity_gpu import _oracle_case
+    from parity_util import TOL
+    name = "tiny_expand"
+    case, dtype, m, x, xs, _ = _oracle_case(name)
+    gold = load(name)
+    p = product_like(m, case, dtype, DEV)
+    assert p._expandable()
+    torch.manual_seed(case["seed_state"])
+    st = p.init_state(batch_size=case["B"], device=DEV, dtype=dtype, mem_init=case.get("mem_init"))
+    xd, xsd = x.to(DEV), [xt.to(DEV) for xt in xs]
+    p._eta_f32(torch.device(DEV), dtype)  # the parameter's one host round trip, before the checked region
+    torch.cuda.synchronize()
+    print(f"[expansion] {name}: prefill {x.shape[1]} + {len(xs)} steps with synchronising ops made errors",
+          flush=True)
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        y, st = p.prefill_chunked(xd, st, block_size=case["block"])
+        ys = []
+        for xt in xsd:
+            yt, st = p.step(xt, st)
+            ys.append(yt)
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    assert st.__dict__.get("_active_stale"), "the active sizes were expected to grow on the device"
+    assert_close(y, from_np(gold["y_prefill"], dtype), dtype, f"{name} prefill y", TOL[dtype])
+    assert_close(torch.cat(ys, 1), from_np(gold["y_decode"], dtype), dtype, f"{name} decode y", TOL[dtype])
+    assert torch.equal(st.allowed.cpu(), from_np(gold["state_allowed"], torch.bool))
+    assert torch.equal(st.mem_last_exact.cpu(), from_np(gold["state_mem_last_exact"], torch.int64))
+    assert [st.recent_idx, st.recent_filled, st.pos, st.active_exact, st.active_summary] == \
+        list(gold["state_ints"])
+    want = json.loads(bytes(gold["metrics_json"]).decode())
+    assert want["expansions_exact"] > 0 or want["expansions_summary"] > 0
+    assert dict(st.metrics) == pytest.approx(want), f"{name}: metrics differ from the golden"
