@@ -115,7 +115,6 @@ _SIGS = {
     "coda_unit_rows": (_i32, [_i32, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i32, _i32, _vp]),
     "coda_project": (_i32, [ctypes.POINTER(ProjDesc), _vp]),
     "coda_project_workspace_bytes": (_i32, [ctypes.POINTER(ProjDesc), ctypes.POINTER(ctypes.c_size_t)]),
-    "coda_project_epilogue": (_i32, [ctypes.POINTER(ProjDesc), _vp, _i64, _vp]),
     "coda_topk_order_host": (_i32, [_vp, _i32, _i32, _i32, _i32, _vp]),
     # the reference's typed epilogue symbols (void, errors in coda_last_error)
     **{"diff_epilogue_forward_" + t: (None, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp])

@@ -288,20 +288,17 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             tab = cache[key] = (c.contiguous(), s_.contiguous())
         return tab[0][p0:need], tab[1][p0:need]
 
-    def _proj_pack(self, dtype: torch.dtype, kind: str):
-        """Packed [q | k | v | lambda | write] weights and biases, per
-        parameter version.  kind "fused" (coda_project): (n_feat, D) weights
-        with, for half-split RoPE, each k head's rows reordered to the pairs
-        (i, i + Dh/2) on adjacent rows, float32 biases; kind "gemm" (a
-        library GEMM + coda_project_epilogue): natural row order, rows padded
-        to a multiple of 8 (16-byte aligned column blocks of the output),
-        biases in `dtype`."""
+    def _proj_pack(self, dtype: torch.dtype):
+        """Packed [q | k | v | lambda | write] weights (n_feat, D) in `dtype`
+        and float32 biases (zero for a linear without one) for coda_project,
+        per parameter version; with half-split RoPE each k head's rows are
+        reordered to the pairs (i, i + Dh/2) on adjacent rows."""
         lins = (self.q_proj, self.k_proj, self.v_proj, self.lambda_proj, self.write_proj)
         ps = [t for lin in lins for t in (lin.weight, lin.bias) if t is not None]
         tag = tuple((t._version, t.data_ptr(), t.dtype, t.device) for t in ps) + (self.rope_interleaved,
                                                                                  self.write_policy)
         cache = self.__dict__.setdefault("_derived_cache", {})
-        hit = cache.get(("proj", kind, dtype))
+        hit = cache.get(("proj", dtype))
         if hit is not None and hit[0] == tag:
             return hit[1]
         H, Hkv, Dh = self.num_heads, self.num_kv_heads, self.head_dim
@@ -309,7 +306,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         with torch.no_grad():
             dev = self.q_proj.weight.device
             wk, bk = self.k_proj.weight, self.k_proj.bias
-            if kind == "fused" and not self.rope_interleaved:
+            if not self.rope_interleaved:
                 half = Dh // 2
                 pair = torch.stack([torch.arange(half), torch.arange(half) + half], 1).reshape(-1)
                 perm = (torch.arange(Hkv)[:, None] * Dh + pair[None]).reshape(-1).to(dev)
@@ -321,16 +318,11 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
                 ws.append(self.write_proj.weight)
                 bt.append(self.write_proj.bias)
             w = torch.cat([t.detach() for t in ws]).to(dtype)
-            bdt = torch.float32 if kind == "fused" else dtype
-            b = torch.cat([t.detach().to(bdt) if t is not None else torch.zeros(wt.shape[0], dtype=bdt, device=dev)
+            b = torch.cat([t.detach().float() if t is not None else torch.zeros(wt.shape[0], device=dev)
                            for t, wt in zip(bt, ws)])
-            pad = (-w.shape[0]) % 8 if kind == "gemm" else 0
-            if pad:
-                w = torch.cat([w, torch.zeros(pad, w.shape[1], dtype=dtype, device=dev)])
-            bpad = (-b.numel()) % (4 if kind == "fused" else 8)
-            b = torch.cat([b, torch.zeros(bpad, dtype=bdt, device=dev)])
+            b = torch.cat([b, torch.zeros((-b.numel()) % 4, device=dev)])
         val = (w.contiguous(), b.contiguous())
-        cache[("proj", kind, dtype)] = (tag, val)
+        cache[("proj", dtype)] = (tag, val)
         return val
 
     def _proj_desc(self, x: torch.Tensor, M: int, L: int, cos: torch.Tensor, sin: torch.Tensor):
@@ -354,11 +346,11 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         592-608).  fused (decode-shaped input, _fused_front_ok): one launch of
         the hand-written projection kernel with its RoPE and sigmoid
         epilogues (coda_project), outputs in the torch path's layouts.
-        Otherwise the torch linears and the RoPE kernel.  The fused path for
-        many token rows (a library GEMM over the packed weights, the epilogue
+        Otherwise the torch linears and the RoPE kernel.  A fused form for
+        many token rows (a library GEMM over the packed weights, an epilogue
         kernel in place, q / k / v / lambda as strided views of its output)
-        is switched off: a full-size prefill with it faulted the GPU once and
-        no cause has been shown yet."""
+        faulted the GPU once in a full-size prefill, with no cause shown; it
+        was removed, and prefill keeps the torch linears."""
         B, L, D = x.shape
         H, Hkv, Dh = self.num_heads, self.num_kv_heads, self.head_dim
         Fq, Fk = H * Dh, Hkv * Dh
@@ -366,15 +358,16 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         if fused:
             if not self._fused_front_ok(x):
                 raise NotImplementedError(
-                    "the fused projection front end serves bf16 inputs of at most 64 token rows; its many-row form "
-                    "(coda_project_epilogue over a library GEMM) is switched off: a full-size run with it on the "
-                    "layer's path faulted the GPU and no cause has been shown yet")
+                    "the fused projection front end serves bf16 inputs of at most 64 token rows (decode); many "
+                    "rows take the torch linears: a many-row fused form (an in-place epilogue over a library GEMM, "
+                    "q / k / v / lambda as strided views of its output) faulted the GPU in a full-size run with no "
+                    "cause shown, and was removed")
             cos, sin = self._rope_rows(p0, L, x.device, x.dtype)
             d = self._proj_desc(x, M, L, cos, sin)
             g = torch.empty((B, L), dtype=torch.float32, device=x.device)
             d.g = g.data_ptr()
             xs = x if (x.is_contiguous() and x.data_ptr() % 16 == 0) else x.contiguous()
-            w, b = self._proj_pack(x.dtype, "fused")
+            w, b = self._proj_pack(x.dtype)
             q = torch.empty((B, L, Fq), dtype=x.dtype, device=x.device)
             k = torch.empty((B, L, Hkv, Dh), dtype=x.dtype, device=x.device)
             v = torch.empty((B, L, Fk), dtype=x.dtype, device=x.device)
@@ -485,8 +478,13 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             self._write_one(state, k_new=k_new, v_new=v_new, g_new=self._write_gate(x))
 
         if attend and include_current_in_attention and write_cache:
-            # the raw k projection: the step ropes it with the query's tables
             self._check_state(state)
+            if self._fused_front_ok(x):
+                # one launch for q / k (roped) / v / lambda / gate
+                q, k_new, v_new, g, lam, cos, sin = self._front(x, q_pos, fused=True)
+                heads = self.decode_step_core(q, k_new, v_new, g.reshape(B), lam, state, cos, sin, k_roped=True)
+                return self.o_proj(heads.view(B, 1, self.num_heads * self.head_dim)), state
+            # the raw k projection: the step ropes it with the query's tables
             cos, sin = self.rope(seq_len=1, offset=q_pos, device=x.device, dtype=x.dtype)
             k_raw, v_new = self._project_kv_raw(x)
             heads = self.decode_step_core(self._project_q(x), k_raw, v_new, self._write_gate(x).reshape(B),

@@ -171,40 +171,6 @@ __global__ __launch_bounds__(64 * WF * WT) void proj_gemm_bf16(const coda_proj_d
     for (int m = m0 + t; m < min(d.M, m0 + MTT); m += NT) d.g[m] = 1.f;
 }
 
-// Epilogue alone, for a GEMM output y (M rows, row stride y_sm) holding
-// bf16(x W^T + b) with W the packed weights in their natural row order:
-// k columns roped in place (pairs (2i, 2i+1) or (i, i + Dh/2) of a head),
-// lambda columns through the sigmoid in place, the gate as float32.  One
-// thread per (row, k pair | lambda | gate).
-__global__ __launch_bounds__(256) void proj_epilogue_bf16(const coda_proj_desc d, bf16_t* __restrict__ y,
-                                                          int64_t y_sm) {
-  using E = Elt<bf16_t>;
-  const int Fq = d.H * d.Dh, Fk = d.Hkv * d.Dh, half = d.Dh / 2;
-  const int n_pairs = Fk / 2, per_row = n_pairs + d.H + 1;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)d.M * per_row) return;
-  const int m = (int)(i / per_row), u = (int)(i % per_row);
-  bf16_t* row = y + (int64_t)m * y_sm;
-  if (u < n_pairs) {
-    const int hk = u / half, p = u % half;
-    bf16_t* kh = row + Fq + (int64_t)hk * d.Dh;
-    const bool inter = d.rope_interleaved != 0;
-    const int c0 = inter ? 2 * p : p, c1 = inter ? 2 * p + 1 : p + half;
-    const int prow = m % d.L;
-    const float cc = E::ld(((const bf16_t*)d.rope_cos)[(int64_t)prow * half + p]);
-    const float ss = E::ld(((const bf16_t*)d.rope_sin)[(int64_t)prow * half + p]);
-    float r0, r1;
-    rope_pair_t<bf16_t>(E::ld(kh[c0]), E::ld(kh[c1]), cc, ss, inter, r0, r1);
-    kh[c0] = E::st(r0);
-    kh[c1] = E::st(r1);
-  } else if (u < n_pairs + d.H) {
-    bf16_t* l = row + Fq + 2 * Fk + (u - n_pairs);
-    *l = E::st(proj_sigmoid(E::ld(*l)));
-  } else {
-    d.g[m] = d.gate ? E::rnd(proj_sigmoid(E::ld(row[Fq + 2 * Fk + d.H]))) : 1.f;
-  }
-}
-
 // Few token rows (M <= 64): the weights are the traffic, so every load of
 // a workgroup is issued at once.  Workgroup (tile, ks) takes 128 features x
 // all rows over k in [512 ks, 512 ks + 512): wave w's 16 weight rows go
@@ -341,8 +307,10 @@ using namespace coda;
 extern "C" int coda_project(const coda_proj_desc* d, void* stream) {
   CODA_REQUIRE(d != nullptr, "coda_project: null descriptor");
   CODA_REQUIRE(d->dtype == CODA_BF16, "coda_project: bf16 only");
-  CODA_REQUIRE(d->M >= 0 && d->D > 0 && d->D % kProjKT == 0, "coda_project: D=%d must be a positive multiple of %d",
-               d->D, kProjKT);
+  CODA_REQUIRE(d->M >= 0 && d->M <= 64, "coda_project: %d token rows; the front end serves decode-shaped inputs "
+               "(at most 64 rows), many rows are library GEMMs", d->M);
+  CODA_REQUIRE(d->D > 0 && d->D % kProjKT == 0, "coda_project: D=%d must be a positive multiple of %d", d->D,
+               kProjKT);
   CODA_REQUIRE(d->H > 0 && d->Hkv > 0 && d->Dh > 0 && d->Dh % 4 == 0 && d->L > 0,
                "coda_project: bad sizes H=%d Hkv=%d Dh=%d L=%d", d->H, d->Hkv, d->Dh, d->L);
   CODA_REQUIRE(d->x && d->w && d->bias && d->rope_cos && d->rope_sin && d->q && d->k && d->v && d->lam && d->g,
@@ -356,9 +324,9 @@ extern "C" int coda_project(const coda_proj_desc* d, void* stream) {
   if (d->M == 0) return CODA_OK;
   const int n_feat = d->H * d->Dh + 2 * d->Hkv * d->Dh + d->H + (d->gate ? 1 : 0);
   hipStream_t st = (hipStream_t)stream;
-  // few token rows (decode): every load of a workgroup at once, K split in
-  // 512-wide ranges; many rows: 128 x 128 tiles
-  if (d->M <= 64 && d->D % kDecKR == 0) {
+  // D a multiple of 512: every load of a workgroup at once, K split in
+  // 512-wide ranges; else 64 x 64 tiles over K
+  if (d->D % kDecKR == 0) {
     const int KS = d->D / kDecKR, tiles = (n_feat + 127) / 128;
     float* part = nullptr;
     unsigned long long* cnt = nullptr;
@@ -376,8 +344,7 @@ extern "C" int coda_project(const coda_proj_desc* d, void* stream) {
                        KS > 1 ? proj_epoch() : 0ull);
     return check_launch("proj_decode_bf16");
   }
-  if (d->M <= 64) return launch_proj<64, 64, 4, 1>(d, n_feat, st);
-  return launch_proj<128, 128, 2, 4>(d, n_feat, st);
+  return launch_proj<64, 64, 4, 1>(d, n_feat, st);
 }
 
 extern "C" int coda_project_workspace_bytes(const coda_proj_desc* d, size_t* bytes) {
@@ -385,17 +352,4 @@ extern "C" int coda_project_workspace_bytes(const coda_proj_desc* d, size_t* byt
   const int n_feat = d->H * d->Dh + 2 * d->Hkv * d->Dh + d->H + (d->gate ? 1 : 0);
   *bytes = (d->M <= 64 && d->D % 512 == 0 && d->D > 512) ? proj_ws_bytes(n_feat, d->D) : 0;
   return CODA_OK;
-}
-
-extern "C" int coda_project_epilogue(const coda_proj_desc* d, void* y, int64_t y_sm, void* stream) {
-  CODA_REQUIRE(d != nullptr && y != nullptr, "coda_project_epilogue: null pointer");
-  CODA_REQUIRE(d->dtype == CODA_BF16, "coda_project_epilogue: bf16 only");
-  CODA_REQUIRE(d->M >= 0 && d->H > 0 && d->Hkv > 0 && d->Dh > 0 && d->Dh % 2 == 0 && d->L > 0,
-               "coda_project_epilogue: bad sizes");
-  CODA_REQUIRE(d->rope_cos && d->rope_sin && d->g, "coda_project_epilogue: pointer missing");
-  const int64_t total = (int64_t)d->M * (d->Hkv * d->Dh / 2 + d->H + 1);
-  if (total == 0) return CODA_OK;
-  hipLaunchKernelGGL(proj_epilogue_bf16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, *d,
-                     (bf16_t*)y, y_sm);
-  return check_launch("proj_epilogue_bf16");
 }

@@ -76,10 +76,9 @@ int coda_device_count(void);
  *   g (M) float32   sigmoid(bf16(x Wg^T + bg)) in bf16; 1 when gate == 0
  * bias (n_feat) float32, 16-byte aligned, in the weights' row order (zero
  * for a linear without bias).
- * Replaces: the projections of CoDAGQALandmarkPerf2.prefill_chunked /
- *   step / attend_step (src/coda_gqa_l/attention.py:396-410, 476-547,
- *   592-608): q_proj, k_proj, v_proj, lambda_proj + sigmoid, write_proj +
- *   sigmoid, and the RoPE of k.
+ * Replaces: the projections of CoDAGQALandmarkPerf2.step
+ *   (src/coda_gqa_l/attention.py:396-410, 516-547): q_proj, k_proj,
+ *   v_proj, lambda_proj + sigmoid, write_proj + sigmoid, and the RoPE of k.
  * ---------------------------------------------------------------------- */
 typedef struct {
   int dtype;               /* CODA_BF16 */
@@ -107,26 +106,19 @@ typedef struct {
   size_t workspace_bytes;
 } coda_proj_desc;
 
-/* Few token rows (M <= 64, D a multiple of 512): the K range is split over
- * 8 workgroups per 64-feature tile, whose fp32 partials the last to finish
- * sums in split order (deterministic); the partials and the tiles' counters
- * (epoch-tagged, so no clearing) live in the workspace.  Calls that share a
- * workspace must not overlap. */
+/* Decode-shaped inputs only: M <= 64 token rows (more rows: CODA_EINVAL;
+ * the layer's prefill projections are library GEMMs).  With D a multiple of
+ * 512 the K range is split over D / 512 workgroups per 128-feature tile,
+ * whose fp32 partials the last to finish sums in split order
+ * (deterministic); the partials and the tiles' counters (epoch-tagged, so no
+ * clearing) live in the workspace.  Calls that share a workspace must not
+ * overlap.  Other D (a multiple of 64): 64 x 64 tiles over all of K. */
 int coda_project(const coda_proj_desc* d, void* stream);
 
 /* Workspace bytes coda_project needs for this descriptor's M, sizes and
  * gate (0 when it needs none). */
 int coda_project_workspace_bytes(const coda_proj_desc* d, size_t* bytes);
 
-/* The epilogues alone, for many token rows where a library GEMM computes
- * y = bf16(x W^T + b) (M rows, row stride y_sm elements) with W the packed
- * weights in their natural row order: in place, RoPE of the k columns
- * (tables at row m % L) and the sigmoid of the lambda columns; g (M)
- * float32 = sigmoid of the write column in bf16 (1 when gate == 0).  Uses
- * M, L, H, Hkv, Dh, rope_*, gate and g of the descriptor.
- * Replaces: the RoPE of k and the sigmoids of prefill_chunked
- *   (src/coda_gqa_l/attention.py:592-608). */
-int coda_project_epilogue(const coda_proj_desc* d, void* y, int64_t y_sm, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused differential attention + epilogue.

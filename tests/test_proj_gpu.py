@@ -1,8 +1,10 @@
-"""The projection front end (coda_project: one MFMA GEMM over the packed
-q / k / v / lambda / write-gate weights with the RoPE and sigmoid
-epilogues), against a torch float32 reference of the same ops on the
-device and against the CPU oracle's project() + RoPE (reference
-attention.py:396-410, 592-608), within the bf16 tolerance."""
+"""The decode-shaped projection front end (coda_project: one MFMA GEMM over
+the packed q / k / v / lambda / write-gate weights with the RoPE and sigmoid
+epilogues, at most 64 token rows), against a torch float32 reference of the
+same ops on the device and against the CPU oracle's project() + RoPE
+(reference attention.py:396-410, 516-547), within the bf16 tolerance; the
+layer's step() takes it, and the step's state and heads equal those of the
+torch-projection path up to GEMM rounding."""
 
 from __future__ import annotations
 
@@ -11,9 +13,7 @@ import torch
 
 from parity_util import assert_close
 
-pytestmark = [pytest.mark.gpu, pytest.mark.skip(
-    reason="fused projection front end off: a full-size bench run with it on the layer path faulted the GPU; "
-           "cause not found yet, so its kernels stay off the GPU")]
+pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
@@ -26,10 +26,10 @@ def _need_gpu():
 SHAPES = {
     "7b_decode_b64": (4096, 32, 8, 64, 1, True, "gated", False),
     "7b_decode_b1": (4096, 32, 8, 1, 1, True, "gated", False),
-    "7b_prefill_b2": (4096, 32, 8, 2, 384, True, "gated", False),
-    "c1_prefill_half_split_bias": (512, 8, 2, 3, 200, False, "gated", True),
-    "mha_no_gate": (256, 4, 4, 5, 70, True, "none", False),
+    "c1_decode_b3_half_split_bias": (512, 8, 2, 3, 1, False, "gated", True),
+    "mha_no_gate_b5": (256, 4, 4, 5, 1, True, "none", False),
     "70b_decode_b8": (8192, 64, 8, 8, 1, True, "gated", False),
+    "7b_two_tokens_b32": (4096, 32, 8, 32, 2, True, "gated", False),
 }
 
 
@@ -80,7 +80,7 @@ def test_front_end_matches_float32_reference(name):
     g_ = torch.Generator(device=DEV).manual_seed(1)
     x = torch.randn(B, L, D, generator=g_, device=DEV, dtype=torch.bfloat16)
     p0 = 37
-    got = m._front(x, p0)
+    got = m._front(x, p0, fused=True)
     ref = _reference(m, x, p0)
     torch.cuda.synchronize()
     for what, a, r in zip(("q", "k", "v", "g", "lam"), got[:5], ref):
@@ -106,9 +106,9 @@ def test_front_end_matches_oracle_project(inter):
         m.write_proj.weight.normal_(0, 0.05)
     p = product_like(m, {"kw": kw}, torch.bfloat16, DEV)
     g = torch.Generator().manual_seed(4)
-    x = torch.randn(2, 300, 512, generator=g).to(torch.bfloat16)
+    x = torch.randn(6, 1, 512, generator=g).to(torch.bfloat16)
     q, k, v, gate, lam = m.project(x)
-    got = p._front(x.to(DEV), 11)
+    got = p._front(x.to(DEV), 11, fused=True)
     # k roped with the product's own tables: a bf16 layer takes positions
     # and angles in bf16 (the buffer's dtype, as the reference), and torch's
     # device and CPU outer products round a few large angles differently
