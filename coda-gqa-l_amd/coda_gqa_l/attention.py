@@ -478,6 +478,9 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             self._write_one(state, k_new=k_new, v_new=v_new, g_new=self._write_gate(x))
 
         if attend and include_current_in_attention and write_cache:
+            y = self._step_fast(x, state)
+            if y is not None:
+                return y, state
             self._check_state(state)
             if self._fused_front_ok(x):
                 # one launch for q / k (roped) / v / lambda / gate
@@ -494,6 +497,129 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         if write_cache:
             write()
         return y, state
+
+    def _step_fast(self, x: torch.Tensor, st: CoDAGQALandmarkStatePerf2) -> Optional[torch.Tensor]:
+        """A steady-state decode step (full ring, fixed bank sizes, no
+        metrics or traces, bf16 decode-shaped input) from descriptors and
+        buffers cached per state: per token the host sets the input and
+        RoPE-row pointers, makes two library calls (coda_project, then
+        coda_decode_step on its outputs) and the o_proj GEMM.  Returns None
+        when the general path must run; the cache is rebuilt whenever a
+        parameter, the state's tensors (object, storage or in-place version)
+        or the batch changes."""
+        if not self._fused_front_ok(x) or st.metrics is not None or st.recent_filled < self.window or \
+                self._expandable() or (self.Me == 0 and self.Ms == 0) or self._tracing():
+            return None
+        fp = self.__dict__.get("_fast")
+        ts = (st.k_buf, st.v_buf, st.allowed, st.g_recent, st.mem_last_exact, st._exact_v_norm, st._sum_lf_k_norm)
+        vers = tuple(-1 if t is None else t._version for t in ts)
+        pvers = self._param_key()
+        B = x.shape[0]
+        if fp is None or fp["st"] is not st or fp["vers"] != vers or fp["pvers"] != pvers or fp["B"] != B or \
+                fp["ptrs"] != tuple(-1 if t is None else t.data_ptr() for t in ts) or fp["dev"] != x.device:
+            fp = self._build_step_fast(x, st, ts, vers, pvers)
+            if fp is None:
+                return None
+        if not (x.is_contiguous() and x.data_ptr() % 16 == 0):
+            x = x.contiguous()
+        pos = int(st.pos)
+        cos_t, sin_t = fp["tab"]
+        if pos >= cos_t.shape[0]:
+            cos_t, sin_t = self._rope_rows(0, pos + 1, x.device, x.dtype)
+            fp["tab"] = (cos_t, sin_t)
+        row = fp["row_bytes"] * pos
+        d, a = fp["proj"], fp["attn"]
+        d.x = x.data_ptr()
+        d.rope_cos = a.rope_cos = cos_t.data_ptr() + row
+        d.rope_sin = a.rope_sin = sin_t.data_ptr() + row
+        stream = _hip.stream_of(x)
+        _hip.check(fp["project"](fp["proj_ref"], stream))
+        routed = fp["routed"]
+        routed.value = 1 if fp["record_pos"] == pos else 0
+        j = int(st.recent_idx)
+        _hip.check(fp["step"](fp["bank_ref"], fp["attn_ref"], fp["k_ptr"], fp["v_ptr"], fp["k_sb"], fp["k_sh"],
+                              fp["g_ptr"], j, int(st.recent_filled), pos, fp["ws_ptr"], fp["ws_bytes"],
+                              fp["routed_ref"], stream))
+        st.recent_idx = 0 if j + 1 == self.window else j + 1
+        st.pos = pos + 1
+        fp["record_pos"] = pos + 1 if routed.value else -1
+        # the general path's carried-record tag no longer matches this state
+        self.__dict__["_route_tag"] = None
+        return self.o_proj(fp["heads_flat"])
+
+    def _param_key(self) -> tuple:
+        """Identity and in-place version of every parameter of the layer and
+        of its (leaf) submodules, without the recursive module walk."""
+        out = []
+        for p in self._parameters.values():
+            if p is not None:
+                out += (id(p), p._version)
+        for mod in self._modules.values():
+            for p in mod._parameters.values():
+                if p is not None:
+                    out += (id(p), p._version)
+        return tuple(out)
+
+    def _build_step_fast(self, x, st, ts, vers, pvers):
+        """Descriptors and persistent buffers of _step_fast (see there)."""
+        self.__dict__["_fast"] = None
+        self._check_state(st)
+        ts = (st.k_buf, st.v_buf, st.allowed, st.g_recent, st.mem_last_exact, st._exact_v_norm, st._sum_lf_k_norm)
+        vers = tuple(-1 if t is None else t._version for t in ts)
+        B, L, D = x.shape
+        H, Hkv, Dh = self.num_heads, self.num_kv_heads, self.head_dim
+        dev, dt = x.device, x.dtype
+        if st.k_buf.dtype != dt:
+            return None
+        Fq, Fk = H * Dh, Hkv * Dh
+        q = torch.empty((B, 1, Fq), dtype=dt, device=dev)
+        k = torch.empty((B, 1, Hkv, Dh), dtype=dt, device=dev)
+        v = torch.empty((B, 1, Fk), dtype=dt, device=dev)
+        lam = torch.empty((B, 1, H), dtype=dt, device=dev)
+        g = torch.empty((B, 1), dtype=torch.float32, device=dev)
+        heads = torch.empty((B, 1, H, Dh), dtype=dt, device=dev)
+        pos = int(st.pos)
+        cos_t, sin_t = self._rope_rows(0, pos + 1, dev, dt)
+        cos_t, sin_t = self.__dict__["_rope_cache"][(torch.device(dev), dt)]
+        d = self._proj_desc(x, B, 1, cos_t, sin_t)
+        w, b = self._proj_pack(dt)
+        d.x_sm, d.w, d.bias = D, w.data_ptr(), b.data_ptr()
+        d.q, d.q_sm, d.k, d.k_sm, d.v, d.v_sm = q.data_ptr(), Fq, k.data_ptr(), Fk, v.data_ptr(), Fk
+        d.lam, d.lam_sm, d.g = lam.data_ptr(), H, g.data_ptr()
+        nb = ctypes.c_size_t(0)
+        _hip.check(_hip.lib().coda_project_workspace_bytes(d, nb))
+        pws = torch.empty(max(nb.value, 16), dtype=torch.uint8, device=dev) if nb.value else None
+        d.workspace, d.workspace_bytes = _hip.ptr(pws), nb.value
+        qv = q.view(B, 1, H, Dh).permute(0, 2, 1, 3)
+        lamv = lam.permute(0, 2, 1)
+        ct, sn = self._theta_tables(dt)
+        a, keep = ops.attention_desc(
+            q=qv, rope_cos=cos_t[pos:pos + 1], rope_sin=sin_t[pos:pos + 1], rope_interleaved=self.rope_interleaved,
+            theta_cos=ct, theta_sin=sn, k_prefix=st.k_buf, v_prefix=st.v_buf,
+            allowed=st.allowed if self.mask_unused_memory else None, k_block=None, v_block=None, lam=lamv,
+            rms_weight=self._rms_weight(dt), eps=self._eps, out=heads.permute(0, 2, 1, 3))
+        eta = self._eta_f32(dev, st.k_buf.dtype) if self.Ms > 0 else None
+        bank = self._bank_desc(st, eta, None, None)
+        nb = ctypes.c_size_t(0)
+        _hip.check(_hip.lib().coda_decode_step_workspace_bytes(bank, a, nb))
+        ws = self._route_workspace(dev, nb.value)
+        # a record the general path left for this very state and position
+        routed_pos = pos if self.__dict__.get("_route_tag") == self._route_key(st, ws) else -1
+        L_ = _hip.lib()
+        routed = ctypes.c_int(0)
+
+        fp = {"st": st, "vers": vers, "pvers": pvers, "B": B, "dev": dev,
+              "ptrs": tuple(-1 if t is None else t.data_ptr() for t in ts),
+              "tab": (cos_t, sin_t), "row_bytes": (Dh // 2) * cos_t.element_size(),
+              "proj": d, "proj_ref": ctypes.byref(d), "attn": a, "attn_ref": ctypes.byref(a),
+              "bank": bank, "bank_ref": ctypes.byref(bank),
+              "keep": (keep, q, k, v, lam, g, heads, w, b, pws, ws, ct, sn, eta, self._rms_weight(dt)),
+              "k_ptr": k.data_ptr(), "v_ptr": v.data_ptr(), "k_sb": Fk, "k_sh": Dh, "g_ptr": g.data_ptr(),
+              "ws_ptr": _hip.ptr(ws), "ws_bytes": nb.value, "routed": routed, "routed_ref": ctypes.byref(routed),
+              "record_pos": routed_pos, "project": L_.coda_project, "step": L_.coda_decode_step,
+              "heads_flat": heads.view(B, 1, H * Dh)}
+        self.__dict__["_fast"] = fp
+        return fp
 
     # ------------------------------------------------------------ prefill
     def prefill_core(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, lam: torch.Tensor,

@@ -13,8 +13,6 @@
 // is packed with each pair (i, i + Dh/2) on adjacent weight rows).
 #include "common.h"
 
-#include <atomic>
-#include <chrono>
 
 namespace coda {
 
@@ -171,125 +169,115 @@ __global__ __launch_bounds__(64 * WF * WT) void proj_gemm_bf16(const coda_proj_d
     for (int m = m0 + t; m < min(d.M, m0 + MTT); m += NT) d.g[m] = 1.f;
 }
 
-// Few token rows (M <= 64): the weights are the traffic, so every load of
-// a workgroup is issued at once.  Workgroup (tile, ks) takes 128 features x
-// all rows over k in [512 ks, 512 ks + 512): wave w's 16 weight rows go
-// straight from global memory into its 16 A fragments (16 bytes per lane
-// and k-step), the 64 token rows once into LDS (B fragments, shared by the
-// 8 waves).  With KS = D / 512 > 1 each workgroup stores its fp32 partial
-// tile (agent-scope atomic stores, the threads adjacent: one 512-byte run
-// per wave and value pair), and the last of the KS workgroups of a tile to
-// arrive (a counter per tile tagged with the launch's epoch, so it needs no
-// clearing) sums the KS partials in split order and runs the epilogue:
-// the result does not depend on arrival order.
-static constexpr int kDecKR = 512;                 // k per workgroup
-static constexpr int kDecPitch = kDecKR + 8;       // LDS row pitch (bf16)
-__global__ __launch_bounds__(512) void proj_decode_bf16(const coda_proj_desc d, int n_feat, float* part,
-                                                        unsigned long long* cnt, unsigned long long epoch) {
-  using E = Elt<bf16_t>;
-  constexpr int NT = 512, NS = kDecKR / 32, BT = 4, NP = BT * 2;
-  extern __shared__ __attribute__((aligned(16))) bf16_t xs_lds[];  // [64][kDecPitch]
-  __shared__ int last_s;
+// Few token rows (M <= 64): the weights are the traffic.  A workgroup owns
+// 16 features over all of K: wave w of 8 takes k in [w K/8, (w + 1) K/8)
+// and streams its 16 weight rows and the token rows of that range straight
+// from memory into MFMA fragments (16 bytes per lane and k-step, LA steps
+// ahead), one 16 x 16 accumulator per 16 tokens; the 8 partials meet in LDS
+// and are summed in wave order (deterministic), then the epilogue runs on
+// 64 MT lanes.  No workspace, no cross-workgroup exchange.  Weights cross
+// HBM once; the token rows (at most 512 KiB) are read by every workgroup
+// from L2.
+static constexpr int kRowsLA = 4;  // k-steps of loads in flight ahead of the products
+// RB row blocks of 16 features per wave: the token rows a wave loads feed
+// RB products each
+template <int NS, int MT, int RB>
+__device__ __forceinline__ void rows_partial(const bf16_t* __restrict__ W, int64_t w_sm, int n_feat,
+                                             const bf16_t* __restrict__ X, int64_t x_sm, int M, int f0,
+                                             pf32x4* part) {
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6, r16 = lane & 15, kq = lane >> 4;
-  const int KS = gridDim.y, ks = blockIdx.y;
-  const int f0 = blockIdx.x * 128;
-  const int k0 = ks * kDecKR;
-  const bf16_t* W = (const bf16_t*)d.w;
-  const bf16_t* X = (const bf16_t*)d.x;
-  // A fragments: weight row f0 + 16 wv + r16, k0 + 32 s + 8 kq
-  pbf16x8_t a[NS];
-  {
-    const bf16_t* wr = W + (int64_t)min(f0 + 16 * wv + r16, n_feat - 1) * d.D + k0 + 8 * kq;
+  const int k0 = wv * (NS * 32) + 8 * kq;
+  const bf16_t* wr[RB];
 #pragma unroll
-    for (int s2 = 0; s2 < NS; ++s2) a[s2] = *reinterpret_cast<const pbf16x8_t*>(wr + 32 * s2);
+  for (int i = 0; i < RB; ++i) wr[i] = W + (int64_t)min(f0 + 16 * i + r16, n_feat - 1) * w_sm + k0;
+  const bf16_t* xr[MT];
+#pragma unroll
+  for (int j = 0; j < MT; ++j) xr[j] = X + (int64_t)min(16 * j + r16, M - 1) * x_sm + k0;
+  pbf16x8_t a[kRowsLA][RB], b[kRowsLA][MT];
+  auto load = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) a[s % kRowsLA][i] = *reinterpret_cast<const pbf16x8_t*>(wr[i] + 32 * s);
+#pragma unroll
+    for (int j = 0; j < MT; ++j) b[s % kRowsLA][j] = *reinterpret_cast<const pbf16x8_t*>(xr[j] + 32 * s);
+  };
+  pf32x4 acc[RB][MT];
+#pragma unroll
+  for (int i = 0; i < RB; ++i)
+#pragma unroll
+    for (int j = 0; j < MT; ++j) acc[i][j] = pf32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < kRowsLA && s < NS; ++s) load(s);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    pbf16x8_t as[RB], bs[MT];
+#pragma unroll
+    for (int i = 0; i < RB; ++i) as[i] = a[s % kRowsLA][i];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) bs[j] = b[s % kRowsLA][j];
+    if (s + kRowsLA < NS) load(s + kRowsLA);
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < MT; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as[i], bs[j], acc[i][j], 0, 0, 0);
   }
-  // token rows [0, 64) x k [k0, k0 + 512) into LDS, 8 pieces per thread
-  {
-    uint4 xv[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = t + u * NT, r = i >> 6, c = i & 63;
-      xv[u] = *reinterpret_cast<const uint4*>(X + (int64_t)min(r, d.M - 1) * d.x_sm + k0 + 8 * c);
-    }
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = t + u * NT, r = i >> 6, c = i & 63;
-      *reinterpret_cast<uint4*>(xs_lds + r * kDecPitch + 8 * c) = xv[u];
-    }
-  }
+    for (int j = 0; j < MT; ++j) part[((wv * RB + i) * MT + j) * 64 + lane] = acc[i][j];
   __syncthreads();
-  pf32x4 acc[BT];
+}
+// Sum of the 8 waves' partials for (row block i, token block j, lane l) =
+// item 64 (MT i + j) + l: features f0 + 16 i + 4 (l / 16) .. + 3 of token
+// 16 j + l % 16
+template <int MT, int RB>
+__device__ __forceinline__ pf32x4 rows_sum(const pf32x4* part, int item) {
+  const int ij = item >> 6, l = item & 63;
+  pf32x4 sum = part[ij * 64 + l];
 #pragma unroll
-  for (int j = 0; j < BT; ++j) acc[j] = pf32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s2 = 0; s2 < NS; ++s2) {
-    pbf16x8_t b[BT];
-#pragma unroll
-    for (int j = 0; j < BT; ++j)
-      b[j] = *reinterpret_cast<const pbf16x8_t*>(xs_lds + (16 * j + r16) * kDecPitch + 32 * s2 + 8 * kq);
-#pragma unroll
-    for (int j = 0; j < BT; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s2], b[j], acc[j], 0, 0, 0);
-  }
-  if (!d.gate && blockIdx.x == 0 && ks == 0 && t < d.M) d.g[t] = 1.f;
-  if (KS > 1) {
-    const int64_t tile = blockIdx.x;
-    unsigned long long* pw = reinterpret_cast<unsigned long long*>(part);
-#pragma unroll
-    for (int j = 0; j < BT; ++j)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const pf32x2 pr = {acc[j][2 * h], acc[j][2 * h + 1]};
-        __hip_atomic_store(pw + ((tile * KS + ks) * NP + j * 2 + h) * NT + t,
-                           __builtin_bit_cast(unsigned long long, pr), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t == 0) {
-      unsigned long long* w = cnt + tile;
-      unsigned long long old = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), nv;
-      for (;;) {
-        nv = (old >> 8) == epoch ? old + 1ull : ((epoch << 8) | 1ull);
-        if (__hip_atomic_compare_exchange_strong(w, &old, nv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT))
-          break;
-      }
-      last_s = (int)(nv & 0xff) == KS;
-    }
-    __syncthreads();
-    if (!last_s) return;
-#pragma unroll
-    for (int j = 0; j < BT; ++j)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const unsigned long long* p0 = pw + ((tile * KS) * NP + j * 2 + h) * NT + t;
-        pf32x2 sum = __builtin_bit_cast(pf32x2, __hip_atomic_load(p0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        for (int q = 1; q < KS; ++q)
-          sum += __builtin_bit_cast(pf32x2, __hip_atomic_load(p0 + (int64_t)q * NP * NT, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT));
-        acc[j][2 * h] = sum[0];
-        acc[j][2 * h + 1] = sum[1];
-      }
-  }
-  // epilogue of features f0 + 16 wv + 4 kq .. + 3, tokens 16 j + r16
-#pragma unroll
-  for (int j = 0; j < BT; ++j) {
-    const int m = 16 * j + r16;
-    if (m < d.M) proj_store4(d, f0 + 16 * wv + 4 * kq, m, acc[j]);
+  for (int w = 1; w < 8; ++w) sum += part[(w * RB * MT + ij) * 64 + l];
+  return sum;
+}
+
+template <int NS, int MT, int RB>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void proj_rows_bf16(
+    const coda_proj_desc d, int n_feat) {
+  __shared__ pf32x4 part[8 * RB * MT * 64];
+  const int f0 = blockIdx.x * 16 * RB;
+  rows_partial<NS, MT, RB>((const bf16_t*)d.w, d.D, n_feat, (const bf16_t*)d.x, d.x_sm, d.M, f0, part);
+  const int t = threadIdx.x;
+  if (!d.gate && blockIdx.x == 0 && t < d.M) d.g[t] = 1.f;
+  for (int item = t; item < 64 * MT * RB; item += 512) {
+    const pf32x4 sum = rows_sum<MT, RB>(part, item);
+    const int i = (item >> 6) / MT, j = (item >> 6) % MT, l = item & 63;
+    const int m = 16 * j + (l & 15), f = f0 + 16 * i + 4 * (l >> 4);
+    if (m < d.M && f < n_feat) proj_store4(d, f, m, sum);
   }
 }
 
-// Workspace of proj_decode_bf16 with KS = D / 512 > 1: the partial tiles
-// and one counter per 128-feature tile.
-static size_t proj_ws_bytes(int n_feat, int D) {
-  const size_t tiles = (size_t)((n_feat + 127) / 128), KS = (size_t)(D / 512);
-  return tiles * KS * 512 * 16 * sizeof(float) + tiles * sizeof(unsigned long long);  // 16 partials per thread
+template <int NS, int RB>
+static int launch_rows_rb(const coda_proj_desc* d, int n_feat, hipStream_t st) {
+  const dim3 grid((n_feat + 16 * RB - 1) / (16 * RB));
+  if (d->M <= 16) hipLaunchKernelGGL((proj_rows_bf16<NS, 1, RB>), grid, dim3(512), 0, st, *d, n_feat);
+  else if (d->M <= 32) hipLaunchKernelGGL((proj_rows_bf16<NS, 2, RB>), grid, dim3(512), 0, st, *d, n_feat);
+  else hipLaunchKernelGGL((proj_rows_bf16<NS, 4, RB>), grid, dim3(512), 0, st, *d, n_feat);
+  return check_launch("proj_rows_bf16");
 }
-static unsigned long long proj_epoch() {
-  static std::atomic<unsigned long long> ep{
-      (unsigned long long)std::chrono::steady_clock::now().time_since_epoch().count() * 0x2545F4914F6CDD1Dull};
-  return ep.fetch_add(1, std::memory_order_relaxed) & ((1ull << 56) - 1);
+// 16 RB features per workgroup: RB 2 up to 16 k-steps per wave (K <= 4096),
+// RB 4 beyond (measured fastest at the 7B and 70B shapes, batch 1 .. 64)
+template <int NS>
+static int launch_rows_ns(const coda_proj_desc* d, int n_feat, hipStream_t st) {
+  return launch_rows_rb<NS, (NS <= 16 ? 2 : 4)>(d, n_feat, st);
 }
-
+static int launch_rows(const coda_proj_desc* d, int n_feat, hipStream_t st) {
+  switch (d->D / 256) {
+    case 2: return launch_rows_ns<2>(d, n_feat, st);
+    case 4: return launch_rows_ns<4>(d, n_feat, st);
+    case 8: return launch_rows_ns<8>(d, n_feat, st);
+    case 16: return launch_rows_ns<16>(d, n_feat, st);
+    case 32: return launch_rows_ns<32>(d, n_feat, st);
+    default: return -1;
+  }
+}
 template <int NTF, int MTT, int WF, int WT>
 static int launch_proj(const coda_proj_desc* d, int n_feat, hipStream_t st) {
   const dim3 grid((n_feat + NTF - 1) / NTF, (d->M + MTT - 1) / MTT);
@@ -324,32 +312,15 @@ extern "C" int coda_project(const coda_proj_desc* d, void* stream) {
   if (d->M == 0) return CODA_OK;
   const int n_feat = d->H * d->Dh + 2 * d->Hkv * d->Dh + d->H + (d->gate ? 1 : 0);
   hipStream_t st = (hipStream_t)stream;
-  // D a multiple of 512: every load of a workgroup at once, K split in
-  // 512-wide ranges; else 64 x 64 tiles over K
-  if (d->D % kDecKR == 0) {
-    const int KS = d->D / kDecKR, tiles = (n_feat + 127) / 128;
-    float* part = nullptr;
-    unsigned long long* cnt = nullptr;
-    if (KS > 1) {
-      const size_t need = proj_ws_bytes(n_feat, d->D);
-      CODA_REQUIRE(d->workspace && d->workspace_bytes >= need && ((uintptr_t)d->workspace % 16) == 0,
-                   "coda_project: workspace %zu < %zu bytes (coda_project_workspace_bytes)", d->workspace_bytes, need);
-      part = (float*)d->workspace;
-      cnt = (unsigned long long*)(part + (size_t)tiles * KS * 512 * 16);
-    }
-    const size_t lds = sizeof(bf16_t) * 64 * kDecPitch;
-    const int rc = lds_limit<proj_decode_bf16>(lds, "coda_project");
-    if (rc) return rc;
-    hipLaunchKernelGGL(proj_decode_bf16, dim3(tiles, KS), dim3(512), lds, st, *d, n_feat, part, cnt,
-                       KS > 1 ? proj_epoch() : 0ull);
-    return check_launch("proj_decode_bf16");
-  }
+  // K 512 .. 8192, a power of two times 256: row tiles over all of K (no
+  // workspace); else 64 x 64 tiles over K
+  if (d->D >= 512 && d->D <= 8192 && d->D % 256 == 0 && ((d->D / 256) & (d->D / 256 - 1)) == 0)
+    return launch_rows(d, n_feat, st);
   return launch_proj<64, 64, 4, 1>(d, n_feat, st);
 }
 
 extern "C" int coda_project_workspace_bytes(const coda_proj_desc* d, size_t* bytes) {
   CODA_REQUIRE(d != nullptr && bytes != nullptr, "coda_project_workspace_bytes: null pointer");
-  const int n_feat = d->H * d->Dh + 2 * d->Hkv * d->Dh + d->H + (d->gate ? 1 : 0);
-  *bytes = (d->M <= 64 && d->D % 512 == 0 && d->D > 512) ? proj_ws_bytes(n_feat, d->D) : 0;
+  *bytes = 0;
   return CODA_OK;
 }

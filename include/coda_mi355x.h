@@ -102,22 +102,22 @@ typedef struct {
   void* lam;
   int64_t lam_sm;
   float* g;
-  void* workspace;         /* coda_project_workspace_bytes; 16-byte aligned, any contents */
+  void* workspace;         /* unused (coda_project_workspace_bytes is 0) */
   size_t workspace_bytes;
 } coda_proj_desc;
 
 /* Decode-shaped inputs only: M <= 64 token rows (more rows: CODA_EINVAL;
- * the layer's prefill projections are library GEMMs).  With D a multiple of
- * 512 the K range is split over D / 512 workgroups per 128-feature tile,
- * whose fp32 partials the last to finish sums in split order
- * (deterministic); the partials and the tiles' counters (epoch-tagged, so no
- * clearing) live in the workspace.  Calls that share a workspace must not
- * overlap.  Other D (a multiple of 64): 64 x 64 tiles over all of K. */
+ * the layer's prefill projections are library GEMMs).  D 512 .. 8192 and a
+ * power of two times 256: each workgroup owns 16 features over all of K,
+ * its 8 waves' K-range partials summed in LDS in wave order
+ * (deterministic).  Other D (a multiple of 64): 64 x 64 tiles over K.  No
+ * workspace. */
 int coda_project(const coda_proj_desc* d, void* stream);
 
-/* Workspace bytes coda_project needs for this descriptor's M, sizes and
- * gate (0 when it needs none). */
+/* Workspace bytes coda_project needs for this descriptor (0: the kernels
+ * keep their partial sums in LDS; kept for callers that size one). */
 int coda_project_workspace_bytes(const coda_proj_desc* d, size_t* bytes);
+
 
 
 /* ------------------------------------------------------------------------

@@ -115,3 +115,47 @@ def test_front_end_matches_oracle_project(inter):
     k = prims.rope(k, got[5].cpu(), got[6].cpu(), inter)
     for what, a, r in zip(("q", "k", "v", "g", "lam"), got[:5], (q, k, v, gate, lam.squeeze(-1))):
         assert_close(a, r, torch.bfloat16, f"oracle project {what}")
+
+
+@torch.no_grad()
+def test_cached_step_equals_general_step():
+    """The layer's cached steady-state step (descriptors and buffers kept
+    per state) and its general step give bit-identical outputs and states
+    over 40 decode tokens at the 7B shape, including tokens after an
+    in-place edit of the state (which must rebuild the cache)."""
+    _need_gpu()
+    import coda_gqa_l
+    from coda_gqa_l.state_io import deep_copy_state
+    print("[cached step] 7B shape B8: 40 steps cached vs general", flush=True)
+    torch.manual_seed(7)
+    m = coda_gqa_l.CoDAGQALandmarkPerf2(embed_dim=4096, num_heads=32, num_kv_heads=8, window=256,
+                                        num_landmarks_exact=64, num_landmarks_summary=64,
+                                        rope_base=1e4).to(DEV, torch.bfloat16).eval()
+    g = torch.Generator(device=DEV).manual_seed(8)
+    B = 8
+    st_a = m.init_state(batch_size=B, device=DEV, dtype=torch.bfloat16)
+    m.prefill_chunked(torch.randn(B, 600, 4096, generator=g, device=DEV, dtype=torch.bfloat16), st_a,
+                      block_size=256, return_outputs=False)
+    st_b = deep_copy_state(st_a)
+    xs = torch.randn(40, B, 1, 4096, generator=g, device=DEV, dtype=torch.bfloat16)
+    ya, yb = [], []
+    for t in range(40):
+        if t == 20:
+            st_a.v_buf[:, :, 300].mul_(0.5)  # an in-place edit through torch
+        ya.append(m.step(xs[t], st_a)[0])
+        assert m.__dict__.get("_fast") is not None, "the cached path did not run"
+    fast = m._step_fast
+    m._step_fast = lambda *args: None
+    try:
+        for t in range(40):
+            if t == 20:
+                st_b.v_buf[:, :, 300].mul_(0.5)
+            yb.append(m.step(xs[t], st_b)[0])
+    finally:
+        m._step_fast = fast
+    torch.cuda.synchronize()
+    for t in range(40):
+        assert torch.equal(ya[t], yb[t]), f"step {t}: outputs differ"
+    for f in ("k_buf", "v_buf", "allowed", "g_recent", "mem_last_exact", "_exact_v_norm", "_sum_lf_k_norm"):
+        assert torch.equal(getattr(st_a, f), getattr(st_b, f)), f"state field {f} differs"
+    assert (st_a.pos, st_a.recent_idx) == (st_b.pos, st_b.recent_idx)
