@@ -21,6 +21,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 _DEFAULT_LIB_PATH = LIB_PATH
 
 CODA_F32, CODA_BF16, CODA_F16 = 0, 1, 2
+CODA_OK, CODA_EUNSUP = 0, 2
 DTYPE_CODE = {torch.float32: CODA_F32, torch.bfloat16: CODA_BF16, torch.float16: CODA_F16}
 NUM_COUNTERS = 8
 (CNT_EXACT_HITS, CNT_EXACT_INSERTS, CNT_EXACT_OVERWRITES, CNT_SUMMARY_UPDATES, CNT_SUMMARY_INSERTS,
@@ -88,6 +89,7 @@ _SIGS = {
     "coda_device_count": (_i32, []),
     "coda_attn_workspace_bytes": (_i32, [ctypes.POINTER(AttnDesc), ctypes.POINTER(ctypes.c_size_t)]),
     "coda_diff_attn_fwd": (_i32, [ctypes.POINTER(AttnDesc), _vp]),
+    "coda_prefill_attn_chunks": (_i32, [ctypes.POINTER(AttnDesc), _i32, _i32, _i32, _i32, _i32, _i64, _i64, _vp]),
     "coda_diff_epilogue_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "coda_diff_sub_only_fwd": (_i32, [_i32, _vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "coda_rope_fwd": (_i32, [_i32, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _vp, _i32, _i32, _i32,
@@ -103,6 +105,11 @@ _SIGS = {
                                _i32, _vp]),
     "coda_block_write": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,
                                 _i32, _i64, _vp, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp]),
+    "coda_block_write_snapshot": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,
+                                         _i32, _i64, _vp, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp]),
+    "coda_block_write_chain": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32,
+                                      _i32, _i32, _i32, _i64, _vp, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp, _vp, _vp,
+                                      _i64, _i64, ctypes.POINTER(ctypes.c_int), _vp]),
     "coda_block_workspace_bytes": (_i32, [ctypes.POINTER(BankDesc), _i32, ctypes.POINTER(ctypes.c_size_t)]),
     "coda_block_write_check": (_i32, [ctypes.POINTER(BankDesc), _i32, _i32]),
     "coda_block_sync_timeouts": (_i32, [ctypes.POINTER(ctypes.c_uint)]),

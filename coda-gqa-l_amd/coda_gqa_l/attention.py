@@ -145,6 +145,14 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             raise ValueError(f"head_norm_mode must be 'full' or 'identity', got {head_norm_mode!r}")
         self.o_proj = nn.Linear(H * Dh, D, bias=False)
         self._eps = float(eps)
+        # prefill_core: run the chunks whose ring window lies in the call as a
+        # bank chain with snapshots and grouped attention launches (False:
+        # chunk by chunk, attention then bank update; the same results up to
+        # the order of the softmax sums)
+        self.pipelined_prefill = True
+        # chunks per attention launch of the pipelined prefill (None: as many
+        # as 256 MiB of bank snapshots hold, at most 1024)
+        self.pipelined_group_chunks: Optional[int] = None
         self._check_bank_sizes()
 
     # ------------------------------------------------------------ state
@@ -657,6 +665,30 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         p0 = int(state.pos)
         t = 0
         c = 0
+        if write_cache and return_heads and self.pipelined_prefill and self._pipelined_ok(q, k, v, state, block_size):
+            # chunks whose ring window lies in this call: the bank chain
+            # leaves per-chunk snapshots, then one attention launch per group
+            c0 = 0 if state.recent_filled == 0 else -(-self.window // block_size)
+            n_chunks = -(-L // block_size)
+            if c0 < n_chunks:
+                while c < c0:
+                    blk = block_size
+                    ops.bounded_attention(
+                        q=q[:, :, t:t + blk], rope_cos=rope_cos[t:t + blk], rope_sin=rope_sin[t:t + blk],
+                        rope_interleaved=self.rope_interleaved, theta_cos=ct, theta_sin=sn, k_prefix=state.k_buf,
+                        v_prefix=state.v_buf, allowed=state.allowed if self.mask_unused_memory else None,
+                        k_block=k[:, :, t:t + blk], v_block=v[:, :, t:t + blk], lam=lam[:, :, t:t + blk],
+                        rms_weight=w, eps=self._eps, out=out[:, t:t + blk].permute(0, 2, 1, 3))
+                    head, filled = self._write_block(
+                        state, k_blk=k[:, :, t:t + blk], v_blk=v[:, :, t:t + blk], g_blk=g[:, t:t + blk],
+                        pos0=p0 + t, ring_head=head, ring_filled=filled, plan_c=plan[c], kmax=kmax, do_e=do_e,
+                        do_s=do_s, workspace=ws, eta=eta)
+                    state.pos = p0 + t + blk
+                    t += blk
+                    c += 1
+                c, t, head, filled = self._prefill_pipelined(
+                    q, k, v, g, lam, rope_cos, rope_sin, state, block_size, out, ct, sn, w, plan, kmax, do_e, do_s,
+                    ws, eta, c, head, filled, p0)
         while t < L:
             blk = min(int(block_size), L - t)
             if return_heads:
@@ -678,6 +710,106 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             self._ring_to_time_order(state, head, filled)
             self._queue_status_check(ws)
         return out
+
+    def _pipelined_ok(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, state: CoDAGQALandmarkStatePerf2,
+                      block_size: int) -> bool:
+        """Whether prefill_core's chunks may run as a bank chain with
+        snapshots followed by one attention launch per group: the conditions
+        of coda_prefill_attn_chunks (bf16, head_dim 64 / 128, G in {1, 2,
+        4, 8}, the MFMA flash path, 31-bit per-lane key offsets) and banks
+        with candidates, so that every chunk's update is one launch."""
+        B, H, L, Dh = q.shape
+        G = H // self.num_kv_heads
+        return (q.dtype == torch.bfloat16 and state.k_buf.dtype == torch.bfloat16 and Dh in (64, 128) and
+                G in (1, 2, 4, 8) and self.Me + self.Ms > 0 and min(int(block_size), L) * G > 8 and
+                k.stride() == v.stride() and k.stride(-1) == 1 and
+                (self.window + int(block_size) + 64) * k.stride(2) < (1 << 30) and
+                (self.Me > 0 and self.exact_candidates_per_block > 0 or
+                 self.Ms > 0 and self.summary_candidates_per_block > 0))
+
+    def _prefill_pipelined(self, q, k, v, g, lam, rope_cos, rope_sin, state, block_size, out, ct, sn, w, plan, kmax,
+                           do_e, do_s, ws, eta, c, head, filled, p0):
+        """Chunks c .. of prefill_core whose ring window lies in this call
+        (attention.py:611-724): per group of chunks, first every chunk's bank
+        update in order, each leaving the bank slots it starts from in a
+        snapshot, then the group's attention in one launch over the call's
+        keys (coda_prefill_attn_chunks).  Falls back to the chunk-by-chunk
+        loop (returning where it stopped) when the one-launch bank update
+        does not run."""
+        B, H, L, Dh = q.shape
+        Hkv, W, S = self.num_kv_heads, self.window, self.Me + self.Ms
+        blk = int(block_size)
+        n_chunks = -(-L // blk)
+        # snapshot buffers of up to 256 MiB (at most 1024 chunks), made once
+        # per shape and kept: calls of any length reuse them
+        per_chunk = 2 * B * Hkv * S * Dh * q.element_size()
+        cap = max(1, min(1024, (256 << 20) // max(per_chunk, 1)))
+        if self.pipelined_group_chunks is not None:
+            cap = max(1, min(cap, int(self.pipelined_group_chunks)))
+        group = min(n_chunks - c, cap)
+        cache = self.__dict__.setdefault("_snap_cache", {})
+        key = (str(q.device), q.dtype, B, Hkv, S, Dh)
+        buf = cache.get(key)
+        if buf is None or buf[0].shape[0] != cap:
+            buf = cache[key] = (torch.empty((cap, B, Hkv, S, Dh), dtype=q.dtype, device=q.device),
+                                torch.empty((cap, B, Hkv, S, Dh), dtype=q.dtype, device=q.device),
+                                torch.empty((cap, B, S), dtype=torch.uint8, device=q.device))
+        sk, sv, sa = buf
+        # chunks that evict run as one chain call when no metrics, flags or
+        # traces are collected per chunk
+        chain = (state.metrics is None and not (self._expandable() and not self.training) and
+                 not self._tracing() and ws is not None)
+        ring = (ctypes.c_int * 2)()
+        while c < n_chunks:
+            ca = c
+            cb = min(n_chunks, ca + group)
+            cc = ca
+            while cc < cb:
+                t = cc * blk
+                n = min(blk, L - t)
+                if chain and filled + n > W:
+                    d = self._bank_desc(state, eta, None, None)
+                    rc = _hip.lib().coda_block_write_chain(
+                        d, k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1), k.stride(2), g.data_ptr(),
+                        g.stride(0), L, blk, cc, cb - cc, head, filled, p0 + t, plan.data_ptr(), kmax,
+                        self.exact_candidates_per_block if do_e else 0,
+                        self.summary_candidates_per_block if do_s else 0, ws.data_ptr(), ws.numel(),
+                        sk[cc - ca].data_ptr(), sv[cc - ca].data_ptr(), sa[cc - ca].data_ptr(), sk[0].numel(),
+                        sa[0].numel(), ring, _hip.stream_of(k))
+                    if rc == _hip.CODA_OK:
+                        head, filled = int(ring[0]), int(ring[1])
+                        state.pos = p0 + min(L, cb * blk)
+                        break
+                    if rc != _hip.CODA_EUNSUP:
+                        _hip.check(rc)
+                    chain = False
+                r = self._write_block(
+                    state, k_blk=k[:, :, t:t + n], v_blk=v[:, :, t:t + n], g_blk=g[:, t:t + n], pos0=p0 + t,
+                    ring_head=head, ring_filled=filled, plan_c=plan[cc], kmax=kmax, do_e=do_e, do_s=do_s,
+                    workspace=ws, eta=eta, snap=(sk[cc - ca], sv[cc - ca], sa[cc - ca]))
+                if r is None:
+                    # the one-launch update does not run here: this group's
+                    # earlier chunks get their attention, the rest run chunk by chunk
+                    if cc > ca:
+                        self._attend_chunks(q, k, v, lam, rope_cos, rope_sin, sk, sv, sa, out, ct, sn, w, ca, cc, blk,
+                                            L)
+                    return cc, t, head, filled
+                head, filled = r
+                state.pos = p0 + t + n
+                cc += 1
+            self._attend_chunks(q, k, v, lam, rope_cos, rope_sin, sk, sv, sa, out, ct, sn, w, ca, cb, blk, L)
+            c = cb
+        return n_chunks, L, head, filled
+
+    def _attend_chunks(self, q, k, v, lam, rope_cos, rope_sin, sk, sv, sa, out, ct, sn, w, ca, cb, blk, L):
+        """The attention of chunks ca .. cb - 1 from their bank snapshots
+        (sk / sv / sa[0 ..]) in one launch."""
+        d, keep = ops.attention_desc(
+            q=q, rope_cos=rope_cos, rope_sin=rope_sin, rope_interleaved=self.rope_interleaved, theta_cos=ct,
+            theta_sin=sn, k_prefix=sk[0], v_prefix=sv[0], allowed=sa[0] if self.mask_unused_memory else None,
+            k_block=k, v_block=v, lam=lam, rms_weight=w, eps=self._eps, out=out.permute(0, 2, 1, 3))
+        _hip.check(_hip.lib().coda_prefill_attn_chunks(d, cb - ca, ca, blk, L, self.window, sk[0].numel(),
+                                                       sa[0].numel(), _hip.stream_of(q)))
 
     def prefill_chunked(self, x_seq: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *, block_size: int = 256,
                         write_cache: bool = True, return_outputs: bool = True

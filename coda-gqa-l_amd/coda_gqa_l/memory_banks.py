@@ -577,11 +577,16 @@ class MemoryBankMixin:
 
     def _write_block(self, st, *, k_blk: torch.Tensor, v_blk: torch.Tensor, g_blk: torch.Tensor, pos0: int,
                      ring_head: int, ring_filled: int, plan_c: torch.Tensor, kmax: int, do_e: bool, do_s: bool,
-                     workspace: Optional[torch.Tensor], eta: Optional[torch.Tensor]):
+                     workspace: Optional[torch.Tensor], eta: Optional[torch.Tensor], snap=None):
         """Evict / update banks / ring write for one chunk (memory_banks.py:438-564).
 
         k_blk, v_blk (B, Hkv, blk, Dh) views; g_blk (B, blk) float32 view.
-        Returns the ring (head, filled) after the chunk.
+        snap: (K, V, visibility bytes) tensors that receive the bank slots
+        as they stand before this chunk's update; the one-launch update
+        writes them (coda_block_write_snapshot), any other chunk copies them
+        first.  Returns the ring (head, filled) after the chunk, or None when
+        snap is given and the one-launch update does not run for this chunk
+        (nothing has run then).
         """
         B, Hkv, blk, Dh = k_blk.shape
         W = self.window
@@ -599,10 +604,22 @@ class MemoryBankMixin:
         if k_blk.stride() != v_blk.stride() or k_blk.stride(-1) != 1:
             v_blk = v_blk.contiguous()
             k_blk = k_blk.contiguous()
-        _hip.check(_hip.lib().coda_block_write(
-            d, k_blk.data_ptr(), v_blk.data_ptr(), k_blk.stride(0), k_blk.stride(1), k_blk.stride(2),
-            g_blk.data_ptr(), g_blk.stride(0), blk, ring_head, ring_filled, int(pos0), _hip.ptr(plan_c), kmax,
-            Te, Ts, ws_ptr, ws_bytes, _hip.stream_of(k_blk)))
+        args = (d, k_blk.data_ptr(), v_blk.data_ptr(), k_blk.stride(0), k_blk.stride(1), k_blk.stride(2),
+                g_blk.data_ptr(), g_blk.stride(0), blk, ring_head, ring_filled, int(pos0), _hip.ptr(plan_c), kmax,
+                Te, Ts, ws_ptr, ws_bytes)
+        if snap is not None and n_ev > 0 and (Te > 0 or Ts > 0):
+            rc = _hip.lib().coda_block_write_snapshot(*args, snap[0].data_ptr(), snap[1].data_ptr(),
+                                                      snap[2].data_ptr(), _hip.stream_of(k_blk))
+            if rc == _hip.CODA_EUNSUP:
+                return None
+            _hip.check(rc)
+        else:
+            if snap is not None:
+                W_ = self.window
+                snap[0].copy_(st.k_buf[:, :, W_:])
+                snap[1].copy_(st.v_buf[:, :, W_:])
+                snap[2].copy_(st.allowed[:, W_:].view(torch.uint8))
+            _hip.check(_hip.lib().coda_block_write(*args, _hip.stream_of(k_blk)))
         if n_ev > 0:
             self._trace_block(tr, plan_c, Te, Ts)
             self._fold_metrics(st, metrics, n_ev, Te > 0, Ts > 0)

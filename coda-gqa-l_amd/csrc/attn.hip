@@ -1825,9 +1825,49 @@ struct F2Layout {
 // Whole tiles inside the prefix or the block load from a wave-uniform base
 // plus per-lane offsets.
 static constexpr int kTabRows = 64;  // query rows whose RoPE tables attn_f3_bf16 stages in LDS
+
+// Chunks of a prefill call in one launch (coda_prefill_attn_chunks):
+// blockIdx.y = chunk c_first + y, covering queries [t0, t0 + Lq) of the
+// call, t0 = c blk, Lq = min(blk, L - t0); its block keys are the call's
+// keys [t0 - win, t0 + Lq) with win = min(t0, W) (the ring window, in time
+// order, then the chunk itself, lower-right causal); its prefix is bank
+// snapshot y (prefix pointers and visibility bytes advanced by y strides).
+// n == 0: one chunk, as the descriptor says.
+struct ChunkGeom {
+  int n, c_first, blk, L, W, pad;
+  int64_t snap_stride;  // elements from one snapshot's K / V to the next
+  int64_t al_stride;    // bytes from one snapshot's visibility bytes to the next
+};
+template <int DH>
+__device__ __forceinline__ coda_attn_desc chunk_view(const coda_attn_desc& a0, const ChunkGeom& cg) {
+  if (cg.n == 0) return a0;
+  coda_attn_desc a = a0;
+  const int y = blockIdx.y;
+  const int64_t t0 = (int64_t)(cg.c_first + y) * cg.blk;
+  const int Lq = min(cg.blk, cg.L - (int)t0);
+  const int win = min((int)t0, cg.W);
+  using B = const bf16_t*;
+  a.q = (B)a0.q + t0 * a0.q_sl;
+  a.lam = (B)a0.lam + t0 * a0.lam_sl;
+  a.out = (bf16_t*)a0.out + t0 * a0.o_sl;
+  if (a0.rope_cos) {
+    a.rope_cos = (B)a0.rope_cos + t0 * (DH / 2);
+    a.rope_sin = (B)a0.rope_sin + t0 * (DH / 2);
+  }
+  a.kb = (B)a0.kb + (t0 - win) * a0.b_sl;
+  a.vb = (B)a0.vb + (t0 - win) * a0.b_sl;
+  a.Lq = Lq;
+  a.Lb = win + Lq;
+  a.kp = (B)a0.kp + y * cg.snap_stride;
+  a.vp = (B)a0.vp + y * cg.snap_stride;
+  if (a0.allowed) a.allowed = a0.allowed + y * cg.al_stride;
+  return a;
+}
+
 template <int DH, int NW, int QM, bool TB>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_f3_bf16(
-    const coda_attn_desc a, int NQ, int nqb, int npairs) {
+    const coda_attn_desc a_, int NQ, int nqb, int npairs, ChunkGeom cg) {
+  const coda_attn_desc a = chunk_view<DH>(a_, cg);
   using Lay = F2Layout<DH>;
   constexpr int NS = 4;
   static_assert(!TB || QM == 0 || QM == 1, "tables staged for the RoPE + rotation query cases");
@@ -2512,7 +2552,7 @@ static bool flash_offsets_fit(const coda_attn_desc* d) {
 // pipelined 32-row flash tiles: 8 waves, G heads x 8 / G groups of 16
 // queries; QM the query case (see attn_f3_bf16)
 template <int DH, int QM, bool TB>
-static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G) {
+static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G, const ChunkGeom& cg) {
   constexpr int NW = 8;
   const int npairs = d->B * d->Hkv;
   const int NQ = NW / G;
@@ -2520,21 +2560,22 @@ static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G) {
   const size_t lds = 4 * (size_t)(F2Layout<DH>::KBYTES + F2Layout<DH>::VBYTES);
   int rc = lds_limit<attn_f3_bf16<DH, NW, QM, TB>>(lds, "coda_diff_attn_fwd");
   if (rc) return rc;
-  hipLaunchKernelGGL((attn_f3_bf16<DH, NW, QM, TB>), dim3(nblk * npairs), dim3(NW * 64), lds, st, *d, NQ, nblk,
-                     npairs);
+  hipLaunchKernelGGL((attn_f3_bf16<DH, NW, QM, TB>), dim3(nblk * npairs, cg.n > 0 ? cg.n : 1), dim3(NW * 64), lds,
+                     st, *d, NQ, nblk, npairs, cg);
   return check_launch("attn_f3_bf16");
 }
 template <int DH>
-static int launch_f3(const coda_attn_desc* d, hipStream_t st, int G) {
+static int launch_f3(const coda_attn_desc* d, hipStream_t st, int G, const ChunkGeom& cg = ChunkGeom{}) {
   // the RoPE + rotation cases stage their tables in LDS while the
   // workgroup's 16 * 8 / G query rows fit (G >= 2)
   const bool tb = 16 * (8 / G) <= kTabRows && G <= 8;
   if (!d->q_noise && d->rope_cos) {
-    if (d->rope_interleaved) return tb ? launch_f3_qm<DH, 0, true>(d, st, G) : launch_f3_qm<DH, 0, false>(d, st, G);
-    return tb ? launch_f3_qm<DH, 1, true>(d, st, G) : launch_f3_qm<DH, 1, false>(d, st, G);
+    if (d->rope_interleaved)
+      return tb ? launch_f3_qm<DH, 0, true>(d, st, G, cg) : launch_f3_qm<DH, 0, false>(d, st, G, cg);
+    return tb ? launch_f3_qm<DH, 1, true>(d, st, G, cg) : launch_f3_qm<DH, 1, false>(d, st, G, cg);
   }
-  if (d->q_noise && !d->rope_cos) return launch_f3_qm<DH, 2, false>(d, st, G);
-  return launch_f3_qm<DH, 3, false>(d, st, G);
+  if (d->q_noise && !d->rope_cos) return launch_f3_qm<DH, 2, false>(d, st, G, cg);
+  return launch_f3_qm<DH, 3, false>(d, st, G, cg);
 }
 template <int DH>
 static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
@@ -2575,6 +2616,31 @@ static int launch_attn(const coda_attn_desc* d, hipStream_t st) {
     return fail(CODA_EUNSUP, "coda_diff_attn_fwd: G=%d with Lq=%d unsupported for bf16 tiles", G, d->Lq);
   }
   return check_launch("attn_tile_bf16");
+}
+
+extern "C" int coda_prefill_attn_chunks(const coda_attn_desc* d, int n_chunks, int c_first, int blk, int L, int W,
+                                        int64_t snap_stride, int64_t al_stride, void* stream) {
+  CODA_REQUIRE(d != nullptr, "coda_prefill_attn_chunks: null descriptor");
+  CODA_REQUIRE(n_chunks > 0 && c_first >= 0 && blk > 0 && W >= 0 && L > (int64_t)(c_first + n_chunks - 1) * blk,
+               "coda_prefill_attn_chunks: chunks %d .. %d of %d tokens in blocks of %d", c_first,
+               c_first + n_chunks - 1, L, blk);
+  // the descriptor as for the widest chunk (a full block behind a full
+  // window): every chunk's view lies within it
+  coda_attn_desc w = *d;
+  w.Lq = blk < L ? blk : L;
+  w.Lb = W + w.Lq;
+  int rc = validate(&w);
+  if (rc) return rc;
+  const int G = w.H / w.Hkv;
+  CODA_REQUIRE(w.dtype == CODA_BF16 && w.Dh >= 64 && (G == 8 || G == 4 || G == 2 || G == 1) && w.causal == 1 &&
+                   !use_rows(&w) && flash_offsets_fit(&w) && !w.q_noise && w.rope_cos,
+               "coda_prefill_attn_chunks: needs bf16, head_dim >= 64, G in {1, 2, 4, 8}, the lower-right causal "
+               "block, queries roped in-kernel and more than one query row per block");
+  CODA_REQUIRE(snap_stride >= 0 && al_stride >= 0, "coda_prefill_attn_chunks: negative snapshot stride");
+  if (w.B == 0) return CODA_OK;
+  ChunkGeom cg{n_chunks, c_first, blk, L, W, 0, snap_stride, al_stride};
+  hipStream_t st = (hipStream_t)stream;
+  return w.Dh == 64 ? launch_f3<64>(&w, st, G, cg) : launch_f3<128>(&w, st, G, cg);
 }
 
 extern "C" int coda_diff_attn_fwd(const coda_attn_desc* d, void* stream) {

@@ -362,6 +362,14 @@ struct BlockGeom {
   int64_t pos0;
   int64_t b_sb, b_sh, b_sl, g_sb;
 };
+// Where the one-launch update copies the bank slots it stages (the state
+// before the chunk's update): K / V (B, Hkv, Me + Ms, Dh), visibility
+// bytes (B, Me + Ms); k == nullptr: no copy.
+struct BankSnap {
+  void* k;
+  void* v;
+  uint8_t* allowed;
+};
 
 __host__ __device__ __forceinline__ int even_up(int x) { return (x + 1) & ~1; }
 __host__ __device__ __forceinline__ int snap_words(int Me, int Ms, int TT) {
@@ -1350,7 +1358,8 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
                                                                     const int32_t* __restrict__ plan_c, float* ws,
                                                                     unsigned long long* flags_all,
                                                                     unsigned long long host_epoch,
-                                                                    unsigned long long* tail, int spin_limit) {
+                                                                    unsigned long long* tail, int spin_limit,
+                                                                    BankSnap snap) {
   using E = Elt<T>;
   constexpr int NV = (DH + 63) / 64, LF = DH / 2, NCOL = DH + LF, CH = DH / 8;
   extern __shared__ __attribute__((aligned(16))) char fsm[];
@@ -1455,7 +1464,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
         if (i < n_ss) {
           const int r = i / CH, c = i % CH;
           vsv[u] = ld8<T>(vb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
-          if (c >= CH / 2) vsk[u] = ld8<T>(kb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
+          if (c >= CH / 2 || snap.k) vsk[u] = ld8<T>(kb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
         }
         if (i < n_ne) vne[u] = ld8<T>(nre + 8 * (int64_t)i);
         if (i < n_ns) vns[u] = ld8<T>(nrs + 8 * (int64_t)i);
@@ -1485,6 +1494,21 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
           const int r = i / CH, c = i % CH;
           st8<T>(own_sv + r * DH + 8 * c, vsv[u]);
           if (c >= CH / 2) st8<T>(own_sk + r * LF + 8 * (c - CH / 2), vsk[u]);
+        }
+        if (snap.k) {
+          // the bank slots as staged, before this chunk's update
+          const int64_t sb = ((int64_t)b * Hkv + h) * (Me + Ms) * DH;
+          if (i < n_ee) {
+            const int r = i / CH, c = i % CH;
+            st8<T>((T*)snap.k + sb + (int64_t)(e0 + r) * DH + 8 * c, vek[u]);
+            st8<T>((T*)snap.v + sb + (int64_t)(e0 + r) * DH + 8 * c, vev[u]);
+          }
+          if (i < n_ss) {
+            const int r = i / CH, c = i % CH;
+            st8<T>((T*)snap.k + sb + (int64_t)(Me + s0 + r) * DH + 8 * c, vsk[u]);
+            st8<T>((T*)snap.v + sb + (int64_t)(Me + s0 + r) * DH + 8 * c, vsv[u]);
+          }
+          if (lead && i < n_us) snap.allowed[(int64_t)b * (Me + Ms) + i] = (uint8_t)(vus[u] & 0xffu);
         }
         if (i < n_ne) {
           float x[8];
@@ -2243,7 +2267,8 @@ static std::atomic<int> g_spin_limit{kSyncSpinLimit};
 
 template <typename T, int DH>
 static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb, const float* gb, BlockGeom g,
-                        const int32_t* plan_c, float* ws, unsigned long long* tail, hipStream_t st) {
+                        const int32_t* plan_c, float* ws, unsigned long long* tail, hipStream_t st,
+                        BankSnap snap) {
   const int TT = g.Te > g.Ts ? g.Te : g.Ts;
   const int pairs = s->B * s->Hkv;
   if (g.n_ev > 0 && TT > 0 && fused_enabled()) {
@@ -2259,10 +2284,13 @@ static int launch_block(const coda_bank_desc* s, const void* kb, const void* vb,
       const int nwg = ((pairs + 7) / 8) * 8 * NZ;
       hipLaunchKernelGGL((block_fused_kernel<T, DH>), dim3(nwg), dim3(kFusedThreads), lds, st, *s, g, NZ,
                          (const T*)kb, (const T*)vb, gb, plan_c, ws, flags, next_epoch(), tail,
-                         g_spin_limit.load(std::memory_order_relaxed));
+                         g_spin_limit.load(std::memory_order_relaxed), snap);
       return check_launch("block_fused");
     }
   }
+  if (snap.k)
+    return fail(CODA_EUNSUP, "coda_block_write_snapshot: the one-launch update does not run for this chunk "
+                             "(Te=%d Ts=%d n_ev=%d)", g.Te, g.Ts, g.n_ev);
   const SplitShape sp = split_shape(s, g.Te, g.Ts, pairs);
   if (g.n_ev > 0 && TT > 0) {
     int rc = lds_limit<block_route_kernel<T, DH>>(sp.lds_route, "coda_block_write");
@@ -2321,10 +2349,10 @@ extern "C" int coda_block_write_check(const coda_bank_desc* s, int Te, int Ts) {
   return CODA_OK;
 }
 
-extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb, int64_t b_sh,
-                                int64_t b_sl, const float* gb, int64_t g_sb, int blk, int ring_head, int ring_filled,
-                                int64_t pos0, const int32_t* plan_c, int Kmax, int Te, int Ts, void* workspace,
-                                size_t workspace_bytes, void* stream) {
+static int block_write_impl(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb, int64_t b_sh,
+                            int64_t b_sl, const float* gb, int64_t g_sb, int blk, int ring_head, int ring_filled,
+                            int64_t pos0, const int32_t* plan_c, int Kmax, int Te, int Ts, void* workspace,
+                            size_t workspace_bytes, void* stream, BankSnap snap) {
   int rc = validate_bank(s, "coda_block_write");
   if (rc) return rc;
   CODA_REQUIRE(kb && vb && gb, "coda_block_write: block pointers missing");
@@ -2351,15 +2379,97 @@ extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const v
   unsigned long long* tail = workspace ? block_tail(s, workspace, workspace_bytes) : nullptr;
   switch (s->Dh) {
     case 32:
-      return bf ? launch_block<bf16_t, 32>(s, kb, vb, gb, g, plan_c, ws, tail, st)
-                : launch_block<float, 32>(s, kb, vb, gb, g, plan_c, ws, tail, st);
+      return bf ? launch_block<bf16_t, 32>(s, kb, vb, gb, g, plan_c, ws, tail, st, snap)
+                : launch_block<float, 32>(s, kb, vb, gb, g, plan_c, ws, tail, st, snap);
     case 64:
-      return bf ? launch_block<bf16_t, 64>(s, kb, vb, gb, g, plan_c, ws, tail, st)
-                : launch_block<float, 64>(s, kb, vb, gb, g, plan_c, ws, tail, st);
+      return bf ? launch_block<bf16_t, 64>(s, kb, vb, gb, g, plan_c, ws, tail, st, snap)
+                : launch_block<float, 64>(s, kb, vb, gb, g, plan_c, ws, tail, st, snap);
     default:
-      return bf ? launch_block<bf16_t, 128>(s, kb, vb, gb, g, plan_c, ws, tail, st)
-                : launch_block<float, 128>(s, kb, vb, gb, g, plan_c, ws, tail, st);
+      return bf ? launch_block<bf16_t, 128>(s, kb, vb, gb, g, plan_c, ws, tail, st, snap)
+                : launch_block<float, 128>(s, kb, vb, gb, g, plan_c, ws, tail, st, snap);
   }
+}
+
+extern "C" int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb, int64_t b_sh,
+                                int64_t b_sl, const float* gb, int64_t g_sb, int blk, int ring_head, int ring_filled,
+                                int64_t pos0, const int32_t* plan_c, int Kmax, int Te, int Ts, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return block_write_impl(s, kb, vb, b_sb, b_sh, b_sl, gb, g_sb, blk, ring_head, ring_filled, pos0, plan_c, Kmax, Te,
+                          Ts, workspace, workspace_bytes, stream, BankSnap{nullptr, nullptr, nullptr});
+}
+
+extern "C" int coda_block_write_snapshot(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb,
+                                         int64_t b_sh, int64_t b_sl, const float* gb, int64_t g_sb, int blk,
+                                         int ring_head, int ring_filled, int64_t pos0, const int32_t* plan_c, int Kmax,
+                                         int Te, int Ts, void* workspace, size_t workspace_bytes, void* snap_k,
+                                         void* snap_v, uint8_t* snap_allowed, void* stream) {
+  CODA_REQUIRE(snap_k && snap_v && snap_allowed, "coda_block_write_snapshot: snapshot pointers missing");
+  CODA_REQUIRE(((uintptr_t)snap_k % 16) == 0 && ((uintptr_t)snap_v % 16) == 0,
+               "coda_block_write_snapshot: snapshot rows must be 16-byte aligned");
+  return block_write_impl(s, kb, vb, b_sb, b_sh, b_sl, gb, g_sb, blk, ring_head, ring_filled, pos0, plan_c, Kmax, Te,
+                          Ts, workspace, workspace_bytes, stream, BankSnap{snap_k, snap_v, snap_allowed});
+}
+
+extern "C" int coda_block_write_chain(const coda_bank_desc* s, const void* kb, const void* vb, int64_t b_sb,
+                                      int64_t b_sh, int64_t b_sl, const float* gb, int64_t g_sb, int L, int blk,
+                                      int c_first, int n_chunks, int ring_head, int ring_filled, int64_t pos0,
+                                      const int32_t* plan, int Kmax, int k_exact, int k_summary, void* workspace,
+                                      size_t workspace_bytes, void* snap_k, void* snap_v, uint8_t* snap_allowed,
+                                      int64_t snap_stride, int64_t snap_al_stride, int* ring_out, void* stream) {
+  int rc = validate_bank(s, "coda_block_write_chain");
+  if (rc) return rc;
+  CODA_REQUIRE(kb && vb && gb && plan && ring_out && snap_k && snap_v && snap_allowed,
+               "coda_block_write_chain: pointer missing");
+  CODA_REQUIRE(blk > 0 && n_chunks > 0 && c_first >= 0 && (int64_t)(c_first + n_chunks - 1) * blk < L,
+               "coda_block_write_chain: chunks %d .. %d of %d tokens in blocks of %d", c_first,
+               c_first + n_chunks - 1, L, blk);
+  CODA_REQUIRE(!s->metrics && !s->frustrated && !s->trace,
+               "coda_block_write_chain: metrics, frustration flags and traces need the per-chunk calls");
+  CODA_REQUIRE(snap_stride >= 0 && snap_al_stride >= 0, "coda_block_write_chain: negative snapshot stride");
+  CODA_REQUIRE(((uintptr_t)snap_k % 16) == 0 && ((uintptr_t)snap_v % 16) == 0 &&
+                   (snap_stride * (s->dtype == CODA_BF16 ? 2 : 4)) % 16 == 0,
+               "coda_block_write_chain: snapshot rows must be 16-byte aligned");
+  // the ring progression first: every chunk must evict and take the
+  // one-launch update, else nothing is enqueued
+  const size_t esz = s->dtype == CODA_BF16 ? 2 : 4;
+  int head = ring_head, filled = ring_filled;
+  for (int i = 0; i < n_chunks; ++i) {
+    const int t = (c_first + i) * blk, n = blk < L - t ? blk : L - t;
+    const int total = filled + n, keep = total < s->W ? total : s->W, n_ev = total - keep;
+    const int Te = s->Me > 0 ? (k_exact < n_ev ? k_exact : n_ev) : 0;
+    const int Ts = s->Ms > 0 ? (k_summary < n_ev ? k_summary : n_ev) : 0;
+    CODA_REQUIRE(n_ev > 0 && (Te > 0 || Ts > 0), "coda_block_write_chain: chunk %d evicts nothing", c_first + i);
+    CODA_REQUIRE(Te <= Kmax && Ts <= Kmax, "coda_block_write_chain: Kmax %d < candidates", Kmax);
+    if (!(fused_enabled() && fused_shape(s, (int)esz, Te, Ts, s->B * s->Hkv).nz > 0))
+      return fail(CODA_EUNSUP, "coda_block_write_chain: chunk %d does not take the one-launch update",
+                  c_first + i);
+    head = filled == s->W ? head : 0;
+    if (keep == s->W) head = (head + n_ev) % s->W;
+    filled = keep;
+  }
+  head = ring_head;
+  filled = ring_filled;
+  for (int i = 0; i < n_chunks; ++i) {
+    const int t = (c_first + i) * blk, n = blk < L - t ? blk : L - t;
+    const int total = filled + n, keep = total < s->W ? total : s->W, n_ev = total - keep;
+    const int Te = s->Me > 0 ? (k_exact < n_ev ? k_exact : n_ev) : 0;
+    const int Ts = s->Ms > 0 ? (k_summary < n_ev ? k_summary : n_ev) : 0;
+    const char* kbc = (const char*)kb + (int64_t)t * b_sl * (int64_t)esz;
+    const char* vbc = (const char*)vb + (int64_t)t * b_sl * (int64_t)esz;
+    rc = block_write_impl(s, kbc, vbc, b_sb, b_sh, b_sl, gb + t, g_sb, n, head, filled, pos0 + (int64_t)i * blk,
+                          plan + (int64_t)(c_first + i) * s->B * Kmax, Kmax, Te, Ts, workspace, workspace_bytes,
+                          stream,
+                          BankSnap{(char*)snap_k + (int64_t)i * snap_stride * (int64_t)esz,
+                                   (char*)snap_v + (int64_t)i * snap_stride * (int64_t)esz,
+                                   snap_allowed + (int64_t)i * snap_al_stride});
+    if (rc) return rc;
+    head = filled == s->W ? head : 0;
+    if (keep == s->W) head = (head + n_ev) % s->W;
+    filled = keep;
+  }
+  ring_out[0] = head;
+  ring_out[1] = filled;
+  return CODA_OK;
 }
 
 // ------------------------------------------------------------ no-alloc variant

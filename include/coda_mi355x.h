@@ -186,6 +186,32 @@ int coda_attn_workspace_bytes(const coda_attn_desc* d, size_t* bytes);
 
 int coda_diff_attn_fwd(const coda_attn_desc* d, void* stream);
 
+/* The attention of chunks c_first .. c_first + n_chunks - 1 of a chunked
+ * prefill call in one launch, from bank snapshots instead of the live state.
+ * Chunk c covers queries [t0, t0 + Lq) of the call, t0 = c * blk,
+ * Lq = min(blk, L - t0); it attends to
+ *   prefix: bank snapshot c - c_first: d->kp / d->vp (B, Hkv, Lp, Dh) with
+ *           strides p_*, advanced by (c - c_first) * snap_stride elements,
+ *           visibility bytes d->allowed (row stride al_sb) advanced by
+ *           (c - c_first) * al_stride bytes (the exact and summary slots as
+ *           the state held them before chunk c's bank update:
+ *           coda_block_write_snapshot writes them);
+ *   block:  the call's keys [t0 - win, t0 + Lq), win = min(t0, W): the
+ *           ring window (the W tokens before the chunk, which is what the
+ *           ring holds when they all belong to this call) and the chunk
+ *           itself, lower-right causal;
+ * d describes the whole call: q / lam / out / rope tables / kb / vb at
+ * token 0 (Lq, Lb are set from the chunks).  bf16, head_dim 64 or 128,
+ * H / Hkv in {1, 2, 4, 8}, queries roped in-kernel (rope tables, no
+ * q_noise), causal == 1; else CODA_EUNSUP before anything runs.  Outputs
+ * equal those of coda_diff_attn_fwd on each chunk with the state's [ring |
+ * exact | summary] prefix, up to the order of the softmax sums.
+ * Replaces: the per-chunk attention of prefill_chunked
+ *   (src/coda_gqa_l/attention.py:611-693) for chunks whose ring window lies
+ *   in the call. */
+int coda_prefill_attn_chunks(const coda_attn_desc* d, int n_chunks, int c_first, int blk, int L, int W,
+                             int64_t snap_stride, int64_t al_stride, void* stream);
+
 /* ------------------------------------------------------------------------
  * Standalone differential epilogue over rows of Dh:
  *   out = RMSNorm(sig - lam * noise) * w     (coda_diff_epilogue_fwd)
@@ -406,6 +432,43 @@ int coda_block_write(const coda_bank_desc* s, const void* kb, const void* vb,
                      int blk, int ring_head, int ring_filled, int64_t pos0,
                      const int32_t* plan_c, int Kmax, int Te, int Ts,
                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* coda_block_write that also copies the exact and summary slots it stages
+ * (the state before this chunk's update) into snap_k / snap_v (B, Hkv,
+ * Me + Ms, Dh), 16-byte aligned, and their visibility bytes into
+ * snap_allowed (B, Me + Ms): the prefix of this chunk's attention for
+ * coda_prefill_attn_chunks.  Only the one-launch update copies: a chunk it
+ * does not run for (no candidates, more than 64 of a kind, Hkv > 64, or
+ * its LDS beyond a CU) returns CODA_EUNSUP before anything runs.
+ * Replaces: together with coda_prefill_attn_chunks, the chunk loop of
+ *   prefill_chunked (src/coda_gqa_l/attention.py:611-724). */
+int coda_block_write_snapshot(const coda_bank_desc* s, const void* kb, const void* vb,
+                              int64_t b_sb, int64_t b_sh, int64_t b_sl, const float* gb, int64_t g_sb,
+                              int blk, int ring_head, int ring_filled, int64_t pos0,
+                              const int32_t* plan_c, int Kmax, int Te, int Ts,
+                              void* workspace, size_t workspace_bytes, void* snap_k, void* snap_v,
+                              uint8_t* snap_allowed, void* stream);
+
+/* coda_block_write_snapshot for chunks c_first .. c_first + n_chunks - 1 of
+ * a prefill call in one library call (the chunk loop on the host side of the
+ * library): chunk c covers tokens [c blk, min(L, (c + 1) blk)) of kb / vb /
+ * gb (given at token 0 of the call), its candidates are plan rows
+ * (c, B, Kmax) of coda_block_plan (k_exact / k_summary per chunk, capped by
+ * its evictions), its snapshot goes to snap_* advanced by (c - c_first)
+ * snap_stride elements / snap_al_stride bytes, pos0 is the position of
+ * chunk c_first.  The ring (head, filled) after the last chunk is returned
+ * in ring_out[0 .. 1].  Every chunk must evict, and s carries no metrics,
+ * frustration flags or trace (else CODA_EINVAL); CODA_EUNSUP when a chunk
+ * would not take the one-launch update.  Either way nothing is enqueued.
+ * Replaces: the chunk loop of prefill_chunked's bank maintenance
+ *   (src/coda_gqa_l/attention.py:611-724, memory_banks.py:438-564). */
+int coda_block_write_chain(const coda_bank_desc* s, const void* kb, const void* vb,
+                           int64_t b_sb, int64_t b_sh, int64_t b_sl, const float* gb, int64_t g_sb,
+                           int L, int blk, int c_first, int n_chunks, int ring_head, int ring_filled,
+                           int64_t pos0, const int32_t* plan, int Kmax, int k_exact, int k_summary,
+                           void* workspace, size_t workspace_bytes, void* snap_k, void* snap_v,
+                           uint8_t* snap_allowed, int64_t snap_stride, int64_t snap_al_stride, int* ring_out,
+                           void* stream);
 
 /* Device scratch for coda_block_write. */
 int coda_block_workspace_bytes(const coda_bank_desc* s, int Kmax, size_t* bytes);

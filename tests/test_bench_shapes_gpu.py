@@ -153,7 +153,9 @@ def _cpu_copy(st):
 def test_one_launch_block_write_equals_four_launch_path(name, monkeypatch):
     """The one-launch chunk update (heads of a sequence meeting at a sync
     word) and the four-launch pipeline (route, decide, apply, ring) leave
-    byte-identical states and decision traces after a chunked prefill."""
+    byte-identical states and decision traces after a chunked prefill; the
+    heads agree within the tolerance (the one-launch path attends from bank
+    snapshots in one launch per group of chunks)."""
     _need_gpu()
     from coda_oracle import OracleLayer
     H, Hkv, Dh, W, Me, Ms, B, L, block, kind, _, dtype = SHAPES[name]
@@ -180,7 +182,9 @@ def test_one_launch_block_write_equals_four_launch_path(name, monkeypatch):
         out[mode] = (heads.cpu(), st, trace)
     h0, s0, t0 = out["0"]
     h1, s1, t1 = out["1"]
-    assert torch.equal(h0, h1), f"{name}: heads differ"
+    # (the four-launch update has no bank snapshots, so its chunks attend
+    # chunk by chunk to the live state: the same keys, other sum orders)
+    assert_close(h0, h1, dtype, f"{name}: heads")
     assert len(t0) == len(t1), f"{name}: {len(t0)} vs {len(t1)} trace events"
     for i, (a, b) in enumerate(zip(t0, t1)):
         assert a[0] == b[0] and all(torch.equal(x, y) for x, y in zip(a[1:], b[1:])), f"{name}: trace event {i} differs"
