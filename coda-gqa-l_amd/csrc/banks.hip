@@ -1328,7 +1328,7 @@ __host__ __device__ __forceinline__ FusedLds fused_lds(int DH, int esz, int Me, 
   L.own_ek = o; o += al16(PE * DH * esz);
   L.own_ev = o; o += al16(PE * DH * esz);
   L.own_sv = o; o += al16(PS * DH * esz);
-  L.own_sk = o; o += al16(PS * LF * esz);
+  L.own_sk = o; o += al16(PS * DH * esz);
   L.gate = o; o += al16(4 * TT);
   L.used = o; o += al16(4 * (Me + Ms));
   L.last = o; o += al16(8 * Me);
@@ -1384,7 +1384,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   T* own_ek = reinterpret_cast<T*>(fsm + L.own_ek);  // [PE][DH] own exact slots: K
   T* own_ev = reinterpret_cast<T*>(fsm + L.own_ev);  // V
   T* own_sv = reinterpret_cast<T*>(fsm + L.own_sv);  // [PS][DH] own summary slots: V
-  T* own_sk = reinterpret_cast<T*>(fsm + L.own_sk);  // [PS][LF] K channels [DH/2, DH)
+  T* own_sk = reinterpret_cast<T*>(fsm + L.own_sk);  // [PS][DH] own summary slots: K
   float* gate = reinterpret_cast<float*>(fsm + L.gate);
   int32_t* used = reinterpret_cast<int32_t*>(fsm + L.used);
   int64_t* last = reinterpret_cast<int64_t*>(fsm + L.last);
@@ -1421,8 +1421,6 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   // epoch of this launch for sequence b: the host value mixed with b's
   // generation word (tail[b]); tail[B] is the status word
   unsigned long long* status = tail + s.B;
-  const unsigned long long gen_b = __hip_atomic_load(tail + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const unsigned long long epoch = (host_epoch + gen_b * 0x9E3779B97F4A7C15ull) & ((1ull << 62) - 1);
   if (t == 0) sync_gave_up = 0;
   const Dec dx = dec_of(s, g, ws, b);  // exchange: idx_s [Ts], best value / slot of the exact tokens
   const int Lr = g.ring_filled, first = max(Lr, g.n_ev), rhead = (Lr == W) ? g.ring_head : 0;
@@ -1464,7 +1462,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
         if (i < n_ss) {
           const int r = i / CH, c = i % CH;
           vsv[u] = ld8<T>(vb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
-          if (c >= CH / 2 || snap.k) vsk[u] = ld8<T>(kb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
+          vsk[u] = ld8<T>(kb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
         }
         if (i < n_ne) vne[u] = ld8<T>(nre + 8 * (int64_t)i);
         if (i < n_ns) vns[u] = ld8<T>(nrs + 8 * (int64_t)i);
@@ -1493,22 +1491,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
         if (i < n_ss) {
           const int r = i / CH, c = i % CH;
           st8<T>(own_sv + r * DH + 8 * c, vsv[u]);
-          if (c >= CH / 2) st8<T>(own_sk + r * LF + 8 * (c - CH / 2), vsk[u]);
-        }
-        if (snap.k) {
-          // the bank slots as staged, before this chunk's update
-          const int64_t sb = ((int64_t)b * Hkv + h) * (Me + Ms) * DH;
-          if (i < n_ee) {
-            const int r = i / CH, c = i % CH;
-            st8<T>((T*)snap.k + sb + (int64_t)(e0 + r) * DH + 8 * c, vek[u]);
-            st8<T>((T*)snap.v + sb + (int64_t)(e0 + r) * DH + 8 * c, vev[u]);
-          }
-          if (i < n_ss) {
-            const int r = i / CH, c = i % CH;
-            st8<T>((T*)snap.k + sb + (int64_t)(Me + s0 + r) * DH + 8 * c, vsk[u]);
-            st8<T>((T*)snap.v + sb + (int64_t)(Me + s0 + r) * DH + 8 * c, vsv[u]);
-          }
-          if (lead && i < n_us) snap.allowed[(int64_t)b * (Me + Ms) + i] = (uint8_t)(vus[u] & 0xffu);
+          st8<T>(own_sk + r * DH + 8 * c, vsk[u]);
         }
         if (i < n_ne) {
           float x[8];
@@ -1532,7 +1515,30 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       }
     }
   }
+  // b's generation word, first used at sync 1: loaded after the staging
+  // loop (a load pending at a loop's head is waited for there), through a
+  // lane-varying zero in the address, which keeps it in a vector register (a
+  // uniform load is copied to a scalar register, and waited for, at once)
+  const int lane0 = (int)__builtin_amdgcn_mbcnt_lo(0u, 0u);
+  const unsigned long long gen_b =
+      __hip_atomic_load(tail + b + lane0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
+  if (snap.k) {
+    // the bank slots as staged, before this chunk's update, copied out of
+    // LDS (a loop of stores only: inside the staging loop, with its loads,
+    // every store would be waited for)
+    const int64_t sb = ((int64_t)b * Hkv + h) * (Me + Ms) * DH;
+    const int n_ee = (e1 - e0) * CH, n_ss = (s1 - s0) * CH;
+    for (int i = t; i < n_ee + n_ss; i += NT) {
+      const bool ex = i < n_ee;
+      const int j = ex ? i : i - n_ee, r = j / CH, c = j % CH;
+      const int64_t row = ex ? e0 + r : Me + s0 + r;
+      st8<T>((T*)snap.k + sb + row * DH + 8 * c, ld8<T>((ex ? own_ek : own_sk) + r * DH + 8 * c));
+      st8<T>((T*)snap.v + sb + row * DH + 8 * c, ld8<T>((ex ? own_ev : own_sv) + r * DH + 8 * c));
+    }
+    if (lead)
+      for (int i = t; i < Me + Ms; i += NT) snap.allowed[(int64_t)b * (Me + Ms) + i] = (uint8_t)used[i];
+  }
   // LRU keys over the pre-update stamps (memory_banks.py:640-660):
   // ascending stamps of used active slots, unused ones first
   if (Te > 0)
@@ -1573,8 +1579,17 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   {
     float* dot_e = ws + ((int64_t)b * Hkv + h) * Te * Me;
     float* dot_s = ws + CODA_WS(ws_dot_s, s, g) + ((int64_t)b * Hkv + h) * Ts * Ms;
-    const int n_e = ne * Me, n_all = n_e + ns * Ms;
-    for (int it = t; it < n_all; it += NT) {
+    const int n_e = ne * Me, n_s = ns * Ms, n_all = n_e + n_s;
+    // each dot is one serial chain (DH or DH/2 steps): the exact dots take
+    // the last n_e threads alone, the summary dots the others, so that no
+    // thread chains an exact dot after a summary one (when n_e <= NT / 2)
+    const bool split = n_e > 0 && 2 * n_e <= NT;
+    const int ns_thr = split ? NT - n_e : NT;
+    const int it0 = split ? (t >= ns_thr ? n_s + (t - ns_thr) : t) : t;
+    const int step = split ? (t >= ns_thr ? n_all : ns_thr) : NT;
+    for (int it1 = it0; it1 < (split && t < ns_thr ? n_s : n_all); it1 += step) {
+      // item order: [exact | summary] in the unsplit case, [summary | exact] in the split one
+      const int it = split ? (it1 < n_s ? n_e + it1 : it1 - n_s) : it1;
       const bool ex = it < n_e;
       const int k = ex ? it / Me : (it - n_e) / Ms, m = ex ? it % Me : (it - n_e) % Ms;
       const float* rw = ex ? nrm_e + m * le : nrm_s + m * lsum;
@@ -1593,23 +1608,29 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       __hip_atomic_store(o, E::rnd(acc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-  // sync 1; meanwhile the LRU victim order (rank of each key among all)
+  // sync 1; meanwhile the LRU victim order (rank of each key among all:
+  // one key per wave and pass, counted by ballots over the others)
+  const unsigned long long epoch = (host_epoch + gen_b * 0x9E3779B97F4A7C15ull) & ((1ull << 62) - 1);
   const bool gave_up1 = group_sync(flags, K, me, 2 * epoch, 2 * epoch + 1, spin_limit, status, &sync_gave_up,
                                    [&](int t1, int nt1) {
-    if (Te > 0)
-      for (int m = t1; m < Me; m += nt1) {
+    if (Te > 0) {
+      const int wb = t1 >> 6, nwb = nt1 >> 6, ln = t1 & 63;
+      for (int m = wb; m < Me; m += nwb) {
         const int64_t km = rk[m].v;
         int lt = 0, eq = 0;
-        for (int j = 0; j < Me; ++j) {
-          const int64_t kj = rk[j].v;
-          lt += kj < km;
-          eq += (kj == km) & (j != m);
+        for (int j0 = 0; j0 < Me; j0 += 64) {
+          const int j = j0 + ln;
+          const bool in = j < Me;
+          const int64_t kj = rk[in ? j : 0].v;
+          lt += __popcll(__ballot(in && kj < km));
+          eq += __popcll(__ballot(in && kj == km && j != m));
         }
-        if (lt < n_lru) {
+        if (ln == 0 && lt < n_lru) {
           if (eq) atomicOr(&ties, 1);
           else lru[lt] = m;
         }
       }
+    }
   });
   if (gave_up1) return;
   // ---- 3. routing of this workgroup's tokens (token i of [Te | Ts] goes
@@ -1939,7 +1960,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
           const float mem = E::ld(own_sv[rl * DH + d]);
           vb[(int64_t)(W + Me + m) * DH + d] = E::st(mem + E::rnd(eta * E::rnd(avg - mem)));
         } else {
-          const float mem = E::ld(own_sk[rl * LF + (col - DH)]);
+          const float mem = E::ld(own_sk[rl * DH + d]);
           const float dk = E::rnd(E::rnd(avg * s.energy_scale) - mem);
           const float nkv = E::rnd(mem + E::rnd(eta * dk));
           kb[(int64_t)(W + Me + m) * DH + d] = E::st(nkv);
