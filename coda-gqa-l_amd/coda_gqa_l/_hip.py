@@ -72,7 +72,7 @@ class ProjDesc(ctypes.Structure):
 
     _fields_ = [
         ("dtype", _i32), ("M", _i32), ("D", _i32), ("L", _i32), ("H", _i32), ("Hkv", _i32), ("Dh", _i32),
-        ("rope_interleaved", _i32), ("gate", _i32), ("pad0", _i32),
+        ("rope_interleaved", _i32), ("gate", _i32), ("w_layout", _i32),
         ("x", _vp), ("x_sm", _i64), ("w", _vp), ("bias", _vp), ("rope_cos", _vp), ("rope_sin", _vp),
         ("q", _vp), ("q_sm", _i64), ("k", _vp), ("k_sm", _i64), ("v", _vp), ("v_sm", _i64),
         ("lam", _vp), ("lam_sm", _i64), ("g", _vp), ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
@@ -107,6 +107,7 @@ _SIGS = {
                                 _i32, _i64, _vp, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp]),
     "coda_block_write_snapshot": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32,
                                          _i32, _i64, _vp, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp, _vp, _vp, _vp]),
+    "coda_project_pack": (_i32, [_vp, _i32, _i32, _i64, _vp, _vp]),
     "coda_block_write_chain": (_i32, [ctypes.POINTER(BankDesc), _vp, _vp, _i64, _i64, _i64, _vp, _i64, _i32, _i32, _i32,
                                       _i32, _i32, _i32, _i64, _vp, _i32, _i32, _i32, _vp, ctypes.c_size_t, _vp, _vp, _vp,
                                       _i64, _i64, ctypes.POINTER(ctypes.c_int), _vp]),

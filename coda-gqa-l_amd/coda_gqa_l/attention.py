@@ -297,10 +297,12 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         return tab[0][p0:need], tab[1][p0:need]
 
     def _proj_pack(self, dtype: torch.dtype):
-        """Packed [q | k | v | lambda | write] weights (n_feat, D) in `dtype`
-        and float32 biases (zero for a linear without one) for coda_project,
-        per parameter version; with half-split RoPE each k head's rows are
-        reordered to the pairs (i, i + Dh/2) on adjacent rows."""
+        """Packed [q | k | v | lambda | write] weights (n_feat, D) in `dtype`,
+        float32 biases (zero for a linear without one) and the weights'
+        layout code for coda_project, per parameter version; with half-split
+        RoPE each k head's rows are reordered to the pairs (i, i + Dh/2) on
+        adjacent rows.  Where the row kernel serves D the weights are kept in
+        its fragment tiles (coda_project_pack, layout 1), else row-major (0)."""
         lins = (self.q_proj, self.k_proj, self.v_proj, self.lambda_proj, self.write_proj)
         ps = [t for lin in lins for t in (lin.weight, lin.bias) if t is not None]
         tag = tuple((t._version, t.data_ptr(), t.dtype, t.device) for t in ps) + (self.rope_interleaved,
@@ -329,7 +331,17 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             b = torch.cat([t.detach().float() if t is not None else torch.zeros(wt.shape[0], device=dev)
                            for t, wt in zip(bt, ws)])
             b = torch.cat([b, torch.zeros((-b.numel()) % 4, device=dev)])
-        val = (w.contiguous(), b.contiguous())
+            w = w.contiguous()
+            layout = 0
+            if dtype == torch.bfloat16 and w.is_cuda:
+                n_feat, D = w.shape
+                wt = torch.empty((-(-n_feat // 64) * 64, D), dtype=dtype, device=dev)
+                rc = _hip.lib().coda_project_pack(w.data_ptr(), n_feat, D, D, wt.data_ptr(), _hip.stream_of(wt))
+                if rc == _hip.CODA_OK:
+                    w, layout = wt, 1
+                elif rc != _hip.CODA_EUNSUP:
+                    _hip.check(rc)
+        val = (w, b.contiguous(), layout)
         cache[("proj", dtype)] = (tag, val)
         return val
 
@@ -375,7 +387,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             g = torch.empty((B, L), dtype=torch.float32, device=x.device)
             d.g = g.data_ptr()
             xs = x if (x.is_contiguous() and x.data_ptr() % 16 == 0) else x.contiguous()
-            w, b = self._proj_pack(x.dtype)
+            w, b, d.w_layout = self._proj_pack(x.dtype)
             q = torch.empty((B, L, Fq), dtype=x.dtype, device=x.device)
             k = torch.empty((B, L, Hkv, Dh), dtype=x.dtype, device=x.device)
             v = torch.empty((B, L, Fk), dtype=x.dtype, device=x.device)
@@ -590,7 +602,7 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
         cos_t, sin_t = self._rope_rows(0, pos + 1, dev, dt)
         cos_t, sin_t = self.__dict__["_rope_cache"][(torch.device(dev), dt)]
         d = self._proj_desc(x, B, 1, cos_t, sin_t)
-        w, b = self._proj_pack(dt)
+        w, b, d.w_layout = self._proj_pack(dt)
         d.x_sm, d.w, d.bias = D, w.data_ptr(), b.data_ptr()
         d.q, d.q_sm, d.k, d.k_sm, d.v, d.v_sm = q.data_ptr(), Fq, k.data_ptr(), Fk, v.data_ptr(), Fk
         d.lam, d.lam_sm, d.g = lam.data_ptr(), H, g.data_ptr()

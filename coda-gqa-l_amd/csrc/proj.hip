@@ -180,23 +180,29 @@ __global__ __launch_bounds__(64 * WF * WT) void proj_gemm_bf16(const coda_proj_d
 // from L2.
 static constexpr int kRowsLA = 4;  // k-steps of loads in flight ahead of the products
 // RB row blocks of 16 features per wave: the token rows a wave loads feed
-// RB products each
-template <int NS, int MT, int RB>
+// RB products each.  TILED: W in fragment tiles (coda_project_pack), where
+// the operand of row block fb at k-step ks is the KiB at (fb D/32 + ks) 512
+// elements, lane l's 16 bytes at 8 l; else row-major with row stride w_sm.
+template <int NS, int MT, int RB, bool TILED>
 __device__ __forceinline__ void rows_partial(const bf16_t* __restrict__ W, int64_t w_sm, int n_feat,
                                              const bf16_t* __restrict__ X, int64_t x_sm, int M, int f0,
                                              pf32x4* part) {
   const int t = threadIdx.x, lane = t & 63, wv = t >> 6, r16 = lane & 15, kq = lane >> 4;
   const int k0 = wv * (NS * 32) + 8 * kq;
   const bf16_t* wr[RB];
+  // element step between k-steps: 32 columns, or one tile
+  constexpr int WS = TILED ? 512 : 32;
 #pragma unroll
-  for (int i = 0; i < RB; ++i) wr[i] = W + (int64_t)min(f0 + 16 * i + r16, n_feat - 1) * w_sm + k0;
+  for (int i = 0; i < RB; ++i)
+    wr[i] = TILED ? W + ((int64_t)(f0 / 16 + i) * (8 * NS) + wv * NS) * 512 + 8 * lane
+                  : W + (int64_t)min(f0 + 16 * i + r16, n_feat - 1) * w_sm + k0;
   const bf16_t* xr[MT];
 #pragma unroll
   for (int j = 0; j < MT; ++j) xr[j] = X + (int64_t)min(16 * j + r16, M - 1) * x_sm + k0;
   pbf16x8_t a[kRowsLA][RB], b[kRowsLA][MT];
   auto load = [&](int s) {
 #pragma unroll
-    for (int i = 0; i < RB; ++i) a[s % kRowsLA][i] = *reinterpret_cast<const pbf16x8_t*>(wr[i] + 32 * s);
+    for (int i = 0; i < RB; ++i) a[s % kRowsLA][i] = *reinterpret_cast<const pbf16x8_t*>(wr[i] + WS * s);
 #pragma unroll
     for (int j = 0; j < MT; ++j) b[s % kRowsLA][j] = *reinterpret_cast<const pbf16x8_t*>(xr[j] + 32 * s);
   };
@@ -238,12 +244,12 @@ __device__ __forceinline__ pf32x4 rows_sum(const pf32x4* part, int item) {
   return sum;
 }
 
-template <int NS, int MT, int RB>
+template <int NS, int MT, int RB, bool TILED>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void proj_rows_bf16(
     const coda_proj_desc d, int n_feat) {
   __shared__ pf32x4 part[8 * RB * MT * 64];
   const int f0 = blockIdx.x * 16 * RB;
-  rows_partial<NS, MT, RB>((const bf16_t*)d.w, d.D, n_feat, (const bf16_t*)d.x, d.x_sm, d.M, f0, part);
+  rows_partial<NS, MT, RB, TILED>((const bf16_t*)d.w, d.D, n_feat, (const bf16_t*)d.x, d.x_sm, d.M, f0, part);
   const int t = threadIdx.x;
   if (!d.gate && blockIdx.x == 0 && t < d.M) d.g[t] = 1.f;
   for (int item = t; item < 64 * MT * RB; item += 512) {
@@ -254,13 +260,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void p
   }
 }
 
+template <int NS, int RB, bool TILED>
+static int launch_rows_t(const coda_proj_desc* d, int n_feat, hipStream_t st) {
+  const dim3 grid((n_feat + 16 * RB - 1) / (16 * RB));
+  if (d->M <= 16) hipLaunchKernelGGL((proj_rows_bf16<NS, 1, RB, TILED>), grid, dim3(512), 0, st, *d, n_feat);
+  else if (d->M <= 32) hipLaunchKernelGGL((proj_rows_bf16<NS, 2, RB, TILED>), grid, dim3(512), 0, st, *d, n_feat);
+  else hipLaunchKernelGGL((proj_rows_bf16<NS, 4, RB, TILED>), grid, dim3(512), 0, st, *d, n_feat);
+  return check_launch("proj_rows_bf16");
+}
 template <int NS, int RB>
 static int launch_rows_rb(const coda_proj_desc* d, int n_feat, hipStream_t st) {
-  const dim3 grid((n_feat + 16 * RB - 1) / (16 * RB));
-  if (d->M <= 16) hipLaunchKernelGGL((proj_rows_bf16<NS, 1, RB>), grid, dim3(512), 0, st, *d, n_feat);
-  else if (d->M <= 32) hipLaunchKernelGGL((proj_rows_bf16<NS, 2, RB>), grid, dim3(512), 0, st, *d, n_feat);
-  else hipLaunchKernelGGL((proj_rows_bf16<NS, 4, RB>), grid, dim3(512), 0, st, *d, n_feat);
-  return check_launch("proj_rows_bf16");
+  return d->w_layout == 1 ? launch_rows_t<NS, RB, true>(d, n_feat, st) : launch_rows_t<NS, RB, false>(d, n_feat, st);
 }
 // 16 RB features per workgroup: RB 2 up to 16 k-steps per wave (K <= 4096),
 // RB 4 beyond (measured fastest at the 7B and 70B shapes, batch 1 .. 64)
@@ -278,6 +288,26 @@ static int launch_rows(const coda_proj_desc* d, int n_feat, hipStream_t st) {
     default: return -1;
   }
 }
+// one thread per 16-byte piece of the tiled copy
+__global__ __launch_bounds__(256) void proj_pack_kernel(const bf16_t* __restrict__ w, int n_feat, int D, int64_t w_sm,
+                                                        bf16_t* __restrict__ out, int64_t n_pieces) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n_pieces) return;
+  const int l = (int)(i & 63), r = l & 15, q = l >> 4;
+  const int64_t tile = i >> 6;
+  const int ksteps = D / 32;
+  const int64_t fb = tile / ksteps;
+  const int ks = (int)(tile % ksteps);
+  const int64_t f = fb * 16 + r;
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (f < n_feat) v = *reinterpret_cast<const uint4*>(w + f * w_sm + 32 * ks + 8 * q);
+  *reinterpret_cast<uint4*>(out + 8 * i) = v;
+}
+
+static bool rows_path(int D) {
+  return D >= 512 && D <= 8192 && D % 256 == 0 && ((D / 256) & (D / 256 - 1)) == 0;
+}
+
 template <int NTF, int MTT, int WF, int WT>
 static int launch_proj(const coda_proj_desc* d, int n_feat, hipStream_t st) {
   const dim3 grid((n_feat + NTF - 1) / NTF, (d->M + MTT - 1) / MTT);
@@ -314,9 +344,23 @@ extern "C" int coda_project(const coda_proj_desc* d, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   // K 512 .. 8192, a power of two times 256: row tiles over all of K (no
   // workspace); else 64 x 64 tiles over K
-  if (d->D >= 512 && d->D <= 8192 && d->D % 256 == 0 && ((d->D / 256) & (d->D / 256 - 1)) == 0)
-    return launch_rows(d, n_feat, st);
+  CODA_REQUIRE(d->w_layout == 0 || (d->w_layout == 1 && rows_path(d->D)),
+               "coda_project: weight layout %d with D=%d (tiles serve the row kernel's D only)", d->w_layout, d->D);
+  if (rows_path(d->D)) return launch_rows(d, n_feat, st);
   return launch_proj<64, 64, 4, 1>(d, n_feat, st);
+}
+
+extern "C" int coda_project_pack(const void* w, int n_feat, int D, int64_t w_sm, void* out, void* stream) {
+  CODA_REQUIRE(w && out && n_feat > 0 && D > 0 && w_sm >= D, "coda_project_pack: bad arguments");
+  if (!rows_path(D)) return fail(CODA_EUNSUP, "coda_project_pack: D=%d does not take the row kernel", D);
+  CODA_REQUIRE(w_sm % 8 == 0 && ((uintptr_t)w % 16) == 0 && ((uintptr_t)out % 16) == 0,
+               "coda_project_pack: rows must be 16-byte aligned");
+  // rows padded to a multiple of 64: the row kernel reads up to 4 row
+  // blocks per workgroup past the last feature
+  const int64_t n_pieces = (int64_t)((n_feat + 63) / 64) * 4 * (D / 32) * 64;
+  hipLaunchKernelGGL(proj_pack_kernel, dim3((unsigned)((n_pieces + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const bf16_t*)w, n_feat, D, w_sm, (bf16_t*)out, n_pieces);
+  return check_launch("proj_pack_kernel");
 }
 
 extern "C" int coda_project_workspace_bytes(const coda_proj_desc* d, size_t* bytes) {

@@ -86,10 +86,10 @@ typedef struct {
   int H, Hkv, Dh;
   int rope_interleaved;
   int gate;                /* 1: write gate from write_proj; 0: g = 1 */
-  int pad0;
+  int w_layout;            /* 0: w row-major (n_feat, D); 1: fragment tiles (coda_project_pack) */
   const void* x;
   int64_t x_sm;
-  const void* w;           /* (n_feat, D) packed weights */
+  const void* w;           /* packed weights, layout w_layout */
   const float* bias;       /* (n_feat) */
   const void* rope_cos;    /* (L, Dh/2) */
   const void* rope_sin;
@@ -108,11 +108,24 @@ typedef struct {
 
 /* Decode-shaped inputs only: M <= 64 token rows (more rows: CODA_EINVAL;
  * the layer's prefill projections are library GEMMs).  D 512 .. 8192 and a
- * power of two times 256: each workgroup owns 16 features over all of K,
+ * power of two times 256: each workgroup owns 32 features over all of K,
  * its 8 waves' K-range partials summed in LDS in wave order
- * (deterministic).  Other D (a multiple of 64): 64 x 64 tiles over K.  No
+ * (deterministic); the weights row-major or in fragment tiles.  Other D (a
+ * multiple of 64): 64 x 64 tiles over K, row-major weights only.  No
  * workspace. */
 int coda_project(const coda_proj_desc* d, void* stream);
+
+/* The weights of coda_project in fragment tiles (w_layout 1): for row block
+ * fb of 16 rows and k-step ks of 32 columns, a 1 KiB tile at element offset
+ * (fb * D/32 + ks) * 512 holding W[16 fb + r][32 ks + 8 q + e] at element
+ * 8 (r + 16 q) + e (r < 16, q < 4, e < 8) -- the order one wave's 16 x 32
+ * MFMA operand load reads, so that a wave streams each row block's K range
+ * as contiguous KiBs.  Rows n_feat .. ceil64(n_feat) - 1 are zero.  w:
+ * (n_feat, D) row-major with row stride w_sm elements; out: ceil64(n_feat)
+ * * D bf16 (ceil64: rounded up to a multiple of 64).  Only for the D that take coda_project's row kernel (512 ..
+ * 8192, a power of two times 256): CODA_EUNSUP otherwise, nothing written.
+ * No counterpart in the reference (its projections are nn.Linear). */
+int coda_project_pack(const void* w, int n_feat, int D, int64_t w_sm, void* out, void* stream);
 
 /* Workspace bytes coda_project needs for this descriptor (0: the kernels
  * keep their partial sums in LDS; kept for callers that size one). */

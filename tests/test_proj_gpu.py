@@ -159,3 +159,49 @@ def test_cached_step_equals_general_step():
     for f in ("k_buf", "v_buf", "allowed", "g_recent", "mem_last_exact", "_exact_v_norm", "_sum_lf_k_norm"):
         assert torch.equal(getattr(st_a, f), getattr(st_b, f)), f"state field {f} differs"
     assert (st_a.pos, st_a.recent_idx) == (st_b.pos, st_b.recent_idx)
+
+
+@pytest.mark.parametrize("name", ["7b_decode_b64", "7b_decode_b1", "c1_decode_b3_half_split_bias", "70b_decode_b8"])
+@torch.no_grad()
+def test_tiled_weights_equal_row_major(name):
+    """coda_project_pack's fragment tiles hold the packed weights in the
+    documented order (untiled with torch they equal the row-major packing,
+    k rows paired for half-split RoPE), and coda_project over the tiles
+    equals coda_project over the row-major copy bit for bit (same products,
+    same summation order)."""
+    _need_gpu()
+    D, H, Hkv, B, L, inter, policy, bias = SHAPES[name]
+    print(f"[proj tiles] {name}: D{D} B{B}", flush=True)
+    m = _layer(D, H, Hkv, inter, policy, bias)
+    wt, b, layout = m._proj_pack(torch.bfloat16)
+    assert layout == 1, "the row kernel's D must take the tiled weights"
+    Dh = D // H
+    wk = m.k_proj.weight
+    if not inter:
+        half = Dh // 2
+        pair = torch.stack([torch.arange(half), torch.arange(half) + half], 1).reshape(-1)
+        wk = wk[(torch.arange(Hkv)[:, None] * Dh + pair[None]).reshape(-1).to(DEV)]
+    rows = [m.q_proj.weight, wk, m.v_proj.weight, m.lambda_proj.weight]
+    if policy != "none":
+        rows.append(m.write_proj.weight)
+    w_rm = torch.cat([r.detach() for r in rows]).to(torch.bfloat16).contiguous()
+    n_feat = w_rm.shape[0]
+    nf64 = wt.shape[0]
+    assert nf64 % 64 == 0 and nf64 >= n_feat
+    # tile (fb, ks): element 8 (r + 16 q) + e holds W[16 fb + r][32 ks + 8 q + e]
+    untiled = wt.view(nf64 // 16, D // 32, 4, 16, 8).permute(0, 3, 1, 2, 4).reshape(nf64, D)
+    assert torch.equal(untiled[:n_feat], w_rm), "tiles differ from the row-major packing"
+    assert not untiled[n_feat:].any(), "padding rows are not zero"
+    g_ = torch.Generator(device=DEV).manual_seed(2)
+    x = torch.randn(B, L, D, generator=g_, device=DEV, dtype=torch.bfloat16)
+    got_t = [t.clone() for t in m._front(x, 5, fused=True)[:5]]
+    cache = m.__dict__["_derived_cache"]
+    tag, _ = cache[("proj", torch.bfloat16)]
+    cache[("proj", torch.bfloat16)] = (tag, (w_rm, b, 0))
+    try:
+        got_r = m._front(x, 5, fused=True)[:5]
+    finally:
+        del cache[("proj", torch.bfloat16)]
+    torch.cuda.synchronize()
+    for what, a, r in zip(("q", "k", "v", "g", "lam"), got_t, got_r):
+        assert torch.equal(a, r), f"{name} {what}: tiled and row-major weights give different results"
