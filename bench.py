@@ -306,19 +306,23 @@ def prefill_hot_path(coda, m, q, k_raw, v, gate, lam, k_out, st, blk, heads):
 
 def chunked_attention_timing(torch, coda, m, q, k, v, lam, cos, sin, heads, blk, reps):
     """The prefill attention as the layer runs it after the bank chain of a
-    fresh call: every chunk of the call in one launch of
-    coda_prefill_attn_chunks from the bank snapshots the chain left (the
-    layer's snapshot buffers, still holding the timed call's), timed over
-    `reps` launches with HIP events on the launch stream.  FLOPs per launch:
-    8 Dh B H per (query, visible key) pair, the visible keys of chunk c being
-    its snapshot's used bank slots (mean over the batch), its ring window and
-    the causal block."""
+    fresh call: the call's last group of chunks (every chunk when the
+    snapshot buffers hold them all) in one launch of coda_prefill_attn_chunks
+    from the bank snapshots the chain left (the layer's snapshot buffers,
+    still holding the timed call's last group), timed over `reps` launches
+    with HIP events on the launch stream.  FLOPs per launch: 8 Dh B H per
+    (query, visible key) pair, the visible keys of chunk c being its
+    snapshot's used bank slots (mean over the batch), its ring window and the
+    causal block."""
     B, H, L, Dh = q.shape
-    n = -(-L // blk)
+    n_all = -(-L // blk)
     snaps = m.__dict__.get("_snap_cache", {}).get((str(q.device), q.dtype, B, m.num_kv_heads, m.Me + m.Ms, Dh))
-    if not m.pipelined_prefill or snaps is None or snaps[0].shape[0] < n:
+    if not m.pipelined_prefill or snaps is None:
         return None
     sk, sv, sa = snaps
+    cap = sk.shape[0]
+    ca = ((n_all - 1) // cap) * cap  # first chunk of the last group (a fresh call's groups start at 0)
+    n = n_all - ca
     ct, sn = m._theta_tables(q.dtype)
     d, keep = coda.ops.attention_desc(
         q=q, rope_cos=cos, rope_sin=sin, rope_interleaved=m.rope_interleaved, theta_cos=ct, theta_sin=sn,
@@ -328,7 +332,7 @@ def chunked_attention_timing(torch, coda, m, q, k, v, lam, cos, sin, heads, blk,
     stream = coda._hip.stream_of(q)
 
     def launch():
-        coda._hip.check(L_.coda_prefill_attn_chunks(d, n, 0, blk, L, m.window, sk[0].numel(), sa[0].numel(), stream))
+        coda._hip.check(L_.coda_prefill_attn_chunks(d, n, ca, blk, L, m.window, sk[0].numel(), sa[0].numel(), stream))
     launch()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -341,10 +345,10 @@ def chunked_attention_timing(torch, coda, m, q, k, v, lam, cos, sin, heads, blk,
     ms = e0.elapsed_time(e1) / reps
     nb = sa[:n].float().sum(dim=-1).mean(dim=1).tolist()
     flops = 0.0
-    for c in range(n):
-        t0 = c * blk
+    for y in range(n):
+        t0 = (ca + y) * blk
         lq = min(blk, L - t0)
-        flops += 8.0 * Dh * B * H * (lq * (nb[c] + min(t0, m.window)) + lq * (lq + 1) / 2)
+        flops += 8.0 * Dh * B * H * (lq * (nb[y] + min(t0, m.window)) + lq * (lq + 1) / 2)
     return ms, flops, n
 
 
@@ -409,7 +413,7 @@ def bench_prefill(torch, coda, m, a, blk):
     if chunked is not None:
         ms, flops, n = chunked
         tflops = flops / (ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": F3_ROPED + " (every chunk of the call in one launch, "
+        roof = {"bound": "mfma", "kernel": F3_ROPED + " (a group of the call's chunks in one launch, "
                                                       "coda_prefill_attn_chunks)",
                 "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "flops_per_launch": flops, "avg_launch_ms": round(ms, 5),
@@ -511,7 +515,7 @@ def bench_prefill_c5(torch, coda, a, B=8, L=8192, blk=256):
     if chunked is not None:
         ms, flops, n = chunked
         tflops = flops / (ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": F3_ROPED + " (every chunk of the call in one launch, "
+        roof = {"bound": "mfma", "kernel": F3_ROPED + " (a group of the call's chunks in one launch, "
                                                       "coda_prefill_attn_chunks)",
                 "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "flops_per_launch": flops, "avg_launch_ms": round(ms, 5),

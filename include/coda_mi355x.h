@@ -419,9 +419,9 @@ int coda_block_plan(const float* g_ring, int ring_head, int ring_filled, int W,
  * (b_sb, b_sh, b_sl); gb (B, blk) float with row stride g_sb; plan_c points
  * at this chunk's (B, Kmax) candidate rows of coda_block_plan.
  * The ring is kept circular: head = oldest slot, filled = occupancy.
- * One launch per chunk when the chunk's working set fits a CU's LDS (one
- * workgroup per (KV head, sequence); the heads of a sequence meet at a
- * per-sequence sync word in the workspace), else four (route, decide,
+ * One launch per chunk when the chunk's working set fits a CU's LDS (up to
+ * 8 workgroups per (KV head, sequence); the workgroups of a sequence meet
+ * at per-sequence sync words in the workspace), else four (route, decide,
  * apply, ring).  Calls that share a workspace must not overlap.
  * The last B + 1 8-byte words of the workspace (at (workspace_bytes / 8) * 8
  * bytes from its start, counting back) are its tail: a generation word per
