@@ -905,6 +905,27 @@ __device__ __forceinline__ void st8(T* p, const Piece8<T> x) {
 #pragma unroll
   for (int i = 0; i < Piece8<T>::PW; ++i) reinterpret_cast<uint4*>(p)[i] = x.w[i];
 }
+// A piece into an LDS row of the fused update's norm caches (bf16 rows are
+// only 8-byte aligned there), and four values of such a row widened to fp32.
+template <typename T>
+__device__ __forceinline__ void st8_row(T* p, const Piece8<T> x) {
+  if constexpr (sizeof(T) == 2) {
+    reinterpret_cast<uint2*>(p)[0] = make_uint2(x.w[0].x, x.w[0].y);
+    reinterpret_cast<uint2*>(p)[1] = make_uint2(x.w[0].z, x.w[0].w);
+  } else {
+    st8<T>(p, x);
+  }
+}
+template <typename T>
+__device__ __forceinline__ float4 ld4_row(const T* p) {
+  if constexpr (sizeof(T) == 2) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    return make_float4(bf2f((bf16_t)(u.x & 0xffffu)), bf2f((bf16_t)(u.x >> 16)), bf2f((bf16_t)(u.y & 0xffffu)),
+                       bf2f((bf16_t)(u.y >> 16)));
+  } else {
+    return *reinterpret_cast<const float4*>(p);
+  }
+}
 // The eight values of a piece as floats.
 template <typename T>
 __device__ __forceinline__ void piece8_f(const Piece8<T>& x, float f[8]) {
@@ -1347,8 +1368,10 @@ __host__ __device__ __forceinline__ FusedLds fused_lds(int DH, int esz, int Me, 
   L.sflag = o; o += al16(4 * Ms);
   L.knew = o; o += al16(4 * PS * LF);
   L.ov = o;
-  // routing rows: head h's norm caches and this workgroup's normalised rows
-  L.total = o + al16(4 * ((Me + ne) * (DH + 4) + (Ms + ns) * (LF + 4)));
+  // routing rows: head h's norm caches in the element type (widened as the
+  // dots read them) and this workgroup's normalised rows in fp32
+  L.total = o + al16(Me * (DH + 4) * esz) + al16(4 * ne * (DH + 4)) + al16(Ms * (LF + 4) * esz) +
+            al16(4 * ns * (LF + 4));
   return L;
 }
 
@@ -1406,10 +1429,17 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   // this workgroup's routing rows: exact candidates e = z, z + NZ, ... and
   // summary candidates z, z + NZ, ... (every workgroup forms both kinds)
   const int ne = z < Te ? (Te - z + NZ - 1) / NZ : 0, ns = z < Ts ? (Ts - z + NZ - 1) / NZ : 0;
-  float* nrm_e = reinterpret_cast<float*>(fsm + L.ov);  // [Me][le]
-  float* cnd_e = nrm_e + (ne > 0 ? Me * le : 0);          // [ne][le]
-  float* nrm_s = cnd_e + ne * le;                         // [Ms][lsum]
-  float* cnd_s = nrm_s + (ns > 0 ? Ms * lsum : 0);        // [ns][lsum]
+  // (rows of le / lsum elements: 8-byte aligned in bf16, 16-byte in fp32,
+  // and 2 (bf16) or 4 (fp32) banks apart from row to row)
+  constexpr int ES = (int)sizeof(T);
+  char* ovp = fsm + L.ov;
+  T* nrm_e = reinterpret_cast<T*>(ovp);                                               // [Me][le]
+  ovp += ne > 0 ? al16(Me * le * ES) : 0;
+  float* cnd_e = reinterpret_cast<float*>(ovp);                                       // [ne][le]
+  ovp += al16(4 * ne * le);
+  T* nrm_s = reinterpret_cast<T*>(ovp);                                               // [Ms][lsum]
+  ovp += ns > 0 ? al16(Ms * lsum * ES) : 0;
+  float* cnd_s = reinterpret_cast<float*>(ovp);                                       // [ns][lsum]
   // this workgroup's bank slots of head h
   const int PE = (Me + NZ - 1) / NZ, e0 = min(Me, z * PE), e1 = min(Me, e0 + PE);
   const int PS = (Ms + NZ - 1) / NZ, s0 = min(Ms, z * PS), s1 = min(Ms, s0 + PS);
@@ -1493,20 +1523,8 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
           st8<T>(own_sv + r * DH + 8 * c, vsv[u]);
           st8<T>(own_sk + r * DH + 8 * c, vsk[u]);
         }
-        if (i < n_ne) {
-          float x[8];
-          piece8_f<T>(vne[u], x);
-          float4* d = reinterpret_cast<float4*>(nrm_e + (i / CH) * le + 8 * (i % CH));
-          d[0] = make_float4(x[0], x[1], x[2], x[3]);
-          d[1] = make_float4(x[4], x[5], x[6], x[7]);
-        }
-        if (i < n_ns) {
-          float x[8];
-          piece8_f<T>(vns[u], x);
-          float4* d = reinterpret_cast<float4*>(nrm_s + (i / CHL) * lsum + 8 * (i % CHL));
-          d[0] = make_float4(x[0], x[1], x[2], x[3]);
-          d[1] = make_float4(x[4], x[5], x[6], x[7]);
-        }
+        if (i < n_ne) st8_row<T>(nrm_e + (i / CH) * le + 8 * (i % CH), vne[u]);
+        if (i < n_ns) st8_row<T>(nrm_s + (i / CHL) * lsum + 8 * (i % CHL), vns[u]);
         if (i < n_raw) {
           st8<T>(raw_k + 8 * i, vrk[u]);
           st8<T>(raw_v + 8 * i, vrv[u]);
@@ -1592,13 +1610,13 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       const int it = split ? (it1 < n_s ? n_e + it1 : it1 - n_s) : it1;
       const bool ex = it < n_e;
       const int k = ex ? it / Me : (it - n_e) / Ms, m = ex ? it % Me : (it - n_e) % Ms;
-      const float* rw = ex ? nrm_e + m * le : nrm_s + m * lsum;
+      const T* rw = ex ? nrm_e + m * le : nrm_s + m * lsum;
       const float* cd = ex ? cnd_e + k * le : cnd_s + k * lsum;
       const int len = ex ? DH : LF;
       float acc = 0.f;
 #pragma unroll 4
       for (int d = 0; d < len; d += 4) {
-        const float4 rv = *reinterpret_cast<const float4*>(rw + d);
+        const float4 rv = ld4_row<T>(rw + d);
         const float4 cv = *reinterpret_cast<const float4*>(cd + d);
         acc = dot_pair(acc, cv.x, rv.x, cv.y, rv.y);
         acc = dot_pair(acc, cv.z, rv.z, cv.w, rv.w);
