@@ -315,14 +315,13 @@ def chunked_attention_timing(torch, coda, m, q, k, v, lam, cos, sin, heads, blk,
     snapshot's used bank slots (mean over the batch), its ring window and the
     causal block."""
     B, H, L, Dh = q.shape
-    n_all = -(-L // blk)
     snaps = m.__dict__.get("_snap_cache", {}).get((str(q.device), q.dtype, B, m.num_kv_heads, m.Me + m.Ms, Dh))
-    if not m.pipelined_prefill or snaps is None:
-        return None
+    last = m.__dict__.get("_last_chunk_group")
+    if not m.pipelined_prefill or snaps is None or last is None or last[2:] != (blk, L):
+        return None  # the timed call did not end in a grouped launch
     sk, sv, sa = snaps
-    cap = sk.shape[0]
-    ca = ((n_all - 1) // cap) * cap  # first chunk of the last group (a fresh call's groups start at 0)
-    n = n_all - ca
+    ca, cb = last[0], last[1]
+    n = cb - ca
     ct, sn = m._theta_tables(q.dtype)
     d, keep = coda.ops.attention_desc(
         q=q, rope_cos=cos, rope_sin=sin, rope_interleaved=m.rope_interleaved, theta_cos=ct, theta_sin=sn,

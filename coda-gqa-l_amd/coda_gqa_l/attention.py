@@ -822,6 +822,9 @@ class CoDAGQALandmarkPerf2(MemoryBankMixin, nn.Module):
             k_block=k, v_block=v, lam=lam, rms_weight=w, eps=self._eps, out=out.permute(0, 2, 1, 3))
         _hip.check(_hip.lib().coda_prefill_attn_chunks(d, cb - ca, ca, blk, L, self.window, sk[0].numel(),
                                                        sa[0].numel(), _hip.stream_of(q)))
+        # (the last grouped launch, for measurement: its chunks' snapshots
+        # stay in the buffers until the next call)
+        self.__dict__["_last_chunk_group"] = (ca, cb, blk, L)
 
     def prefill_chunked(self, x_seq: torch.Tensor, state: CoDAGQALandmarkStatePerf2, *, block_size: int = 256,
                         write_cache: bool = True, return_outputs: bool = True

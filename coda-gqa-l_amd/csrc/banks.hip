@@ -1541,22 +1541,6 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   const unsigned long long gen_b =
       __hip_atomic_load(tail + b + lane0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  if (snap.k) {
-    // the bank slots as staged, before this chunk's update, copied out of
-    // LDS (a loop of stores only: inside the staging loop, with its loads,
-    // every store would be waited for)
-    const int64_t sb = ((int64_t)b * Hkv + h) * (Me + Ms) * DH;
-    const int n_ee = (e1 - e0) * CH, n_ss = (s1 - s0) * CH;
-    for (int i = t; i < n_ee + n_ss; i += NT) {
-      const bool ex = i < n_ee;
-      const int j = ex ? i : i - n_ee, r = j / CH, c = j % CH;
-      const int64_t row = ex ? e0 + r : Me + s0 + r;
-      st8<T>((T*)snap.k + sb + row * DH + 8 * c, ld8<T>((ex ? own_ek : own_sk) + r * DH + 8 * c));
-      st8<T>((T*)snap.v + sb + row * DH + 8 * c, ld8<T>((ex ? own_ev : own_sv) + r * DH + 8 * c));
-    }
-    if (lead)
-      for (int i = t; i < Me + Ms; i += NT) snap.allowed[(int64_t)b * (Me + Ms) + i] = (uint8_t)used[i];
-  }
   // LRU keys over the pre-update stamps (memory_banks.py:640-660):
   // ascending stamps of used active slots, unused ones first
   if (Te > 0)
@@ -1648,6 +1632,22 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
           else lru[lt] = m;
         }
       }
+    }
+    if (snap.k) {
+      // the bank slots as staged, before this chunk's update, copied out of
+      // LDS while the sync waits (a loop of stores only: inside the staging
+      // loop, with its loads, every store would be waited for)
+      const int64_t sb = ((int64_t)b * Hkv + h) * (Me + Ms) * DH;
+      const int n_ee = (e1 - e0) * CH, n_ss = (s1 - s0) * CH;
+      for (int i = t1; i < n_ee + n_ss; i += nt1) {
+        const bool ex = i < n_ee;
+        const int j = ex ? i : i - n_ee, r = j / CH, c = j % CH;
+        const int64_t row = ex ? e0 + r : Me + s0 + r;
+        st8<T>((T*)snap.k + sb + row * DH + 8 * c, ld8<T>((ex ? own_ek : own_sk) + r * DH + 8 * c));
+        st8<T>((T*)snap.v + sb + row * DH + 8 * c, ld8<T>((ex ? own_ev : own_sv) + r * DH + 8 * c));
+      }
+      if (lead)
+        for (int i = t1; i < Me + Ms; i += nt1) snap.allowed[(int64_t)b * (Me + Ms) + i] = (uint8_t)used[i];
     }
   });
   if (gave_up1) return;
@@ -1951,33 +1951,50 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
     }
   }
   // ---- 4c. summary accumulate + EMA of this workgroup's slots
-  // (memory_banks.py:880-932): thread (group q, column col) takes slots
-  // s0 + q, s0 + q + NG, ...; column col < DH is V channel col, else K
-  // channel DH/2 + col - DH
+  // (memory_banks.py:880-932): one wave per slot, lane l taking columns l,
+  // l + 64, ... (column col < DH is V channel col, else K channel
+  // DH/2 + col - DH), all of them over the slot's tokens in token order (the
+  // fp32 scatter_add order); then the slot's new LF key row through LDS and
+  // its norm-cache row, within the wave
   if (Ts > 0) {
     const float eta_h = s.eta[h];
-    constexpr int NG = kFusedThreads / NCOL;
-    const int q = t / NCOL, col = t % NCOL;
-    if (q < NG) {
-      const bool is_v = col < DH;
-      const int d = is_v ? col : LF + (col - DH);
-      const T* tokv = (is_v ? raw_v : raw_k) + d;
-      for (int m = s0 + q; m < s1; m += NG) {
-        if (!(sflag[m] & 1)) continue;
-        uint64_t r = smask[m];
+    constexpr int NCW = (NCOL + 63) / 64;
+    for (int m = s0 + wv; m < s1; m += NW) {
+      if (!(sflag[m] & 1)) continue;
+      const uint64_t msk = smask[m];
+      const float eta = (s.overwrite_on_insert && (sflag[m] & 2)) ? 1.f : eta_h;
+      const float cnt = fmaxf(scnt[m], eps_r<T>());
+      const int rl = m - s0;
+      const T* tokv[NCW];
+      float a[NCW];
+#pragma unroll
+      for (int jc = 0; jc < NCW; ++jc) {
+        const int col = min(lane + 64 * jc, NCOL - 1);
+        tokv[jc] = (col < DH ? raw_v : raw_k) + (col < DH ? col : LF + (col - DH));
+      }
+      {
+        uint64_t r = msk;
         int tt = __builtin_ctzll(r);
-        float a = E::rnd(E::ld(tokv[tt * DH]) * wtok[tt]);
+        float wt = wtok[tt];
+#pragma unroll
+        for (int jc = 0; jc < NCW; ++jc) a[jc] = E::rnd(E::ld(tokv[jc][tt * DH]) * wt);
         for (r &= r - 1; r; r &= r - 1) {
           tt = __builtin_ctzll(r);
-          a += E::rnd(E::ld(tokv[tt * DH]) * wtok[tt]);
+          wt = wtok[tt];
+#pragma unroll
+          for (int jc = 0; jc < NCW; ++jc) a[jc] += E::rnd(E::ld(tokv[jc][tt * DH]) * wt);
         }
-        const float eta = (s.overwrite_on_insert && (sflag[m] & 2)) ? 1.f : eta_h;
-        const float avg = E::rnd(E::rnd(a) / fmaxf(scnt[m], eps_r<T>()));
-        const int rl = m - s0;
-        if (is_v) {
-          const float mem = E::ld(own_sv[rl * DH + d]);
-          vb[(int64_t)(W + Me + m) * DH + d] = E::st(mem + E::rnd(eta * E::rnd(avg - mem)));
+      }
+#pragma unroll
+      for (int jc = 0; jc < NCW; ++jc) {
+        const int col = lane + 64 * jc;
+        if (col >= NCOL) continue;
+        const float avg = E::rnd(E::rnd(a[jc]) / cnt);
+        if (col < DH) {
+          const float mem = E::ld(own_sv[rl * DH + col]);
+          vb[(int64_t)(W + Me + m) * DH + col] = E::st(mem + E::rnd(eta * E::rnd(avg - mem)));
         } else {
+          const int d = LF + (col - DH);
           const float mem = E::ld(own_sk[rl * DH + d]);
           const float dk = E::rnd(E::rnd(avg * s.energy_scale) - mem);
           const float nkv = E::rnd(mem + E::rnd(eta * dk));
@@ -1985,11 +2002,8 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
           knew[rl * LF + (col - DH)] = nkv;  // new LF key for the norm cache
         }
       }
-    }
-    __syncthreads();
-    for (int m = s0 + wv; m < s1; m += NW) {
-      if (!(sflag[m] & 1)) continue;
-      const int rl = m - s0;
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LF keys are in LDS
+      __builtin_amdgcn_wave_barrier();
       float x[NV];
       bool act[NV];
 #pragma unroll
