@@ -1386,8 +1386,7 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
   using E = Elt<T>;
   constexpr int NV = (DH + 63) / 64, LF = DH / 2, NCOL = DH + LF, CH = DH / 8;
   extern __shared__ __attribute__((aligned(16))) char fsm[];
-  __shared__ int ties, any_used_s, sync_gave_up;
-  __shared__ int dec_wave[kFusedThreads / 64], dec_cnt[5];
+  __shared__ int ties, sync_gave_up;
   // workgroup -> (sequence, head, z): workgroups are dealt round robin to
   // the 8 XCDs, so the NZ workgroups of one (sequence, head) pair take
   // consecutive turns of one XCD (they share its L2); the workgroups of a
@@ -1549,7 +1548,6 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       rk[m] = sel::Item<int64_t>{u ? last[m] : kNegBig, (int64_t)m};
     }
   if (t == 0) ties = 0;
-  if (t < 5) dec_cnt[t] = 0;
   __syncthreads();
   // ---- 2. this workgroup's routing rows, normalised (exact: V, all DH
   // channels; summary: K channels [DH/2, DH)), then their dots with head
@@ -1756,118 +1754,93 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       wtok[i] = (!s.gated || gt >= s.tau_summary) ? E::rnd(gt) : 0.f;
     }
   }
-  if (wv == 0) {
+  __syncthreads();
+  // exact decisions on wave 0 (at most 64 tokens: lane tt takes token tt),
+  // the summary slots' token masks on the other waves, side by side
+  const int sum_w0 = Te > 0 ? 1 : 0;  // first wave of the summary masks
+  if (Te > 0 && wv == 0) {
+    // (exact flags and touch stamps start cleared; the staged stamps are no
+    // longer read)
     int u = 0;
-    for (int m = lane; m < Me; m += 64) u |= used[m] != 0;
-    u = wave_or(u);
-    if (lane == 0) any_used_s = u;
-  }
-  __syncthreads();
-  if (Te > 0) {
-    // exact decisions, one thread per token; the rank of a novel kept token
-    // (the reference's cumsum(novel & keep) - 1) from the ballots of the
-    // waves before it and the lanes before it
-    const int any_used = any_used_s;
+    for (int m = lane; m < Me; m += 64) {
+      u |= used[m] != 0;
+      eflag[m] = 0;
+      last[m] = kNegBig;
+    }
+    const int any_used = wave_or(u);
+    // the rank of a novel kept token (the reference's cumsum(novel & keep)
+    // - 1) from the ballot of the lanes before it
     const uint64_t lt_mask = lane ? (~0ull >> (64 - lane)) : 0ull;
-    int carry = 0;  // novel kept tokens of the earlier passes
-    for (int base = 0; base < Te; base += NT) {
-      const int tt = base + t;
-      const bool in = tt < Te;
-      const int ti = in ? tt : Te - 1;
-      const bool keep = s.gated ? (gate[ti] >= s.tau_exact) : true;
-      const float bv = bv_e[ti];
-      const bool novel = !any_used || bv < E::rnd(s.tau_novel);
-      const bool hit = any_used && bv >= E::rnd(s.tau_match);
-      const bool nk = in && novel && keep;
-      const uint64_t bal = __ballot(nk);
-      if (lane == 0) dec_wave[wv] = __popcll(bal);
-      __syncthreads();
-      int before = carry, total = carry;
-      for (int w = 0; w < NW; ++w) {
-        const int c = dec_wave[w];
-        before += w < wv ? c : 0;
-        total += c;
-      }
-      const int rank = before + __popcll(bal & lt_mask) + (nk ? 1 : 0) - 1;
-      const bool cap = nk && rank < Ae;
-      int idx = bi_e[ti];
-      if (cap) idx = lru[min(max(rank, 0), n_lru - 1)];
-      const bool touch = keep && (!novel || cap);
-      const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
-      if (in) {
-        idx_e[tt] = idx;
-        fl_e[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
-      }
-      if (lead && (s.metrics || s.frustrated)) {
-        const int c_ow = __popcll(__ballot(in && ow)), c_cap = __popcll(__ballot(in && cap));
-        const int c_hit = __popcll(__ballot(in && hit && keep)), c_gated = __popcll(__ballot(in && !keep));
-        const int c_fr = __popcll(__ballot(nk && !cap));
-        if (lane == 0) {
-          atomicAdd(&dec_cnt[0], c_ow);
-          atomicAdd(&dec_cnt[1], c_cap);
-          atomicAdd(&dec_cnt[2], c_hit);
-          atomicAdd(&dec_cnt[3], c_gated);
-          atomicAdd(&dec_cnt[4], c_fr);
+    const int tt = lane;
+    const bool in = tt < Te;
+    const int ti = in ? tt : Te - 1;
+    const bool keep = s.gated ? (gate[ti] >= s.tau_exact) : true;
+    const float bv = bv_e[ti];
+    const bool novel = !any_used || bv < E::rnd(s.tau_novel);
+    const bool hit = any_used && bv >= E::rnd(s.tau_match);
+    const bool nk = in && novel && keep;
+    const uint64_t bal = __ballot(nk);
+    const int rank = __popcll(bal & lt_mask) + (nk ? 1 : 0) - 1;
+    const bool cap = nk && rank < Ae;
+    int idx = bi_e[ti];
+    if (cap) idx = lru[min(max(rank, 0), n_lru - 1)];
+    const bool touch = keep && (!novel || cap);
+    const bool ow = s.refresh_on_hit ? (keep && (cap || hit)) : cap;
+    if (in) {
+      idx_e[tt] = idx;
+      fl_e[tt] = (ow ? 1 : 0) | (touch ? 2 : 0);
+      // the slot's flags through LDS atomics (after this wave's clears, in
+      // its LDS order): written (an overwriting token) and touched (max
+      // position of the touching tokens)
+      if (ow) atomicOr(&eflag[idx], 1);
+      if (touch) atomicMax(reinterpret_cast<long long*>(&last[idx]), (long long)(g.pos0 - g.ring_filled + pcl[tt]));
+    }
+    if (lead && (s.metrics || s.frustrated)) {
+      const int c_ow = __popcll(__ballot(in && ow)), c_cap = __popcll(__ballot(in && cap));
+      const int c_hit = __popcll(__ballot(in && hit && keep)), c_gated = __popcll(__ballot(in && !keep));
+      const int c_fr = __popcll(__ballot(nk && !cap));
+      if (lane == 0) {
+        if (s.metrics) {
+          atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, c_ow);
+          atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, c_fr);
+          atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, c_cap);
+          atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, c_hit);
+          if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, c_gated);
         }
+        if (s.frustrated) atomic_add_i64(s.frustrated + 0, c_fr);
       }
-      carry = total;
-      __syncthreads();
-    }
-    if (lead && t == 0) {
-      if (s.metrics) {
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_OVERWRITES, dec_cnt[0]);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_FRUSTRATED, dec_cnt[4]);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_INSERTS, dec_cnt[1]);
-        atomic_add_i64(s.metrics + CODA_CNT_EXACT_HITS, dec_cnt[2]);
-        if (s.gated) atomic_add_i64(s.metrics + CODA_CNT_TOKENS_GATED_OUT, dec_cnt[3]);
-      }
-      if (s.frustrated) atomic_add_i64(s.frustrated + 0, dec_cnt[4]);
     }
   }
-  // (exact flags and touch stamps start cleared; the staged stamps are no
-  // longer read)
-  for (int m = t; m < Me; m += NT) {
-    eflag[m] = 0;
-    last[m] = kNegBig;
-  }
-  // summary slots, 8 per wave and pass: token masks (ballots over the
-  // tokens), then lane u sums slot u's weights in token order (fp32: the
-  // scatter_add order) and sets its active / newly used flags
-  for (int m0 = 8 * wv; m0 < Ms; m0 += 8 * NW) {
-    uint64_t mine = 0;
+  if (wv >= sum_w0) {
+    // summary slots, 8 per wave and pass: token masks (ballots over the
+    // tokens), then lane u sums slot u's weights in token order (fp32: the
+    // scatter_add order) and sets its active / newly used flags
+    for (int m0 = 8 * (wv - sum_w0); m0 < Ms; m0 += 8 * (NW - sum_w0)) {
+      uint64_t mine = 0;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const uint64_t mk = __ballot(lane < Ts && idx_s[min(lane, max(Ts, 1) - 1)] == m0 + u);
-      if (lane == u) mine = mk;
-    }
-    const int m = m0 + lane;
-    if (lane < 8 && m < Ms) {
-      float c = 0.f;
-      for (uint64_t r = mine; r; r &= r - 1) c += wtok[__builtin_ctzll(r)];
-      c = E::rnd(c);
-      smask[m] = mine;
-      scnt[m] = c;
-      const bool active = c > 0.f;
-      sflag[m] = (active ? 1 : 0) | ((active && used[Me + m] == 0) ? 2 : 0);
+      for (int u = 0; u < 8; ++u) {
+        const uint64_t mk = __ballot(lane < Ts && idx_s[min(lane, max(Ts, 1) - 1)] == m0 + u);
+        if (lane == u) mine = mk;
+      }
+      const int m = m0 + lane;
+      if (lane < 8 && m < Ms) {
+        float c = 0.f;
+        for (uint64_t r = mine; r; r &= r - 1) c += wtok[__builtin_ctzll(r)];
+        c = E::rnd(c);
+        smask[m] = mine;
+        scnt[m] = c;
+        const bool active = c > 0.f;
+        sflag[m] = (active ? 1 : 0) | ((active && used[Me + m] == 0) ? 2 : 0);
+      }
     }
   }
   __syncthreads();
-  // exact slots, one thread per token through LDS atomics: written (an
-  // overwriting token) and touched (max position of the touching tokens)
-  if (Te > 0) {
-    for (int tt = t; tt < Te; tt += NT) {
-      const int m = idx_e[tt], f = fl_e[tt];
-      if (f & 1) atomicOr(&eflag[m], 1);
-      if (f & 2) atomicMax(reinterpret_cast<long long*>(&last[m]), (long long)(g.pos0 - g.ring_filled + pcl[tt]));
-    }
-    __syncthreads();
-    if (lead)
+  if (lead) {
+    if (Te > 0)
       for (int m = t; m < Me; m += NT) {
         if (last[m] != kNegBig) s.mem_last[(int64_t)b * Me + m] = last[m];  // LRU: max pos of the touching tokens
         if (eflag[m]) al[W + m] = 1;
       }
-  }
-  if (lead) {
     int32_t* tr = s.trace ? s.trace + (int64_t)b * (2 * Te + Ts) : nullptr;
     if (tr) {
       for (int tt = t; tt < Te; tt += NT) {
