@@ -429,6 +429,16 @@ __device__ __forceinline__ const T* cand_row(const coda_bank_desc& s, const Bloc
   return kbk + b * g.b_sb + h * g.b_sh + (int64_t)(e - g.ring_filled) * g.b_sl;
 }
 
+// Where candidate e's gate is (ring slot or block token), without a load.
+__device__ __forceinline__ const float* cand_gate_ptr(const coda_bank_desc& s, const BlockGeom& g, const float* gb,
+                                                      int b, int e) {
+  int slot = e;
+  if (g.ring_filled == s.W) {
+    slot = g.ring_head + e;
+    slot -= slot >= s.W ? s.W : 0;
+  }
+  return e < g.ring_filled ? s.g_recent + (int64_t)b * s.W + slot : gb + (int64_t)b * g.g_sb + (e - g.ring_filled);
+}
 __device__ __forceinline__ float cand_gate(const coda_bank_desc& s, const BlockGeom& g, const float* gb, int b,
                                            int e) {
   if (e < g.ring_filled) {
@@ -1472,39 +1482,43 @@ __global__ __launch_bounds__(kFusedThreads) void block_fused_kernel(const coda_b
       int64_t vla[UR];
       Piece8<T> vek[UR], vev[UR], vsv[UR], vsk[UR], vne[UR], vns[UR], vrk[UR], vrv[UR];
       float vg[UR];
+      // every load unconditional, from a clamped index or (an empty array)
+      // the workspace: the compiler then counts the loads in flight and
+      // waits for the plan entries alone before the candidate rows, where a
+      // load under a branch makes it wait for everything
 #pragma unroll
       for (int u = 0; u < UR; ++u) {
         const int i = base + u * NT;
-        rr[u] = i < n_raw ? pc[i / CH] : 0;
+        rr[u] = pc[min(i, n_raw - 1) / CH];
       }
 #pragma unroll
       for (int u = 0; u < UR; ++u) {
         const int i = base + u * NT;
-        vpc[u] = i < TT ? pc[i] : 0;
-        vus[u] = i < n_us ? al[W + i] : 0;
-        vla[u] = i < Me ? s.mem_last[(int64_t)b * Me + i] : 0;
-        if (i < n_ee) {
-          const int r = i / CH, c = i % CH;
-          vek[u] = ld8<T>(kb + (int64_t)(W + e0 + r) * DH + 8 * c);
-          vev[u] = ld8<T>(vb + (int64_t)(W + e0 + r) * DH + 8 * c);
+        vpc[u] = pc[min(i, TT - 1)];
+        vus[u] = al[W + min(i, n_us - 1)];
+        vla[u] = *(Me > 0 ? s.mem_last + (int64_t)b * Me + min(i, Me - 1) : reinterpret_cast<const int64_t*>(ws));
+        {
+          const int ic = min(i, max(n_ee, 1) - 1), r = ic / CH, c = ic % CH;
+          const int64_t o = (int64_t)(W + e0 + r) * DH + 8 * c;
+          vek[u] = ld8<T>(n_ee > 0 ? kb + o : reinterpret_cast<const T*>(ws));
+          vev[u] = ld8<T>(n_ee > 0 ? vb + o : reinterpret_cast<const T*>(ws));
         }
-        if (i < n_ss) {
-          const int r = i / CH, c = i % CH;
-          vsv[u] = ld8<T>(vb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
-          vsk[u] = ld8<T>(kb + (int64_t)(W + Me + s0 + r) * DH + 8 * c);
+        {
+          const int ic = min(i, max(n_ss, 1) - 1), r = ic / CH, c = ic % CH;
+          const int64_t o = (int64_t)(W + Me + s0 + r) * DH + 8 * c;
+          vsv[u] = ld8<T>(n_ss > 0 ? vb + o : reinterpret_cast<const T*>(ws));
+          vsk[u] = ld8<T>(n_ss > 0 ? kb + o : reinterpret_cast<const T*>(ws));
         }
-        if (i < n_ne) vne[u] = ld8<T>(nre + 8 * (int64_t)i);
-        if (i < n_ns) vns[u] = ld8<T>(nrs + 8 * (int64_t)i);
+        vne[u] = ld8<T>(n_ne > 0 ? nre + 8 * (int64_t)min(i, n_ne - 1) : reinterpret_cast<const T*>(ws));
+        vns[u] = ld8<T>(n_ns > 0 ? nrs + 8 * (int64_t)min(i, n_ns - 1) : reinterpret_cast<const T*>(ws));
       }
 #pragma unroll
       for (int u = 0; u < UR; ++u) {
         const int i = base + u * NT;
-        if (i < n_raw) {
-          const int c = i % CH;
-          vrk[u] = ld8<T>(cand_row<T, DH>(s, g, kbk, b, h, rr[u], false) + 8 * c);
-          vrv[u] = ld8<T>(cand_row<T, DH>(s, g, vbk, b, h, rr[u], true) + 8 * c);
-          vg[u] = c == 0 ? cand_gate(s, g, gb, b, rr[u]) : 0.f;
-        }
+        const int c = min(i, n_raw - 1) % CH;
+        vrk[u] = ld8<T>(cand_row<T, DH>(s, g, kbk, b, h, rr[u], false) + 8 * c);
+        vrv[u] = ld8<T>(cand_row<T, DH>(s, g, vbk, b, h, rr[u], true) + 8 * c);
+        vg[u] = *cand_gate_ptr(s, g, gb, b, rr[u]);
       }
 #pragma unroll
       for (int u = 0; u < UR; ++u) {
