@@ -1897,6 +1897,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     pair = id / nqb;
     qb = id % nqb;
   }
+  // causal: the q-blocks with the most keys go out first, so the last
+  // workgroups of the launch are short ones
+  if (a_.causal) qb = nqb - 1 - qb;
   const int hk = pair % a.Hkv, b = pair / a.Hkv;
   const int G = a.H / a.Hkv;
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
