@@ -285,11 +285,24 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-# the prefill attention kernels the dispatch (attn.hip launch_f3) runs, named
-# as rocprofv3 prints them: queries roped in-kernel with the noise rotation
-# (layer path), and given noise queries (the diff_flash_attn seam, configs[3])
-F3_ROPED = "attn_f3_bf16<128, 8, 0, true>"
-F3_GIVEN_NOISE = "attn_f3_bf16<128, 8, 2, false>"
+# the prefill attention kernels the dispatch (attn.hip launch_f3_qm) runs,
+# named as rocprofv3 prints them: queries roped in-kernel with the noise
+# rotation (layer path), and given noise queries (the diff_flash_attn seam,
+# configs[3], whose 4096 workgroups of 8 waves fill the chip)
+F3_GIVEN_NOISE = "attn_f3_bf16<128, 8, 2, false, 4>"
+
+
+def f3_roped(torch, G, Lq, B, Hkv, chunks):
+    """The roped-query attention kernel of a launch over `chunks` chunks
+    (0: one chunk, as the descriptor says) of Lq queries: 4 waves and two
+    tile stages for launches of several chunks and for grids whose 8-wave
+    workgroups would leave CUs idle (G <= 4), else 8 waves and four stages
+    (attn.hip launch_f3_qm)."""
+    rows8 = 16 * (8 // G)
+    n8 = -(-Lq // rows8) * B * Hkv * max(chunks, 1)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    small = G <= 4 and (chunks > 1 or n8 < cus)
+    return "attn_f3_bf16<128, %d, 0, true, %d>" % ((4, 2) if small else (8, 4))
 
 
 def prefill_hot_path(coda, m, q, k_raw, v, gate, lam, k_out, st, blk, heads):
@@ -404,20 +417,23 @@ def bench_prefill(torch, coda, m, a, blk):
         chunked = chunked_attention_timing(torch, coda, m, q, k, v, lam, cos, sin, heads, blk, 5)
     flops1 = prefill_chunk_flops(m, B, blk, n_prefix)
     tflops1 = flops1 / (attn_ms * 1e-3) / 1e12
-    single = {"kernel": F3_ROPED, "what": "one chunk at the full 384-slot state prefix (the dispatch of the first "
-                                          "chunks of a call that continues a state)",
+    G = m.num_heads // m.num_kv_heads
+    k1 = f3_roped(torch, G, blk, B, m.num_kv_heads, 0)
+    single = {"kernel": k1, "what": "one chunk at the full 384-slot state prefix (the dispatch of the first "
+                                    "chunks of a call that continues a state)",
               "achieved": round(tflops1, 2), "frac": round(tflops1 / BF16_PEAK_TFLOPS, 4), "flops_per_launch": flops1,
               "avg_launch_ms": round(attn_ms, 5), "valid_prefix_slots": n_prefix,
-              "traffic": profile_traffic("prefill_chunk_b%d_blk%d %s" % (B, blk, F3_ROPED))}
+              "traffic": profile_traffic("prefill_chunk_b%d_blk%d %s" % (B, blk, k1))}
     if chunked is not None:
         ms, flops, n = chunked
         tflops = flops / (ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": F3_ROPED + " (a group of the call's chunks in one launch, "
-                                                      "coda_prefill_attn_chunks)",
+        kn = f3_roped(torch, G, blk, B, m.num_kv_heads, n)
+        roof = {"bound": "mfma", "kernel": kn + " (a group of the call's chunks in one launch, "
+                                                "coda_prefill_attn_chunks)",
                 "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "flops_per_launch": flops, "avg_launch_ms": round(ms, 5),
                 "chunks_per_launch": n, "us_per_chunk": round(ms * 1e3 / n, 3),
-                "traffic": profile_traffic("prefill_call_b%d_blk%d %s" % (B, blk, F3_ROPED)),
+                "traffic": profile_traffic("prefill_call_b%d_blk%d %s" % (B, blk, kn)),
                 "single_chunk": single}
     else:
         roof = dict({"bound": "mfma", "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s"}, **single)
@@ -508,14 +524,16 @@ def bench_prefill_c5(torch, coda, a, B=8, L=8192, blk=256):
         chunked = chunked_attention_timing(torch, coda, m, q, k, v, lam, cos, sin, heads, blk, 5)
     flops1 = prefill_chunk_flops(m, B, blk, n_prefix)
     tflops1 = flops1 / (attn_ms * 1e-3) / 1e12
-    single = {"kernel": F3_ROPED, "what": "one chunk at the full state prefix", "achieved": round(tflops1, 2),
+    k1 = f3_roped(torch, m.num_heads // m.num_kv_heads, blk, B, m.num_kv_heads, 0)
+    single = {"kernel": k1, "what": "one chunk at the full state prefix", "achieved": round(tflops1, 2),
               "frac": round(tflops1 / BF16_PEAK_TFLOPS, 4), "flops_per_launch": flops1,
               "avg_launch_ms": round(attn_ms, 5), "valid_prefix_slots": n_prefix}
     if chunked is not None:
         ms, flops, n = chunked
         tflops = flops / (ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "kernel": F3_ROPED + " (a group of the call's chunks in one launch, "
-                                                      "coda_prefill_attn_chunks)",
+        kn = f3_roped(torch, m.num_heads // m.num_kv_heads, blk, B, m.num_kv_heads, n)
+        roof = {"bound": "mfma", "kernel": kn + " (a group of the call's chunks in one launch, "
+                                                "coda_prefill_attn_chunks)",
                 "achieved": round(tflops, 2), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "flops_per_launch": flops, "avg_launch_ms": round(ms, 5),
                 "chunks_per_launch": n, "us_per_chunk": round(ms * 1e3 / n, 3), "single_chunk": single}

@@ -1820,11 +1820,28 @@ struct F2Layout {
 //   phase C: the 4 NDB products of O += V(it)^T P(it), each followed by the
 //            mask and running-max work of two entries of S(it + 1);
 //   then the lazy rescale (only when a row max moves by more than 2^8).
-// Four tiles live in LDS (it, it + 1, and it + 2, it + 3 loading), so one
-// barrier per tile suffices and a tile's loads have two iterations to land.
+// NS = 4: four tiles live in LDS (it, it + 1, and it + 2, it + 3 loading),
+// so one barrier per tile suffices and a tile's loads have two iterations
+// to land; 128 KiB, one workgroup a CU.  NS = 2: K and V in two buffers
+// each, K one tile ahead (iteration it reads K(it + 1) and V(it) while
+// K(it + 2) and V(it + 1) load into the buffers of K(it) and V(it - 1));
+// 64 KiB, so two workgroups of 4 waves share a CU and one's prologue,
+// epilogue and barriers overlap the other's products; a tile's loads have
+// one iteration to land.
 // Whole tiles inside the prefix or the block load from a wave-uniform base
 // plus per-lane offsets.
 static constexpr int kTabRows = 64;  // query rows whose RoPE tables attn_f3_bf16 stages in LDS
+template <int DH>
+constexpr int f3_tab_pitch() { return DH / 2 + 8; }  // table row pitch in LDS (bf16)
+// NS = 2: the tables sit in the second V buffer and may run past it
+template <int DH>
+constexpr int f3_table_offset() { return 2 * F2Layout<DH>::KBYTES + F2Layout<DH>::VBYTES; }
+template <int DH, int NS>
+constexpr size_t f3_lds_bytes() {
+  constexpr size_t tiles = (size_t)NS * (F2Layout<DH>::KBYTES + F2Layout<DH>::VBYTES);
+  constexpr size_t tabs = f3_table_offset<DH>() + 2 * 2 * (size_t)kTabRows * f3_tab_pitch<DH>() + 2 * 2 * 8 * (DH / 2);
+  return NS == 4 || tabs < tiles ? tiles : tabs;
+}
 
 // Chunks of a prefill call in one launch (coda_prefill_attn_chunks):
 // blockIdx.y = chunk c_first + y, covering queries [t0, t0 + Lq) of the
@@ -1864,14 +1881,14 @@ __device__ __forceinline__ coda_attn_desc chunk_view(const coda_attn_desc& a0, c
   return a;
 }
 
-template <int DH, int NW, int QM, bool TB>
+template <int DH, int NW, int QM, bool TB, int NS>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_f3_bf16(
     const coda_attn_desc a_, int NQ, int nqb, int npairs, ChunkGeom cg) {
   const coda_attn_desc a = chunk_view<DH>(a_, cg);
   using Lay = F2Layout<DH>;
-  constexpr int NS = 4;
+  static_assert(NS == 2 || NS == 4, "tile stages");
   static_assert(!TB || QM == 0 || QM == 1, "tables staged for the RoPE + rotation query cases");
-  constexpr int kTabPitch = DH / 2 + 8;  // table row pitch in LDS (bf16)
+  constexpr int kTabPitch = f3_tab_pitch<DH>();
   constexpr int KT = Lay::KT, NKS = Lay::NKS, NDB = Lay::NDB, KCH = Lay::KCH, VCH = Lay::VCH;
   constexpr int KCW = (KCH + NW - 1) / NW, VCW = (VCH + NW - 1) / NW;
   static_assert(KCH % NW == 0 && VCH % NW == 0, "tile pieces split evenly over the waves");
@@ -1883,9 +1900,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   // loop would spill)
   __shared__ float lam_lds[NW * 16];
   // TB: cos / sin rows of the workgroup's queries, cos / sin of its heads'
-  // noise angles
-  __shared__ __attribute__((aligned(16))) bf16_t tab_rope[TB ? 2 : 1][TB ? kTabRows * kTabPitch : 8];
-  __shared__ __attribute__((aligned(16))) bf16_t tab_th[TB ? 2 : 1][TB ? 8 * (DH / 2) : 8];
+  // noise angles.  NS 2: in the second V buffer (its first tile load goes
+  // out after the barrier that follows every wave's table reads)
+  constexpr bool TBS = TB && NS == 4;
+  __shared__ __attribute__((aligned(16))) bf16_t tab_rope_s[TBS ? 2 : 1][TBS ? kTabRows * kTabPitch : 8];
+  __shared__ __attribute__((aligned(16))) bf16_t tab_th_s[TBS ? 2 : 1][TBS ? 8 * (DH / 2) : 8];
+  bf16_t* const tab_rope0 = TBS ? &tab_rope_s[0][0] : (bf16_t*)(f3_smem + f3_table_offset<DH>());
+  bf16_t* const tab_rope1 = TBS ? &tab_rope_s[1][0] : tab_rope0 + kTabRows * kTabPitch;
+  bf16_t* const tab_th0 = TBS ? &tab_th_s[0][0] : tab_rope0 + 2 * kTabRows * kTabPitch;
+  bf16_t* const tab_th1 = TBS ? &tab_th_s[1][0] : tab_th0 + 8 * (DH / 2);
 
   const int id = blockIdx.x;
   int qb, pair;
@@ -1929,24 +1952,38 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int v_r = lane / Lay::CPR, v_c = 8 * Lay::vchunk(v_r, lane % Lay::CPR);
   const uint32_t kofP = 2u * (uint32_t)(k_r * psl + k_c), kofB = 2u * (uint32_t)(k_r * bsl + k_c);
   const uint32_t vofP = 2u * (uint32_t)(v_r * psl + v_c), vofB = 2u * (uint32_t)(v_r * bsl + v_c);
-  auto tile_load = [&](int kt0, int bi) {
-    char* kd = f3_smem + bi * STAGE;
-    char* vd = kd + Lay::KBYTES;
+  // K / V buffers of tile t
+  auto kbuf = [&](int t) -> char* {
+    return NS == 4 ? f3_smem + (t % 4) * STAGE : f3_smem + (t & 1) * Lay::KBYTES;
+  };
+  auto vbuf = [&](int t) -> char* {
+    return NS == 4 ? f3_smem + (t % 4) * STAGE + Lay::KBYTES : f3_smem + 2 * Lay::KBYTES + (t & 1) * Lay::VBYTES;
+  };
+  // tile t's K (WK) and / or V (WV) pieces of this wave
+  auto tile_part = [&](auto wk_c, auto wv_c, int t) {
+    constexpr bool WK = decltype(wk_c)::value, WV = decltype(wv_c)::value;
+    const int kt0 = t * KT;
+    char* kd = kbuf(t);
+    char* vd = vbuf(t);
     const bool in_p = kt0 + KT <= a.Lp, in_b = kt0 >= a.Lp && kt0 + KT <= Lk;
     if (in_p || in_b) {
       const char* kb0 = in_p ? (const char*)(kpb + (int64_t)kt0 * psl) : (const char*)(kbb + (int64_t)(kt0 - a.Lp) * bsl);
       const char* vb0 = in_p ? (const char*)(vpb + (int64_t)kt0 * psl) : (const char*)(vbb + (int64_t)(kt0 - a.Lp) * bsl);
       const int sl2 = 2 * (in_p ? psl : bsl);
       const uint32_t kof = in_p ? kofP : kofB, vof = in_p ? vofP : vofB;
+      if constexpr (WK) {
 #pragma unroll
-      for (int j = 0; j < KCW; ++j) {
-        const int ci = wv + NW * j, kb = ci / NKS, ks = ci % NKS;
-        lds_load16(kb0 + (int64_t)(32 * kb) * sl2 + 32 * ks + kof, kd + ci * 1024);
+        for (int j = 0; j < KCW; ++j) {
+          const int ci = wv + NW * j, kb = ci / NKS, ks = ci % NKS;
+          lds_load16(kb0 + (int64_t)(32 * kb) * sl2 + 32 * ks + kof, kd + ci * 1024);
+        }
       }
+      if constexpr (WV) {
 #pragma unroll
-      for (int j = 0; j < VCW; ++j) {
-        const int vi = wv + NW * j;
-        lds_load16(vb0 + (int64_t)(Lay::RPI * vi) * sl2 + vof, vd + vi * 1024);
+        for (int j = 0; j < VCW; ++j) {
+          const int vi = wv + NW * j;
+          lds_load16(vb0 + (int64_t)(Lay::RPI * vi) * sl2 + vof, vd + vi * 1024);
+        }
       }
     } else {
       // a tile across the prefix / block boundary or the end: per row
@@ -1955,18 +1992,25 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         kidx = kidx < Lk ? kidx : 0;
         return kidx < a.Lp ? pb + (int64_t)kidx * psl : bb + (int64_t)(kidx - a.Lp) * bsl;
       };
+      if constexpr (WK) {
 #pragma unroll
-      for (int j = 0; j < KCW; ++j) {
-        const int ci = wv + NW * j, kb = ci / NKS, ks = ci % NKS;
-        lds_load16(row_of(kpb, kbb, kt0 + 32 * kb + k_r) + 16 * ks + k_c, kd + ci * 1024);
+        for (int j = 0; j < KCW; ++j) {
+          const int ci = wv + NW * j, kb = ci / NKS, ks = ci % NKS;
+          lds_load16(row_of(kpb, kbb, kt0 + 32 * kb + k_r) + 16 * ks + k_c, kd + ci * 1024);
+        }
       }
+      if constexpr (WV) {
 #pragma unroll
-      for (int j = 0; j < VCW; ++j) {
-        const int vi = wv + NW * j;
-        lds_load16(row_of(vpb, vbb, kt0 + Lay::RPI * vi + v_r) + v_c, vd + vi * 1024);
+        for (int j = 0; j < VCW; ++j) {
+          const int vi = wv + NW * j;
+          lds_load16(row_of(vpb, vbb, kt0 + Lay::RPI * vi + v_r) + v_c, vd + vi * 1024);
+        }
       }
     }
   };
+  using TrueC = std::integral_constant<bool, true>;
+  using FalseC = std::integral_constant<bool, false>;
+  auto tile_load = [&](int t) { tile_part(TrueC{}, TrueC{}, t); };
   constexpr int LPT = KCW + VCW;  // direct loads per wave and tile
 
   // ---- prologue.  VMEM loads complete in issue order, so the loads the
@@ -2152,7 +2196,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
           const int cc = th ? c - nrope : c;
           const int lgn = th ? lg_g : lg_row;
           const int which = cc >> (lgn + lg_tch), rr = (cc >> lg_tch) & ((1 << lgn) - 1), ch = cc & (TCH - 1);
-          bf16_t* dst = th ? &tab_th[which][rr * half + 8 * ch] : &tab_rope[which][rr * kTabPitch + 8 * ch];
+          bf16_t* dst = th ? (which ? tab_th1 : tab_th0) + rr * half + 8 * ch
+                           : (which ? tab_rope1 : tab_rope0) + rr * kTabPitch + 8 * ch;
           *reinterpret_cast<uint4*>(dst) = tv[u];
         }
       }
@@ -2162,21 +2207,27 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
       for (int u = 0; u < NOWN; ++u) {
         const int d0 = 16 * (ks_base + u) + 8 * hl;
         if (inter) {
-          rc2[u] = *reinterpret_cast<const uint2*>(&tab_rope[0][rl * kTabPitch + d0 / 2]);
-          rs2[u] = *reinterpret_cast<const uint2*>(&tab_rope[1][rl * kTabPitch + d0 / 2]);
+          rc2[u] = *reinterpret_cast<const uint2*>(tab_rope0 + rl * kTabPitch + d0 / 2);
+          rs2[u] = *reinterpret_cast<const uint2*>(tab_rope1 + rl * kTabPitch + d0 / 2);
         } else {
           const int f0 = d0 < half ? d0 : d0 - half;
-          rc[u] = *reinterpret_cast<const uint4*>(&tab_rope[0][rl * kTabPitch + f0]);
-          rs[u] = *reinterpret_cast<const uint4*>(&tab_rope[1][rl * kTabPitch + f0]);
+          rc[u] = *reinterpret_cast<const uint4*>(tab_rope0 + rl * kTabPitch + f0);
+          rs[u] = *reinterpret_cast<const uint4*>(tab_rope1 + rl * kTabPitch + f0);
         }
-        tcs[u] = *reinterpret_cast<const uint2*>(&tab_th[0][g * half + d0 / 2]);
-        tsn[u] = *reinterpret_cast<const uint2*>(&tab_th[1][g * half + d0 / 2]);
+        tcs[u] = *reinterpret_cast<const uint2*>(tab_th0 + g * half + d0 / 2);
+        tsn[u] = *reinterpret_cast<const uint2*>(tab_th1 + g * half + d0 / 2);
       }
     }
-    // tiles 0 .. NS-2 behind everything else
+    // tiles 0 .. NS-2 behind everything else (NS 2: K(0), K(1), V(0))
+    if constexpr (NS == 4) {
 #pragma unroll
-    for (int t = 0; t < NS - 1; ++t)
-      if (t < ntile) tile_load(t * KT, t);
+      for (int t = 0; t < NS - 1; ++t)
+        if (t < ntile) tile_load(t);
+    } else {
+      if (ntile > 0) tile_part(TrueC{}, FalseC{}, 0);
+      if (ntile > 1) tile_part(TrueC{}, FalseC{}, 1);
+      if (ntile > 0) tile_part(FalseC{}, TrueC{}, 0);
+    }
 #pragma unroll
     for (int u = 0; u < NOWN; ++u) {
       const int d0 = 16 * (ks_base + u) + 8 * hl;
@@ -2312,7 +2363,10 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 
   // ---- S(0), masked, max folded
   if (ntile > 0) {
-    vm_wait(LPT * (min(ntile, NS - 1) - 1));
+    if constexpr (NS == 4)
+      vm_wait(LPT * (min(ntile, NS - 1) - 1));
+    else
+      vm_wait(ntile > 1 ? KCW + VCW : VCW);
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_s_barrier();
     const uint32_t ka = lds_addr(f3_smem) + 16 * lane;
@@ -2347,11 +2401,22 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int kt0 = it * KT, kt1 = kt0 + KT;
     // tile it + 1 has landed and every wave has finished iteration it - 1
     // (so tile it - 1's buffer may take tile it + 2)
-    if (has_next) {
-      vm_wait(it + 2 < ntile ? LPT : 0);
+    if constexpr (NS == 4) {
+      if (has_next) {
+        vm_wait(it + 2 < ntile ? LPT : 0);
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_s_barrier();
+        if (it + 3 < ntile) tile_load(it + 3);
+      }
+    } else {
+      // K(it + 1) and V(it), the only loads in flight, have landed and every
+      // wave has finished iteration it - 1 (so K(it)'s buffer may take
+      // K(it + 2) and V(it - 1)'s V(it + 1))
+      vm_wait(0);
       __builtin_amdgcn_s_waitcnt(0xc07f);
       __builtin_amdgcn_s_barrier();
-      if (it + 3 < ntile) tile_load(kt1 + 2 * KT, (it + 3) % NS);
+      if (it + 2 < ntile) tile_part(TrueC{}, FalseC{}, it + 2);
+      if (has_next) tile_part(FalseC{}, TrueC{}, it + 1);
     }
     const float mu = m_s == -INFINITY ? 0.f : m_s;
     uint32_t pw[16];  // P(it) as bf16 pairs: word e / 2 holds entries e, e + 1 (e = 16 kb + j)
@@ -2366,7 +2431,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     };
     // ---- phase A: S(it + 1) products, each with one pair of P(it)
     if (has_next) {
-      const uint32_t ka = lds_addr(f3_smem + ((it + 1) % NS) * STAGE) + 16 * lane;
+      const uint32_t ka = lds_addr(kbuf(it + 1)) + 16 * lane;
       u32x4v_t kr[4];
       auto k_issue = [&](auto f_c) {
         constexpr int f = decltype(f_c)::value;
@@ -2397,7 +2462,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     // there is no next tile, whose max is then dropped)
     float mx = -INFINITY;
     {
-      const uint32_t va = lds_addr(f3_smem + (it % NS) * STAGE + Lay::KBYTES);
+      const uint32_t va = lds_addr(vbuf(it));
       constexpr int NPV = 4 * NDB;
       uint2 rd[3][2];
       auto v_issue = [&](auto q_c) {
@@ -2554,18 +2619,43 @@ static bool flash_offsets_fit(const coda_attn_desc* d) {
 
 // pipelined 32-row flash tiles: 8 waves, G heads x 8 / G groups of 16
 // queries; QM the query case (see attn_f3_bf16)
-template <int DH, int QM, bool TB>
-static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G, const ChunkGeom& cg) {
-  constexpr int NW = 8;
+template <int DH, int QM, bool TB, int NW, int NS>
+static int launch_f3_nw(const coda_attn_desc* d, hipStream_t st, int G, const ChunkGeom& cg) {
   const int npairs = d->B * d->Hkv;
   const int NQ = NW / G;
   const int nblk = (d->Lq + 16 * NQ - 1) / (16 * NQ);
-  const size_t lds = 4 * (size_t)(F2Layout<DH>::KBYTES + F2Layout<DH>::VBYTES);
-  int rc = lds_limit<attn_f3_bf16<DH, NW, QM, TB>>(lds, "coda_diff_attn_fwd");
+  const size_t lds = f3_lds_bytes<DH, NS>();
+  int rc = lds_limit<attn_f3_bf16<DH, NW, QM, TB, NS>>(lds, "coda_diff_attn_fwd");
   if (rc) return rc;
-  hipLaunchKernelGGL((attn_f3_bf16<DH, NW, QM, TB>), dim3(nblk * npairs, cg.n > 0 ? cg.n : 1), dim3(NW * 64), lds,
-                     st, *d, NQ, nblk, npairs, cg);
+  hipLaunchKernelGGL((attn_f3_bf16<DH, NW, QM, TB, NS>), dim3(nblk * npairs, cg.n > 0 ? cg.n : 1), dim3(NW * 64),
+                     lds, st, *d, NQ, nblk, npairs, cg);
   return check_launch("attn_f3_bf16");
+}
+// compute units of the current device (read once per device)
+static int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+// 4-wave workgroups with two tile stages (two a CU) for launches of several
+// chunks and for grids whose 8-wave workgroups would leave CUs idle (G <= 4:
+// a 4-wave workgroup still holds every head of its KV head); a one-chunk or
+// unbounded grid that gives every CU an 8-wave workgroup keeps 8 waves and
+// four stages, whose deeper prefetch serves a grid that starts all at once
+template <int DH, int QM, bool TB>
+static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G, const ChunkGeom& cg) {
+  if (G <= 4) {
+    const int64_t rows8 = 16 * (8 / G);
+    const int64_t n8 = (d->Lq + rows8 - 1) / rows8 * d->B * d->Hkv * (cg.n > 0 ? cg.n : 1);
+    if (cg.n > 1 || n8 < device_cus()) return launch_f3_nw<DH, QM, TB, 4, 2>(d, st, G, cg);
+  }
+  return launch_f3_nw<DH, QM, TB, 8, 4>(d, st, G, cg);
 }
 template <int DH>
 static int launch_f3(const coda_attn_desc* d, hipStream_t st, int G, const ChunkGeom& cg = ChunkGeom{}) {

@@ -39,6 +39,9 @@ ATTN_CASES = [
     (torch.bfloat16, 2, 4, 4, 33, 300, 32, True),
     (torch.bfloat16, 1, 64, 8, 40, 296, 128, True),
     (torch.bfloat16, 1, 16, 2, 2, 50, 64, True),
+    # a grid of 256 eight-wave workgroups (head_dim 64, G = 2): the launcher's
+    # 8-wave, four-stage variant (smaller G <= 4 grids take 4 waves, two stages)
+    (torch.bfloat16, 8, 8, 4, 512, 512, 64, True),
 ]
 
 

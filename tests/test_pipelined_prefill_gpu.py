@@ -159,3 +159,37 @@ def test_pipelined_paths_equal_chunk_by_chunk(name, monkeypatch):
         assert_close(h, h_ref, dtype, f"{name} {mode}: heads")
         compare_states(st, _cpu_copy(st_ref), dtype, W, Me, f"{name} {mode} vs chunk by chunk")
     p.check_bank_status()
+
+
+@pytest.mark.parametrize("case", ["four_launch_fallback", "short_calls"])
+@torch.no_grad()
+def test_pipelined_prefill_fallbacks_match_oracle(case, monkeypatch):
+    """Where the chain cannot run, the layer falls back without losing
+    state: with the one-launch update switched off (CODA_BLOCK_FUSED=0) the
+    chain call returns CODA_EUNSUP before enqueueing anything and the call
+    continues chunk by chunk on the four-launch update; calls shorter than
+    one block, and calls of exactly one block, take the ordinary paths.
+    Heads and the whole state against the oracle after every call."""
+    _need_gpu()
+    from coda_oracle import prims
+    name = "g4_b4_blk128_groups3"
+    H, Hkv, Dh, W, Me, Ms, B, L, block, kind, _ = CASES[name]
+    print(f"[pipelined fallbacks] {case}", flush=True)
+    dtype = torch.bfloat16
+    m, p, st_o = _layers(name)
+    st_p = to_product_state(st_o, DEV)
+    if case == "four_launch_fallback":
+        monkeypatch.setenv("CODA_BLOCK_FUSED", "0")
+        lengths = (L, block * 2 + 17)
+    else:
+        lengths = (100, block, 3, block * 3 + 1, 57)
+    g = torch.Generator().manual_seed(56)
+    for call, Lc in enumerate(lengths):
+        q, k, v, gate, lam = _inputs(m, B, Lc, kind, g)
+        c, s = m.rope_tables(Lc, st_o.pos, dtype)
+        heads_o = m.prefill_core(prims.rope(q, c, s, m.rope_interleaved), k, v, gate, lam, st_o, block_size=block)
+        heads_p = _run(p, st_p, q, k, v, gate, lam, c, s, block)
+        torch.cuda.synchronize()
+        assert_close(heads_p.permute(0, 2, 1, 3), heads_o, dtype, f"{case} call {call} ({Lc} tokens) heads")
+        compare_states(st_p, st_o, dtype, W, Me, f"{case} call {call} ({Lc} tokens)")
+    p.check_bank_status()
