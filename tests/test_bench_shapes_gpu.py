@@ -17,7 +17,8 @@ from __future__ import annotations
 import pytest
 import torch
 
-from parity_util import assert_close, compare_states, compare_traces, product_like, to_product_state
+from parity_util import (assert_close, assert_heads, compare_states, compare_traces, fp32_attention, product_like,
+                         to_product_state)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -32,6 +33,10 @@ SHAPES = {
     # the 7B layer itself at the decode bench's batch: B * Hkv = 512, so the
     # routing and write-back kernels run one workgroup per (sequence, head)
     "c2_full_b64_blk256": (32, 8, 128, 256, 64, 64, 64, 640, 256, "const", 4, torch.bfloat16),
+    # the 7B layer at configs[1]'s other decode batches (B = 1: 8 workgroups
+    # for 256 CUs; B = 16: 128)
+    "c1_full_b1_blk256": (32, 8, 128, 256, 64, 64, 1, 896, 256, "random", 8, torch.bfloat16),
+    "c1_full_b16_blk256": (32, 8, 128, 256, 64, 64, 16, 640, 256, "random", 6, torch.bfloat16),
     # configs[4] per-KV-head shape (70B: 64 / 8 heads -> G = 8), large cache
     "c5_g8_b4_blk256": (16, 2, 128, 512, 128, 128, 4, 2048, 256, "random", 4, torch.bfloat16),
     "c5_full_b2_blk256": (64, 8, 128, 512, 128, 128, 2, 1280, 256, "const", 4, torch.bfloat16),
@@ -64,12 +69,19 @@ def _inputs(m, B, L, dtype, kind, g):
 
 
 def _prefill_both(m, p, st_o, st_p, q, k, v, gate, lam, block, dtype, what):
-    """One prefill call on each side; heads, slot decisions (every chunk's
-    candidates, exact and summary routing) and the whole state compared."""
+    """One prefill call on each side; heads (against the oracle and against
+    its attention evaluated in fp32 on a copy of the same state), slot
+    decisions (every chunk's candidates, exact and summary routing) and the
+    whole state compared."""
+    import copy
     from coda_oracle import prims
     L = q.shape[2]
     c, s = m.rope_tables(L, st_o.pos, dtype)
     q_r = prims.rope(q, c, s, m.rope_interleaved)
+    st_f = copy.deepcopy(st_o)
+    with fp32_attention(m):
+        heads_f = m.prefill_core(q_r, k, v, gate, lam, st_f, block_size=block)
+    del st_f
     tr_o = []
     p.decision_trace = []
     heads_o = m.prefill_core(q_r, k, v, gate, lam, st_o, block_size=block, trace=tr_o)
@@ -78,8 +90,8 @@ def _prefill_both(m, p, st_o, st_p, q, k, v, gate, lam, block, dtype, what):
     torch.cuda.synchronize()
     n = compare_traces(p.decision_trace, tr_o, m, f"{what} decisions")
     p.decision_trace = None
-    assert_close(heads_p.permute(0, 2, 1, 3), heads_o, dtype, f"{what} heads")
-    del heads_o, heads_p
+    assert_heads(heads_p.permute(0, 2, 1, 3), heads_o, heads_f, dtype, f"{what} heads")
+    del heads_o, heads_p, heads_f
     compare_states(st_p, st_o, dtype, m.window, m.Me, what)
     return n
 
@@ -128,13 +140,15 @@ def test_bench_shape_trajectory_matches_oracle(name):
         raw = t % 4 in (1, 2)
         banks.write_one(m, st_o, prims.rope(kn, ct, sn, m.rope_interleaved) if raw else kn, vn, gn, tr_o)
         ho = m.attend_core(qt, lamt, st_o, qp)
+        with fp32_attention(m):
+            hf = m.attend_core(qt, lamt, st_o, qp)
         hp = p.decode_step_core(qt.to(DEV), kn.to(DEV), vn.to(DEV), gn.reshape(B).to(DEV), lamt.squeeze(-1).to(DEV),
                                 st_p, ct.to(DEV), sn.to(DEV), k_roped=not raw)
         torch.cuda.synchronize()
         if traced:
             compare_traces(p.decision_trace, tr_o, m, f"{name} decode step {t} decisions")
         p.decision_trace = None
-        assert_close(hp.permute(0, 2, 1, 3), ho, dtype, f"{name} decode step {t} heads")
+        assert_heads(hp.permute(0, 2, 1, 3), ho, hf, dtype, f"{name} decode step {t} heads")
         compare_states(st_p, st_o, dtype, W, Me, f"{name} decode step {t}")
 
 
