@@ -288,20 +288,20 @@ def main():
 # the prefill attention kernels the dispatch (attn.hip launch_f3_qm) runs,
 # named as rocprofv3 prints them: queries roped in-kernel with the noise
 # rotation (layer path), and given noise queries (the diff_flash_attn seam,
-# configs[3], whose 4096 workgroups of 8 waves fill the chip)
-F3_GIVEN_NOISE = "attn_f3_bf16<128, 8, 2, false, 4>"
+# 4096 eight-wave workgroups' worth, so the 4-wave kernel)
+F3_GIVEN_NOISE = "attn_f3_bf16<128, 4, 2, false, 2>"
 
 
 def f3_roped(torch, G, Lq, B, Hkv, chunks):
     """The roped-query attention kernel of a launch over `chunks` chunks
     (0: one chunk, as the descriptor says) of Lq queries: 4 waves and two
-    tile stages for launches of several chunks and for grids whose 8-wave
-    workgroups would leave CUs idle (G <= 4), else 8 waves and four stages
-    (attn.hip launch_f3_qm)."""
+    tile stages for G <= 4, except a one-launch grid whose 8-wave
+    workgroups fill the CUs once (at least one a CU, fewer than two): 8
+    waves and four stages (attn.hip launch_f3_qm)."""
     rows8 = 16 * (8 // G)
     n8 = -(-Lq // rows8) * B * Hkv * max(chunks, 1)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    small = G <= 4 and (chunks > 1 or n8 < cus)
+    small = G <= 4 and (chunks > 1 or n8 < cus or n8 >= 2 * cus)
     return "attn_f3_bf16<128, %d, 0, true, %d>" % ((4, 2) if small else (8, 4))
 
 

@@ -2649,17 +2649,20 @@ static int device_cus() {
   }
   return n;
 }
-// 4-wave workgroups with two tile stages (two a CU) for launches of several
-// chunks and for grids whose 8-wave workgroups would leave CUs idle (G <= 4:
-// a 4-wave workgroup still holds every head of its KV head); a one-chunk or
-// unbounded grid that gives every CU an 8-wave workgroup keeps 8 waves and
-// four stages, whose deeper prefetch serves a grid that starts all at once
+// 4-wave workgroups with two tile stages (two a CU) for G <= 4 (a 4-wave
+// workgroup still holds every head of its KV head), except a one-launch grid
+// whose 8-wave workgroups fill the CUs once (at least one a CU, fewer than
+// two): it keeps 8 waves and four stages, whose deeper prefetch serves a
+// grid that starts all at once (measured: a block-256 chunk at B = 4, 36 vs
+// 38 us; 4 waves win for grouped launches, small grids and configs[3]'s
+// 4096 workgroups)
 template <int DH, int QM, bool TB>
 static int launch_f3_qm(const coda_attn_desc* d, hipStream_t st, int G, const ChunkGeom& cg) {
   if (G <= 4) {
     const int64_t rows8 = 16 * (8 / G);
     const int64_t n8 = (d->Lq + rows8 - 1) / rows8 * d->B * d->Hkv * (cg.n > 0 ? cg.n : 1);
-    if (cg.n > 1 || n8 < device_cus()) return launch_f3_nw<DH, QM, TB, 4, 2>(d, st, G, cg);
+    const int64_t cus = device_cus();
+    if (cg.n > 1 || n8 < cus || n8 >= 2 * cus) return launch_f3_nw<DH, QM, TB, 4, 2>(d, st, G, cg);
   }
   return launch_f3_nw<DH, QM, TB, 8, 4>(d, st, G, cg);
 }

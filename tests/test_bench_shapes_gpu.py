@@ -37,6 +37,9 @@ SHAPES = {
     # for 256 CUs; B = 16: 128)
     "c1_full_b1_blk256": (32, 8, 128, 256, 64, 64, 1, 896, 256, "random", 8, torch.bfloat16),
     "c1_full_b16_blk256": (32, 8, 128, 256, 64, 64, 16, 640, 256, "random", 6, torch.bfloat16),
+    # configs[2]'s layer at B = 4: the second call's first chunks run one by
+    # one, 256 eight-wave attention workgroups (the 8-wave, four-stage kernel)
+    "c2_full_b4_blk256": (32, 8, 128, 256, 64, 64, 4, 1024, 256, "random", 4, torch.bfloat16),
     # configs[4] per-KV-head shape (70B: 64 / 8 heads -> G = 8), large cache
     "c5_g8_b4_blk256": (16, 2, 128, 512, 128, 128, 4, 2048, 256, "random", 4, torch.bfloat16),
     "c5_full_b2_blk256": (64, 8, 128, 512, 128, 128, 2, 1280, 256, "const", 4, torch.bfloat16),
