@@ -2623,8 +2623,8 @@ static bool flash_offsets_fit(const coda_attn_desc* d) {
          (d->Lb == 0 || (d->b_sl >= 0 && ((int64_t)d->Lb + 64) * d->b_sl < lim));
 }
 
-// pipelined 32-row flash tiles: 8 waves, G heads x 8 / G groups of 16
-// queries; QM the query case (see attn_f3_bf16)
+// pipelined 32-row flash tiles: NW waves, G heads x NW / G groups of 16
+// queries, NS tile stages; QM the query case (see attn_f3_bf16)
 template <int DH, int QM, bool TB, int NW, int NS>
 static int launch_f3_nw(const coda_attn_desc* d, hipStream_t st, int G, const ChunkGeom& cg) {
   const int npairs = d->B * d->Hkv;
