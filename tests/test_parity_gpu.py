@@ -266,6 +266,36 @@ def test_unbounded_matches_oracle():
         assert_close(y, yo, dtype, f"unbounded y {dtype}", TOL[dtype] * 3)
 
 
+@pytest.mark.parametrize("B,H,Hkv,L,Dh", [(1, 32, 8, 1024, 128), (8, 8, 4, 512, 64)])
+@torch.no_grad()
+def test_flash_variants_agree_bitwise(B, H, Hkv, L, Dh):
+    """The two forms of the MFMA flash kernel give the same bits: the launch
+    takes 8 waves and four tile stages when its 8-wave grid fills the CUs
+    once (here the full problem: 256 such workgroups), and 4 waves and two
+    stages for a smaller grid (here its first two KV heads' share alone);
+    each wave's work and order are the same, so the heads of those KV heads
+    must be bit-identical (causal, given noise queries, bf16)."""
+    _need_gpu()
+    import coda_gqa_l
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the grid sizes here are chosen for a 256-CU part")
+    print(f"[flash variants] B{B} H{H} Hkv{Hkv} L{L} Dh{Dh}", flush=True)
+    g = torch.Generator().manual_seed(77)
+    dt = torch.bfloat16
+    q = torch.randn(B, H, L, Dh, generator=g).to(dt).to(DEV)
+    qn = torch.randn(B, H, L, Dh, generator=g).to(dt).to(DEV)
+    k = torch.randn(B, Hkv, L, Dh, generator=g).to(dt).to(DEV)
+    v = torch.randn(B, Hkv, L, Dh, generator=g).to(dt).to(DEV)
+    lam = torch.rand(B, H, L, 1, generator=g).mul(0.8).add(0.1).to(dt).to(DEV)
+    w = (1 + 0.1 * torch.randn(Dh, generator=g)).to(dt).to(DEV)
+    G = H // Hkv
+    full = coda_gqa_l.diff_flash_attn(q, qn, k, v, lam, w, is_causal=True)
+    part = coda_gqa_l.diff_flash_attn(q[:, :2 * G].contiguous(), qn[:, :2 * G].contiguous(), k[:, :2].contiguous(),
+                                      v[:, :2].contiguous(), lam[:, :2 * G].contiguous(), w, is_causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(full[:, :2 * G], part), "the 8-wave and 4-wave flash kernels disagree"
+
+
 @torch.no_grad()
 def test_unbounded_c4_full_length_matches_oracle():
     """configs[3] at its own size: causal differential attention, B 2, H32 /
